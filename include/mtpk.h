@@ -1,0 +1,177 @@
+/* libmtpk — MI355X (gfx950) kernels for the MTP speculative-decode step: MXFP4 routed-expert
+ * MoE, fused router top-k, argmax, greedy / rejection acceptance with rollback indices.
+ *
+ * C ABI: plain device pointers, element counts and a HIP stream handle (hipStream_t passed as
+ * void*; NULL = the default stream). The caller owns every buffer; no entry point allocates or
+ * synchronises, and the launch shape of each depends only on its size arguments, so every
+ * call can be captured into a HIP graph. Return value: 0 on success, MTPK_EINVAL / MTPK_ENODEV
+ * for a rejected call (nothing launched), or a positive hipError_t reported by the launch.
+ * Reference paths below point into the reference engine's repository.
+ */
+#ifndef MTPK_H
+#define MTPK_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MTPK_OK 0
+#define MTPK_EINVAL (-1) /* argument outside the contract: shape, dtype, alignment, null */
+#define MTPK_ENODEV (-2) /* no usable HIP device */
+
+/* Element type codes used by the dtype arguments. */
+#define MTPK_F32 0
+#define MTPK_BF16 1
+#define MTPK_I32 2
+#define MTPK_I64 3
+#define MTPK_U8 4
+
+#define MTPK_MAX_EXPERTS 4096 /* local experts one MoE call may address */
+#define MTPK_MAX_TOP_K 32     /* router_fused.MAX_TOP_K (router_fused.py:37) */
+#define MTPK_MAX_ROUTER_EXPERTS 1024
+#define MTPK_MOE_UNIT_TOKENS 16 /* token columns per MoE work unit (one MFMA N tile) */
+
+/* Human-readable text for a status code (static storage). */
+const char* mtpk_status_string(int status);
+
+/* ABI revision of this header; bumped on any signature change. */
+int mtpk_abi_version(void);
+
+/* ---------------------------------------------------------------- MXFP4 dequant
+ * Replaces `mxfp4.dequant_mxfp4` (mxfp4.py:32-51) for device tensors; the in-kernel decode it
+ * exposes is the one `mxfp4_gemv._dequant_tile`/`_e8m0` define (mxfp4_gemv.py:335-382).
+ * packed u8 [rows, k/2] (low nibble = even element), scale u8 [rows, k/32] (e8m0) ->
+ * out f32 [rows, k]. k % 32 == 0.
+ * mode 0: exact fp32, fp4 * 2^(s-127), scale byte 0 -> +0.0, 255 -> +inf.
+ * mode 1: the MoE kernels' in-register decode (hardware fp4 -> bf16 convert with the block
+ *         scale folded in), widened to fp32; exact for scale bytes 2..252. */
+int mtpk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,
+                       int mode, float* out, void* stream);
+
+/* ---------------------------------------------------------------- routed MXFP4 MoE
+ * Weights in the `load_experts` layout (model.py:758-804): gate_up u8 [E, 2I, H/2] (rows
+ * 0..I-1 gate, I..2I-1 up), gate_up_scale u8 [E, 2I, H/32], down u8 [E, H, I/2],
+ * down_scale u8 [E, H, I/32]; E = expert_hi - expert_lo local experts. Routing is the flat
+ * `(a_expert, a_weight)` of `_routed_fused` (model.py:3096-3100): assignment a = t*top_k + j,
+ * a_expert int32|int64 global ids, a_weight f32|bf16. An assignment is live iff
+ * expert_lo <= a_expert < expert_hi and a_weight != 0 (mxfp4_gemv.py:472-474); dead ones are
+ * dropped on the GPU. x and out are bf16 or f32 [T, H] (row-major, contiguous). */
+
+/* Upper bound on work units for `assignments` over `local_experts` (units of at most
+ * MTPK_MOE_UNIT_TOKENS assignments of one expert). */
+int64_t mtpk_moe_max_units(int64_t assignments, int64_t local_experts);
+
+/* Bytes of workspace `mtpk_fused_moe` needs for these sizes (x_dtype = MTPK_BF16|MTPK_F32). */
+int64_t mtpk_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t local_experts,
+                                 int64_t inter, int64_t hidden, int x_dtype);
+
+/* Work-list build: replaces `mxfp4_gemv.bw_prep`/`_bw_prep_kernel` (mxfp4_gemv.py:1962-2029,
+ * :2320-2376) and `moe_hip.prep` (moe_hip.py:268-285). Counting sort of live assignments by
+ * local expert into sorted i32 [assignments] (expert-grouped; order inside one expert's run
+ * is unspecified), units i32 [3*max_units] = (local expert, first position in sorted,
+ * count <= MTPK_MOE_UNIT_TOKENS), n_units i32 [1]. One workgroup. */
+int mtpk_moe_prep(const void* a_expert, int expert_dtype, const void* a_weight, int weight_dtype,
+                  int64_t assignments, int expert_lo, int expert_hi, int32_t* sorted,
+                  int32_t* units, int64_t max_units, int32_t* n_units, void* stream);
+
+/* gate_up + SiLU: replaces `_gate_up_silu_kernel` (mxfp4_gemv.py:441-493) and the C ABI
+ * `moe_hip_gate_up` (moe_hip.hip:403-421). inter[a, n] = silu(gate_e[n].x_t) * (up_e[n].x_t)
+ * for every live assignment a, written as `inter_planes` bf16 planes of [assignments, I]
+ * (plane p at inter + p*assignments*I) whose sum is the fp32 value: 2 planes for bf16 x,
+ * 3 for f32 x. `x_planes` holds x as bf16 planes [x_nplanes, T, H] (1 plane for bf16 x; f32 x
+ * is first split by `mtpk_split_planes`). */
+int mtpk_moe_gate_up(const uint16_t* x_planes, int x_nplanes, int64_t tokens, int64_t hidden,
+                     const uint8_t* gate_up, const uint8_t* gate_up_scale, int64_t local_experts,
+                     int64_t inter_dim, const int32_t* sorted, const int32_t* units,
+                     const int32_t* n_units, int64_t max_units, int top_k, uint16_t* inter,
+                     int inter_planes, int64_t assignments, void* stream);
+
+/* down: replaces the projection half of `_down_combine_kernel` (mxfp4_gemv.py:496-542) and
+ * `moe_hip_down` (moe_hip.hip:403-452). y f32 [assignments, H] = down_e . inter[a] for every
+ * live assignment (rows of dead assignments are not written). */
+int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, int64_t inter_dim,
+                  const uint8_t* down, const uint8_t* down_scale, int64_t local_experts,
+                  int64_t hidden, const int32_t* sorted, const int32_t* units,
+                  const int32_t* n_units, int64_t max_units, float* y, void* stream);
+
+/* Combine: replaces `bw_combine` / `_dedup_combine_kernel` (mxfp4_gemv.py:1187-1211,
+ * :2240-2264). out[t, n] = sum_{j=0..top_k-1, live} a_weight[a] * y[a, n], in that fixed j
+ * order (no atomics, bit-reproducible); tokens with no live assignment get exact zeros. */
+int mtpk_moe_combine(const float* y, const void* a_expert, int expert_dtype, const void* a_weight,
+                     int weight_dtype, int64_t tokens, int top_k, int64_t hidden, int expert_lo,
+                     int expert_hi, void* out, int out_dtype, void* stream);
+
+/* f32 [n] -> `nplanes` bf16 planes [nplanes, n] whose sum is the input (2 planes: 16
+ * significant bits; 3 planes: all 24). */
+int mtpk_split_planes(const float* src, int64_t n, int nplanes, uint16_t* planes, void* stream);
+
+/* The whole routed MoE in one call (prep, gate_up, down, combine, and the f32 split when
+ * x is f32): the drop-in for `mxfp4_gemv.fused_moe` (mxfp4_gemv.py:1020-1122) and
+ * `moe_hip.fused_moe_hip` (moe_hip.py:357-409). x_dtype = out_dtype = MTPK_BF16 | MTPK_F32.
+ * workspace must hold mtpk_moe_workspace_bytes(...) bytes, 256-byte aligned. */
+int mtpk_fused_moe(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                   const uint8_t* gate_up, const uint8_t* gate_up_scale, const uint8_t* down,
+                   const uint8_t* down_scale, int64_t local_experts, int64_t inter_dim,
+                   const void* a_expert, int expert_dtype, const void* a_weight, int weight_dtype,
+                   int top_k, int expert_lo, int expert_hi, void* workspace,
+                   int64_t workspace_bytes, void* out, void* stream);
+
+/* ---------------------------------------------------------------- router top-k
+ * Replaces `router_fused.route` / `_fused_route_kernel` (router_fused.py:56-151) and the torch
+ * chain in `Model.moe` (model.py:2840-2843). routing [tokens, >= experts_out] f32|bf16 with
+ * row stride `row_stride` elements; softmax (fp32) over the first experts_out columns,
+ * top_k largest (ties: lower expert index first), renormalised to sum 1.
+ * top_w f32 [tokens, top_k], top_i i32|i64 [tokens, top_k], highest weight first. */
+int mtpk_route_topk(const void* routing, int routing_dtype, int64_t tokens, int64_t row_stride,
+                    int experts_out, int top_k, float* top_w, void* top_i, int index_dtype,
+                    void* stream);
+
+/* ---------------------------------------------------------------- argmax
+ * Replaces `logits.argmax(-1)` of the verify step (graph_mtp.py:539-540) and of
+ * `mtp.greedy_token` (mtp.py:640-658). logits f32|bf16 [rows, vocab] with row stride
+ * `row_stride` elements; out_index i64 [rows] = first index of the row maximum (-0.0 ties
+ * +0.0). `partials` is u64 scratch of mtpk_argmax_partials(rows, vocab) entries. */
+int64_t mtpk_argmax_partials(int64_t rows, int64_t vocab);
+int mtpk_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
+                     int64_t row_stride, uint64_t* partials, int64_t* out_index, void* stream);
+
+/* ---------------------------------------------------------------- greedy acceptance
+ * Replaces `_accept_len` + `_commit_limit` + `_fixed_prefix_pack_index` (graph_mtp.py:440-474),
+ * the accept-length tail of `verify_round_step` (graph_mtp.py:541-580) and
+ * `LaneTables.update` (mtp_overlap.py:53-71), for B <= 1024 rows and t = k + 1 columns.
+ * Inputs: step_argmax i64 [B, t] (row stride sa_stride), draft i64 [B, k] (row stride
+ * draft_stride, e.g. token_matrix[:, 1:]), active u8 [B], pos i64 [B], budget i64 [B],
+ * stops i64 [B, n_stops] padded with -1, conv_k1 = conv kernel width - 1.
+ * Outputs (any may be NULL except accept_len):
+ *   accept_len i64 [B]  commit-limited accept length a
+ *   lengths i64 [B]     a + 1 on active rows, 1 on padding rows
+ *   packed_src i64 [B*t], packed_cu i32 [B+1]   fixed-size prefix-pack gather map
+ *   conv_idx i64 [B, conv_k1]   min(lengths + w, conv_k1 + t - 1)
+ *   keep u8 [B, t]      active && s <= a
+ *   bonus i64 [B]       step_argmax[j, a]
+ *   next_pos i64 [B], budget_left i64 [B], live u8 [B]   lane-table update values
+ *   hidden_src i64 [B]  j*t + a, the verify row whose hidden state seeds the next draft */
+int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
+                       int64_t draft_stride, const uint8_t* active, const int64_t* pos,
+                       const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
+                       int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                       int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                       int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                       int64_t* hidden_src, void* stream);
+
+/* ---------------------------------------------------------------- test probes
+ * In-bounds probe of the compiler builtin this library's MoE relies on: one wave computes
+ * d = A(16x32) * B(32x16) with v_mfma_f32_16x16x32_bf16 from per-lane operand registers
+ * a_lanes/b_lanes bf16 [64, 8] and writes its four result registers per lane to d_lanes
+ * f32 [64, 4]. The caller checks the lane layout against a host matmul. No counterpart in the
+ * reference (it verifies a gfx950 instruction's register layout). */
+int mtpk_probe_mfma_16x16x32(const uint16_t* a_lanes, const uint16_t* b_lanes, float* d_lanes,
+                             void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MTPK_H */

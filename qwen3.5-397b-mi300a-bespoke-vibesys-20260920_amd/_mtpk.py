@@ -1,0 +1,148 @@
+"""ctypes binding of `libmtpk.so` (include/mtpk.h), the C ABI every device op here goes through.
+
+The library is built in-tree (`build_lib.py`) and loaded from this directory. When it is
+missing or does not load, every device entry point raises: there is no silent fallback.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_int, c_int64, c_void_p
+from pathlib import Path
+
+import torch
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libmtpk.so"
+
+F32, BF16, I32, I64, U8 = 0, 1, 2, 3, 4
+EINVAL, ENODEV = -1, -2
+ABI_VERSION = 1
+MAX_TOP_K = 32
+MAX_EXPERTS = 4096
+MAX_ROUTER_EXPERTS = 1024
+UNIT_TOKENS = 16
+
+_SIGNATURES: dict[str, tuple[object, list]] = {
+    "mtpk_status_string": (ctypes.c_char_p, [c_int]),
+    "mtpk_abi_version": (c_int, []),
+    "mtpk_dequant_mxfp4": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
+    "mtpk_moe_max_units": (c_int64, [c_int64, c_int64]),
+    "mtpk_moe_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int]),
+    "mtpk_moe_prep": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int, c_void_p, c_void_p, c_int64,
+         c_void_p, c_void_p],
+    ),
+    "mtpk_moe_gate_up": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
+         c_void_p, c_void_p, c_int64, c_int, c_void_p, c_int, c_int64, c_void_p],
+    ),
+    "mtpk_moe_down": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
+         c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
+    ),
+    "mtpk_moe_combine": (
+        c_int,
+        [c_void_p, c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int64, c_int, c_int,
+         c_void_p, c_int, c_void_p],
+    ),
+    "mtpk_split_planes": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p]),
+    "mtpk_fused_moe": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+         c_int64, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int64,
+         c_void_p, c_void_p],
+    ),
+    "mtpk_route_topk": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, c_int, c_int, c_void_p, c_void_p, c_int, c_void_p],
+    ),
+    "mtpk_argmax_partials": (c_int64, [c_int64, c_int64]),
+    "mtpk_argmax_rows": (
+        c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p]
+    ),
+    "mtpk_greedy_accept": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
+         c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "mtpk_probe_mfma_16x16x32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+}
+
+EXPORTED = tuple(_SIGNATURES)
+"""Every entry point `include/mtpk.h` declares."""
+
+_lib: ctypes.CDLL | None = None
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded library; raises `RuntimeError` if it is not built or does not load."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"libmtpk.so is not built at {LIB_PATH}; run `python __graft_entry__.py build` "
+            "(or build_lib.py) first"
+        )
+    try:
+        handle = ctypes.CDLL(str(LIB_PATH))
+    except OSError as exc:
+        raise RuntimeError(f"libmtpk.so failed to load: {exc}") from exc
+    for name, (restype, argtypes) in _SIGNATURES.items():
+        fn = getattr(handle, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    if handle.mtpk_abi_version() != ABI_VERSION:
+        raise RuntimeError("libmtpk.so ABI version does not match the Python binding")
+    _lib = handle
+    return handle
+
+
+def check(status: int, what: str) -> None:
+    """Raise on a nonzero status; the message names the entry point and the cause."""
+    if status != 0:
+        text = lib().mtpk_status_string(status).decode()
+        if status == EINVAL:
+            raise ValueError(f"{what}: {text}")
+        raise RuntimeError(f"{what}: {text} (status {status})")
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def stream_of(device: torch.device) -> int:
+    """Handle of torch's current stream on `device` (what the kernels launch on)."""
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def float_code(dtype: torch.dtype) -> int:
+    if dtype == torch.float32:
+        return F32
+    if dtype == torch.bfloat16:
+        return BF16
+    raise ValueError(f"unsupported float dtype {dtype} (float32 or bfloat16)")
+
+
+def index_code(dtype: torch.dtype) -> int:
+    if dtype == torch.int32:
+        return I32
+    if dtype == torch.int64:
+        return I64
+    raise ValueError(f"unsupported index dtype {dtype} (int32 or int64)")
+
+
+def require_device(*tensors: torch.Tensor) -> torch.device:
+    """All tensors on one HIP device; returns it. CPU tensors are a caller error here."""
+    dev = tensors[0].device
+    for t in tensors:
+        if t.device.type != "cuda":
+            raise ValueError("libmtpk entry points take device tensors")
+        if t.device != dev:
+            raise ValueError("all tensors must be on the same device")
+    return dev

@@ -1,0 +1,241 @@
+// Verify-step tail for gfx950: row argmax over the vocabulary and greedy acceptance with its
+// rollback indices.
+//
+// argmax: the vocabulary is cut into chunks so rows x chunks workgroups stream the logits at
+// HBM rate; each workgroup reduces (value, index) keys whose maximum is the first-occurrence
+// argmax (mtpk_common.h argmax_key), so the split and the reduction order cannot change the
+// answer. A second tiny kernel takes the max over a row's chunk keys.
+// greedy accept: one workgroup, one thread per verify row (B <= 1024), plus a block scan for
+// the prefix-pack offsets.
+
+#include "mtpk_device.h"
+#include "mtpk_host.h"
+
+namespace mtpk {
+
+constexpr int kArgmaxThreads = 256;
+
+__global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
+    const void* __restrict__ logits, int dt, int64_t stride, int64_t vocab, int64_t chunk,
+    int vec, uint64_t* __restrict__ partials) {
+  const int64_t row = blockIdx.y;
+  const int64_t begin = (int64_t)blockIdx.x * chunk;
+  const int64_t end = begin + chunk < vocab ? begin + chunk : vocab;
+  const int tid = threadIdx.x;
+  uint64_t best = 0;
+  if (vec && dt == MTPK_BF16) {
+    const uint16_t* base = reinterpret_cast<const uint16_t*>(logits) + row * stride;
+    for (int64_t i = begin + (int64_t)tid * 8; i < end; i += (int64_t)kArgmaxThreads * 8) {
+      if (i + 8 <= end) {
+        const u32x4_t v = ld16(base + i);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint32_t w = v[q];
+          const uint64_t k0 = argmax_key(bf16_to_f32((uint16_t)(w & 0xffffu)), (uint32_t)(i + 2 * q));
+          const uint64_t k1 = argmax_key(bf16_to_f32((uint16_t)(w >> 16)), (uint32_t)(i + 2 * q + 1));
+          best = k0 > best ? k0 : best;
+          best = k1 > best ? k1 : best;
+        }
+      } else {
+        for (int64_t q = i; q < end; ++q) {
+          const uint64_t k = argmax_key(bf16_to_f32(base[q]), (uint32_t)q);
+          best = k > best ? k : best;
+        }
+      }
+    }
+  } else if (vec && dt == MTPK_F32) {
+    const float* base = reinterpret_cast<const float*>(logits) + row * stride;
+    for (int64_t i = begin + (int64_t)tid * 4; i < end; i += (int64_t)kArgmaxThreads * 4) {
+      if (i + 4 <= end) {
+        const u32x4_t v = ld16(base + i);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const uint64_t k = argmax_key(bits_f32(v[q]), (uint32_t)(i + q));
+          best = k > best ? k : best;
+        }
+      } else {
+        for (int64_t q = i; q < end; ++q) {
+          const uint64_t k = argmax_key(base[q], (uint32_t)q);
+          best = k > best ? k : best;
+        }
+      }
+    }
+  } else {
+    for (int64_t i = begin + tid; i < end; i += kArgmaxThreads) {
+      const uint64_t k = argmax_key(load_float(logits, dt, row * stride + i), (uint32_t)i);
+      best = k > best ? k : best;
+    }
+  }
+  best = wave_max_u64(best);
+  __shared__ uint64_t part[kArgmaxThreads / kWave];
+  if ((tid & (kWave - 1)) == 0) part[tid / kWave] = best;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t b = part[0];
+    for (int w = 1; w < kArgmaxThreads / kWave; ++w) b = part[w] > b ? part[w] : b;
+    partials[row * gridDim.x + blockIdx.x] = b;
+  }
+}
+
+__global__ __launch_bounds__(256) void k_argmax_final(const uint64_t* __restrict__ partials,
+                                                      int64_t rows, int chunks,
+                                                      int64_t* __restrict__ out) {
+  const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (row >= rows) return;
+  uint64_t b = 0;
+  for (int c = 0; c < chunks; ++c) {
+    const uint64_t k = partials[row * chunks + c];
+    b = k > b ? k : b;
+  }
+  out[row] = (int64_t)argmax_key_index(b);
+}
+
+constexpr int kAcceptThreads = 1024;
+
+__global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
+    const int64_t* __restrict__ sa, int64_t ss, const int64_t* __restrict__ draft, int64_t ds,
+    const uint8_t* __restrict__ active, const int64_t* __restrict__ pos,
+    const int64_t* __restrict__ budget, const int64_t* __restrict__ stops, int n_stops, int B,
+    int t, int conv_k1, int64_t* __restrict__ accept_len, int64_t* __restrict__ lengths,
+    int64_t* __restrict__ packed_src, int32_t* __restrict__ packed_cu,
+    int64_t* __restrict__ conv_idx, uint8_t* __restrict__ keep, int64_t* __restrict__ bonus,
+    int64_t* __restrict__ next_pos, int64_t* __restrict__ budget_left,
+    uint8_t* __restrict__ live, int64_t* __restrict__ hidden_src) {
+  __shared__ int cu[kAcceptThreads + 1];
+  __shared__ int wtot[kAcceptThreads / kWave];
+  const int j = threadIdx.x, lane = j & (kWave - 1), wv = j / kWave;
+  const int k = t - 1;
+  int len = 0;
+  if (j < B) {
+    const int64_t* row = sa + (int64_t)j * ss;
+    int acc = 0;
+    while (acc < k && draft[(int64_t)j * ds + acc] == row[acc]) ++acc;
+    int first_stop = t;
+    for (int s = 0; s < t && first_stop == t; ++s)
+      for (int q = 0; q < n_stops; ++q)
+        if (stops[(int64_t)j * n_stops + q] == row[s]) {
+          first_stop = s;
+          break;
+        }
+    const int64_t bud = budget[j];
+    int64_t lim = acc < first_stop ? acc : first_stop;
+    if (bud - 1 < lim) lim = bud - 1;
+    if (lim < 0) lim = 0;
+    const int a = (int)lim;
+    const bool act = active[j] != 0;
+    len = act ? a + 1 : 1;
+    accept_len[j] = a;
+    if (lengths) lengths[j] = len;
+    const int64_t bn = row[a];
+    if (bonus) bonus[j] = bn;
+    if (next_pos) next_pos[j] = pos[j] + a + 1;
+    const int64_t left = bud - (a + 1);
+    if (budget_left) budget_left[j] = left;
+    if (live) {
+      bool stopped = false;
+      for (int q = 0; q < n_stops; ++q) stopped |= stops[(int64_t)j * n_stops + q] == bn;
+      live[j] = (!stopped && left > 0) ? 1 : 0;
+    }
+    if (hidden_src) hidden_src[j] = (int64_t)j * t + a;
+    if (keep)
+      for (int s = 0; s < t; ++s) keep[(int64_t)j * t + s] = (act && s <= a) ? 1 : 0;
+    if (conv_idx)
+      for (int w = 0; w < conv_k1; ++w) {
+        const int v = len + w;
+        conv_idx[(int64_t)j * conv_k1 + w] = v < conv_k1 + t - 1 ? v : conv_k1 + t - 1;
+      }
+  }
+  const int inc = wave_incl_scan(len, lane);
+  if (lane == kWave - 1) wtot[wv] = inc;
+  __syncthreads();
+  int off = 0;
+  for (int w = 0; w < wv; ++w) off += wtot[w];
+  if (j < B) cu[j + 1] = off + inc;
+  if (j == 0) cu[0] = 0;
+  __syncthreads();
+  if (packed_cu) {
+    if (j < B) packed_cu[j] = cu[j];
+    if (j == 0) packed_cu[B] = cu[B];  // B may equal the thread count
+  }
+  if (packed_src) {
+    const int total = B * t;
+    for (int dst = j; dst < total; dst += kAcceptThreads) {
+      // lane = #{i in 1..B : cu[i] <= dst}, clamped to B - 1 (graph_mtp.py:445)
+      int lo = 1, hi = B + 1;
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (cu[mid] <= dst)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      int ln = lo - 1;
+      if (ln > B - 1) ln = B - 1;
+      int local = dst - cu[ln];
+      local = local < 0 ? 0 : (local > t - 1 ? t - 1 : local);
+      packed_src[dst] = (int64_t)ln * t + local;
+    }
+  }
+}
+
+}  // namespace mtpk
+
+using namespace mtpk;
+
+extern "C" {
+
+int64_t mtpk_argmax_partials(int64_t rows, int64_t vocab) {
+  if (rows <= 0 || vocab <= 0) return 0;
+  // Enough workgroups to stream at HBM rate (about 8 per CU on 256 CUs), chunks of >= 2048.
+  int64_t chunks = (2048 + rows - 1) / rows;
+  const int64_t by_len = (vocab + 2047) / 2048;
+  if (chunks > by_len) chunks = by_len;
+  if (chunks < 1) chunks = 1;
+  if (chunks > 4096) chunks = 4096;
+  return rows * chunks;
+}
+
+int mtpk_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
+                     int64_t row_stride, uint64_t* partials, int64_t* out_index, void* stream) {
+  if (!logits || !partials || !out_index) return MTPK_EINVAL;
+  if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (rows < 0 || rows > 65535 || vocab <= 0 || vocab > INT32_MAX || row_stride < vocab)
+    return MTPK_EINVAL;
+  if (rows == 0) return 0;
+  const int64_t chunks = mtpk_argmax_partials(rows, vocab) / rows;
+  const int per_vec = dtype == MTPK_BF16 ? 8 : 4;
+  int64_t chunk = (vocab + chunks - 1) / chunks;
+  chunk = (chunk + per_vec - 1) / per_vec * per_vec;
+  const int vec = aligned16(logits) && (row_stride % per_vec) == 0;
+  const hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_argmax_partial, dim3((unsigned)chunks, (unsigned)rows),
+                     dim3(kArgmaxThreads), 0, st, logits, dtype, row_stride, vocab, chunk, vec,
+                     partials);
+  int rc = status_of(hipGetLastError());
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_argmax_final, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0, st,
+                     partials, rows, (int)chunks, out_index);
+  return status_of(hipGetLastError());
+}
+
+int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
+                       int64_t draft_stride, const uint8_t* active, const int64_t* pos,
+                       const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
+                       int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                       int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                       int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                       int64_t* hidden_src, void* stream) {
+  if (!step_argmax || !active || !budget || !accept_len) return MTPK_EINVAL;
+  if (batch <= 0 || batch > kAcceptThreads || t < 1 || t > 64) return MTPK_EINVAL;
+  if (t > 1 && !draft) return MTPK_EINVAL;
+  if (n_stops < 0 || (n_stops > 0 && !stops) || conv_k1 < 0) return MTPK_EINVAL;
+  if (next_pos && !pos) return MTPK_EINVAL;
+  if (sa_stride < t || (t > 1 && draft_stride < t - 1)) return MTPK_EINVAL;
+  hipLaunchKernelGGL(k_greedy_accept, dim3(1), dim3(kAcceptThreads), 0, (hipStream_t)stream,
+                     step_argmax, sa_stride, draft, draft_stride, active, pos, budget, stops,
+                     n_stops, batch, t, conv_k1, accept_len, lengths, packed_src, packed_cu,
+                     conv_idx, keep, bonus, next_pos, budget_left, live, hidden_src);
+  return status_of(hipGetLastError());
+}
+
+}  // extern "C"

@@ -1,0 +1,101 @@
+// Device-side building blocks shared by the libmtpk translation units (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "mtpk.h"
+#include "mtpk_common.h"
+
+namespace mtpk {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+
+constexpr int kWave = 64;
+
+__device__ inline u32x4_t ld16(const void* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+__device__ inline u32x4_t zero16() { return u32x4_t{0u, 0u, 0u, 0u}; }
+
+// Eight e2m1 codes of one packed dword (code j = nibble j, low nibble first) times the block
+// scale, as eight bf16 in element order: the hardware fp4 -> bf16 convert with the e8m0 scale
+// applied (one instruction per byte). `scale` is the fp32 2^(s-127).
+__device__ inline bf16x8_t decode8(uint32_t w, float scale) {
+  const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
+  const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
+  const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);
+  const bf16x2_t p3 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 3);
+  const u32x4_t r{__builtin_bit_cast(uint32_t, p0), __builtin_bit_cast(uint32_t, p1),
+                  __builtin_bit_cast(uint32_t, p2), __builtin_bit_cast(uint32_t, p3)};
+  return __builtin_bit_cast(bf16x8_t, r);
+}
+
+__device__ inline bf16x8_t as_bf16x8(u32x4_t v) { return __builtin_bit_cast(bf16x8_t, v); }
+
+__device__ inline f32x4_t mfma16x16x32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// Typed scalar loads/stores selected by a runtime dtype code.
+__device__ inline int64_t load_index(const void* p, int dtype, int64_t i) {
+  return dtype == MTPK_I64 ? reinterpret_cast<const int64_t*>(p)[i]
+                           : (int64_t)reinterpret_cast<const int32_t*>(p)[i];
+}
+
+__device__ inline float load_float(const void* p, int dtype, int64_t i) {
+  return dtype == MTPK_F32 ? reinterpret_cast<const float*>(p)[i]
+                           : bf16_to_f32(reinterpret_cast<const uint16_t*>(p)[i]);
+}
+
+__device__ inline void store_float(void* p, int dtype, int64_t i, float v) {
+  if (dtype == MTPK_F32)
+    reinterpret_cast<float*>(p)[i] = v;
+  else
+    reinterpret_cast<uint16_t*>(p)[i] = f32_to_bf16(v);
+}
+
+__device__ inline void store_index(void* p, int dtype, int64_t i, int64_t v) {
+  if (dtype == MTPK_I64)
+    reinterpret_cast<int64_t*>(p)[i] = v;
+  else
+    reinterpret_cast<int32_t*>(p)[i] = (int32_t)v;
+}
+
+// Wave-wide reductions over 64 lanes (butterfly: every lane ends with the result).
+__device__ inline float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, kWave));
+  return v;
+}
+
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, kWave);
+  return v;
+}
+
+__device__ inline uint64_t wave_max_u64(uint64_t v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const uint32_t lo = __shfl_xor((uint32_t)v, o, kWave);
+    const uint32_t hi = __shfl_xor((uint32_t)(v >> 32), o, kWave);
+    const uint64_t w = ((uint64_t)hi << 32) | lo;
+    v = w > v ? w : v;
+  }
+  return v;
+}
+
+// Inclusive prefix sum across the wave.
+__device__ inline int wave_incl_scan(int v, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const int u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+}  // namespace mtpk
