@@ -36,6 +36,13 @@ EXPERT_BYTES = 4_194_304 + 262_144 + 2_097_152 + 131_072  # gate_up + scales + d
 GATE_UP_BYTES = 4_194_304 + 262_144
 PEAK_GBS = 8000.0
 METRIC = json.loads((ROOT / "BASELINE.json").read_text())["metric"]
+WORKLOAD_TEXT = {
+    "M192": "C3 routed MXFP4 MoE verify layer, M=192 (B=48, k=3), Zipf(1.1) top-10 of 512, "
+            "H=4096 I=1024, 5% zero weights",
+    "M32": "C3 routed MXFP4 MoE verify layer, M=32 (B=8, k=3), Zipf(1.1) top-10 of 512, "
+           "H=4096 I=1024, 5% zero weights",
+    "M1": "C2 routed MXFP4 MoE decode layer, M=1, router softmax top-10 of 512, H=4096 I=1024",
+}
 
 
 def log(msg: str) -> None:
@@ -72,7 +79,8 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--workloads", default="M1,M32,M192",
-                    help="comma list of M1, M32, M192 (M192 is always run: it carries `value`)")
+                    help="comma list of M1, M32, M192; `value` is measured on M192 when listed, "
+                         "else on the last one listed")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -115,7 +123,13 @@ def main() -> int:
         return x, a_e, a_w, d_live(ne, nw)
 
     results = {}
-    wanted = set(args.workloads.split(",")) | {"M192"}
+    wanted = args.workloads.split(",")
+    rows_of = {"M1": 1, "M32": 32, "M192": 192}
+    if not wanted or any(w not in rows_of for w in wanted):
+        print(f"--workloads takes a comma list of {sorted(rows_of)}", file=sys.stderr)
+        return 2
+    head = "M192" if "M192" in wanted else wanted[-1]
+    head_m = rows_of[head]
     for name, m, kind in (("M1", 1, "router"), ("M32", 32, "zipf"), ("M192", 192, "zipf")):
         if name not in wanted:
             continue
@@ -149,8 +163,9 @@ def main() -> int:
         log(f"{name}: {us:.1f} us/layer (graph replay), {byts / us / 1e3:.0f} GB/s, D_live~{np.mean(dls):.0f}")
         results[name]["_state"] = (runner, ins, outs, dls)
 
-    # timed region for `value`: K eager steps at M=192 with HIP events around gate_up and down
-    runner, ins, outs, dls = results["M192"].pop("_state")
+    # timed region for `value`: K eager steps of the headline workload with HIP events around
+    # gate_up and down
+    runner, ins, outs, dls = results[head].pop("_state")
     for k in results:
         results[k].pop("_state", None)
     ev = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
@@ -169,15 +184,15 @@ def main() -> int:
     ms = t0.elapsed_time(t1) / args.steps
     gu_ms = float(np.mean([a.elapsed_time(b) for a, b in ev["gate_up"]]))
     dn_ms = float(np.mean([a.elapsed_time(b) for a, b in ev["down"]]))
-    step_bytes = [layer_bytes(192, dls[s % L]) for s in range(args.steps)]
+    step_bytes = [layer_bytes(head_m, dls[s % L]) for s in range(args.steps)]
     value = float(np.mean(step_bytes)) / (ms * 1e-3) / 1e9
-    gu_bytes = float(np.mean([dls[s % L] * GATE_UP_BYTES + 192 * H * 2 for s in range(args.steps)]))
+    gu_bytes = float(np.mean([dls[s % L] * GATE_UP_BYTES + head_m * H * 2 for s in range(args.steps)]))
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    log(f"eager M192: {ms * 1e3:.1f} us/step, gate_up {gu_ms * 1e3:.1f} us ({gu_gbs:.0f} GB/s), "
+    log(f"eager {head}: {ms * 1e3:.1f} us/step, gate_up {gu_ms * 1e3:.1f} us ({gu_gbs:.0f} GB/s), "
         f"down {dn_ms * 1e3:.1f} us, wall {wall:.2f}s")
 
     cpu = None
-    if not args.no_cpu:
+    if not args.no_cpu and head == "M192":
         cpu = cpu_baseline(layers[0], ins[0], dls[0], args.cpu_seconds)
 
     line = {
@@ -194,9 +209,8 @@ def main() -> int:
         "dtype": "bf16",
         "data": "synthetic (random MXFP4 bytes 0..255, e8m0 scales 118..130, bf16 N(0,1) x)",
         "config": {
-            "workload": "C3 routed MXFP4 MoE verify layer, M=192 (B=48, k=3), Zipf(1.1) top-10 of 512, "
-                        "H=4096 I=1024, 5% zero weights",
-            "rows": 192, "hidden": H, "intermediate": I, "experts": E, "top_k": TOP_K,
+            "workload": WORKLOAD_TEXT[head],
+            "rows": head_m, "hidden": H, "intermediate": I, "experts": E, "top_k": TOP_K,
             "layer_copies": L, "timing": "eager stream, HIP events",
         },
         "frac_of_peak": round(value / PEAK_GBS, 4),
@@ -204,7 +218,7 @@ def main() -> int:
         "gbs_graph": {k: round(v["gbs"], 1) for k, v in results.items()},
         "d_live": {k: round(v["d_live_mean"], 1) for k, v in results.items()},
         "roofline": {
-            "kernel": "k_moe_gate_up<1,2,2>",
+            "kernel": "k_moe_gate_up<1,2,4,4> (direct)" if runner.direct else "k_moe_gate_up<1,2,1,4>",
             "bound": "hbm",
             "achieved": round(gu_gbs, 1),
             "peak": PEAK_GBS,

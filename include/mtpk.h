@@ -96,6 +96,30 @@ int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, 
                   int64_t hidden, const int32_t* sorted, const int32_t* units,
                   const int32_t* n_units, int64_t max_units, float* y, void* stream);
 
+/* Largest token count `mtpk_fused_moe` serves with the direct pipeline below (no prep, no y,
+ * no separate combine); wider batches take prep -> gate_up -> down -> combine. */
+int mtpk_moe_direct_max_tokens(void);
+
+/* gate_up + SiLU with one work unit per assignment, read straight from the routing (the
+ * per-assignment form of `_gate_up_silu_kernel`, mxfp4_gemv.py:441-493, including its in-kernel
+ * drop of unowned / zero-weight assignments at :472-474). Same output as `mtpk_moe_gate_up`;
+ * inter planes are [tokens*top_k, I]. */
+int mtpk_moe_gate_up_direct(const uint16_t* x_planes, int x_nplanes, int64_t tokens,
+                            int64_t hidden, const uint8_t* gate_up, const uint8_t* gate_up_scale,
+                            int64_t local_experts, int64_t inter_dim, const void* a_expert,
+                            int expert_dtype, const void* a_weight, int weight_dtype, int top_k,
+                            int expert_lo, int expert_hi, uint16_t* inter, int inter_planes,
+                            void* stream);
+
+/* down + weighted combine per token: replaces `_down_combine_kernel` (mxfp4_gemv.py:496-542).
+ * out[t] = sum over t's live assignments of a_weight * (down_e . inter[a]), no atomics and no
+ * dependence on scheduling; tokens with no live assignment get exact zeros. */
+int mtpk_moe_down_combine(const uint16_t* inter, int inter_planes, int64_t inter_dim,
+                          const uint8_t* down, const uint8_t* down_scale, int64_t local_experts,
+                          int64_t hidden, const void* a_expert, int expert_dtype,
+                          const void* a_weight, int weight_dtype, int64_t tokens, int top_k,
+                          int expert_lo, int expert_hi, void* out, int out_dtype, void* stream);
+
 /* Combine: replaces `bw_combine` / `_dedup_combine_kernel` (mxfp4_gemv.py:1187-1211,
  * :2240-2264). out[t, n] = sum_{j=0..top_k-1, live} a_weight[a] * y[a, n], in that fixed j
  * order (no atomics, bit-reproducible); tokens with no live assignment get exact zeros. */

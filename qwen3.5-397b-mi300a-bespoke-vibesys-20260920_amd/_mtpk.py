@@ -7,13 +7,15 @@ missing or does not load, every device entry point raises: there is no silent fa
 from __future__ import annotations
 
 import ctypes
+import os
 from ctypes import c_int, c_int64, c_void_p
 from pathlib import Path
 
 import torch
 
 HERE = Path(__file__).resolve().parent
-LIB_PATH = HERE / "libmtpk.so"
+LIB_PATH = Path(os.environ.get("MTPK_LIB", str(HERE / "libmtpk.so")))
+"""The in-tree build; `MTPK_LIB` points the binding at another build of the same sources."""
 
 F32, BF16, I32, I64, U8 = 0, 1, 2, 3, 4
 EINVAL, ENODEV = -1, -2
@@ -43,6 +45,17 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         c_int,
         [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
          c_void_p, c_void_p, c_int64, c_void_p, c_void_p],
+    ),
+    "mtpk_moe_direct_max_tokens": (c_int, []),
+    "mtpk_moe_gate_up_direct": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p,
+         c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p],
+    ),
+    "mtpk_moe_down_combine": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int,
+         c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p, c_int, c_void_p],
     ),
     "mtpk_moe_combine": (
         c_int,

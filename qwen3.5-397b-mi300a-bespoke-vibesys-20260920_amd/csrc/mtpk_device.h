@@ -20,6 +20,65 @@ __device__ inline u32x4_t ld16(const void* p) { return *reinterpret_cast<const u
 
 __device__ inline u32x4_t zero16() { return u32x4_t{0u, 0u, 0u, 0u}; }
 
+// Raw buffer loads. A buffer resource covers [base, base + bytes); a load whose byte offset
+// lies outside returns zeros and touches no memory, so a lane that has nothing to load gets
+// the offset kOutOfRange instead of a branch around its load (branches around loads make the
+// compiler wait for every outstanding load at the join, which would drain the trip ring).
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOutOfRange = 0x80000000u;
+constexpr int kRsrcWord3 = 0x00020000;  // raw (unformatted) 32-bit buffer, gfx9 family
+
+__device__ inline rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                           kRsrcWord3);
+}
+
+__device__ inline u32x4_t buf16(rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+__device__ inline uint32_t buf1(rsrc_t r, uint32_t off) {
+  return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
+}
+
+__device__ inline int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
+
+// The e8m0 scales of D consecutive trips of one weight row: bytes [4 tr0, 4 tr0 + 4D) of the
+// row, one 8- or 16-byte load instead of D byte loads. Trip tr0 + s of lane group g reads byte
+// 4s + g, i.e. byte g of dword s.
+template <int D>
+struct ScaleChunk;
+
+template <>
+struct ScaleChunk<2> {
+  uint32_t d[2];
+  __device__ inline void load(rsrc_t r, uint32_t off) {
+    typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
+    const u32x2_t v = __builtin_bit_cast(u32x2_t, __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, 0));
+    d[0] = v[0];
+    d[1] = v[1];
+  }
+  __device__ inline uint32_t byte(int s, int g) const { return (d[s] >> (8 * g)) & 0xffu; }
+};
+
+template <>
+struct ScaleChunk<4> {
+  uint32_t d[4];
+  __device__ inline void load(rsrc_t r, uint32_t off) {
+    const u32x4_t v = buf16(r, off);
+    d[0] = v[0];
+    d[1] = v[1];
+    d[2] = v[2];
+    d[3] = v[3];
+  }
+  __device__ inline uint32_t byte(int s, int g) const { return (d[s] >> (8 * g)) & 0xffu; }
+};
+
+// Scheduling fence between the steps of a trip ring: the compiler may not move any instruction
+// across it, so each step's refill loads stay behind that step's MFMAs and the loads consumed
+// next are always the oldest outstanding ones (the wait before them leaves D-1 trips in flight).
+__device__ inline void ring_fence() { __builtin_amdgcn_sched_barrier(0); }
+
 // Eight e2m1 codes of one packed dword (code j = nibble j, low nibble first) times the block
 // scale, as eight bf16 in element order: the hardware fp4 -> bf16 convert with the e8m0 scale
 // applied (one instruction per byte). `scale` is the fp32 2^(s-127).

@@ -1,12 +1,17 @@
 // Routed MXFP4 MoE for gfx950: work-list prep, gate_up + SiLU, down, fixed-order combine.
 //
-// Data flow for one call (all on the caller's stream, no host sync, static launch shapes):
-//   prep      routing -> expert-grouped `sorted` + work units (expert, first, count <= 16)
-//   gate_up   per (unit, 16 intermediate rows): MXFP4 decoded in registers, bf16 MFMA with the
-//             unit's activation rows, K split over the 4 waves of the workgroup and reduced in
-//             LDS; SiLU(gate) * up written as bf16 hi/lo planes (16 significant bits)
-//   down      per (unit, 64 hidden rows): same decode, MFMA over both inter planes; fp32 y
-//   combine   per token: sum of weight * y over its top_k assignments in j order
+// Two pipelines, chosen by batch size (launch shapes depend only on tokens and top_k; no host
+// sync), all on the caller's stream:
+//   unit path (tokens > 4): prep -> gate_up -> down -> combine
+//     prep      routing -> expert-grouped `sorted` + work units (expert, first, count <= 16)
+//     gate_up   per (unit, 16 intermediate rows): MXFP4 decoded in registers by the hardware
+//               fp4 converter, bf16 MFMA with the unit's activation rows; SiLU(gate) * up stored
+//               as bf16 hi/lo planes (16 significant bits)
+//     down      per (unit, 64 hidden rows): same decode, MFMA over both planes; fp32 y
+//     combine   per token: sum of weight * y over its top_k assignments in j order
+//   direct path (tokens <= 4): gate_up with one unit per assignment (no prep), then a
+//     per-token down that also combines (no y, no combine launch)
+// Each wave keeps a ring of trips (weight + activation loads) in flight ahead of the MFMAs.
 // The weight stream is the only HBM-sized traffic; nothing dequantised is ever stored.
 // Lane mapping and K coverage of one MFMA tile: see mtpk_common.h ("MoE lane mapping").
 
@@ -91,198 +96,452 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
   }
 }
 
+// ---------------------------------------------------------------- work units
+//
+// Unit mode: units come from the prep kernel's list (expert, first position in `sorted`,
+// count <= 16). Direct mode (small batches): every assignment is its own unit, read straight from
+// the routing with the live test applied in place, so no prep launch is needed.
+
+struct UnitSrc {
+  const int32_t* units;
+  const int32_t* sorted;
+  const int32_t* n_units;
+  int max_units;
+  const void* a_expert;
+  const void* a_weight;
+  int edt, wdt, lo, n_experts, assignments, direct;
+};
+
+__device__ inline int unit_count(const UnitSrc& s) {
+  return s.direct ? s.assignments : min(*s.n_units, s.max_units);
+}
+
+__device__ inline void unit_get(const UnitSrc& s, int u, int& e, int& first, int& cnt) {
+  if (s.direct) {
+    const int64_t ex = load_index(s.a_expert, s.edt, u) - s.lo;
+    const bool live = ex >= 0 && ex < s.n_experts && load_float(s.a_weight, s.wdt, u) != 0.f;
+    e = live ? (int)ex : 0;
+    first = u;
+    cnt = live ? 1 : 0;
+  } else {
+    e = s.units[3 * u];
+    first = s.units[3 * u + 1];
+    cnt = s.units[3 * u + 2];
+  }
+}
+
+__device__ inline int unit_member(const UnitSrc& s, int pos) { return s.direct ? pos : s.sorted[pos]; }
+
+// SiLU(gate) * up, stored as OP bf16 planes (hi, lo) or (hi, mid, lo) whose sum is the value.
+template <int OP>
+__device__ inline void store_planes(uint16_t* dst, int64_t plane, float v) {
+  if (OP == 2) {
+    uint16_t hi, lo;
+    split_bf16(v, &hi, &lo);
+    dst[0] = hi;
+    dst[plane] = lo;
+  } else {
+    uint16_t hi, mid, lo;
+    split3_bf16(v, &hi, &mid, &lo);
+    dst[0] = hi;
+    dst[plane] = mid;
+    dst[2 * plane] = lo;
+  }
+}
+
 // ---------------------------------------------------------------- gate_up + SiLU
 //
-// Work item = (unit u, tile of 16 intermediate rows nt); items are unit-major. The four waves
-// of a workgroup take trips w, w+4, ... of the K loop (a trip is 4 scale blocks = 128 K per
-// wave: one 16-byte weight load per lane per projection) and reduce their partial tiles in LDS.
-// XP = bf16 planes of x (1: bf16 activations; 3: an fp32 activation split exactly).
-// OP = bf16 planes written for inter (2 or 3). C = trips whose loads are issued together.
+// Item = (unit, 16 intermediate rows n): the gate rows n and the matching up rows I + n share
+// every activation load, so SiLU(gate) * up is formed in registers. Each wave streams its trips
+// (a trip = one 32-element scale block per lane group, i.e. 128 K of 16 rows: one 16-byte load
+// per lane per projection) through a ring of D trips in flight: the loads of trip i + D are
+// issued right after trip i is consumed, so every wave keeps D trips outstanding.
+// SPLIT = 4: the workgroup's 4 waves share one item, each taking a contiguous quarter of the K
+// trips, and reduce their partial tiles in LDS (small batches: 4x the waves in flight).
+// SPLIT = 1: every wave owns whole items (wide batches). XP = bf16 planes of x; OP = planes of
+// the stored intermediate. SV: the scales of D trips arrive in one 4D-byte load per row
+// (rows whose scale bytes are a multiple of 16), else one byte load per trip.
 
-template <int XP, int OP, int C>
+template <int XP>
+struct GuTrip {
+  u32x4_t wg, wu;
+  uint32_t sg, su;
+  u32x4_t xv[XP][4];
+};
+
+template <int XP, int OP, int SPLIT, int D, bool SV>
 __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up(
     const uint16_t* __restrict__ x, int64_t x_plane, int K, const uint8_t* __restrict__ wq,
-    const uint8_t* __restrict__ ws, int I, const int32_t* __restrict__ sorted,
-    const int32_t* __restrict__ units, const int32_t* __restrict__ n_units_p, int max_units,
-    int top_k, uint16_t* __restrict__ inter, int64_t inter_plane) {
-  __shared__ f32x4_t red[kMoeWaves - 1][2][kWave];
-  const int n_units = min(*n_units_p, max_units);
+    const uint8_t* __restrict__ ws, int I, UnitSrc src, int top_k, uint16_t* __restrict__ inter,
+    int64_t inter_plane) {
+  __shared__ f32x4_t red[SPLIT > 1 ? SPLIT - 1 : 1][2][kWave];
   const int ntile = I >> 4;
-  const int n_items = n_units * ntile;
+  const int n_items = unit_count(src) * ntile;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
   const int nb = K >> 5, ntrip = (nb + 3) >> 2;
+  const int T = (ntrip + SPLIT - 1) / SPLIT;
+  const int tbase = SPLIT > 1 ? wave * T : 0;
   const int64_t row_bytes = K >> 1;
+  const int item0 = SPLIT > 1 ? (int)blockIdx.x : (int)blockIdx.x * kMoeWaves + wave;
+  const int istep = SPLIT > 1 ? (int)gridDim.x : (int)gridDim.x * kMoeWaves;
+  const rsrc_t rx = make_rsrc(x, (uint32_t)(XP * x_plane * 2));
+  const uint32_t exp_bytes = (uint32_t)(2 * I) * (uint32_t)row_bytes;
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+  for (int item = item0; item < n_items; item += istep) {
     const int u = item / ntile, nt = item - u * ntile;
-    const int e = units[3 * u], first = units[3 * u + 1], cnt = units[3 * u + 2];
+    int e, first, cnt;
+    unit_get(src, u, e, first, cnt);
+    if (cnt == 0) continue;  // uniform over the item's waves
     const bool alive = ln.c < cnt;
-    const int tok = sorted[first + (alive ? ln.c : 0)] / top_k;
-    const int64_t grow = (int64_t)e * (2 * I) + nt * 16 + ln.c;
-    const uint8_t* pg = wq + grow * row_bytes;
-    const uint8_t* pu = pg + (int64_t)I * row_bytes;
-    const uint8_t* sg = ws + grow * nb;
-    const uint8_t* su = sg + (int64_t)I * nb;
-    const uint16_t* px = x + (int64_t)tok * K;
+    const int tok = unit_member(src, first + (alive ? ln.c : 0)) / top_k;
+    const int eu = uniform(e);
+    const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
+    const rsrc_t rs = make_rsrc(ws + (int64_t)eu * (2 * I) * nb, (uint32_t)(2 * I * nb));
+    const uint32_t row = (uint32_t)(nt * 16 + ln.c);
+    const uint32_t og = row * (uint32_t)row_bytes, ou = og + (uint32_t)I * (uint32_t)row_bytes;
+    const uint32_t osg = row * (uint32_t)nb, osu = osg + (uint32_t)(I * nb);
+    const uint32_t ox = alive ? (uint32_t)tok * (uint32_t)K * 2u : kOutOfRange;
 
-    f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
-    for (int t0 = wave; t0 < ntrip; t0 += kMoeWaves * C) {
-      u32x4_t wg[C], wu[C], xv[C][XP][4];
-      uint32_t sgv[C], suv[C];
-#pragma unroll
-      for (int cc = 0; cc < C; ++cc) {
-        const int tr = t0 + kMoeWaves * cc, blk = moe_block(tr, ln.g);
-        const bool ok = tr < ntrip && blk < nb;
-        wg[cc] = ok ? ld16(pg + blk * 16) : zero16();
-        wu[cc] = ok ? ld16(pu + blk * 16) : zero16();
-        sgv[cc] = ok ? sg[blk] : 0u;
-        suv[cc] = ok ? su[blk] : 0u;
-#pragma unroll
-        for (int p = 0; p < XP; ++p)
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-            xv[cc][p][h] = (ok && alive) ? ld16(px + p * x_plane + blk * 32 + 8 * h) : zero16();
+    // Offsets of valid loads stay below 2^31 (buffers are checked to be smaller), so OR-ing
+    // bit 31 into an offset sends that load out of range without a select or a branch.
+    auto issue = [&](GuTrip<XP>& r, int i) {
+      const int tr = tbase + i;
+      const int blk = moe_block(tr, ln.g);
+      const uint32_t bad = (uint32_t)!(i < T && tr < ntrip && blk < nb) << 31;
+      const uint32_t kb = (uint32_t)blk * 16u;
+      r.wg = buf16(rw, (og + kb) | bad);
+      r.wu = buf16(rw, (ou + kb) | bad);
+      if (!SV) {
+        r.sg = buf1(rs, (osg + (uint32_t)blk) | bad);
+        r.su = buf1(rs, (osu + (uint32_t)blk) | bad);
       }
 #pragma unroll
-      for (int cc = 0; cc < C; ++cc) {
-        const float fg = e8m0_to_f32(sgv[cc]), fu = e8m0_to_f32(suv[cc]);
+      for (int p = 0; p < XP; ++p)
 #pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const bf16x8_t bg = decode8(wg[cc][h], fg), bu = decode8(wu[cc][h], fu);
+        for (int h = 0; h < 4; ++h)
+          r.xv[p][h] = buf16(rx, (ox + (uint32_t)(p * x_plane + blk * 32 + 8 * h) * 2u) | bad);
+    };
+    ScaleChunk<D> cg, cu, ng, nu;
+    auto issue_chunk = [&](ScaleChunk<D>& a, ScaleChunk<D>& b, int i) {
+      const int tr = tbase + i;
+      const uint32_t bad = (uint32_t)!(i < T && tr < ntrip) << 31;
+      a.load(rs, (osg + 4u * (uint32_t)tr) | bad);
+      b.load(rs, (osu + 4u * (uint32_t)tr) | bad);
+    };
+    f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](const GuTrip<XP>& r, int s) {
+      const float fg = e8m0_to_f32(SV ? cg.byte(s, ln.g) : r.sg);
+      const float fu = e8m0_to_f32(SV ? cu.byte(s, ln.g) : r.su);
 #pragma unroll
-          for (int p = 0; p < XP; ++p) {
-            const bf16x8_t av = as_bf16x8(xv[cc][p][h]);
-            accg = mfma16x16x32(av, bg, accg);
-            accu = mfma16x16x32(av, bu, accu);
-          }
+      for (int h = 0; h < 4; ++h) {
+        const bf16x8_t bg = decode8(r.wg[h], fg), bu = decode8(r.wu[h], fu);
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+          const bf16x8_t av = as_bf16x8(r.xv[p][h]);
+          accg = mfma16x16x32(av, bg, accg);
+          accu = mfma16x16x32(av, bu, accu);
+        }
+      }
+    };
+    GuTrip<XP> ring[D];
+    if (SV) issue_chunk(cg, cu, 0);
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      issue(ring[s], s);
+      ring_fence();
+    }
+    for (int t = 0; t < T; t += D) {
+      if (SV) issue_chunk(ng, nu, t + D);
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        consume(ring[s], s);
+        issue(ring[s], t + s + D);
+        ring_fence();
+      }
+      if (SV) {
+        cg = ng;
+        cu = nu;
+      }
+    }
+
+    const int n = nt * 16 + ln.c;
+    if (SPLIT > 1) {
+      if (wave > 0) {
+        red[wave - 1][0][lane] = accg;
+        red[wave - 1][1][lane] = accu;
+      }
+      __syncthreads();
+      if (wave == 0) {
+#pragma unroll
+        for (int w = 0; w < SPLIT - 1; ++w) {
+          accg += red[w][0][lane];
+          accu += red[w][1][lane];
         }
       }
     }
-    if (wave > 0) {
-      red[wave - 1][0][lane] = accg;
-      red[wave - 1][1][lane] = accu;
-    }
-    __syncthreads();
-    if (wave == 0) {
-#pragma unroll
-      for (int w = 0; w < kMoeWaves - 1; ++w) {
-        accg += red[w][0][lane];
-        accu += red[w][1][lane];
-      }
-      const int n = nt * 16 + ln.c;
+    if (SPLIT == 1 || wave == 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = moe_out_slot(ln.g, i);
         if (m < cnt) {
-          const int64_t a = sorted[first + m];
+          const int64_t a = unit_member(src, first + m);
           const float gt = accg[i];
-          const float v = gt / (1.f + __expf(-gt)) * accu[i];
-          uint16_t* dst = inter + a * I + n;
-          if (OP == 2) {
-            uint16_t hi, lo;
-            split_bf16(v, &hi, &lo);
-            dst[0] = hi;
-            dst[inter_plane] = lo;
-          } else {
-            uint16_t hi, mid, lo;
-            split3_bf16(v, &hi, &mid, &lo);
-            dst[0] = hi;
-            dst[inter_plane] = mid;
-            dst[2 * inter_plane] = lo;
-          }
+          store_planes<OP>(inter + a * I + n, inter_plane, gt / (1.f + __expf(-gt)) * accu[i]);
         }
       }
+    }
+    if (SPLIT > 1) __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- down (unit mode)
+//
+// Wave item = (unit, R tiles of 16 hidden rows) over the whole K (= intermediate) loop: the
+// unit's activation operand (IP planes of the intermediate) is loaded once per trip and reused
+// by the R row tiles, and the trips stream through a ring of D in flight. y f32 per assignment.
+
+template <int IP, int R>
+struct DnTrip {
+  u32x4_t w[R];
+  uint32_t s[R];
+  u32x4_t av[IP][4];
+};
+
+template <int IP, int R, int D, bool SV>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_down(
+    const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, int H, UnitSrc src, float* __restrict__ y) {
+  const int rtiles = H >> 4;
+  const int ntile = (rtiles + R - 1) / R;
+  const int n_items = unit_count(src) * ntile;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int nb = K >> 5, ntrip = (nb + 3) >> 2;
+  const int64_t row_bytes = K >> 1;
+  const rsrc_t ra = make_rsrc(inter, (uint32_t)(IP * inter_plane * 2));
+  const uint32_t exp_bytes = (uint32_t)H * (uint32_t)row_bytes;
+
+  for (int item = blockIdx.x * kMoeWaves + wave; item < n_items; item += gridDim.x * kMoeWaves) {
+    const int u = item / ntile, nt = item - u * ntile;
+    int e, first, cnt;
+    unit_get(src, u, e, first, cnt);
+    if (cnt == 0) continue;
+    const bool alive = ln.c < cnt;
+    const uint32_t oa =
+        alive ? (uint32_t)unit_member(src, first + ln.c) * (uint32_t)K * 2u : kOutOfRange;
+    const int eu = uniform(e);
+    const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
+    const rsrc_t rs = make_rsrc(ws + (int64_t)eu * H * nb, (uint32_t)(H * nb));
+    // Tiles past the last row tile (only when H/16 is not a multiple of R) recompute the last
+    // tile and are not stored, which keeps the loads free of a per-tile condition.
+    uint32_t ow[R], os[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int rt = min(nt * R + r, rtiles - 1);
+      const uint32_t row = (uint32_t)(rt * 16 + ln.c);
+      ow[r] = row * (uint32_t)row_bytes;
+      os[r] = row * (uint32_t)nb;
+    }
+    auto issue = [&](DnTrip<IP, R>& t, int tr) {
+      const int blk = moe_block(tr, ln.g);
+      const uint32_t bad = (uint32_t)!(tr < ntrip && blk < nb) << 31;
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        t.w[r] = buf16(rw, (ow[r] + (uint32_t)blk * 16u) | bad);
+        if (!SV) t.s[r] = buf1(rs, (os[r] + (uint32_t)blk) | bad);
+      }
+#pragma unroll
+      for (int p = 0; p < IP; ++p)
+#pragma unroll
+        for (int h = 0; h < 4; ++h)
+          t.av[p][h] = buf16(ra, (oa + (uint32_t)(p * inter_plane + blk * 32 + 8 * h) * 2u) | bad);
+    };
+    ScaleChunk<D> cs[R], ns[R];
+    auto issue_chunk = [&](ScaleChunk<D>* c, int tr) {
+      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
+#pragma unroll
+      for (int r = 0; r < R; ++r) c[r].load(rs, (os[r] + 4u * (uint32_t)tr) | bad);
+    };
+    f32x4_t acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](const DnTrip<IP, R>& t, int s) {
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float fs = e8m0_to_f32(SV ? cs[r].byte(s, ln.g) : t.s[r]);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const bf16x8_t b = decode8(t.w[r][h], fs);
+#pragma unroll
+          for (int p = 0; p < IP; ++p) acc[r] = mfma16x16x32(as_bf16x8(t.av[p][h]), b, acc[r]);
+        }
+      }
+    };
+    DnTrip<IP, R> ring[D];
+    if (SV) issue_chunk(cs, 0);
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      issue(ring[s], s);
+      ring_fence();
+    }
+    for (int t = 0; t < ntrip; t += D) {
+      if (SV) issue_chunk(ns, t + D);
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        consume(ring[s], s);
+        issue(ring[s], t + s + D);
+        ring_fence();
+      }
+      if (SV)
+#pragma unroll
+        for (int r = 0; r < R; ++r) cs[r] = ns[r];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (nt * R + r >= rtiles) continue;
+      const int n = (nt * R + r) * 16 + ln.c;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = moe_out_slot(ln.g, i);
+        if (m < cnt) y[(int64_t)unit_member(src, first + m) * H + n] = acc[r][i];
+      }
+    }
+  }
+}
+
+// ---------------------------------------------------------------- down + combine (direct mode)
+//
+// Small batches: workgroup item = (token t, 16 hidden rows). Wave w takes the token's
+// assignments j = w, w+4, ...; for each live one it streams that expert's 16 rows (one token
+// column, so the A operand is lane c == 0) and adds weight_j * (down_e . inter_a); the four
+// waves' partial rows are summed in LDS in wave order and written as the token's output. No y
+// round trip and no separate combine launch; the result does not depend on scheduling.
+
+template <int IP, int D, bool SV>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_down_token(
+    const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, int H, const void* __restrict__ a_expert, int edt,
+    const void* __restrict__ a_weight, int wdt, int lo, int n_experts, int tokens, int top_k,
+    void* __restrict__ out, int odt) {
+  __shared__ float red[kMoeWaves][16];
+  const int rtiles = H >> 4;
+  const int n_items = tokens * rtiles;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int nb = K >> 5, ntrip = (nb + 3) >> 2;
+  const int64_t row_bytes = K >> 1;
+  const rsrc_t ra = make_rsrc(inter, (uint32_t)(IP * inter_plane * 2));
+  const uint32_t exp_bytes = (uint32_t)H * (uint32_t)row_bytes;
+
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int t = item / rtiles, rt = item - t * rtiles;
+    float tot = 0.f;
+    for (int j = wave; j < top_k; j += kMoeWaves) {
+      const int64_t a = (int64_t)t * top_k + j;
+      const int64_t ex = load_index(a_expert, edt, a) - lo;
+      const float wj = load_float(a_weight, wdt, a);
+      if (!(ex >= 0 && ex < n_experts && wj != 0.f)) continue;  // uniform per wave
+      const int eu = uniform((int)ex);
+      const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
+      const rsrc_t rs = make_rsrc(ws + (int64_t)eu * H * nb, (uint32_t)(H * nb));
+      const uint32_t row = (uint32_t)(rt * 16 + ln.c);
+      const uint32_t ow = row * (uint32_t)row_bytes, os = row * (uint32_t)nb;
+      const uint32_t oa = ln.c == 0 ? (uint32_t)a * (uint32_t)K * 2u : kOutOfRange;
+      auto issue = [&](DnTrip<IP, 1>& r, int tr) {
+        const int blk = moe_block(tr, ln.g);
+        const uint32_t bad = (uint32_t)!(tr < ntrip && blk < nb) << 31;
+        r.w[0] = buf16(rw, (ow + (uint32_t)blk * 16u) | bad);
+        if (!SV) r.s[0] = buf1(rs, (os + (uint32_t)blk) | bad);
+#pragma unroll
+        for (int p = 0; p < IP; ++p)
+#pragma unroll
+          for (int h = 0; h < 4; ++h)
+            r.av[p][h] = buf16(ra, (oa + (uint32_t)(p * inter_plane + blk * 32 + 8 * h) * 2u) | bad);
+      };
+      ScaleChunk<D> cs, ns;
+      auto issue_chunk = [&](ScaleChunk<D>& c, int tr) {
+        c.load(rs, (os + 4u * (uint32_t)tr) | ((uint32_t)!(tr < ntrip) << 31));
+      };
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+      auto consume = [&](const DnTrip<IP, 1>& r, int s) {
+        const float fs = e8m0_to_f32(SV ? cs.byte(s, ln.g) : r.s[0]);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const bf16x8_t b = decode8(r.w[0][h], fs);
+#pragma unroll
+          for (int p = 0; p < IP; ++p) acc = mfma16x16x32(as_bf16x8(r.av[p][h]), b, acc);
+        }
+      };
+      DnTrip<IP, 1> ring[D];
+      if (SV) issue_chunk(cs, 0);
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        issue(ring[s], s);
+        ring_fence();
+      }
+      for (int tr = 0; tr < ntrip; tr += D) {
+        if (SV) issue_chunk(ns, tr + D);
+#pragma unroll
+        for (int s = 0; s < D; ++s) {
+          consume(ring[s], s);
+          issue(ring[s], tr + s + D);
+          ring_fence();
+        }
+        if (SV) cs = ns;
+      }
+      tot += wj * acc[0];  // lanes 0..15 hold row m = 0 (the token) of column n = c
+    }
+    if (lane < 16) red[wave][lane] = tot;
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+      float v = red[0][lane];
+#pragma unroll
+      for (int w = 1; w < kMoeWaves; ++w) v += red[w][lane];
+      store_float(out, odt, (int64_t)t * H + rt * 16 + lane, v);
     }
     __syncthreads();
   }
 }
 
-// ---------------------------------------------------------------- down
+// ---------------------------------------------------------------- combine (unit mode)
 //
-// Work item = (unit u, 64 hidden rows): wave w owns 16 rows and the whole K (= intermediate)
-// loop; IP = bf16 planes of inter; C = trips per load batch.
-
-template <int IP, int C>
-__global__ __launch_bounds__(kMoeThreads) void k_moe_down(
-    const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
-    const uint8_t* __restrict__ ws, int H, const int32_t* __restrict__ sorted,
-    const int32_t* __restrict__ units, const int32_t* __restrict__ n_units_p, int max_units,
-    float* __restrict__ y) {
-  const int n_units = min(*n_units_p, max_units);
-  const int rtiles = H >> 4;
-  const int ntile = (rtiles + kMoeWaves - 1) / kMoeWaves;
-  const int n_items = n_units * ntile;
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
-  const MoeLane ln = moe_lane(lane);
-  const int nb = K >> 5, ntrip = (nb + 3) >> 2;
-  const int64_t row_bytes = K >> 1;
-
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int u = item / ntile, nt = item - u * ntile;
-    const int rt = nt * kMoeWaves + wave;
-    if (rt >= rtiles) continue;
-    const int e = units[3 * u], first = units[3 * u + 1], cnt = units[3 * u + 2];
-    const bool alive = ln.c < cnt;
-    const int64_t a_lane = sorted[first + (alive ? ln.c : 0)];
-    const int64_t row = (int64_t)e * H + rt * 16 + ln.c;
-    const uint8_t* pw = wq + row * row_bytes;
-    const uint8_t* ps = ws + row * nb;
-    const uint16_t* pa = inter + a_lane * K;
-
-    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
-    for (int t0 = 0; t0 < ntrip; t0 += C) {
-      u32x4_t wv[C], av[C][IP][4];
-      uint32_t sv[C];
-#pragma unroll
-      for (int cc = 0; cc < C; ++cc) {
-        const int tr = t0 + cc, blk = moe_block(tr, ln.g);
-        const bool ok = tr < ntrip && blk < nb;
-        wv[cc] = ok ? ld16(pw + blk * 16) : zero16();
-        sv[cc] = ok ? ps[blk] : 0u;
-#pragma unroll
-        for (int p = 0; p < IP; ++p)
-#pragma unroll
-          for (int h = 0; h < 4; ++h)
-            av[cc][p][h] = (ok && alive) ? ld16(pa + p * inter_plane + blk * 32 + 8 * h) : zero16();
-      }
-#pragma unroll
-      for (int cc = 0; cc < C; ++cc) {
-        const float fs = e8m0_to_f32(sv[cc]);
-#pragma unroll
-        for (int h = 0; h < 4; ++h) {
-          const bf16x8_t b = decode8(wv[cc][h], fs);
-#pragma unroll
-          for (int p = 0; p < IP; ++p) acc = mfma16x16x32(as_bf16x8(av[cc][p][h]), b, acc);
-        }
-      }
-    }
-    const int n = rt * 16 + ln.c;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int m = moe_out_slot(ln.g, i);
-      if (m < cnt) y[(int64_t)sorted[first + m] * H + n] = acc[i];
-    }
-  }
-}
-
-// ---------------------------------------------------------------- combine
+// out[t, n..n+3] = sum_j w_j * y[t*top_k + j, n..n+3] over live assignments, in j order. The
+// routing of a group of four j is loaded before their y rows so the loads overlap.
 
 __global__ __launch_bounds__(256) void k_moe_combine(
     const float* __restrict__ y, const void* __restrict__ a_expert, int edt,
     const void* __restrict__ a_weight, int wdt, int top_k, int H, int lo, int hi,
     void* __restrict__ out, int odt) {
   const int t = blockIdx.y;
-  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
-  float acc = 0.f;
-  for (int j = 0; j < top_k; ++j) {
-    const int64_t a = (int64_t)t * top_k + j;
-    const int64_t e = load_index(a_expert, edt, a);
-    const float w = load_float(a_weight, wdt, a);
-    if (e >= lo && e < hi && w != 0.f) acc += w * y[a * H + n];
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < top_k; j0 += 4) {
+    float w[4];
+    int64_t a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = j0 + q;
+      a[q] = (int64_t)t * top_k + j;
+      w[q] = 0.f;
+      if (j < top_k) {
+        const int64_t e = load_index(a_expert, edt, a[q]);
+        const float wv = load_float(a_weight, wdt, a[q]);
+        if (e >= lo && e < hi) w[q] = wv;
+      }
+    }
+    u32x4_t yv[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) yv[q] = w[q] != 0.f ? ld16(y + a[q] * H + n) : zero16();
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (w[q] != 0.f)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += w[q] * bits_f32(yv[q][c]);
   }
-  store_float(out, odt, (int64_t)t * H + n, acc);
+#pragma unroll
+  for (int c = 0; c < 4; ++c) store_float(out, odt, (int64_t)t * H + n + c, acc[c]);
 }
 
 // ---------------------------------------------------------------- plane split
@@ -349,50 +608,116 @@ __global__ __launch_bounds__(64) void k_probe_mfma(const uint16_t* __restrict__ 
 
 namespace {
 
-struct MoeLaunch {
-  int grid_gate_up, grid_down;
-};
-
-template <typename KernelT>
-int persistent_grid(KernelT kernel, int64_t items, int& cache) {
-  if (items <= 0) return 0;
-  if (cache == 0) cache = occupancy_per_cu(kernel, kMoeThreads);
-  const int64_t cap = (int64_t)device_cu_count() * cache;
-  return (int)(items < cap ? items : cap);
-}
+// Batches of at most this many tokens take the direct path: per-assignment gate_up (no prep)
+// and the per-token down + combine (no y, no combine launch).
+constexpr int kDirectMaxTokens = 4;
 
 bool dtype_index_ok(int d) { return d == MTPK_I32 || d == MTPK_I64; }
 bool dtype_float_ok(int d) { return d == MTPK_F32 || d == MTPK_BF16; }
 
-constexpr int kGateUpChunk = 2;
-constexpr int kDownChunk = 2;
+template <typename KernelT>
+int grid_for(KernelT kernel, int64_t wgs_needed, int& cache) {
+  if (wgs_needed <= 0) return 0;
+  if (cache == 0) cache = occupancy_per_cu(kernel, kMoeThreads);
+  const int64_t cap = (int64_t)device_cu_count() * cache;
+  return (int)(wgs_needed < cap ? wgs_needed : cap);
+}
 
-template <int XP, int OP>
-int launch_gate_up(const uint16_t* x, int64_t x_plane, int K, const uint8_t* wq,
-                   const uint8_t* ws, int I, const int32_t* sorted, const int32_t* units,
-                   const int32_t* n_units, int max_units, int top_k, uint16_t* inter,
-                   int64_t inter_plane, hipStream_t st) {
+template <int XP, int OP, int SPLIT, int D, bool SV>
+int launch_gate_up_t(const uint16_t* x, int64_t x_plane, int K, const uint8_t* wq,
+                     const uint8_t* ws, int I, const UnitSrc& src, int64_t max_units, int top_k,
+                     uint16_t* inter, int64_t inter_plane, hipStream_t st) {
   static int occ = 0;
-  auto kern = k_moe_gate_up<XP, OP, kGateUpChunk>;
-  const int grid = persistent_grid(kern, (int64_t)max_units * (I >> 4), occ);
+  auto kern = k_moe_gate_up<XP, OP, SPLIT, D, SV>;
+  const int64_t items = max_units * (I >> 4);
+  const int64_t wgs = SPLIT > 1 ? items : (items + kMoeWaves - 1) / kMoeWaves;
+  const int grid = grid_for(kern, wgs, occ);
   if (grid == 0) return 0;
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, x, x_plane, K, wq, ws, I,
-                     sorted, units, n_units, max_units, top_k, inter, inter_plane);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, x, x_plane, K, wq, ws, I, src,
+                     top_k, inter, inter_plane);
   return status_of(hipGetLastError());
 }
 
-template <int IP>
-int launch_down(const uint16_t* inter, int64_t inter_plane, int K, const uint8_t* wq,
-                const uint8_t* ws, int H, const int32_t* sorted, const int32_t* units,
-                const int32_t* n_units, int max_units, float* y, hipStream_t st) {
+// Scale rows whose byte count is a multiple of 16 take the chunked scale loads (SV); for SPLIT
+// = 4 each wave's quarter of the trips must also be a multiple of the ring depth.
+bool chunked_scales(int K, int split, int D) {
+  const int nb = K >> 5, ntrip = (nb + 3) >> 2, T = (ntrip + split - 1) / split;
+  return nb % 16 == 0 && T % D == 0;
+}
+
+// SPLIT = 4 while the item count would leave fewer than four waves per SIMD busy.
+int launch_gate_up(int xp, const uint16_t* x, int64_t x_plane, int K, const uint8_t* wq,
+                   const uint8_t* ws, int I, const UnitSrc& src, int64_t max_units, int top_k,
+                   uint16_t* inter, int64_t inter_plane, hipStream_t st) {
+  const bool split = max_units * (I >> 4) < (int64_t)device_cu_count() * 16;
+#define MTPK_GU(XP_, OP_, SP_, D_)                                                           \
+  (chunked_scales(K, SP_, D_)                                                                \
+       ? launch_gate_up_t<XP_, OP_, SP_, D_, true>(x, x_plane, K, wq, ws, I, src, max_units, \
+                                                   top_k, inter, inter_plane, st)            \
+       : launch_gate_up_t<XP_, OP_, SP_, D_, false>(x, x_plane, K, wq, ws, I, src, max_units, \
+                                                    top_k, inter, inter_plane, st))
+  if (xp == 1) return split ? MTPK_GU(1, 2, 4, 4) : MTPK_GU(1, 2, 1, 4);
+  return split ? MTPK_GU(3, 3, 4, 2) : MTPK_GU(3, 3, 1, 2);
+#undef MTPK_GU
+}
+
+template <int IP, int R, int D, bool SV>
+int launch_down_t(const uint16_t* inter, int64_t inter_plane, int K, const uint8_t* wq,
+                  const uint8_t* ws, int H, const UnitSrc& src, int64_t max_units, float* y,
+                  hipStream_t st) {
   static int occ = 0;
-  auto kern = k_moe_down<IP, kDownChunk>;
-  const int64_t ntile = ((H >> 4) + kMoeWaves - 1) / kMoeWaves;
-  const int grid = persistent_grid(kern, (int64_t)max_units * ntile, occ);
+  auto kern = k_moe_down<IP, R, D, SV>;
+  const int64_t items = max_units * (((H >> 4) + R - 1) / R);
+  const int grid = grid_for(kern, (items + kMoeWaves - 1) / kMoeWaves, occ);
   if (grid == 0) return 0;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, inter, inter_plane, K, wq, ws,
-                     H, sorted, units, n_units, max_units, y);
+                     H, src, y);
   return status_of(hipGetLastError());
+}
+
+template <int IP, int D, bool SV>
+int launch_down_token_t(const uint16_t* inter, int64_t inter_plane, int K, const uint8_t* wq,
+                        const uint8_t* ws, int H, const void* a_expert, int edt,
+                        const void* a_weight, int wdt, int lo, int n_experts, int tokens,
+                        int top_k, void* out, int odt, hipStream_t st) {
+  static int occ = 0;
+  auto kern = k_moe_down_token<IP, D, SV>;
+  const int grid = grid_for(kern, (int64_t)tokens * (H >> 4), occ);
+  if (grid == 0) return 0;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, inter, inter_plane, K, wq, ws,
+                     H, a_expert, edt, a_weight, wdt, lo, n_experts, tokens, top_k, out, odt);
+  return status_of(hipGetLastError());
+}
+
+UnitSrc unit_list(const int32_t* units, const int32_t* sorted, const int32_t* n_units,
+                  int64_t max_units) {
+  UnitSrc s{};
+  s.units = units;
+  s.sorted = sorted;
+  s.n_units = n_units;
+  s.max_units = (int)max_units;
+  s.direct = 0;
+  return s;
+}
+
+UnitSrc unit_direct(const void* a_expert, int edt, const void* a_weight, int wdt, int lo, int hi,
+                    int64_t assignments) {
+  UnitSrc s{};
+  s.a_expert = a_expert;
+  s.a_weight = a_weight;
+  s.edt = edt;
+  s.wdt = wdt;
+  s.lo = lo;
+  s.n_experts = hi - lo;
+  s.assignments = (int)assignments;
+  s.direct = 1;
+  return s;
+}
+
+bool gemm_shapes_ok(int64_t hidden, int64_t inter_dim, int64_t local_experts) {
+  return hidden > 0 && hidden % 32 == 0 && inter_dim > 0 && inter_dim % 32 == 0 &&
+         hidden <= (1 << 20) && inter_dim <= (1 << 20) && local_experts > 0 &&
+         local_experts <= MTPK_MAX_EXPERTS;
 }
 
 }  // namespace
@@ -402,6 +727,8 @@ int launch_down(const uint16_t* inter, int64_t inter_plane, int K, const uint8_t
 using namespace mtpk;
 
 extern "C" {
+
+int mtpk_moe_direct_max_tokens(void) { return kDirectMaxTokens; }
 
 int64_t mtpk_moe_max_units(int64_t assignments, int64_t local_experts) {
   if (assignments <= 0 || local_experts <= 0) return 0;
@@ -442,22 +769,37 @@ int mtpk_moe_gate_up(const uint16_t* x_planes, int x_nplanes, int64_t tokens, in
                      int inter_planes, int64_t assignments, void* stream) {
   if (!x_planes || !gate_up || !gate_up_scale || !sorted || !units || !n_units || !inter)
     return MTPK_EINVAL;
-  if (hidden <= 0 || hidden % 32 || inter_dim <= 0 || inter_dim % 32 || top_k <= 0)
-    return MTPK_EINVAL;
-  if (hidden > (1 << 20) || inter_dim > (1 << 20) || local_experts <= 0) return MTPK_EINVAL;
+  if (!gemm_shapes_ok(hidden, inter_dim, local_experts) || top_k <= 0) return MTPK_EINVAL;
   if (!aligned16(x_planes) || !aligned16(gate_up) || !aligned16(inter)) return MTPK_EINVAL;
   if (max_units <= 0 || max_units > INT32_MAX / inter_dim) return MTPK_EINVAL;
-  const hipStream_t st = (hipStream_t)stream;
-  const int64_t xp = tokens * hidden, ip = assignments * inter_dim;
-  if (x_nplanes == 1 && inter_planes == 2)
-    return launch_gate_up<1, 2>(x_planes, xp, (int)hidden, gate_up, gate_up_scale,
-                                (int)inter_dim, sorted, units, n_units, (int)max_units, top_k,
-                                inter, ip, st);
-  if (x_nplanes == 3 && inter_planes == 3)
-    return launch_gate_up<3, 3>(x_planes, xp, (int)hidden, gate_up, gate_up_scale,
-                                (int)inter_dim, sorted, units, n_units, (int)max_units, top_k,
-                                inter, ip, st);
-  return MTPK_EINVAL;
+  if (!((x_nplanes == 1 && inter_planes == 2) || (x_nplanes == 3 && inter_planes == 3)))
+    return MTPK_EINVAL;
+  return launch_gate_up(x_nplanes, x_planes, tokens * hidden, (int)hidden, gate_up, gate_up_scale,
+                        (int)inter_dim, unit_list(units, sorted, n_units, max_units), max_units,
+                        top_k, inter, assignments * inter_dim, (hipStream_t)stream);
+}
+
+int mtpk_moe_gate_up_direct(const uint16_t* x_planes, int x_nplanes, int64_t tokens,
+                            int64_t hidden, const uint8_t* gate_up, const uint8_t* gate_up_scale,
+                            int64_t local_experts, int64_t inter_dim, const void* a_expert,
+                            int expert_dtype, const void* a_weight, int weight_dtype, int top_k,
+                            int expert_lo, int expert_hi, uint16_t* inter, int inter_planes,
+                            void* stream) {
+  if (!x_planes || !gate_up || !gate_up_scale || !a_expert || !a_weight || !inter)
+    return MTPK_EINVAL;
+  if (!gemm_shapes_ok(hidden, inter_dim, local_experts) || top_k <= 0) return MTPK_EINVAL;
+  if (!dtype_index_ok(expert_dtype) || !dtype_float_ok(weight_dtype)) return MTPK_EINVAL;
+  if ((int64_t)expert_hi - expert_lo != local_experts) return MTPK_EINVAL;
+  if (!aligned16(x_planes) || !aligned16(gate_up) || !aligned16(inter)) return MTPK_EINVAL;
+  if (tokens < 0 || tokens * top_k > INT32_MAX / inter_dim) return MTPK_EINVAL;
+  if (!((x_nplanes == 1 && inter_planes == 2) || (x_nplanes == 3 && inter_planes == 3)))
+    return MTPK_EINVAL;
+  const int64_t a = tokens * top_k;
+  if (a == 0) return 0;
+  return launch_gate_up(
+      x_nplanes, x_planes, tokens * hidden, (int)hidden, gate_up, gate_up_scale, (int)inter_dim,
+      unit_direct(a_expert, expert_dtype, a_weight, weight_dtype, expert_lo, expert_hi, a), a,
+      top_k, inter, a * inter_dim, (hipStream_t)stream);
 }
 
 int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, int64_t inter_dim,
@@ -465,18 +807,51 @@ int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, 
                   int64_t hidden, const int32_t* sorted, const int32_t* units,
                   const int32_t* n_units, int64_t max_units, float* y, void* stream) {
   if (!inter || !down || !down_scale || !sorted || !units || !n_units || !y) return MTPK_EINVAL;
-  if (hidden <= 0 || hidden % 32 || inter_dim <= 0 || inter_dim % 32 || local_experts <= 0)
-    return MTPK_EINVAL;
+  if (!gemm_shapes_ok(hidden, inter_dim, local_experts)) return MTPK_EINVAL;
   if (!aligned16(inter) || !aligned16(down)) return MTPK_EINVAL;
   if (max_units <= 0 || max_units > INT32_MAX / hidden) return MTPK_EINVAL;
   const hipStream_t st = (hipStream_t)stream;
   const int64_t ip = assignments * inter_dim;
+  const UnitSrc src = unit_list(units, sorted, n_units, max_units);
+  const bool sv = chunked_scales((int)inter_dim, 1, 2);
   if (inter_planes == 2)
-    return launch_down<2>(inter, ip, (int)inter_dim, down, down_scale, (int)hidden, sorted, units,
-                          n_units, (int)max_units, y, st);
+    return sv ? launch_down_t<2, 4, 2, true>(inter, ip, (int)inter_dim, down, down_scale,
+                                             (int)hidden, src, max_units, y, st)
+              : launch_down_t<2, 4, 2, false>(inter, ip, (int)inter_dim, down, down_scale,
+                                              (int)hidden, src, max_units, y, st);
   if (inter_planes == 3)
-    return launch_down<3>(inter, ip, (int)inter_dim, down, down_scale, (int)hidden, sorted, units,
-                          n_units, (int)max_units, y, st);
+    return sv ? launch_down_t<3, 2, 2, true>(inter, ip, (int)inter_dim, down, down_scale,
+                                             (int)hidden, src, max_units, y, st)
+              : launch_down_t<3, 2, 2, false>(inter, ip, (int)inter_dim, down, down_scale,
+                                              (int)hidden, src, max_units, y, st);
+  return MTPK_EINVAL;
+}
+
+int mtpk_moe_down_combine(const uint16_t* inter, int inter_planes, int64_t inter_dim,
+                          const uint8_t* down, const uint8_t* down_scale, int64_t local_experts,
+                          int64_t hidden, const void* a_expert, int expert_dtype,
+                          const void* a_weight, int weight_dtype, int64_t tokens, int top_k,
+                          int expert_lo, int expert_hi, void* out, int out_dtype, void* stream) {
+  if (!inter || !down || !down_scale || !a_expert || !a_weight || !out) return MTPK_EINVAL;
+  if (!gemm_shapes_ok(hidden, inter_dim, local_experts) || top_k <= 0) return MTPK_EINVAL;
+  if (!dtype_index_ok(expert_dtype) || !dtype_float_ok(weight_dtype) || !dtype_float_ok(out_dtype))
+    return MTPK_EINVAL;
+  if ((int64_t)expert_hi - expert_lo != local_experts) return MTPK_EINVAL;
+  if (!aligned16(inter) || !aligned16(down)) return MTPK_EINVAL;
+  if (tokens < 0 || tokens * (hidden >> 4) > INT32_MAX || tokens * top_k > INT32_MAX / inter_dim)
+    return MTPK_EINVAL;
+  if (tokens == 0) return 0;
+  const hipStream_t st = (hipStream_t)stream;
+  const int64_t ip = tokens * top_k * inter_dim;
+#define MTPK_DT(IP_, D_, SV_)                                                              \
+  launch_down_token_t<IP_, D_, SV_>(inter, ip, (int)inter_dim, down, down_scale, (int)hidden, \
+                                    a_expert, expert_dtype, a_weight, weight_dtype, expert_lo, \
+                                    (int)local_experts, (int)tokens, top_k, out, out_dtype, st)
+  if (inter_planes == 2)
+    return chunked_scales((int)inter_dim, 1, 4) ? MTPK_DT(2, 4, true) : MTPK_DT(2, 4, false);
+  if (inter_planes == 3)
+    return chunked_scales((int)inter_dim, 1, 2) ? MTPK_DT(3, 2, true) : MTPK_DT(3, 2, false);
+#undef MTPK_DT
   return MTPK_EINVAL;
 }
 
@@ -486,9 +861,10 @@ int mtpk_moe_combine(const float* y, const void* a_expert, int expert_dtype, con
   if (!y || !a_expert || !a_weight || !out) return MTPK_EINVAL;
   if (!dtype_index_ok(expert_dtype) || !dtype_float_ok(weight_dtype) || !dtype_float_ok(out_dtype))
     return MTPK_EINVAL;
-  if (tokens < 0 || tokens > 65535 || hidden <= 0 || top_k <= 0) return MTPK_EINVAL;
+  if (tokens < 0 || tokens > 65535 || hidden <= 0 || hidden % 4 || top_k <= 0) return MTPK_EINVAL;
+  if (!aligned16(y)) return MTPK_EINVAL;
   if (tokens == 0) return 0;
-  const dim3 grid((unsigned)((hidden + 255) / 256), (unsigned)tokens);
+  const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
   hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
                      expert_hi, out, out_dtype);
@@ -543,6 +919,15 @@ int mtpk_fused_moe(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
   uint16_t* inter = reinterpret_cast<uint16_t*>(p);
   p += align256((int64_t)ip * a * inter_dim * 2);
   float* y = reinterpret_cast<float*>(p);
+  if (tokens <= kDirectMaxTokens) {
+    rc = mtpk_moe_gate_up_direct(xplanes, xp, tokens, hidden, gate_up, gate_up_scale,
+                                 local_experts, inter_dim, a_expert, expert_dtype, a_weight,
+                                 weight_dtype, top_k, expert_lo, expert_hi, inter, ip, stream);
+    if (rc) return rc;
+    return mtpk_moe_down_combine(inter, ip, inter_dim, down, down_scale, local_experts, hidden,
+                                 a_expert, expert_dtype, a_weight, weight_dtype, tokens, top_k,
+                                 expert_lo, expert_hi, out, x_dtype, stream);
+  }
   rc = mtpk_moe_prep(a_expert, expert_dtype, a_weight, weight_dtype, a, expert_lo, expert_hi,
                      sorted, units, mu, n_units, stream);
   if (rc) return rc;

@@ -170,8 +170,9 @@ def moe_scratch(max_tokens: int, top_k: int, local_experts: int, intermediate: i
 
 
 class MoeLayerRunner:
-    """Static buffers for one routed-MoE shape `(tokens, top_k, experts, I, H)` and the four
-    kernels launched one by one on the current stream: prep, gate_up, down, combine.
+    """Static buffers for one routed-MoE shape `(tokens, top_k, experts, I, H)` and its kernels
+    launched one by one on the current stream: prep, gate_up, down, combine, or for batches of
+    at most `mtpk_moe_direct_max_tokens()` tokens the direct pair gate_up, down + combine.
 
     Nothing is allocated per call, so a call can be captured into a HIP graph and replayed;
     `events`, when given, is a dict whose `torch.cuda.Event` pairs are recorded around each
@@ -190,6 +191,7 @@ class MoeLayerRunner:
         self.unit = torch.empty(max(3 * self.u_max, 3), dtype=torch.int32, device=device)
         self.n_units = torch.zeros(1, dtype=torch.int32, device=device)
         self.inter = torch.empty(2 * a * intermediate, dtype=torch.bfloat16, device=device)
+        self.direct = tokens <= int(lib.mtpk_moe_direct_max_tokens())
         self.y = torch.empty(a * hidden, dtype=torch.float32, device=device)
 
     def run(self, x: torch.Tensor, experts: dict, a_expert: torch.Tensor, a_weight: torch.Tensor,
@@ -200,6 +202,25 @@ class MoeLayerRunner:
         if x.dtype != torch.bfloat16 or x.shape != (self.tokens, self.hidden):
             raise ValueError("x must be bf16 [tokens, hidden] of the runner's shape")
         ec, wc = _mtpk.index_code(a_expert.dtype), _mtpk.float_code(a_weight.dtype)
+        if self.direct:
+            if events:
+                events["gate_up"][0].record()
+            _mtpk.check(lib.mtpk_moe_gate_up_direct(
+                x.data_ptr(), 1, self.tokens, self.hidden, experts["gate_up"].data_ptr(),
+                experts["gate_up_scale"].data_ptr(), self.local, self.inter_dim,
+                a_expert.data_ptr(), ec, a_weight.data_ptr(), wc, self.top_k, lo, hi,
+                self.inter.data_ptr(), 2, st), "mtpk_moe_gate_up_direct")
+            if events:
+                events["gate_up"][1].record()
+                events["down"][0].record()
+            _mtpk.check(lib.mtpk_moe_down_combine(
+                self.inter.data_ptr(), 2, self.inter_dim, experts["down"].data_ptr(),
+                experts["down_scale"].data_ptr(), self.local, self.hidden, a_expert.data_ptr(),
+                ec, a_weight.data_ptr(), wc, self.tokens, self.top_k, lo, hi, out.data_ptr(),
+                _mtpk.float_code(out.dtype), st), "mtpk_moe_down_combine")
+            if events:
+                events["down"][1].record()
+            return out
         _mtpk.check(lib.mtpk_moe_prep(a_expert.data_ptr(), ec, a_weight.data_ptr(), wc,
                                       self.assignments, lo, hi, self.sorted.data_ptr(),
                                       self.unit.data_ptr(), self.u_max, self.n_units.data_ptr(), st),

@@ -4,8 +4,9 @@
 //  decode      fp4_to_f32 * e8m0_to_f32 against the closed form, all 256 bytes x 256 scales
 //  split       split_bf16 / split3_bf16 reconstruction bounds
 //  argmax_key  key order == (value desc, index asc), with -0.0 == +0.0
-//  gate_up     the gate_up kernel's wave/trip/lane/slot decomposition (loop bounds copied from
-//              the kernel) covers every K exactly once and reproduces the dot products
+//  gate_up     the gate_up kernel's wave/trip/lane/slot decomposition (contiguous quarters of
+//              the trips per wave, ring steps) covers every K exactly once and reproduces the
+//              dot products
 //  down        same for the down kernel's loops
 //  prep        the prep kernel's phases, emulated thread by thread, give a valid expert-grouped
 //              work list with counts <= 16
@@ -135,11 +136,16 @@ static bool emulate_tile(const uint8_t* packed, const uint8_t* scale, int K, int
   const int waves = split_waves ? 4 : 1;
   std::vector<double> acc(16 * 16, 0.0);
   std::vector<int> visits((size_t)K, 0);
+  // Split waves take contiguous quarters of the trips (T each); the ring walks trips
+  // i = 0..T-1 in steps of C with the same validity test as the kernel's issue step.
+  const int T = split_waves ? (ntrip + 3) / 4 : ntrip;
   for (int wave = 0; wave < waves; ++wave) {
-    const int step = split_waves ? 4 * C : C;
-    for (int t0 = split_waves ? wave : 0; t0 < ntrip; t0 += step) {
+    const int tbase = split_waves ? wave * T : 0;
+    for (int t0 = 0; t0 < T; t0 += C) {
       for (int cc = 0; cc < C; ++cc) {
-        const int tr = t0 + (split_waves ? 4 * cc : cc);
+        const int i = t0 + cc;
+        const int tr = tbase + i;
+        if (i >= T) continue;
         for (int lane = 0; lane < 64; ++lane) {
           const MoeLane ln = moe_lane(lane);
           const int blk = moe_block(tr, ln.g);
