@@ -504,6 +504,290 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_token(
   }
 }
 
+// ---------------------------------------------------------------- LDS-staged unit kernels
+//
+// Wide batches: the 4 waves of a workgroup work on one unit, each on its own weight rows, so
+// the unit's activation rows are shared. They are staged cooperatively into LDS in K chunks
+// (double-buffered, one barrier per chunk) and every wave reads its MFMA A operand from LDS
+// (ds_read_b128); only weights and scales go through the per-wave trip ring. This takes the
+// activation loads off the vector memory path, where every lane of a wave costs address work
+// even when most of the unit's 16 token slots are empty.
+
+// Wait for this wave's LDS operations, then workgroup barrier. Vector memory loads (the trip
+// ring) stay in flight across it.
+__device__ inline void lds_barrier() {
+  ring_fence();
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0) only (gfx9 encoding)
+  __builtin_amdgcn_s_barrier();
+  ring_fence();
+}
+
+__device__ inline u32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+
+__device__ inline void lds16_store(uint8_t* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
+
+// K elements of the activation rows staged per chunk, and the LDS bytes of one token row
+// (NPL planes, padded by 16 bytes so the 16 token rows fall on different banks).
+template <int KC, int NPL>
+struct StageGeom {
+  static constexpr int kPlaneBytes = KC * 2;
+  static constexpr int kRow = KC * 2 * NPL + 16;
+  static constexpr int kBuf = 16 * kRow;
+  static constexpr int kBytesPerThread = 16 * KC * 2 * NPL / kMoeThreads;  // 64
+  static_assert(kBytesPerThread == 64, "one staging step is 4 x 16 bytes per thread");
+};
+
+// gate_up, LDS variant (bf16 x, hi/lo intermediate, chunked scales). Item = (unit, 4 tiles of
+// 16 intermediate rows), wave w takes tile 4q + w. Chunks of 512 K = 4 trips = one ring turn.
+template <int D>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
+    const uint16_t* __restrict__ x, int64_t x_elems, int K, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, int I, UnitSrc src, int top_k, uint16_t* __restrict__ inter,
+    int64_t inter_plane) {
+  constexpr int KC = 512, TPC = KC / 128;
+  static_assert(D == TPC, "one ring turn per staged chunk");
+  using G = StageGeom<KC, 1>;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][G::kBuf];
+  const int ntile = I >> 4, ngroup = (ntile + kMoeWaves - 1) / kMoeWaves;
+  const int n_items = unit_count(src) * ngroup;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int nb = K >> 5, ntrip = nb >> 2, nchunk = K / KC;
+  const int64_t row_bytes = K >> 1;
+  const rsrc_t rx = make_rsrc(x, (uint32_t)(x_elems * 2));
+  const uint32_t exp_bytes = (uint32_t)(2 * I) * (uint32_t)row_bytes;
+  // staging: thread -> (token row sr, 64-byte segment sseg) of a chunk
+  const int sr = tid >> 4, sseg = tid & 15;
+
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int u = item / ngroup, q = item - u * ngroup;
+    int e, first, cnt;
+    unit_get(src, u, e, first, cnt);
+    if (cnt == 0) continue;  // uniform over the workgroup
+    const int nt_raw = q * kMoeWaves + wave;
+    const bool wave_ok = nt_raw < ntile;
+    const int nt = wave_ok ? nt_raw : ntile - 1;
+    const int eu = uniform(e);
+    const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
+    const rsrc_t rs = make_rsrc(ws + (int64_t)eu * (2 * I) * nb, (uint32_t)(2 * I * nb));
+    const uint32_t row = (uint32_t)(nt * 16 + ln.c);
+    const uint32_t og = row * (uint32_t)row_bytes, ou = og + (uint32_t)I * (uint32_t)row_bytes;
+    const uint32_t osg = row * (uint32_t)nb, osu = osg + (uint32_t)(I * nb);
+    const uint32_t sx = sr < cnt ? (uint32_t)(unit_member(src, first + sr) / top_k) * (uint32_t)K * 2u +
+                                       (uint32_t)sseg * 64u
+                                 : kOutOfRange;
+    u32x4_t sreg[4];
+    auto stage_load = [&](int c) {
+      const uint32_t bad = (uint32_t)!(c < nchunk) << 31;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sreg[k] = buf16(rx, (sx + (uint32_t)c * (KC * 2) + 16u * k) | bad);
+    };
+    auto stage_store = [&](int b) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k) lds16_store(&xs[b][sr * G::kRow + sseg * 64 + 16 * k], sreg[k]);
+    };
+
+    auto issue = [&](u32x4_t& wg, u32x4_t& wu, int tr) {
+      const int blk = moe_block(tr, ln.g);
+      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
+      const uint32_t kb = (uint32_t)blk * 16u;
+      wg = buf16(rw, (og + kb) | bad);
+      wu = buf16(rw, (ou + kb) | bad);
+    };
+    ScaleChunk<D> cg, cu, ng, nu;
+    auto issue_chunk = [&](ScaleChunk<D>& a, ScaleChunk<D>& b, int tr) {
+      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
+      a.load(rs, (osg + 4u * (uint32_t)tr) | bad);
+      b.load(rs, (osu + 4u * (uint32_t)tr) | bad);
+    };
+    f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](const u32x4_t& wg, const u32x4_t& wu, int s, const uint8_t* buf) {
+      const float fg = e8m0_to_f32(cg.byte(s, ln.g)), fu = e8m0_to_f32(cu.byte(s, ln.g));
+      const uint8_t* arow = buf + ln.c * G::kRow + ((4 * s + ln.g) * 32) * 2;
+      u32x4_t a[4];
+#pragma unroll
+      for (int h = 0; h < 4; ++h) a[h] = lds16(arow + 16 * h);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const bf16x8_t bg = decode8(wg[h], fg), bu = decode8(wu[h], fu);
+        accg = mfma16x16x32(as_bf16x8(a[h]), bg, accg);
+        accu = mfma16x16x32(as_bf16x8(a[h]), bu, accu);
+      }
+    };
+
+    // prologue: chunk 0 staged, chunk 1 loading, scales and weights of the first D trips
+    stage_load(0);
+    stage_store(0);
+    stage_load(1);
+    issue_chunk(cg, cu, 0);
+    u32x4_t rg[D], ru[D];
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      issue(rg[s], ru[s], s);
+      ring_fence();
+    }
+    lds_barrier();
+    for (int c = 0; c < nchunk; ++c) {
+      const int t = c * D;
+      const uint8_t* buf = xs[c & 1];
+      issue_chunk(ng, nu, t + D);
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        consume(rg[s], ru[s], s, buf);
+        issue(rg[s], ru[s], t + s + D);
+        ring_fence();
+      }
+      cg = ng;
+      cu = nu;
+      if (c + 1 < nchunk) stage_store((c + 1) & 1);
+      stage_load(c + 2);
+      lds_barrier();
+    }
+
+    if (wave_ok) {
+      const int n = nt * 16 + ln.c;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = moe_out_slot(ln.g, i);
+        if (m < cnt) {
+          const int64_t a = unit_member(src, first + m);
+          const float gt = accg[i];
+          store_planes<2>(inter + a * I + n, inter_plane, gt / (1.f + __expf(-gt)) * accu[i]);
+        }
+      }
+    }
+  }
+}
+
+// down, LDS variant (hi/lo intermediate planes, chunked scales). Item = (unit, 4 x R tiles of
+// 16 hidden rows), wave w takes tiles (4q + w) R .. + R. Chunks of 256 K = 2 trips = one turn
+// of the D = 2 ring; each chunk stages both planes.
+template <int R, int D>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
+    const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, int H, UnitSrc src, float* __restrict__ y) {
+  constexpr int KC = 256, TPC = KC / 128;
+  static_assert(D == TPC, "one ring turn per staged chunk");
+  using G = StageGeom<KC, 2>;
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][G::kBuf];
+  const int rtiles = H >> 4;
+  const int ngroup = (rtiles + kMoeWaves * R - 1) / (kMoeWaves * R);
+  const int n_items = unit_count(src) * ngroup;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int nb = K >> 5, ntrip = nb >> 2, nchunk = K / KC;
+  const int64_t row_bytes = K >> 1;
+  const rsrc_t ra = make_rsrc(inter, (uint32_t)(2 * inter_plane * 2));
+  const uint32_t exp_bytes = (uint32_t)H * (uint32_t)row_bytes;
+  // staging: thread -> (token row sr, plane sp, 64-byte segment) of a chunk
+  const int sr = tid >> 4, sp = (tid >> 3) & 1, sseg = tid & 7;
+
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int u = item / ngroup, q = item - u * ngroup;
+    int e, first, cnt;
+    unit_get(src, u, e, first, cnt);
+    if (cnt == 0) continue;
+    const int eu = uniform(e);
+    const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
+    const rsrc_t rs = make_rsrc(ws + (int64_t)eu * H * nb, (uint32_t)(H * nb));
+    uint32_t ow[R], os[R];
+    const int tile0 = (q * kMoeWaves + wave) * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int rt = min(tile0 + r, rtiles - 1);
+      const uint32_t row = (uint32_t)(rt * 16 + ln.c);
+      ow[r] = row * (uint32_t)row_bytes;
+      os[r] = row * (uint32_t)nb;
+    }
+    const uint32_t sa = sr < cnt ? (uint32_t)unit_member(src, first + sr) * (uint32_t)K * 2u +
+                                       (uint32_t)sp * (uint32_t)inter_plane * 2u + (uint32_t)sseg * 64u
+                                 : kOutOfRange;
+    u32x4_t sreg[4];
+    auto stage_load = [&](int c) {
+      const uint32_t bad = (uint32_t)!(c < nchunk) << 31;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sreg[k] = buf16(ra, (sa + (uint32_t)c * (KC * 2) + 16u * k) | bad);
+    };
+    auto stage_store = [&](int b) {
+#pragma unroll
+      for (int k = 0; k < 4; ++k)
+        lds16_store(&xs[b][sr * G::kRow + sp * G::kPlaneBytes + sseg * 64 + 16 * k], sreg[k]);
+    };
+    auto issue = [&](u32x4_t* w, int tr) {
+      const int blk = moe_block(tr, ln.g);
+      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
+#pragma unroll
+      for (int r = 0; r < R; ++r) w[r] = buf16(rw, (ow[r] + (uint32_t)blk * 16u) | bad);
+    };
+    ScaleChunk<D> cs[R], ns[R];
+    auto issue_chunk = [&](ScaleChunk<D>* cc, int tr) {
+      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
+#pragma unroll
+      for (int r = 0; r < R; ++r) cc[r].load(rs, (os[r] + 4u * (uint32_t)tr) | bad);
+    };
+    f32x4_t acc[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    auto consume = [&](const u32x4_t* w, int s, const uint8_t* buf) {
+      const uint8_t* arow = buf + ln.c * G::kRow + ((4 * s + ln.g) * 32) * 2;
+      u32x4_t a[2][4];
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int h = 0; h < 4; ++h) a[p][h] = lds16(arow + p * G::kPlaneBytes + 16 * h);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const float fs = e8m0_to_f32(cs[r].byte(s, ln.g));
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const bf16x8_t b = decode8(w[r][h], fs);
+          acc[r] = mfma16x16x32(as_bf16x8(a[0][h]), b, acc[r]);
+          acc[r] = mfma16x16x32(as_bf16x8(a[1][h]), b, acc[r]);
+        }
+      }
+    };
+
+    stage_load(0);
+    stage_store(0);
+    stage_load(1);
+    issue_chunk(cs, 0);
+    u32x4_t ring[D][R];
+#pragma unroll
+    for (int s = 0; s < D; ++s) {
+      issue(ring[s], s);
+      ring_fence();
+    }
+    lds_barrier();
+    for (int c = 0; c < nchunk; ++c) {
+      const int t = c * D;
+      const uint8_t* buf = xs[c & 1];
+      issue_chunk(ns, t + D);
+#pragma unroll
+      for (int s = 0; s < D; ++s) {
+        consume(ring[s], s, buf);
+        issue(ring[s], t + s + D);
+        ring_fence();
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) cs[r] = ns[r];
+      if (c + 1 < nchunk) stage_store((c + 1) & 1);
+      stage_load(c + 2);
+      lds_barrier();
+    }
+
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      if (tile0 + r >= rtiles) continue;
+      const int n = (tile0 + r) * 16 + ln.c;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = moe_out_slot(ln.g, i);
+        if (m < cnt) y[(int64_t)unit_member(src, first + m) * H + n] = acc[r][i];
+      }
+    }
+  }
+}
+
 // ---------------------------------------------------------------- combine (unit mode)
 //
 // out[t, n..n+3] = sum_j w_j * y[t*top_k + j, n..n+3] over live assignments, in j order. The
@@ -645,11 +929,28 @@ bool chunked_scales(int K, int split, int D) {
   return nb % 16 == 0 && T % D == 0;
 }
 
+// Unit-mode gate_up with the activation rows staged in LDS (bf16 x, K a multiple of 512).
+int launch_gate_up_lds(const uint16_t* x, int64_t x_elems, int K, const uint8_t* wq,
+                       const uint8_t* ws, int I, const UnitSrc& src, int64_t max_units, int top_k,
+                       uint16_t* inter, int64_t inter_plane, hipStream_t st) {
+  static int occ = 0;
+  auto kern = k_moe_gate_up_lds<4>;
+  const int64_t items = max_units * (((I >> 4) + kMoeWaves - 1) / kMoeWaves);
+  const int grid = grid_for(kern, items, occ);
+  if (grid == 0) return 0;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, x, x_elems, K, wq, ws, I, src,
+                     top_k, inter, inter_plane);
+  return status_of(hipGetLastError());
+}
+
 // SPLIT = 4 while the item count would leave fewer than four waves per SIMD busy.
 int launch_gate_up(int xp, const uint16_t* x, int64_t x_plane, int K, const uint8_t* wq,
                    const uint8_t* ws, int I, const UnitSrc& src, int64_t max_units, int top_k,
                    uint16_t* inter, int64_t inter_plane, hipStream_t st) {
   const bool split = max_units * (I >> 4) < (int64_t)device_cu_count() * 16;
+  if (xp == 1 && !split && K % 512 == 0)
+    return launch_gate_up_lds(x, x_plane, K, wq, ws, I, src, max_units, top_k, inter, inter_plane,
+                              st);
 #define MTPK_GU(XP_, OP_, SP_, D_)                                                           \
   (chunked_scales(K, SP_, D_)                                                                \
        ? launch_gate_up_t<XP_, OP_, SP_, D_, true>(x, x_plane, K, wq, ws, I, src, max_units, \
@@ -669,6 +970,20 @@ int launch_down_t(const uint16_t* inter, int64_t inter_plane, int K, const uint8
   auto kern = k_moe_down<IP, R, D, SV>;
   const int64_t items = max_units * (((H >> 4) + R - 1) / R);
   const int grid = grid_for(kern, (items + kMoeWaves - 1) / kMoeWaves, occ);
+  if (grid == 0) return 0;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, inter, inter_plane, K, wq, ws,
+                     H, src, y);
+  return status_of(hipGetLastError());
+}
+
+int launch_down_lds(const uint16_t* inter, int64_t inter_plane, int K, const uint8_t* wq,
+                    const uint8_t* ws, int H, const UnitSrc& src, int64_t max_units, float* y,
+                    hipStream_t st) {
+  static int occ = 0;
+  constexpr int R = 4;
+  auto kern = k_moe_down_lds<R, 2>;
+  const int64_t items = max_units * (((H >> 4) + kMoeWaves * R - 1) / (kMoeWaves * R));
+  const int grid = grid_for(kern, items, occ);
   if (grid == 0) return 0;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, inter, inter_plane, K, wq, ws,
                      H, src, y);
@@ -814,6 +1129,9 @@ int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, 
   const int64_t ip = assignments * inter_dim;
   const UnitSrc src = unit_list(units, sorted, n_units, max_units);
   const bool sv = chunked_scales((int)inter_dim, 1, 2);
+  if (inter_planes == 2 && inter_dim % 256 == 0)
+    return launch_down_lds(inter, ip, (int)inter_dim, down, down_scale, (int)hidden, src,
+                           max_units, y, st);
   if (inter_planes == 2)
     return sv ? launch_down_t<2, 4, 2, true>(inter, ip, (int)inter_dim, down, down_scale,
                                              (int)hidden, src, max_units, y, st)
