@@ -70,6 +70,22 @@ def layer_bytes(m, dl):
     return dl * EXPERT_BYTES + 2 * m * H * 2
 
 
+def profiled_traffic(kernel: str) -> float | None:
+    """HBM bytes per launch of `kernel` (fetched + written, calibrated) from the committed
+    rocprofv3 PMC summary profiles/moe_kernels_mi355x.md, or None if it has no row for it."""
+    path = ROOT / "profiles" / "moe_kernels_mi355x.md"
+    if not path.exists():
+        return None
+    for line in path.read_text().splitlines():
+        cells = [c.strip() for c in line.strip().strip("|").split("|")]
+        if len(cells) == 6 and cells[0] == f"`{kernel}`":
+            try:
+                return (float(cells[4]) + float(cells[5])) * 1e9
+            except ValueError:
+                return None
+    return None
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -78,6 +94,9 @@ def main() -> int:
     ap.add_argument("--layers", type=int, default=4)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
+                    help="also run a plain device copy of this many MiB (3 launches) so a PMC "
+                         "profile can scale FETCH_SIZE/WRITE_SIZE by a known byte count")
     ap.add_argument("--workloads", default="M1,M32,M192",
                     help="comma list of M1, M32, M192; `value` is measured on M192 when listed, "
                          "else on the last one listed")
@@ -121,6 +140,16 @@ def main() -> int:
             ne, nw = zipf_routing(m, seed=100 * m + li)
             a_e, a_w = torch.from_numpy(ne).to(dev), torch.from_numpy(nw).to(dev)
         return x, a_e, a_w, d_live(ne, nw)
+
+    if args.calibrate_copy:
+        n = args.calibrate_copy << 20
+        src_c = torch.empty(n, dtype=torch.uint8, device=dev).fill_(1)
+        dst_c = torch.empty_like(src_c)
+        for _ in range(3):
+            dst_c.copy_(src_c)
+        torch.cuda.synchronize()
+        log(f"calibration copy: 3 x {args.calibrate_copy} MiB")
+        del src_c, dst_c
 
     results = {}
     wanted = args.workloads.split(",")
@@ -218,13 +247,15 @@ def main() -> int:
         "gbs_graph": {k: round(v["gbs"], 1) for k, v in results.items()},
         "d_live": {k: round(v["d_live_mean"], 1) for k, v in results.items()},
         "roofline": {
-            "kernel": "k_moe_gate_up<1,2,4,4> (direct)" if runner.direct else "k_moe_gate_up<1,2,1,4>",
+            "kernel": "k_moe_gate_up<1,2,4,4,true> (direct)" if runner.direct else "k_moe_gate_up_lds<4>",
             "bound": "hbm",
             "achieved": round(gu_gbs, 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": None if runner.direct else profiled_traffic("mtpk::k_moe_gate_up_lds<4>"),
+            "traffic_source": "profiles/moe_kernels_mi355x.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                              "copy-calibrated)",
             "avg_us": round(gu_ms * 1e3, 2),
             "algorithmic_bytes": round(gu_bytes),
         },
