@@ -163,3 +163,115 @@ def kv_write_rows(pos: torch.Tensor, block_table: torch.Tensor, t: int, block_si
     grid = pos[:, None] + torch.arange(t, device=pos.device)[None, :]
     block_id = torch.gather(block_table.long(), 1, (grid // block_size).long())
     return block_id * block_size + grid % block_size
+
+
+# ---------------------------------------------------------------- the device round
+
+
+def draft_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int,
+                     forced: torch.Tensor | None = None, forced_n: torch.Tensor | None = None) -> None:
+    """`m.k` MTP draft steps for the first `b` lanes of `buf`, drafts written into
+    `buf.token_matrix[:, 1:]` (`graph_mtp.py:477-504`). Device-only, no host read. A lane with
+    `forced_n[j] > 0` feeds (and keeps) its forced tokens instead of its first drafts."""
+    hid = mtp_mod.draft_seed(model, model.hidden_cache[lanes])
+    tok = buf.token_matrix[:b, :1]
+    table = model.blocks.table[lanes]
+    for s in range(m.k):
+        pos = buf.pos[:b] + s
+        rows = model.blocks.physical_rows(lanes, pos[:, None])[:, 0]
+        hid, tok = mtp_mod.draft_step(model, m, hid, tok, pos, rows, table)
+        if forced is not None:
+            tok = torch.where((forced_n > s)[:, None], forced[:, s : s + 1], tok)
+        buf.token_matrix[:b, s + 1] = tok[:, 0]
+
+
+def verify_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int, ctx_len: int,
+                      forced_n: torch.Tensor | None = None) -> None:
+    """Verify forward over `buf.token_matrix[:b]`, argmax, acceptance with every rollback
+    index (`mtpk_greedy_accept`), then the commit of DeltaNet state, MTP cache rows and the
+    cached hidden seed to each lane's accepted length (`graph_mtp.py:513-582`). Device-only."""
+    t = buf.t
+    dev = buf.pos.device
+    pos = buf.pos[:b]
+    res = model.forward_rows(buf.token_matrix[:b], lanes, pos, ctx_len)
+    buf.step_argmax[:b] = model.argmax(model.logits(res.hidden)).view(b, t)
+    out = AcceptResult(buf.accept_len[:b], buf.lengths[:b], buf.packed_src[: b * t],
+                       buf.packed_cu[: b + 1], buf.conv_idx[:b], buf.keep[:b], buf.bonus[:b],
+                       buf.next_pos[:b], buf.budget_left[:b], buf.live[:b], buf.hidden_src[:b])
+    greedy_accept(buf.step_argmax[:b], buf.token_matrix[:b, 1:], buf.active[:b], pos,
+                  buf.budget[:b], buf.stops[:b], buf.conv_k1, out=out)
+    if forced_n is not None:
+        # A forced lane commits its forced tokens plus one target token; stop ids and the
+        # budget do not apply to forced tokens (`graph_verify_wide.py:196-200`).
+        a = torch.where(forced_n > 0, forced_n, out.accept_len)
+        out.accept_len.copy_(a)
+        out.lengths.copy_(torch.where(buf.active[:b], a + 1, torch.ones_like(a)))
+        out.keep.copy_(buf.active[:b, None] & (torch.arange(t, device=dev)[None, :] <= a[:, None]))
+        out.hidden_src.copy_(torch.arange(b, device=dev) * t + a)
+        win = torch.arange(buf.conv_k1, device=dev)
+        out.conv_idx.copy_(torch.clamp(out.lengths[:, None] + win[None, :], max=buf.conv_k1 + t - 1))
+    model.commit(res, lanes, out.lengths, conv_idx=out.conv_idx)
+    grid = pos[:, None] + torch.arange(t, device=dev)[None, :]
+    raw_seed = model.hidden_cache[lanes]
+    previous = torch.cat([raw_seed[:, None], res.hidden[:, :-1]], dim=1)
+    mtp_mod.cache_target_rows(model, m, buf.token_matrix[:b], previous, grid,
+                              model.blocks.physical_rows(lanes, grid), out.keep)
+    model.hidden_cache[lanes] = res.hidden.reshape(b * t, -1)[out.hidden_src]
+
+
+class MTPVerifyRunner:
+    """Device speculative rounds over static buffers (`graph_mtp.MTPVerifyRunner`,
+    `graph_mtp.py:893-918`): fill, draft, verify + accept + commit, one host read."""
+
+    def __init__(self, model, capacity: int) -> None:
+        if model.mtp is None:
+            raise ValueError("model has no MTP layer")
+        self.model, self.mtp = model, model.mtp
+        self.t = self.mtp.k + 1
+        c = model.cfg
+        self.buf = MTPVerifyBuffers(capacity, self.t, c.hidden, model.blocks.max_blocks, model.device,
+                                    model.dtype, conv_k1=c.conv_k - 1)
+        self.capacity = capacity
+
+    def fill(self, slots, tokens, positions, budgets, stops, forced):
+        buf, b, t = self.buf, len(slots), self.t
+        if not 1 <= b <= self.capacity or len(set(slots)) != b:
+            raise ValueError(f"need 1..{self.capacity} distinct slots, got {slots}")
+        if stops is not None and any(len(s) > mtp_mod.MAX_STOP_IDS for s in stops):
+            raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
+        for s, p in zip(slots, positions, strict=True):
+            self.model.blocks.grow(s, p + t)
+        dev = buf.pos.device
+        big = 1 << 40
+        host = torch.tensor([[tk, p, big if budgets is None else budgets[j]]
+                             for j, (tk, p) in enumerate(zip(tokens, positions, strict=True))], dtype=torch.long)
+        host = host.to(dev)
+        buf.token_matrix[:b, 0] = host[:, 0]
+        buf.pos[:b] = host[:, 1]
+        buf.budget[:b] = host[:, 2]
+        buf.active[:b] = True
+        st = torch.full((b, mtp_mod.MAX_STOP_IDS), -1, dtype=torch.long)
+        for j, ids in enumerate(stops or []):
+            st[j, : len(ids)] = torch.tensor(list(ids), dtype=torch.long)
+        buf.stops[:b] = st.to(dev)
+        if not forced or not any(forced):
+            return None, None
+        k = self.mtp.k
+        ft = torch.zeros(b, k, dtype=torch.long)
+        fn = torch.zeros(b, dtype=torch.long)
+        for j, ids in enumerate(forced):
+            ids = list(ids)[:k]
+            fn[j] = len(ids)
+            ft[j, : len(ids)] = torch.tensor(ids, dtype=torch.long)
+        return ft.to(dev), fn.to(dev)
+
+    def speculative_decode(self, slots: list[int], tokens: list[int], positions: list[int],
+                           budgets=None, stops=None, forced=None) -> list[list[int]]:
+        """Each slot's committed ids for one round (`Model.speculative_decode`'s contract)."""
+        b = len(slots)
+        ft, fn = self.fill(slots, tokens, positions, budgets, stops, forced)
+        lanes = self.model.lane_index(slots)
+        draft_round_step(self.model, self.mtp, self.buf, lanes, b, ft, fn)
+        verify_round_step(self.model, self.mtp, self.buf, lanes, b, max(positions) + self.t, fn)
+        rows = torch.cat([self.buf.step_argmax[:b], self.buf.accept_len[:b, None]], dim=1).tolist()
+        return [row[: row[-1] + 1] for row in rows]

@@ -1,4 +1,10 @@
-"""MTP draft/verify/accept — the reference's `mtp` interface (`mtp.py`), acceptance half.
+"""MTP draft / verify / accept — the reference's `mtp` interface (`mtp.py`).
+
+The MTP head (`MTP`, `attach`, `draft_step`, `draft`, `cache_target_rows`) is one decoder
+layer fed by `fc(cat(norm(embed(token)), norm(hidden)))` (`mtp.py:191-549`); its attention
+reads its own K/V pool through the target's block tables and its MoE is the same routed MXFP4
+call as a target layer's. `verify_and_commit` / `speculative_decode` are the eager round
+(`mtp.py:729-817`, `model.py:4183-4220`); `graph_mtp.MTPVerifyRunner` is the device round.
 
 Host-side acceptance keeps the reference's pure functions (`greedy_accept_length`,
 `commit_limit`, `mtp.py:691-726`); the device-side greedy token is the fused argmax kernel
@@ -10,6 +16,7 @@ from __future__ import annotations
 
 import os
 from collections.abc import Sequence
+from dataclasses import dataclass
 
 import torch
 
@@ -92,3 +99,181 @@ def greedy_token(model, normed: torch.Tensor) -> torch.Tensor:
     if logits.device.type == "cuda":
         return argmax_rows(logits)[..., None]
     return logits.float().argmax(-1, keepdim=True)
+
+
+# ---------------------------------------------------------------- the MTP head
+
+
+@dataclass
+class MTP:
+    """The MTP module and its paged KV cache (`mtp.py:114-128`). `weights` holds one decoder
+    layer (`in_norm`, `post_norm`, gated attention, router, shared expert, MXFP4 experts) keyed
+    like a target layer; the pool is indexed by the target's block tables."""
+
+    k: int
+    weights: dict
+    fc: torch.Tensor
+    pre_fc_norm_embedding: torch.Tensor
+    pre_fc_norm_hidden: torch.Tensor
+    norm: torch.Tensor
+    pool: dict
+
+
+def attach(model, k: int | None = None, seed: int = 1, expert_mode: str = "quantized") -> MTP:
+    """Random-init MTP layer for `model` (the same initialisers as its target layers), stored
+    as `model.mtp`. `k` defaults to `MTP_K`."""
+    import verify_model as vm
+
+    c, dev, dt = model.cfg, model.device, model.dtype
+    gen = torch.Generator(device="cpu" if c.hidden < 1024 else dev).manual_seed(seed)
+    w = {"in_norm": vm._normal((c.hidden,), 0.02, dt, dev, gen),
+         "post_norm": vm._normal((c.hidden,), 0.02, dt, dev, gen)}
+    w.update(vm.attention_weights(c, dt, dev, gen))
+    w.update(vm.moe_weights(c, dt, dev, gen, expert_mode))
+    shape = (model.blocks.rows, c.kv_heads, c.head_dim)
+    m = MTP(
+        k=MTP_K if k is None else k,
+        weights=w,
+        fc=vm._normal((c.hidden, 2 * c.hidden), 0.02, dt, dev, gen),
+        pre_fc_norm_embedding=vm._normal((c.hidden,), 0.02, dt, dev, gen),
+        pre_fc_norm_hidden=vm._normal((c.hidden,), 0.02, dt, dev, gen),
+        norm=vm._normal((c.hidden,), 0.02, dt, dev, gen),
+        pool={"k": torch.zeros(shape, dtype=dt, device=dev), "v": torch.zeros(shape, dtype=dt, device=dev)},
+    )
+    model.mtp = m
+    return m
+
+
+def draft_seed(model, raw_hidden: torch.Tensor) -> torch.Tensor:
+    """Step 0's hidden input: the target's final-normed last hidden state (`mtp.py:433-437`,
+    the default `post` seed)."""
+    import verify_model as vm
+
+    return vm.rmsnorm(raw_hidden, model.final_norm, model.cfg.eps)
+
+
+def _combine_rows(model, mtp: MTP, hidden: torch.Tensor, tokens: torch.Tensor) -> torch.Tensor:
+    """`fc(cat(norm(embed(tokens)), norm(hidden)))` for matching leading dims
+    (`mtp.py:191-230`)."""
+    import verify_model as vm
+
+    eps = model.cfg.eps
+    emb = vm.rmsnorm(model.embed[tokens], mtp.pre_fc_norm_embedding, eps)
+    hid = vm.rmsnorm(hidden, mtp.pre_fc_norm_hidden, eps)
+    return torch.nn.functional.linear(torch.cat([emb, hid], dim=-1), mtp.fc)
+
+
+def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: torch.Tensor,
+               write_rows: torch.Tensor, block_table: torch.Tensor,
+               block_valid: torch.Tensor | None = None,
+               active: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """One MTP decoder-layer step on device-resident tensors (`mtp.py:506-549`):
+    `(hid [B, hidden], tok [B, 1])` -> the next pair. `rope_pos` `[B]` is the fed token's
+    position, `write_rows` `[B]` its MTP pool row, `block_table` `[B, blocks]` the lanes' tables.
+    `block_valid` and `active` are accepted for signature compatibility: the attention reads
+    the table up to its width and masks by position, and inactive lanes write their own rows."""
+    import verify_model as vm
+
+    c, w = model.cfg, mtp.weights
+    x = _combine_rows(model, mtp, hid[:, None, :], tok)  # [B, 1, hidden]
+    h = vm.rmsnorm(x, w["in_norm"], c.eps)
+    x = x + vm.gated_attention(model, w, mtp.pool, h, rope_pos, write_rows.reshape(-1, 1),
+                               block_table, block_table.shape[1])
+    hm = vm.rmsnorm(x, w["post_norm"], c.eps)
+    x = x + model.moe(w, hm[:, 0])[:, None]
+    normed = vm.rmsnorm(x, mtp.norm, c.eps)[:, 0]
+    nxt = model.argmax(model.unembed(normed))[:, None]
+    return normed, nxt
+
+
+def draft(model, mtp: MTP, hidden: torch.Tensor, tokens: list[int], slots: list[int],
+          positions: list[int]) -> list[list[int]]:
+    """`mtp.k` greedy MTP steps from each slot's last committed token and the target's raw
+    hidden state (`mtp.py:391-430`); one host read for the whole round."""
+    dev = model.device
+    lanes = model.lane_index(slots)
+    for s, p in zip(slots, positions, strict=True):
+        model.blocks.grow(s, p + mtp.k)
+    hid = draft_seed(model, hidden)
+    tok = torch.tensor([[t] for t in tokens], dtype=torch.long, device=dev)
+    base = torch.tensor(positions, dtype=torch.long, device=dev)
+    table = model.blocks.table[lanes]
+    out = torch.empty(len(slots), mtp.k, dtype=torch.long, device=dev)
+    for step in range(mtp.k):
+        pos = base + step
+        rows = model.blocks.physical_rows(lanes, pos[:, None])[:, 0]
+        hid, tok = draft_step(model, mtp, hid, tok, pos, rows, table)
+        out[:, step] = tok[:, 0]
+    return out.tolist()
+
+
+def cache_target_rows(model, mtp: MTP, tokens: torch.Tensor, raw_previous_hidden: torch.Tensor,
+                      positions: torch.Tensor, write_rows: torch.Tensor,
+                      keep: torch.Tensor | None = None) -> None:
+    """Write the MTP layer's canonical K/V for fed tokens from the target's hidden stream
+    (`mtp.py:440-485`): token `tokens[b, s]` at `positions[b, s]` paired with the target's raw
+    hidden state of the previous position. Rows with `keep` False are left as they are."""
+    import verify_model as vm
+
+    c, w = model.cfg, mtp.weights
+    x = _combine_rows(model, mtp, draft_seed(model, raw_previous_hidden), tokens)
+    x = vm.rmsnorm(x, w["in_norm"], c.eps)
+    lead = tokens.shape
+    k = vm.rmsnorm(torch.nn.functional.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim),
+                   w["k_norm"], c.eps)
+    v = torch.nn.functional.linear(x, w["v_proj"]).view(*lead, c.kv_heads, c.head_dim)
+    pos = positions.long()
+    k = vm.apply_rope(k, model.cos[pos][..., None, :], model.sin[pos][..., None, :])
+    rows = write_rows.reshape(-1).long()
+    k = k.reshape(-1, c.kv_heads, c.head_dim)
+    v = v.reshape(-1, c.kv_heads, c.head_dim)
+    if keep is not None:
+        live = keep.reshape(-1)
+        k = torch.where(live[:, None, None], k, mtp.pool["k"][rows])
+        v = torch.where(live[:, None, None], v, mtp.pool["v"][rows])
+    mtp.pool["k"][rows] = k
+    mtp.pool["v"][rows] = v
+
+
+def verify_and_commit(model, mtp: MTP, slots: list[int], base_tokens: list[int],
+                      draft_tokens: list[list[int]], positions: list[int],
+                      budgets: Sequence[int] | None = None,
+                      stops: Sequence[Sequence[int]] | None = None) -> list[list[int]]:
+    """One wide verify forward over the `[B, k + 1]` fed tokens, greedy acceptance, and the
+    commit of every per-slot state to the accepted length (`mtp.py:729-817`). Returns each
+    slot's committed ids (accepted drafts plus the bonus token)."""
+    dev = model.device
+    b, k = len(slots), mtp.k
+    t = k + 1
+    lanes = model.lane_index(slots)
+    for s, p in zip(slots, positions, strict=True):
+        model.blocks.grow(s, p + t)
+    ids = torch.tensor([[base_tokens[j], *draft_tokens[j]] for j in range(b)], dtype=torch.long, device=dev)
+    base = torch.tensor(positions, dtype=torch.long, device=dev)
+    raw_seed = model.hidden_cache[lanes]
+    res = model.forward_rows(ids, lanes, base, max(positions) + t)
+    step_argmax = model.argmax(model.logits(res.hidden)).reshape(b, t)
+    rows = step_argmax.tolist()
+    accept = [
+        commit_limit(greedy_accept_length(draft_tokens[j], rows[j][:k]), rows[j],
+                     None if budgets is None else budgets[j], () if stops is None else stops[j])
+        for j in range(b)
+    ]
+    acc = torch.tensor(accept, dtype=torch.long, device=dev)
+    model.commit(res, lanes, acc + 1)
+    grid = base[:, None] + torch.arange(t, device=dev)[None, :]
+    previous = torch.cat([raw_seed[:, None], res.hidden[:, :-1]], dim=1)
+    keep = torch.arange(t, device=dev)[None, :] <= acc[:, None]
+    cache_target_rows(model, mtp, ids, previous, grid, model.blocks.physical_rows(lanes, grid), keep)
+    model.hidden_cache[lanes] = res.hidden[torch.arange(b, device=dev), acc]
+    return [rows[j][: accept[j] + 1] for j in range(b)]
+
+
+def speculative_decode(model, slots: list[int], tokens: list[int], positions: list[int],
+                       budgets: Sequence[int] | None = None,
+                       stops: Sequence[Sequence[int]] | None = None) -> list[list[int]]:
+    """Draft then verify (`Model.speculative_decode`, `model.py:4183-4220`): each slot's
+    committed ids for this round."""
+    m = model.mtp
+    drafts = draft(model, m, model.hidden_cache[model.lane_index(slots)], tokens, slots, positions)
+    return verify_and_commit(model, m, slots, tokens, drafts, positions, budgets, stops)

@@ -60,3 +60,31 @@ def dequant_in_kernel(packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor
     """fp32 view of the MoE kernels' own in-register decode (hardware fp4 -> bf16 convert with
     the block scale folded in). Exact for scale bytes 2..252; a test probe, not a serving op."""
     return _dequant_device(packed, scale, mode=1)
+
+
+_FP4_MAGNITUDES = (0.0, 0.5, 1.0, 1.5, 2.0, 3.0, 4.0, 6.0)
+
+
+def quantize_mxfp4(w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """OCP MX quantisation of a float `[..., K]` tensor to `(packed u8 [..., K/2], e8m0 scale
+    u8 [..., K/32])`, on `w`'s device.
+
+    Per block of 32 the shared exponent is `floor(log2(amax)) - 2` (e2m1's largest exponent),
+    so the block maximum lands in [4, 8) and saturates at 6; each element takes the nearest
+    e2m1 magnitude (ties to the smaller one) and its sign. An all-zero block gets scale byte 127
+    and zero codes. This is how the random expert payloads of the small models are made.
+    """
+    *lead, k = w.shape
+    if k % BLOCK:
+        raise ValueError(f"last dim {k} is not a multiple of {BLOCK}")
+    blocks = w.float().reshape(*lead, k // BLOCK, BLOCK)
+    amax = blocks.abs().amax(-1)
+    exp = torch.where(amax > 0, torch.floor(torch.log2(amax.clamp_min(2.0 ** -126))) - 2,
+                      torch.zeros_like(amax)).clamp(-127, 127)
+    mags = torch.tensor(_FP4_MAGNITUDES, device=w.device)
+    scaled = blocks.abs() / torch.exp2(exp)[..., None]
+    code = (scaled[..., None] - mags).abs().argmin(-1)
+    code = code + 8 * ((blocks < 0) & (code > 0))
+    code = code.reshape(*lead, k).to(torch.uint8)
+    packed = code[..., 0::2] | (code[..., 1::2] << 4)
+    return packed.contiguous(), (exp + 127).to(torch.uint8).contiguous()

@@ -1,0 +1,631 @@
+"""Compact Qwen3.5-MoE target model for the MTP verify path.
+
+What the speculative step needs of the target, and nothing else: token embedding, a stack of
+Gated-DeltaNet and gated GQA attention layers each followed by the routed MXFP4 MoE plus the
+shared expert, the final norm and the LM head; a paged KV cache with 16-row blocks; per-slot
+DeltaNet conv/recurrent state; and the cached last hidden state the MTP head is seeded from.
+The layer math follows the reference's `Model` (`model.py:587-649` norms/RoPE/SwiGLU,
+`model.py:2158-2290` gated attention, `model.py:2396-2470` DeltaNet, `model.py:2758-2873`
+MoE) and its wide verify forward (`decode_layer_verify`, `model.py:3974-3995`).
+
+Verify and commit are split differently from the reference. `deltanet_verify` computes all
+`t` rows' outputs from the committed state WITHOUT writing any state back, and returns the
+per-row activations; `deltanet_commit` then advances the stored conv window and recurrent
+state by exactly `lengths[j]` rows of slot j. The reference writes the speculative state for
+all `t` rows, snapshots the pre-verify state and replays the accepted prefix over it
+(`deltanet_verify` / `deltanet_verify_rollback`, `model.py:3738-3972`); the result is the
+same state, without the `[B, heads, k_dim, v_dim]` clone and its HBM round trip. Plain decode
+is the same pair at `t = 1`, so a speculative round and a sequence of decode steps run the
+same per-row arithmetic.
+
+Device tensors take the HIP kernels for the routed MoE (`mxfp4_gemv.fused_moe`), the router
+(`router_fused.route`) and the argmax (`mtp.argmax_rows`), and raise if the library is
+missing. CPU tensors take the reference's torch spellings of the same ops (its CPU engine:
+`mxfp4_gemv.reference_moe`, softmax/topk, `argmax`), which is what config 1 exercises.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn.functional as F
+
+import mxfp4
+import mxfp4_gemv
+import router_fused
+
+ATTN = "full_attention"
+DELTANET = "linear_attention"
+
+
+@dataclass(frozen=True)
+class Cfg:
+    """Model shape (the fields of the reference's `Cfg`, `model.py:530-551`, plus the expert
+    intermediate width and the KV block size)."""
+
+    hidden: int
+    vocab: int
+    layer_types: tuple[str, ...]
+    eps: float
+    heads: int
+    kv_heads: int
+    head_dim: int
+    rot_dim: int
+    rope_theta: float
+    k_heads: int
+    v_heads: int
+    k_dim: int
+    v_dim: int
+    conv_k: int
+    experts: int
+    top_k: int
+    inter: int
+    shared_inter: int
+    block_size: int = 16
+    eos: tuple[int, ...] = ()
+
+    @property
+    def conv_dim(self) -> int:
+        return 2 * self.k_heads * self.k_dim + self.v_heads * self.v_dim
+
+    @property
+    def in_proj_sizes(self) -> list[int]:
+        """Output widths of the fused DeltaNet input projection: qkv, z, beta, a
+        (`model.py:860-867`)."""
+        return [self.conv_dim, self.v_heads * self.v_dim, self.v_heads, self.v_heads]
+
+
+def tiny_cfg() -> Cfg:
+    """The CPU plumbing model: hidden 64, 3 DeltaNet + 1 attention layer (4 q / 2 kv heads of
+    16), 8 experts top-2 with intermediate 32, one shared expert, vocab 512."""
+    return Cfg(
+        hidden=64, vocab=512, layer_types=(DELTANET, DELTANET, DELTANET, ATTN), eps=1e-6,
+        heads=4, kv_heads=2, head_dim=16, rot_dim=4, rope_theta=10000.0,
+        k_heads=2, v_heads=4, k_dim=16, v_dim=16, conv_k=4,
+        experts=8, top_k=2, inter=32, shared_inter=32, eos=(1,),
+    )  # fmt: skip
+
+
+def verify_cfg() -> Cfg:
+    """Real Qwen3.5-397B-A17B layer dimensions at reduced depth: 3 DeltaNet + 1 gated GQA
+    attention layer (32 q / 2 kv heads of 256, RoPE on the first 64 channels), 512 experts
+    top-10 of intermediate 1024 plus a shared expert of 1024, vocab 248320."""
+    return Cfg(
+        hidden=4096, vocab=248320, layer_types=(DELTANET, DELTANET, DELTANET, ATTN), eps=1e-6,
+        heads=32, kv_heads=2, head_dim=256, rot_dim=64, rope_theta=1.0e7,
+        k_heads=16, v_heads=64, k_dim=128, v_dim=128, conv_k=4,
+        experts=512, top_k=10, inter=1024, shared_inter=1024,
+    )  # fmt: skip
+
+
+# ---------------------------------------------------------------- layer math
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """Qwen3.5 RMSNorm: normalise in fp32, scale by `1 + w` (`model.py:587-604`)."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
+    return (y * (1.0 + w.float())).to(x.dtype)
+
+
+def gated_rmsnorm(x: torch.Tensor, gate: torch.Tensor, w: torch.Tensor, eps: float,
+                  dtype: torch.dtype) -> torch.Tensor:
+    """DeltaNet output norm: RMS-normalise, scale by `w` (no +1), times `silu(gate)`
+    (`model.py:613-619`)."""
+    xf = x.float()
+    y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
+    return (y * F.silu(gate.float())).to(dtype)
+
+
+def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    return x * torch.rsqrt((x * x).sum(-1, keepdim=True) + eps)
+
+
+def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotate-half RoPE on the first `rot_dim` channels of the last axis (`model.py:631-635`);
+    `cos`/`sin` broadcast against `x[..., :rot_dim]`."""
+    r = cos.shape[-1]
+    rot, rest = x[..., :r].float(), x[..., r:]
+    h = r // 2
+    turned = torch.cat((-rot[..., h:], rot[..., :h]), dim=-1)
+    return torch.cat(((rot * cos + turned * sin).to(x.dtype), rest), dim=-1)
+
+
+def rope_table(cfg: Cfg, positions: int, device: torch.device) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 `cos`, `sin` `[positions, rot_dim]` (`model.py:2396-2418`)."""
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(0, cfg.rot_dim, 2, device=device).float() / cfg.rot_dim))
+    pos = torch.arange(positions, device=device).float()
+    ang = pos[:, None] * inv[None, :]
+    emb = torch.cat((ang, ang), dim=-1)
+    return emb.cos(), emb.sin()
+
+
+def causal_conv_rows(window: torch.Tensor, weight: torch.Tensor, t: int) -> torch.Tensor:
+    """Depthwise causal conv + SiLU over `t` new columns. `window` is `[B, C, conv_k - 1 + t]`
+    (the stored window, then the new raw inputs), `weight` `[C, conv_k]`; returns fp32
+    `[B, C, t]`. Taps are summed in a fixed order per element, so a row's value does not
+    depend on how many rows are computed together (`model.py:2631-2636`)."""
+    kk = weight.shape[-1]
+    w = weight.float()
+    win = window.float()
+    acc = win[:, :, 0:t] * w[None, :, 0:1]
+    for j in range(1, kk):
+        acc = acc + win[:, :, j : j + t] * w[None, :, j : j + 1]
+    return F.silu(acc)
+
+
+def delta_rule_step(state: torch.Tensor, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                    g: torch.Tensor, beta: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """One gated delta-rule step for every (slot, head) (`model.py:651-697`):
+    `S <- exp(g) S;  S <- S + k ((v - S^T k) beta)^T;  out = S^T q`. `state` `[B, H, dk, dv]`
+    fp32, `q`/`k` `[B, H, dk]` (normalised), `v` `[B, H, dv]`, `g`/`beta` `[B, H]`. Returns the
+    new state and `out` `[B, H, dv]`; the input state is not modified."""
+    s = state * g.exp()[..., None, None]
+    mem = torch.einsum("bhkv,bhk->bhv", s, k)
+    delta = (v - mem) * beta[..., None]
+    s = s + k[..., :, None] * delta[..., None, :]
+    out = torch.einsum("bhkv,bhk->bhv", s, q)
+    return s, out
+
+
+def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                    block_table: torch.Tensor, base_pos: torch.Tensor, ctx_blocks: int,
+                    block_size: int, scale: float) -> torch.Tensor:
+    """Causal attention of `t` new query rows per lane over the paged cache
+    (`verify_attention_paged`, `model.py:1120-1205`). `q` `[B, heads, t, hd]`; pools
+    `[rows, kv_heads, hd]` already hold this round's rows; query row `s` of lane `b` sits at
+    `base_pos[b] + s` and sees every cached position up to its own. `ctx_blocks` bounds the
+    gather (a host value, at least every lane's block count). fp32 math, q's dtype out."""
+    b, heads, t, hd = q.shape
+    kvh = k_pool.shape[1]
+    group = heads // kvh
+    blocks = block_table[:, :ctx_blocks].long()
+    tok = torch.arange(block_size, device=q.device)
+    rows = (blocks[:, :, None] * block_size + tok).reshape(b, -1)  # [B, S]
+    s_len = rows.shape[1]
+    keys = k_pool[rows].float().permute(0, 2, 3, 1).contiguous()  # [B, kvh, hd, S]
+    vals = v_pool[rows].float().permute(0, 2, 1, 3).contiguous()  # [B, kvh, S, hd]
+    qg = q.float().reshape(b, kvh, group * t, hd)
+    scores = torch.matmul(qg, keys) * scale  # [B, kvh, group*t, S]
+    qpos = base_pos.long()[:, None] + torch.arange(t, device=q.device)[None, :]  # [B, t]
+    live = torch.arange(s_len, device=q.device)[None, None, :] <= qpos[:, :, None]  # [B, t, S]
+    live = live[:, None, None].expand(b, 1, group, t, s_len).reshape(b, 1, group * t, s_len)
+    probs = scores.masked_fill(~live, float("-inf")).softmax(-1)
+    out = torch.matmul(probs, vals)  # [B, kvh, group*t, hd]
+    return out.reshape(b, heads, t, hd).to(q.dtype)
+
+
+def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_pos: torch.Tensor,
+                    write_rows: torch.Tensor, block_table: torch.Tensor, ctx_blocks: int) -> torch.Tensor:
+    """Gated GQA attention of `t` rows per lane (`h` `[B, t, hidden]`, normed): q/gate
+    projection, q/k RMSNorm, partial RoPE at `base_pos + s`, this round's K/V written at
+    `write_rows` `[B, t]` of `pool`, causal paged attention, `o_proj(out * sigmoid(gate))`
+    (`model.py:2158-2290`, `model.py:3519-3577`; the MTP layer's `_attn_rows`, `mtp.py:233-279`,
+    is the same call on its own pool)."""
+    c = model.cfg
+    b, t, _ = h.shape
+    qg = F.linear(h, w["q_proj"]).view(b, t, c.heads, 2 * c.head_dim)
+    q, gate = qg[..., : c.head_dim], qg[..., c.head_dim :]
+    q = rmsnorm(q, w["q_norm"], c.eps)
+    k = rmsnorm(F.linear(h, w["k_proj"]).view(b, t, c.kv_heads, c.head_dim), w["k_norm"], c.eps)
+    v = F.linear(h, w["v_proj"]).view(b, t, c.kv_heads, c.head_dim)
+    pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
+    cos, sin = model.cos[pos][:, :, None], model.sin[pos][:, :, None]  # [B, t, 1, rot]
+    q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+    rows = write_rows.reshape(-1).long()
+    pool["k"][rows] = k.reshape(-1, c.kv_heads, c.head_dim)
+    pool["v"][rows] = v.reshape(-1, c.kv_heads, c.head_dim)
+    out = paged_attention(q.transpose(1, 2), pool["k"], pool["v"], block_table, base_pos, ctx_blocks,
+                          c.block_size, c.head_dim ** -0.5)
+    out = out.transpose(1, 2).reshape(b, t, -1)
+    return F.linear(out * torch.sigmoid(gate.reshape(b, t, -1)), w["o_proj"])
+
+
+# ---------------------------------------------------------------- paged KV block tables
+
+
+class BlockTables:
+    """Per-lane block tables over one pool of `block_size`-row blocks (`block_pool.py`'s role).
+
+    Block 0 is never handed out: unused table entries point at it, so a padded read stays in
+    bounds and reads rows no lane owns (`block_pool.py:38`). Blocks are handed out in a seeded
+    shuffled order so that a lane's physical rows are not contiguous.
+    """
+
+    def __init__(self, lanes: int, max_seq: int, block_size: int, device: torch.device,
+                 seed: int = 0) -> None:
+        self.lanes, self.block_size = lanes, block_size
+        self.max_blocks = (max_seq + block_size - 1) // block_size
+        self.n_blocks = lanes * self.max_blocks + 1
+        gen = torch.Generator().manual_seed(seed)
+        self._free = (torch.randperm(self.n_blocks - 1, generator=gen) + 1).tolist()
+        self.host = [[] for _ in range(lanes)]
+        self.table = torch.zeros(lanes, self.max_blocks, dtype=torch.int32, device=device)
+        self.device = device
+
+    @property
+    def rows(self) -> int:
+        return self.n_blocks * self.block_size
+
+    def grow(self, lane: int, length: int) -> None:
+        """Make lane `lane` hold at least `length` positions (idempotent below that)."""
+        need = (length + self.block_size - 1) // self.block_size
+        if need > self.max_blocks:
+            raise ValueError(f"lane {lane}: {length} positions exceed the table's {self.max_blocks} blocks")
+        have = self.host[lane]
+        if need <= len(have):
+            return
+        new = [self._free.pop() for _ in range(need - len(have))]
+        self.table[lane, len(have) : need] = torch.tensor(new, dtype=torch.int32).to(self.device)
+        have.extend(new)
+
+    def release(self, lane: int) -> None:
+        self._free.extend(reversed(self.host[lane]))
+        self.host[lane] = []
+        self.table[lane].zero_()
+
+    def physical_rows(self, lanes: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """Physical pool rows of positions `pos` `[B, t]` of lanes `lanes` `[B]` (device)."""
+        blk = torch.gather(self.table[lanes.long()].long(), 1, pos.long() // self.block_size)
+        return blk * self.block_size + pos.long() % self.block_size
+
+
+# ---------------------------------------------------------------- weights
+
+
+def _normal(shape, std, dtype, device, gen) -> torch.Tensor:
+    """N(0, std) drawn on the generator's device, stored as `dtype` on `device`."""
+    return (torch.randn(*shape, generator=gen, device=gen.device, dtype=torch.float32) * std).to(device, dtype)
+
+
+def random_experts(cfg: Cfg, device: torch.device, gen: torch.Generator, mode: str) -> dict:
+    """MXFP4 expert payloads in the `load_experts` layout (`model.py:758-804`): `gate_up`
+    `[E, 2I, H/2]` (gate rows then up rows), `down` `[E, H, I/2]`, e8m0 scales per 32.
+
+    `mode="quantized"`: fp32 N(0, 0.02) weights quantised with `mxfp4.quantize_mxfp4`.
+    `mode="bytes"`: packed bytes uniform over 0..255 and scale bytes uniform over 118..130.
+    """
+    e, i, h = cfg.experts, cfg.inter, cfg.hidden
+    if mode == "quantized":
+        gu = _normal((e * 2 * i, h), 0.02, torch.float32, gen.device, gen)
+        dn = _normal((e * h, i), 0.02, torch.float32, gen.device, gen)
+        gq, gs = mxfp4.quantize_mxfp4(gu)
+        dq, ds = mxfp4.quantize_mxfp4(dn)
+        parts = {"gate_up": gq.view(e, 2 * i, h // 2), "gate_up_scale": gs.view(e, 2 * i, h // 32),
+                 "down": dq.view(e, h, i // 2), "down_scale": ds.view(e, h, i // 32)}
+        return {name: ten.to(device) for name, ten in parts.items()}
+    if mode != "bytes":
+        raise ValueError(f"unknown expert init {mode!r}")
+
+    def u8(shape, lo, hi):
+        return torch.randint(lo, hi + 1, shape, generator=gen, device=gen.device,
+                             dtype=torch.int32).to(device, torch.uint8)
+
+    return {"gate_up": u8((e, 2 * i, h // 2), 0, 255), "gate_up_scale": u8((e, 2 * i, h // 32), 118, 130),
+            "down": u8((e, h, i // 2), 0, 255), "down_scale": u8((e, h, i // 32), 118, 130)}
+
+
+def attention_weights(cfg: Cfg, dtype, device, gen) -> dict:
+    qd, kd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
+    return {
+        "q_proj": _normal((2 * qd, cfg.hidden), 0.02, dtype, device, gen),  # per head: q then gate
+        "k_proj": _normal((kd, cfg.hidden), 0.02, dtype, device, gen),
+        "v_proj": _normal((kd, cfg.hidden), 0.02, dtype, device, gen),
+        "o_proj": _normal((cfg.hidden, qd), 0.02, dtype, device, gen),
+        "q_norm": _normal((cfg.head_dim,), 0.02, dtype, device, gen),
+        "k_norm": _normal((cfg.head_dim,), 0.02, dtype, device, gen),
+    }
+
+
+def deltanet_weights(cfg: Cfg, dtype, device, gen) -> dict:
+    vh = cfg.v_heads
+    a_log = torch.log(torch.rand(vh, generator=gen, device=gen.device) * 15.0 + 1.0).to(device)
+    return {
+        "in_proj_all": _normal((sum(cfg.in_proj_sizes), cfg.hidden), 0.02, dtype, device, gen),
+        "conv": _normal((cfg.conv_dim, cfg.conv_k), 0.2, dtype, device, gen),
+        "A_log": a_log.float(),
+        "dt_bias": torch.rand(vh, generator=gen, device=gen.device).to(device),
+        "dn_norm": (1.0 + _normal((cfg.v_dim,), 0.02, torch.float32, device, gen)).to(dtype),
+        "out_proj": _normal((cfg.hidden, vh * cfg.v_dim), 0.02, dtype, device, gen),
+    }
+
+
+def moe_weights(cfg: Cfg, dtype, device, gen, expert_mode: str) -> dict:
+    return {
+        # router rows, then the shared expert's gate row (`model.py:2811-2843`)
+        "router_gate": _normal((cfg.experts + 1, cfg.hidden), 0.02, dtype, device, gen),
+        "shared_gate_up": _normal((2 * cfg.shared_inter, cfg.hidden), 0.02, dtype, device, gen),
+        "shared_down": _normal((cfg.hidden, cfg.shared_inter), 0.02, dtype, device, gen),
+        "experts": random_experts(cfg, device, gen, expert_mode),
+    }
+
+
+# ---------------------------------------------------------------- the model
+
+
+@dataclass
+class DeltaNetRows:
+    """What `deltanet_commit` needs from a verify forward of one DeltaNet layer: the raw
+    conv inputs and the per-row recurrence inputs, `[B, t, ...]`."""
+
+    raw_qkv: torch.Tensor  # [B, conv_dim, t], model dtype
+    q: torch.Tensor  # [B, t, v_heads, k_dim] fp32, normalised and scaled
+    k: torch.Tensor  # [B, t, v_heads, k_dim] fp32, normalised
+    v: torch.Tensor  # [B, t, v_heads, v_dim] fp32
+    g: torch.Tensor  # [B, t, v_heads] fp32
+    beta: torch.Tensor  # [B, t, v_heads] fp32
+
+
+@dataclass
+class VerifyOut:
+    """A forward over `[B, t]` fed tokens: the raw (pre-final-norm) hidden states and, per
+    DeltaNet layer, the rows its commit replays."""
+
+    hidden: torch.Tensor
+    dn_rows: dict[int, DeltaNetRows] = field(default_factory=dict)
+
+
+class Model:
+    """The target stack with its per-slot state. `lanes` is the slot-pool size; every call
+    takes the slots it works on as a `[B]` list or tensor."""
+
+    def __init__(self, cfg: Cfg, device: torch.device | str = "cpu", dtype: torch.dtype = torch.float32,
+                 lanes: int = 2, max_seq: int = 256, seed: int = 0, expert_mode: str = "quantized",
+                 moe_rows: int | None = None, init_device: str | None = None) -> None:
+        """Random-init weights from `seed`. They are drawn on `init_device` (default: the CPU
+        for models below hidden 1024, so a small model has the same weights on every device;
+        the model's device otherwise) and stored on `device`. `moe_rows` sizes the routed-MoE
+        workspace (rows per call; default `4 * lanes`)."""
+        self.cfg, self.dtype = cfg, dtype
+        self.device = torch.device(device)
+        self.lanes, self.max_seq = lanes, max_seq
+        dev = self.device
+        gdev = init_device or ("cpu" if cfg.hidden < 1024 else dev)
+        gen = torch.Generator(device=gdev).manual_seed(seed)
+        self.gen = gen
+        self.embed = _normal((cfg.vocab, cfg.hidden), 0.02, dtype, dev, gen)
+        self.lm_head = _normal((cfg.vocab, cfg.hidden), 0.02, dtype, dev, gen)
+        self.final_norm = _normal((cfg.hidden,), 0.02, dtype, dev, gen)
+        self.layers: list[dict] = []
+        for ty in cfg.layer_types:
+            w = {"in_norm": _normal((cfg.hidden,), 0.02, dtype, dev, gen),
+                 "post_norm": _normal((cfg.hidden,), 0.02, dtype, dev, gen)}
+            w.update(attention_weights(cfg, dtype, dev, gen) if ty == ATTN else deltanet_weights(cfg, dtype, dev, gen))
+            w.update(moe_weights(cfg, dtype, dev, gen, expert_mode))
+            self.layers.append(w)
+        self.blocks = BlockTables(lanes, max_seq, cfg.block_size, dev, seed)
+        self.pool: list[dict] = []
+        for ty in cfg.layer_types:
+            if ty == ATTN:
+                shape = (self.blocks.rows, cfg.kv_heads, cfg.head_dim)
+                self.pool.append({"k": torch.zeros(shape, dtype=dtype, device=dev),
+                                  "v": torch.zeros(shape, dtype=dtype, device=dev)})
+            else:
+                self.pool.append({
+                    "conv": torch.zeros(lanes, cfg.conv_dim, cfg.conv_k - 1, dtype=dtype, device=dev),
+                    "rec": torch.zeros(lanes, cfg.v_heads, cfg.k_dim, cfg.v_dim, dtype=torch.float32, device=dev),
+                })
+        self.hidden_cache = torch.zeros(lanes, cfg.hidden, dtype=dtype, device=dev)
+        self.cos, self.sin = rope_table(cfg, max_seq, dev)
+        self.mtp = None
+        self.moe_ws = None
+        if dev.type == "cuda":
+            rows = moe_rows or lanes * 4
+            self.moe_ws = mxfp4_gemv.moe_scratch(max(rows, 16), cfg.top_k, cfg.experts, cfg.inter,
+                                                 cfg.hidden, dev, dtype)
+
+    # ------------------------------------------------------------ blocks
+
+    def lane_index(self, lanes) -> torch.Tensor:
+        if torch.is_tensor(lanes):
+            return lanes.to(self.device, torch.long)
+        return torch.tensor(list(lanes), dtype=torch.long, device=self.device)
+
+    def reset(self, lane: int) -> None:
+        """Forget slot `lane`'s sequence: blocks, DeltaNet state and cached hidden."""
+        self.blocks.release(lane)
+        for ty, p in zip(self.cfg.layer_types, self.pool):
+            if ty != ATTN:
+                p["conv"][lane].zero_()
+                p["rec"][lane].zero_()
+        self.hidden_cache[lane].zero_()
+
+    # ------------------------------------------------------------ sublayers
+
+    def moe(self, w: dict, h: torch.Tensor) -> torch.Tensor:
+        """Routed MXFP4 experts + gated shared expert over rows `h` `[N, hidden]`
+        (`model.py:2811-2873`)."""
+        c = self.cfg
+        routing = F.linear(h, w["router_gate"])
+        if h.device.type == "cuda":
+            top_w, top_i = router_fused.route(routing, c.experts, c.top_k, index_dtype=torch.int32)
+        else:
+            probs = routing[:, : c.experts].float().softmax(-1)
+            top_w, top_i = probs.topk(c.top_k, dim=-1)
+            top_w = top_w / top_w.sum(-1, keepdim=True)
+        assign = (top_i.reshape(-1), top_w.reshape(-1))
+        if mxfp4_gemv.available(h.device):
+            routed = mxfp4_gemv.fused_moe(h.contiguous(), w["experts"], assign, c.top_k, (0, c.experts),
+                                          inter=self.moe_ws)
+        elif h.device.type == "cuda":
+            raise RuntimeError("SEED_FUSED_MOE=0 has no device path in this build")
+        else:
+            routed = mxfp4_gemv.reference_moe(h, w["experts"], assign, c.top_k, (0, c.experts),
+                                              mxfp4.dequant_mxfp4)
+        gate, up = F.linear(h, w["shared_gate_up"]).chunk(2, dim=-1)
+        shared = F.linear(F.silu(gate) * up, w["shared_down"])
+        return routed + torch.sigmoid(routing[:, c.experts :]) * shared
+
+    def attention_rows(self, w: dict, pool: dict, h: torch.Tensor, lanes: torch.Tensor,
+                       base_pos: torch.Tensor, ctx_len: int) -> torch.Tensor:
+        """Gated GQA attention for `t` rows per lane at positions `base_pos + s` over the
+        lanes' own block tables (`attn_verify`, `model.py:3519-3577`). `ctx_len` is a host
+        bound on `base_pos + t`."""
+        c = self.cfg
+        t = h.shape[1]
+        pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
+        rows = self.blocks.physical_rows(lanes, pos)
+        ctx_blocks = (ctx_len + c.block_size - 1) // c.block_size
+        return gated_attention(self, w, pool, h, base_pos, rows, self.blocks.table[lanes], ctx_blocks)
+
+    def deltanet_verify(self, w: dict, pool: dict, h: torch.Tensor,
+                        lanes: torch.Tensor) -> tuple[torch.Tensor, DeltaNetRows]:
+        """Gated DeltaNet over `t` rows per lane from the committed state, which is read and
+        not written (`deltanet_verify`, `model.py:3738-3905`)."""
+        c = self.cfg
+        b, t, _ = h.shape
+        proj = F.linear(h, w["in_proj_all"])
+        qkv, z, b_raw, a_raw = proj.split(c.in_proj_sizes, dim=-1)
+        raw = qkv.transpose(1, 2)  # [B, C, t]
+        window = torch.cat([pool["conv"][lanes], raw], dim=-1)
+        mixed = causal_conv_rows(window, w["conv"], t).to(h.dtype).transpose(1, 2)  # [B, t, C]
+        kd = c.k_heads * c.k_dim
+        q = mixed[..., :kd].reshape(b, t, c.k_heads, c.k_dim).float()
+        k = mixed[..., kd : 2 * kd].reshape(b, t, c.k_heads, c.k_dim).float()
+        v = mixed[..., 2 * kd :].reshape(b, t, c.v_heads, c.v_dim).float()
+        rep = c.v_heads // c.k_heads
+        q = (l2norm(q) * c.k_dim ** -0.5).repeat_interleave(rep, dim=2)
+        k = l2norm(k).repeat_interleave(rep, dim=2)
+        beta = torch.sigmoid(b_raw.float())
+        g = -w["A_log"].float().exp() * F.softplus(a_raw.float() + w["dt_bias"].float())
+        state = pool["rec"][lanes]
+        outs = []
+        for s in range(t):
+            state, o = delta_rule_step(state, q[:, s], k[:, s], v[:, s], g[:, s], beta[:, s])
+            outs.append(o)
+        out = torch.stack(outs, dim=1)  # [B, t, vh, vd] fp32
+        normed = gated_rmsnorm(out, z.reshape(b, t, c.v_heads, c.v_dim), w["dn_norm"], c.eps, h.dtype)
+        mixer = F.linear(normed.reshape(b, t, -1), w["out_proj"])
+        return mixer, DeltaNetRows(raw.contiguous(), q, k, v, g, beta)
+
+    def deltanet_commit(self, pool: dict, rows: DeltaNetRows, lanes: torch.Tensor,
+                        lengths: torch.Tensor, conv_idx: torch.Tensor | None = None) -> None:
+        """Advance slot `lanes[j]`'s conv window and recurrent state by `lengths[j]` of the
+        verified rows (1..t) (`deltanet_verify_rollback`, `model.py:3907-3972`). `conv_idx`
+        `[B, conv_k - 1]`, when given, is the acceptance kernel's window index
+        `min(lengths + w, conv_k - 2 + t)`; it is computed here otherwise."""
+        c = self.cfg
+        k1 = c.conv_k - 1
+        t = rows.q.shape[1]
+        n = lengths.to(self.device, torch.long)
+        window = torch.cat([pool["conv"][lanes], rows.raw_qkv], dim=-1)  # [B, C, k1 + t]
+        if conv_idx is not None:
+            idx = conv_idx.long()
+        else:
+            idx = (n[:, None] + torch.arange(k1, device=self.device)[None, :]).clamp(max=k1 + t - 1)
+        pool["conv"][lanes] = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
+        state = pool["rec"][lanes]
+        for s in range(t):
+            nxt, _ = delta_rule_step(state, rows.q[:, s], rows.k[:, s], rows.v[:, s], rows.g[:, s], rows.beta[:, s])
+            state = torch.where((s < n)[:, None, None, None], nxt, state)
+        pool["rec"][lanes] = state
+
+    # ------------------------------------------------------------ forward
+
+    def forward_rows(self, ids: torch.Tensor, lanes, base_pos: torch.Tensor, ctx_len: int) -> VerifyOut:
+        """The wide forward over fed tokens `ids` `[B, t]` at positions `base_pos[b] + s`
+        (`verify_and_commit`'s layer loop, `mtp.py:767-772`). Writes the rows' K/V; DeltaNet
+        state is left for `commit`. `ctx_len` is a host bound on `max(base_pos) + t`."""
+        c = self.cfg
+        lanes = self.lane_index(lanes)
+        base_pos = base_pos.to(self.device, torch.long)
+        x = self.embed[ids.to(self.device)]
+        res = VerifyOut(x)
+        for i, ty in enumerate(c.layer_types):
+            w, pool = self.layers[i], self.pool[i]
+            h = rmsnorm(x, w["in_norm"], c.eps)
+            if ty == ATTN:
+                mixer = self.attention_rows(w, pool, h, lanes, base_pos, ctx_len)
+            else:
+                mixer, rows = self.deltanet_verify(w, pool, h, lanes)
+                res.dn_rows[i] = rows
+            x = x + mixer
+            hm = rmsnorm(x, w["post_norm"], c.eps)
+            b, t, _ = hm.shape
+            x = x + self.moe(w, hm.reshape(b * t, -1)).view(b, t, -1)
+        res.hidden = x
+        return res
+
+    def commit(self, res: VerifyOut, lanes, lengths: torch.Tensor,
+               conv_idx: torch.Tensor | None = None) -> None:
+        """Advance every DeltaNet layer's state of `lanes` by `lengths` verified rows."""
+        lanes = self.lane_index(lanes)
+        for i, rows in res.dn_rows.items():
+            self.deltanet_commit(self.pool[i], rows, lanes, lengths, conv_idx)
+
+    def unembed(self, normed: torch.Tensor) -> torch.Tensor:
+        return F.linear(normed, self.lm_head)
+
+    def logits(self, hidden: torch.Tensor) -> torch.Tensor:
+        return self.unembed(rmsnorm(hidden, self.final_norm, self.cfg.eps))
+
+    def argmax(self, logits: torch.Tensor) -> torch.Tensor:
+        """First-occurrence argmax over the vocab (the HIP kernel on a device)."""
+        if logits.device.type == "cuda":
+            import mtp as mtp_mod
+
+            return mtp_mod.argmax_rows(logits)
+        return logits.float().argmax(-1)
+
+    def cached_hidden(self, lane: int) -> torch.Tensor:
+        return self.hidden_cache[lane : lane + 1]
+
+    def cache_hidden(self, lane: int, h: torch.Tensor) -> None:
+        self.hidden_cache[lane].copy_(h.reshape(-1))
+
+    # ------------------------------------------------------------ sequence entry points
+
+    def prefill(self, lane: int, tokens: list[int]) -> torch.Tensor:
+        """Run a prompt into slot `lane` from position 0; returns the last row's logits
+        `[vocab]` and leaves the slot's state, the MTP cache and the cached hidden after the
+        whole prompt."""
+        t = len(tokens)
+        self.reset(lane)
+        self.blocks.grow(lane, t)
+        ids = torch.tensor([tokens], dtype=torch.long, device=self.device)
+        base = torch.zeros(1, dtype=torch.long, device=self.device)
+        res = self.forward_rows(ids, [lane], base, t)
+        self.commit(res, [lane], torch.tensor([t], device=self.device))
+        if self.mtp is not None:
+            import mtp as mtp_mod
+
+            previous = torch.cat([torch.zeros_like(res.hidden[:, :1]), res.hidden[:, :-1]], dim=1)
+            pos = torch.arange(t, device=self.device)[None, :]
+            rows = self.blocks.physical_rows(self.lane_index([lane]), pos)
+            mtp_mod.cache_target_rows(self, self.mtp, ids, previous, pos, rows)
+        self.cache_hidden(lane, res.hidden[0, -1])
+        return self.logits(res.hidden[0, -1:])[0]
+
+    def decode(self, lanes: list[int], tokens: list[int], positions: list[int]) -> torch.Tensor:
+        """One ordinary decode step: token `tokens[j]` at `positions[j]` of slot `lanes[j]`.
+        Returns logits `[B, vocab]`; commits the state and extends the MTP cache."""
+        for lane, p in zip(lanes, positions, strict=True):
+            self.blocks.grow(lane, p + 1)
+        ids = torch.tensor([[tk] for tk in tokens], dtype=torch.long, device=self.device)
+        base = torch.tensor(positions, dtype=torch.long, device=self.device)
+        res = self.forward_rows(ids, lanes, base, max(positions) + 1)
+        lane_t = self.lane_index(lanes)
+        self.commit(res, lane_t, torch.ones(len(lanes), dtype=torch.long, device=self.device))
+        if self.mtp is not None:
+            import mtp as mtp_mod
+
+            previous = self.hidden_cache[lane_t][:, None]
+            pos = base[:, None]
+            mtp_mod.cache_target_rows(self, self.mtp, ids, previous, pos,
+                                      self.blocks.physical_rows(lane_t, pos))
+        self.hidden_cache[lane_t] = res.hidden[:, 0]
+        return self.logits(res.hidden[:, 0])
+
+
+def greedy_reference(model: Model, lane: int, token: int, pos: int, n: int) -> list[int]:
+    """`n` tokens of plain greedy decode from `token` at `pos` in slot `lane` (the sequential
+    baseline a speculative round must reproduce, `test_mtp.py:488-513`)."""
+    out = []
+    for _ in range(n):
+        logits = model.decode([lane], [token], [pos])
+        token = int(model.argmax(logits)[0])
+        out.append(token)
+        pos += 1
+    return out
+

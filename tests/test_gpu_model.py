@@ -1,0 +1,123 @@
+"""The MTP step on the GPU: draft head, verify forward and acceptance on the HIP kernels.
+
+Config 1's model runs on the device in fp32 with the same weights as the CPU model; its
+speculative rounds (`graph_mtp.MTPVerifyRunner`: MTP draft steps, wide verify, the acceptance
+kernel and the commit) must reproduce plain greedy decode, and its logits must agree with the
+CPU path. Config 5's layer dimensions are exercised at a few lanes and a short context.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import graph_mtp
+import mtp
+import verify_model as vm
+from tests import model_helpers as mh
+
+pytestmark = pytest.mark.gpu
+
+
+def test_config1_prefill_logits_match_cpu(dev) -> None:
+    ids = mh.prompts(2)
+    cpu, gpu = mh.build("cpu"), mh.build(dev)
+    for lane, p in enumerate(ids):
+        want = cpu.prefill(lane, p)
+        got = gpu.prefill(lane, p).cpu()
+        torch.testing.assert_close(got, want, rtol=1e-4, atol=2e-5)
+        assert int(got.argmax()) == int(want.argmax())
+
+
+@pytest.mark.parametrize("k", [1, 3])
+def test_config1_speculative_rounds_match_greedy(dev, k: int) -> None:
+    """2 prompts of 16 ids, 32 tokens: the device rounds commit the CPU greedy sequence."""
+    ids = mh.prompts()
+    truth = mh.greedy_truth(mh.build("cpu", k=k), ids, mh.GEN_TOKENS)
+    model = mh.build(dev, k=k)
+    runner = graph_mtp.MTPVerifyRunner(model, capacity=2)
+    got, toks, pos = [], [], []
+    for lane, p in enumerate(ids):
+        base = int(model.argmax(model.prefill(lane, p)[None])[0])
+        got.append([base])
+        toks.append(base)
+        pos.append(len(p))
+    while min(len(g) for g in got) < mh.GEN_TOKENS + 1:
+        committed = runner.speculative_decode([0, 1], toks, pos)
+        for j, c in enumerate(committed):
+            assert 1 <= len(c) <= k + 1
+            got[j].extend(c)
+            pos[j] += len(c)
+            toks[j] = c[-1]
+    for g, t in zip(got, truth, strict=True):
+        assert g[: mh.GEN_TOKENS + 1] == t
+
+
+@pytest.mark.parametrize("accept", [1, 2, 3])
+def test_config1_forced_round_matches_sequential(dev, accept: int) -> None:
+    """Forced drafts (the greedy continuation) accepted unconditionally: committed ids and all
+    slot state equal `accept + 1` plain decode steps on the device."""
+    k, lane = 3, 0
+    ids = mh.prompts(1)
+    truth = mh.greedy_truth(mh.build(dev, k=k, lanes=1), ids, k + 1)[0]
+    seq = mh.build(dev, k=k, lanes=1)
+    seq.prefill(lane, ids[0])
+    vm.greedy_reference(seq, lane, truth[0], len(ids[0]), accept + 1)
+    spec = mh.build(dev, k=k, lanes=1)
+    spec.prefill(lane, ids[0])
+    runner = graph_mtp.MTPVerifyRunner(spec, capacity=1)
+    committed = runner.speculative_decode([lane], [truth[0]], [len(ids[0])], forced=[truth[1 : accept + 1]])
+    assert committed == [truth[1 : accept + 2]]
+    mh.assert_slot_state_close(spec, seq, lane, len(ids[0]) + accept + 1, rtol=1e-4, atol=1e-5)
+
+
+def test_config1_runner_matches_eager_verify(dev) -> None:
+    """The device round (acceptance kernel, device commit) and the eager host-accept round
+    commit the same ids and leave the same state, with budgets and stop ids in play."""
+    k = 3
+    ids = mh.prompts(2)
+    a, b = mh.build(dev, k=k), mh.build(dev, k=k)
+    toks, pos = [], []
+    for lane, p in enumerate(ids):
+        toks.append(int(a.argmax(a.prefill(lane, p)[None])[0]))
+        b.prefill(lane, p)
+        pos.append(len(p))
+    runner = graph_mtp.MTPVerifyRunner(a, capacity=4)
+    budgets, stops = [2, 50], [[3], [7, 9]]
+    for _ in range(3):
+        got = runner.speculative_decode([0, 1], toks, pos, budgets, stops)
+        drafts = runner.buf.token_matrix[:2, 1:].tolist()
+        want = mtp.verify_and_commit(b, b.mtp, [0, 1], toks, drafts, pos, budgets, stops)
+        assert got == want
+        for j, c in enumerate(got):
+            pos[j] += len(c)
+            toks[j] = c[-1]
+    for lane in range(2):
+        mh.assert_slot_state_close(a, b, lane, pos[lane], rtol=1e-5, atol=1e-6)
+
+
+def test_config5_dims_round(dev) -> None:
+    """Real layer dimensions (3 DeltaNet + 1 gated GQA, 512 experts top-10, vocab 248320) at 4
+    lanes: rounds commit 1..k+1 valid ids and keep every state finite."""
+    k = 3
+    model = vm.Model(vm.verify_cfg(), dev, torch.bfloat16, lanes=4, max_seq=96, seed=0,
+                     expert_mode="bytes", moe_rows=16)
+    mtp.attach(model, k=k, seed=1, expert_mode="bytes")
+    gen = torch.Generator().manual_seed(9)
+    toks, pos = [], []
+    for lane in range(4):
+        p = torch.randint(0, model.cfg.vocab, (5 + 3 * lane,), generator=gen).tolist()
+        toks.append(int(model.argmax(model.prefill(lane, p)[None])[0]))
+        pos.append(len(p))
+    runner = graph_mtp.MTPVerifyRunner(model, capacity=4)
+    for _ in range(3):
+        got = runner.speculative_decode([0, 1, 2, 3], toks, pos)
+        for j, c in enumerate(got):
+            assert 1 <= len(c) <= k + 1
+            assert all(0 <= x < model.cfg.vocab for x in c)
+            pos[j] += len(c)
+            toks[j] = c[-1]
+    assert torch.isfinite(model.hidden_cache.float()).all()
+    for ty, p in zip(model.cfg.layer_types, model.pool, strict=True):
+        if ty != vm.ATTN:
+            assert torch.isfinite(p["rec"]).all() and torch.isfinite(p["conv"].float()).all()
