@@ -185,6 +185,36 @@ int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int6
                        int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                        int64_t* hidden_src, void* stream);
 
+/* ---------------------------------------------------------------- rejection sampling
+ * Sampling-mode acceptance for an MTP round at temperature T > 0. The reference engine has no
+ * counterpart: it runs MTP rounds only for all-greedy batches (scheduler.py:1775-1793,
+ * model.py:4197-4201); this follows Leviathan et al. 2023, Alg. 1. With p_i = softmax(target_i
+ * / T) and q_i = softmax(draft_i / T): draft x_i is accepted iff u_accept[b,i] * q_i(x_i) <=
+ * p_i(x_i); at the first rejection a token is drawn from norm(max(0, p_i - q_i)) (from p_i if
+ * that is all zero), else the bonus is drawn from p_k. A draw from weights w with uniform r is
+ * the smallest v with cumsum(w)[v] > r * sum(w) (the last positive index if rounding leaves
+ * none). Inputs: target f32|bf16 [B, k+1, vocab] and draft [B, k, vocab], contiguous;
+ * draft_tokens i64 [B, k]; u_accept f32 [B, k]; u_sample f32 [B].
+ * Outputs: accept_len i64 [B]; token i64 [B] (the resampled or bonus token); emitted i64
+ * [B, k+1] (may be NULL) = accepted drafts, then `token` repeated, which is a step_argmax for
+ * mtpk_greedy_accept that yields the same accept length and every rollback index; margin f32
+ * [B, k] (may be NULL) = p_i(x_i) - u_i q_i(x_i), >= 0 accepts. fp32 arithmetic, fixed
+ * reduction order. `workspace` (16-byte aligned) of mtpk_rejection_workspace_bytes bytes. */
+int64_t mtpk_rejection_workspace_bytes(int64_t batch, int k, int64_t vocab);
+int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int64_t batch, int k,
+                          int64_t vocab, const int64_t* draft_tokens, const float* u_accept,
+                          const float* u_sample, float temperature, void* workspace,
+                          int64_t workspace_bytes, int64_t* accept_len, int64_t* token,
+                          int64_t* emitted, float* margin, void* stream);
+
+/* Temperature sampling of one token per row, the draft step's sampler in sampling mode (the
+ * reference's draft step is greedy only: mtp.py:640-658). logits f32|bf16 [rows, vocab]
+ * contiguous, u f32 [rows]; token i64 [rows] = inverse-CDF draw from softmax(logits / T). */
+int64_t mtpk_sample_workspace_bytes(int64_t rows, int64_t vocab);
+int mtpk_sample_rows(const void* logits, int dtype, int64_t rows, int64_t vocab, float temperature,
+                     const float* u, void* workspace, int64_t workspace_bytes, int64_t* token,
+                     void* stream);
+
 /* ---------------------------------------------------------------- test probes
  * In-bounds probe of the compiler builtin this library's MoE relies on: one wave computes
  * d = A(16x32) * B(32x16) with v_mfma_f32_16x16x32_bf16 from per-lane operand registers

@@ -83,6 +83,18 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
+    "mtpk_rejection_workspace_bytes": (c_int64, [c_int64, c_int, c_int64]),
+    "mtpk_rejection_sample": (
+        c_int,
+        [c_void_p, c_void_p, c_int, c_int64, c_int, c_int64, c_void_p, c_void_p, c_void_p,
+         ctypes.c_float, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "mtpk_sample_workspace_bytes": (c_int64, [c_int64, c_int64]),
+    "mtpk_sample_rows": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, ctypes.c_float, c_void_p, c_void_p, c_int64, c_void_p,
+         c_void_p],
+    ),
     "mtpk_probe_mfma_16x16x32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
 }
 

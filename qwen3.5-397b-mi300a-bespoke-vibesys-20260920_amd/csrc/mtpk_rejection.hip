@@ -1,0 +1,435 @@
+// Speculative rejection sampling and temperature sampling over the vocabulary, for gfx950.
+//
+// Method (Leviathan, Kalman & Matias 2023, Alg. 1; Chen et al. 2023): with p_i =
+// softmax(target_i / T) and q_i = softmax(draft_i / T), draft token x_i is accepted iff
+// u_i * q_i(x_i) <= p_i(x_i); at the first rejection i a token is drawn from
+// norm(max(0, p_i - q_i)) (from p_i if that residual is all zero), and if all k drafts are
+// accepted the bonus token is drawn from p_k. A draw from weights w with uniform r is the
+// smallest index v with cumsum(w)[v] > r * sum(w), or the last positive index if rounding
+// leaves none.
+//
+// Four launches, all streaming the logits at HBM rate with 16-byte loads:
+//   stats : (chunk, row) workgroups -> per-chunk (max, sum exp(z - max)) of z = logit / T
+//   decide: one wave per item -> row softmax constants; for rejection, the accept length
+//   mass  : (chunk, item) workgroups -> per-chunk sums of the item's draw weights
+//   pick  : one workgroup per item -> the chunk where the cumulative mass crosses r * total,
+//           then a block scan inside it; writes the token (and the emitted row)
+// Every sum runs in a fixed order, so results are deterministic for fixed shapes.
+
+#include "mtpk_device.h"
+#include "mtpk_host.h"
+
+namespace mtpk {
+
+constexpr int kRsThreads = 256;
+constexpr int kRsPerThread = 16;
+constexpr int kRsChunk = kRsThreads * kRsPerThread;  // 4096 logits per workgroup
+
+// One draw: weights from target row `trow` (and draft row `drow` for a residual, else -1).
+struct RsItem {
+  int trow, drow, a, pad;
+  float mt, st, mq, sq;
+};
+
+struct RsRows {
+  const void* target;
+  const void* draft;
+  int dt;
+  int64_t vocab;
+  int vec;  // 16-byte vector loads allowed
+};
+
+// The 16 logits of thread `tid` in chunk `c` of a row, scaled by 1/T; invalid slots -> -inf.
+__device__ inline void rs_load(const void* base, int dt, int vec, int64_t row, int64_t vocab, int c,
+                               int tid, float inv_t, float (&z)[kRsPerThread]) {
+  const int64_t i0 = (int64_t)c * kRsChunk + (int64_t)tid * kRsPerThread;
+  if (vec && i0 + kRsPerThread <= vocab) {
+    if (dt == MTPK_BF16) {
+      const uint16_t* p = reinterpret_cast<const uint16_t*>(base) + row * vocab + i0;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const u32x4_t v = ld16(p + 8 * h);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          z[8 * h + 2 * q] = bf16_to_f32((uint16_t)(v[q] & 0xffffu)) * inv_t;
+          z[8 * h + 2 * q + 1] = bf16_to_f32((uint16_t)(v[q] >> 16)) * inv_t;
+        }
+      }
+    } else {
+      const float* p = reinterpret_cast<const float*>(base) + row * vocab + i0;
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const u32x4_t v = ld16(p + 4 * h);
+#pragma unroll
+        for (int q = 0; q < 4; ++q) z[4 * h + q] = bits_f32(v[q]) * inv_t;
+      }
+    }
+    return;
+  }
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) {
+    const int64_t i = i0 + e;
+    z[e] = i < vocab ? load_float(base, dt, row * vocab + i) * inv_t : -INFINITY;
+  }
+}
+
+// Block-wide reductions over 256 threads (4 waves), result broadcast to every thread.
+__device__ inline float block_max(float v, float* red) {
+  v = wave_max(v);
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = v;
+  __syncthreads();
+  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+__device__ inline float block_sum(float v, float* red) {
+  v = wave_sum(v);
+  const int tid = threadIdx.x;
+  __syncthreads();
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = v;
+  __syncthreads();
+  return (red[0] + red[1]) + (red[2] + red[3]);
+}
+
+// rows [0, n_target) are target rows, [n_target, n_target + n_draft) draft rows.
+__global__ __launch_bounds__(kRsThreads) void k_rs_stats(RsRows rr, int64_t n_target, float inv_t,
+                                                        float2* __restrict__ part) {
+  __shared__ float red[kRsThreads / kWave];
+  const int c = blockIdx.x, nchunk = gridDim.x;
+  const int64_t r = blockIdx.y;
+  const bool is_t = r < n_target;
+  const void* base = is_t ? rr.target : rr.draft;
+  const int64_t row = is_t ? r : r - n_target;
+  float z[kRsPerThread];
+  rs_load(base, rr.dt, rr.vec, row, rr.vocab, c, threadIdx.x, inv_t, z);
+  float m = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) m = fmaxf(m, z[e]);
+  m = block_max(m, red);
+  float s = 0.f;
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) s += __expf(z[e] - m);
+  s = block_sum(s, red);
+  if (threadIdx.x == 0) part[r * nchunk + c] = make_float2(m, s);
+}
+
+// Combine a row's chunk partials (one wave): max M and sum S of exp(z - M).
+__device__ inline float2 rs_row_stats(const float2* part, int64_t r, int nchunk) {
+  const int lane = threadIdx.x & (kWave - 1);
+  float m = -INFINITY;
+  for (int c = lane; c < nchunk; c += kWave) m = fmaxf(m, part[r * nchunk + c].x);
+  m = wave_max(m);
+  float s = 0.f;
+  for (int c = lane; c < nchunk; c += kWave) {
+    const float2 v = part[r * nchunk + c];
+    s += v.y * __expf(v.x - m);
+  }
+  return make_float2(m, wave_sum(s));
+}
+
+// Rejection decision, one wave per lane b: accept length, margins, and the item to draw.
+__global__ __launch_bounds__(kWave) void k_rs_decide(RsRows rr, const float2* __restrict__ part,
+                                                    int nchunk, int B, int k, float inv_t,
+                                                    const int64_t* __restrict__ draft_tokens,
+                                                    const float* __restrict__ u_accept,
+                                                    RsItem* __restrict__ items,
+                                                    int64_t* __restrict__ accept_len,
+                                                    float* __restrict__ margin) {
+  const int b = blockIdx.x;
+  const int t = k + 1;
+  const int64_t n_target = (int64_t)B * t;
+  int a = k;
+  float2 sa_t = make_float2(0.f, 1.f), sa_q = make_float2(0.f, 1.f);
+  for (int i = 0; i < t; ++i) {
+    const float2 st = rs_row_stats(part, (int64_t)b * t + i, nchunk);
+    float2 sq = make_float2(0.f, 1.f);
+    float mg = 0.f;
+    if (i < k) {
+      sq = rs_row_stats(part, n_target + (int64_t)b * k + i, nchunk);
+      const int64_t x = draft_tokens[(int64_t)b * k + i];
+      if (x >= 0 && x < rr.vocab) {
+        const float lt = load_float(rr.target, rr.dt, ((int64_t)b * t + i) * rr.vocab + x) * inv_t;
+        const float lq = load_float(rr.draft, rr.dt, ((int64_t)b * k + i) * rr.vocab + x) * inv_t;
+        const float p = __expf(lt - st.x) / st.y, q = __expf(lq - sq.x) / sq.y;
+        mg = p - u_accept[(int64_t)b * k + i] * q;
+      } else {
+        mg = -1.f;  // a token outside the vocabulary is never accepted
+      }
+      if (margin && threadIdx.x == 0) margin[(int64_t)b * k + i] = mg;
+    }
+    if (i == a) {
+      sa_t = st;
+      sa_q = sq;
+    }
+    if (i < k && a == k && mg < 0.f) {
+      a = i;
+      sa_t = st;
+      sa_q = sq;
+    }
+  }
+  if (threadIdx.x == 0) {
+    RsItem it;
+    it.trow = b * t + a;
+    it.drow = a < k ? b * k + a : -1;
+    it.a = a;
+    it.pad = 0;
+    it.mt = sa_t.x;
+    it.st = sa_t.y;
+    it.mq = sa_q.x;
+    it.sq = sa_q.y;
+    items[b] = it;
+    accept_len[b] = a;
+  }
+}
+
+// Plain sampling: item r draws from target row r.
+__global__ __launch_bounds__(kWave) void k_rs_rows(const float2* __restrict__ part, int nchunk,
+                                                  RsItem* __restrict__ items) {
+  const int r = blockIdx.x;
+  const float2 st = rs_row_stats(part, r, nchunk);
+  if (threadIdx.x == 0) {
+    RsItem it;
+    it.trow = r;
+    it.drow = -1;
+    it.a = 0;
+    it.pad = 0;
+    it.mt = st.x;
+    it.st = st.y;
+    it.mq = 0.f;
+    it.sq = 1.f;
+    items[r] = it;
+  }
+}
+
+// Draw weights of this thread's 16 slots: residual max(0, p - q) and target p.
+__device__ inline void rs_weights(const RsRows& rr, const RsItem& it, int c, float inv_t,
+                                  float (&wr)[kRsPerThread], float (&wp)[kRsPerThread]) {
+  float z[kRsPerThread];
+  rs_load(rr.target, rr.dt, rr.vec, it.trow, rr.vocab, c, threadIdx.x, inv_t, z);
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) wp[e] = __expf(z[e] - it.mt) / it.st;
+  if (it.drow >= 0) {
+    rs_load(rr.draft, rr.dt, rr.vec, it.drow, rr.vocab, c, threadIdx.x, inv_t, z);
+#pragma unroll
+    for (int e = 0; e < kRsPerThread; ++e) wr[e] = fmaxf(wp[e] - __expf(z[e] - it.mq) / it.sq, 0.f);
+  } else {
+#pragma unroll
+    for (int e = 0; e < kRsPerThread; ++e) wr[e] = 0.f;
+  }
+}
+
+__global__ __launch_bounds__(kRsThreads) void k_rs_mass(RsRows rr, const RsItem* __restrict__ items,
+                                                       float inv_t, float2* __restrict__ mass) {
+  __shared__ float red[kRsThreads / kWave];
+  const int c = blockIdx.x, nchunk = gridDim.x;
+  const int item = blockIdx.y;
+  const RsItem it = items[item];
+  float wr[kRsPerThread], wp[kRsPerThread];
+  rs_weights(rr, it, c, inv_t, wr, wp);
+  float sr = 0.f, sp = 0.f;
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) {
+    sr += wr[e];
+    sp += wp[e];
+  }
+  sr = block_sum(sr, red);
+  sp = block_sum(sp, red);
+  if (threadIdx.x == 0) mass[(int64_t)item * nchunk + c] = make_float2(sr, sp);
+}
+
+__device__ inline float wave_incl_scan_f(float v, int lane) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const float u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+__global__ __launch_bounds__(kRsThreads) void k_rs_pick(
+    RsRows rr, const RsItem* __restrict__ items, const float2* __restrict__ mass, int nchunk,
+    float inv_t, const float* __restrict__ u_sample, int64_t* __restrict__ token,
+    const int64_t* __restrict__ draft_tokens, int k, int64_t* __restrict__ emitted) {
+  __shared__ float wtot[kRsThreads / kWave];
+  __shared__ int s_chunk, s_use_r, s_fallback, s_best;
+  __shared__ float s_before, s_target;
+  const int item = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  const RsItem it = items[item];
+  if (tid == 0) {
+    float tr = 0.f, tp = 0.f;
+    for (int c = 0; c < nchunk; ++c) {
+      const float2 m = mass[(int64_t)item * nchunk + c];
+      tr += m.x;
+      tp += m.y;
+    }
+    const int use_r = it.drow >= 0 && tr > 0.f;
+    const float total = use_r ? tr : tp;
+    const float target = u_sample[item] * total;
+    float cum = 0.f;
+    int chunk = -1, last_pos = 0;
+    for (int c = 0; c < nchunk; ++c) {
+      const float2 m = mass[(int64_t)item * nchunk + c];
+      const float w = use_r ? m.x : m.y;
+      if (w > 0.f) last_pos = c;
+      if (cum + w > target) {
+        chunk = c;
+        break;
+      }
+      cum += w;
+    }
+    s_fallback = chunk < 0;
+    s_chunk = chunk < 0 ? last_pos : chunk;
+    s_use_r = use_r;
+    s_before = cum;
+    s_target = target;
+    s_best = INT32_MAX;
+  }
+  __syncthreads();
+  const int c = s_chunk;
+  float wr[kRsPerThread], wp[kRsPerThread];
+  rs_weights(rr, it, c, inv_t, wr, wp);
+  float w[kRsPerThread];
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) w[e] = s_use_r ? wr[e] : wp[e];
+  float mine = 0.f;
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) mine += w[e];
+  const float inc = wave_incl_scan_f(mine, lane);
+  if (lane == kWave - 1) wtot[wv] = inc;
+  __syncthreads();
+  float off = s_before;
+  for (int q = 0; q < wv; ++q) off += wtot[q];
+  float run = off + inc - mine;
+  const int64_t i0 = (int64_t)c * kRsChunk + (int64_t)tid * kRsPerThread;
+  int hit = INT32_MAX, lastp = -1;
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) {
+    run += w[e];
+    if (w[e] > 0.f) lastp = (int)(i0 + e);
+    if (hit == INT32_MAX && !s_fallback && run > s_target && w[e] > 0.f) hit = (int)(i0 + e);
+  }
+  atomicMin(&s_best, hit);
+  __syncthreads();
+  // Rounding can leave no crossing inside the chunk: take the chunk's last positive slot.
+  const int need_last = s_best == INT32_MAX;
+  __syncthreads();
+  if (need_last) {
+    if (tid == 0) s_best = -1;
+    __syncthreads();
+    atomicMax(&s_best, lastp);
+    __syncthreads();
+  }
+  if (tid == 0) {
+    const int64_t v = s_best < 0 ? 0 : s_best;
+    token[item] = v;
+    if (emitted) {
+      const int t = k + 1;
+      for (int i = 0; i < t; ++i)
+        emitted[(int64_t)item * t + i] = i < it.a ? draft_tokens[(int64_t)item * k + i] : v;
+    }
+  }
+}
+
+int64_t rs_chunks(int64_t vocab) { return (vocab + kRsChunk - 1) / kRsChunk; }
+
+}  // namespace mtpk
+
+using namespace mtpk;
+
+extern "C" {
+
+int64_t mtpk_rejection_workspace_bytes(int64_t batch, int k, int64_t vocab) {
+  if (batch <= 0 || k < 0 || vocab <= 0) return 0;
+  const int64_t nchunk = rs_chunks(vocab);
+  const int64_t rows = batch * (2 * (int64_t)k + 1);
+  return align256(rows * nchunk * (int64_t)sizeof(float2)) +
+         align256(batch * (int64_t)sizeof(RsItem)) +
+         align256(batch * nchunk * (int64_t)sizeof(float2));
+}
+
+int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int64_t batch, int k,
+                          int64_t vocab, const int64_t* draft_tokens, const float* u_accept,
+                          const float* u_sample, float temperature, void* workspace,
+                          int64_t workspace_bytes, int64_t* accept_len, int64_t* token,
+                          int64_t* emitted, float* margin, void* stream) {
+  if (!target || !u_sample || !workspace || !accept_len || !token) return MTPK_EINVAL;
+  if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (batch <= 0 || batch > 65535 || k < 0 || k > 63 || vocab <= 0 || vocab > INT32_MAX / 2)
+    return MTPK_EINVAL;
+  if (k > 0 && (!draft || !draft_tokens || !u_accept)) return MTPK_EINVAL;
+  if (!(temperature > 0.f) || !(temperature < INFINITY)) return MTPK_EINVAL;
+  if (workspace_bytes < mtpk_rejection_workspace_bytes(batch, k, vocab)) return MTPK_EINVAL;
+  if (!aligned16(workspace)) return MTPK_EINVAL;
+  const int64_t nchunk = rs_chunks(vocab);
+  if (nchunk > 65535) return MTPK_EINVAL;
+  const int t = k + 1;
+  const int64_t rows = batch * (t + (int64_t)k);
+  if (rows > 65535) return MTPK_EINVAL;
+  const int per_vec = dtype == MTPK_BF16 ? 8 : 4;
+  RsRows rr{target, draft, dtype, vocab,
+            (int)(aligned16(target) && (k == 0 || aligned16(draft)) && vocab % per_vec == 0)};
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  float2* part = reinterpret_cast<float2*>(ws);
+  ws += align256(batch * (2 * (int64_t)k + 1) * nchunk * (int64_t)sizeof(float2));
+  RsItem* items = reinterpret_cast<RsItem*>(ws);
+  ws += align256(batch * (int64_t)sizeof(RsItem));
+  float2* mass = reinterpret_cast<float2*>(ws);
+  const float inv_t = 1.f / temperature;
+  const hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_rs_stats, dim3((unsigned)nchunk, (unsigned)rows), dim3(kRsThreads), 0, st,
+                     rr, batch * t, inv_t, part);
+  int rc = status_of(hipGetLastError());
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_rs_decide, dim3((unsigned)batch), dim3(kWave), 0, st, rr, part, (int)nchunk,
+                     (int)batch, k, inv_t, draft_tokens, u_accept, items, accept_len, margin);
+  if ((rc = status_of(hipGetLastError()))) return rc;
+  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)batch), dim3(kRsThreads), 0, st,
+                     rr, items, inv_t, mass);
+  if ((rc = status_of(hipGetLastError()))) return rc;
+  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, items, mass,
+                     (int)nchunk, inv_t, u_sample, token, draft_tokens, k, emitted);
+  return status_of(hipGetLastError());
+}
+
+int64_t mtpk_sample_workspace_bytes(int64_t rows, int64_t vocab) {
+  return mtpk_rejection_workspace_bytes(rows, 0, vocab);
+}
+
+int mtpk_sample_rows(const void* logits, int dtype, int64_t rows, int64_t vocab, float temperature,
+                     const float* u, void* workspace, int64_t workspace_bytes, int64_t* token,
+                     void* stream) {
+  if (!logits || !u || !workspace || !token) return MTPK_EINVAL;
+  if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (rows <= 0 || rows > 65535 || vocab <= 0 || vocab > INT32_MAX / 2) return MTPK_EINVAL;
+  if (!(temperature > 0.f) || !(temperature < INFINITY)) return MTPK_EINVAL;
+  if (workspace_bytes < mtpk_sample_workspace_bytes(rows, vocab) || !aligned16(workspace))
+    return MTPK_EINVAL;
+  const int64_t nchunk = rs_chunks(vocab);
+  if (nchunk > 65535) return MTPK_EINVAL;
+  const int per_vec = dtype == MTPK_BF16 ? 8 : 4;
+  RsRows rr{logits, nullptr, dtype, vocab, (int)(aligned16(logits) && vocab % per_vec == 0)};
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  float2* part = reinterpret_cast<float2*>(ws);
+  ws += align256(rows * nchunk * (int64_t)sizeof(float2));
+  RsItem* items = reinterpret_cast<RsItem*>(ws);
+  ws += align256(rows * (int64_t)sizeof(RsItem));
+  float2* mass = reinterpret_cast<float2*>(ws);
+  const float inv_t = 1.f / temperature;
+  const hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_rs_stats, dim3((unsigned)nchunk, (unsigned)rows), dim3(kRsThreads), 0, st,
+                     rr, rows, inv_t, part);
+  int rc = status_of(hipGetLastError());
+  if (rc) return rc;
+  hipLaunchKernelGGL(k_rs_rows, dim3((unsigned)rows), dim3(kWave), 0, st, part, (int)nchunk, items);
+  if ((rc = status_of(hipGetLastError()))) return rc;
+  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)rows), dim3(kRsThreads), 0, st,
+                     rr, items, inv_t, mass);
+  if ((rc = status_of(hipGetLastError()))) return rc;
+  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)rows), dim3(kRsThreads), 0, st, rr, items, mass,
+                     (int)nchunk, inv_t, u, token, nullptr, 0, nullptr);
+  return status_of(hipGetLastError());
+}
+
+}  // extern "C"

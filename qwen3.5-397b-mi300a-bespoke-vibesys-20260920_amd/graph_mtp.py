@@ -275,3 +275,65 @@ class MTPVerifyRunner:
         verify_round_step(self.model, self.mtp, self.buf, lanes, b, max(positions) + self.t, fn)
         rows = torch.cat([self.buf.step_argmax[:b], self.buf.accept_len[:b, None]], dim=1).tolist()
         return [row[: row[-1] + 1] for row in rows]
+
+
+# ---------------------------------------------------------------- sampling-mode acceptance
+
+
+def rejection_workspace(batch: int, k: int, vocab: int, device: torch.device) -> torch.Tensor:
+    n = int(_mtpk.lib().mtpk_rejection_workspace_bytes(batch, k, vocab))
+    return torch.empty(max(n, 1), dtype=torch.uint8, device=device)
+
+
+def rejection_sample(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_tokens: torch.Tensor,
+                     u_accept: torch.Tensor, u_sample: torch.Tensor, temperature: float, *,
+                     workspace: torch.Tensor | None = None,
+                     with_margin: bool = False) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor | None]:
+    """Speculative rejection sampling on the device (`mtpk_rejection_sample`): returns
+    `(accept_len i64 [B], token i64 [B], emitted i64 [B, k+1], margin f32 [B, k] or None)`.
+
+    `target_logits` `[B, k+1, V]` and `draft_logits` `[B, k, V]` (f32 or bf16, same dtype),
+    `draft_tokens` i64 `[B, k]`, uniforms f32 `u_accept` `[B, k]` and `u_sample` `[B]`.
+    `emitted` is the accepted drafts then the drawn token: fed to `greedy_accept` as the
+    step argmax it gives the same accept length and every rollback index."""
+    device = _mtpk.require_device(target_logits, draft_logits, draft_tokens, u_accept, u_sample)
+    b, t, vocab = target_logits.shape
+    k = t - 1
+    if draft_logits.shape != (b, k, vocab) or draft_logits.dtype != target_logits.dtype:
+        raise ValueError("draft_logits must be [B, k, V] of target_logits' dtype")
+    if draft_tokens.shape != (b, k) or draft_tokens.dtype != torch.int64:
+        raise ValueError("draft_tokens must be int64 [B, k]")
+    if u_accept.shape != (b, k) or u_sample.shape != (b,):
+        raise ValueError("u_accept must be [B, k] and u_sample [B]")
+    if not temperature > 0:
+        raise ValueError("rejection sampling needs temperature > 0 (greedy rounds use greedy_accept)")
+    tl, dl = target_logits.contiguous(), draft_logits.contiguous()
+    ua, us = u_accept.float().contiguous(), u_sample.float().contiguous()
+    dt = draft_tokens.contiguous()
+    ws = workspace if workspace is not None else rejection_workspace(b, k, vocab, device)
+    long = dict(dtype=torch.long, device=device)
+    acc, tok, emitted = torch.empty(b, **long), torch.empty(b, **long), torch.empty(b, t, **long)
+    margin = torch.empty(b, max(k, 1), dtype=torch.float32, device=device) if with_margin else None
+    _mtpk.check(
+        _mtpk.lib().mtpk_rejection_sample(
+            tl.data_ptr(), dl.data_ptr(), _mtpk.float_code(tl.dtype), b, k, vocab, dt.data_ptr(),
+            ua.data_ptr(), us.data_ptr(), float(temperature), ws.data_ptr(), ws.numel(),
+            acc.data_ptr(), tok.data_ptr(), emitted.data_ptr(),
+            margin.data_ptr() if margin is not None else None, _mtpk.stream_of(device),
+        ),
+        "mtpk_rejection_sample",
+    )  # fmt: skip
+    return acc, tok, emitted, margin[:, :k] if margin is not None else None
+
+
+def rejection_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_tokens: torch.Tensor,
+                     u_accept: torch.Tensor, u_sample: torch.Tensor, temperature: float,
+                     active: torch.Tensor, pos: torch.Tensor, budget: torch.Tensor, stops: torch.Tensor,
+                     conv_k1: int) -> tuple[AcceptResult, torch.Tensor]:
+    """Sampling-mode acceptance with the round's rollback indices: rejection sampling, then
+    `greedy_accept` over the emitted tokens (which applies the stop ids and the budget).
+    Returns `(AcceptResult, emitted [B, k+1])`; committed ids are `emitted[j, :a+1]`."""
+    _, _, emitted, _ = rejection_sample(target_logits, draft_logits, draft_tokens, u_accept, u_sample,
+                                        temperature)
+    res = greedy_accept(emitted, draft_tokens, active, pos, budget, stops, conv_k1)
+    return res, emitted

@@ -277,3 +277,23 @@ def speculative_decode(model, slots: list[int], tokens: list[int], positions: li
     m = model.mtp
     drafts = draft(model, m, model.hidden_cache[model.lane_index(slots)], tokens, slots, positions)
     return verify_and_commit(model, m, slots, tokens, drafts, positions, budgets, stops)
+
+
+def sample_rows(logits: torch.Tensor, temperature: float, u: torch.Tensor) -> torch.Tensor:
+    """One inverse-CDF draw per row from `softmax(logits / T)` with uniforms `u` `[rows]`
+    (`mtpk_sample_rows`), int64 `[rows]`: the draft step's sampler at temperature > 0."""
+    device = _mtpk.require_device(logits, u)
+    if not temperature > 0:
+        raise ValueError("sample_rows needs temperature > 0")
+    flat = logits.reshape(-1, logits.shape[-1]).contiguous()
+    rows, vocab = flat.shape
+    uu = u.reshape(-1).float().contiguous()
+    if uu.numel() != rows:
+        raise ValueError("u must hold one uniform per row")
+    lib = _mtpk.lib()
+    ws = torch.empty(max(int(lib.mtpk_sample_workspace_bytes(rows, vocab)), 1), dtype=torch.uint8, device=device)
+    out = torch.empty(rows, dtype=torch.long, device=device)
+    _mtpk.check(lib.mtpk_sample_rows(flat.data_ptr(), _mtpk.float_code(flat.dtype), rows, vocab,
+                                     float(temperature), uu.data_ptr(), ws.data_ptr(), ws.numel(),
+                                     out.data_ptr(), _mtpk.stream_of(device)), "mtpk_sample_rows")
+    return out.reshape(logits.shape[:-1])

@@ -58,3 +58,13 @@ def test_rejected_arguments_launch_nothing(lib):
                                   None, None, None, None, None, None, None, None, None, None,
                                   None, None) == -1
     assert lib.mtpk_moe_prep(None, 3, None, 0, 10, 0, 512, None, None, 10, None, None) == -1
+    # rejection sampling: null inputs, then a non-positive temperature with valid-looking
+    # pointers (nothing is dereferenced before the checks)
+    fake = 0x1000
+    assert lib.mtpk_rejection_sample(None, None, 1, 4, 3, 100, None, None, None, 0.7, None, 0,
+                                     None, None, None, None, None) == -1
+    assert lib.mtpk_rejection_sample(fake, fake, 1, 4, 3, 100, fake, fake, fake, 0.0, fake, 1 << 30,
+                                     fake, fake, None, None, None) == -1
+    assert lib.mtpk_sample_rows(fake, 1, 4, 100, -1.0, fake, fake, 1 << 30, fake, None) == -1
+    assert lib.mtpk_rejection_workspace_bytes(48, 3, 248320) >= 48 * 7 * 61 * 8
+    assert lib.mtpk_sample_workspace_bytes(4, 100) == lib.mtpk_rejection_workspace_bytes(4, 0, 100)
