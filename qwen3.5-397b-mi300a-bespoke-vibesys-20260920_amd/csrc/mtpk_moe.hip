@@ -504,6 +504,253 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_token(
   }
 }
 
+// ---------------------------------------------------------------- single-token units (direct mode)
+//
+// In direct mode every unit is one assignment, i.e. one token column of the MFMA tile. The
+// activation row is then staged once in LDS (lanes c >= 1 read a zero row) instead of being
+// loaded per trip, so a trip is only the weight loads and a wave keeps its whole K range in
+// flight at once (one memory latency per item instead of one per ring turn).
+
+constexpr int kSingleTrips = 8;    // trips a wave keeps in flight (its whole K range)
+constexpr int kSingleQuarter = kSingleTrips * 128;  // K elements per wave in gate_up
+
+// The e8m0 scales of 8 consecutive trips of one weight row: 32 bytes, two 16-byte loads.
+struct ScaleRow8 {
+  u32x4_t lo, hi;
+  __device__ inline void load(rsrc_t r, uint32_t off, uint32_t bad) {
+    lo = buf16(r, off | bad);
+    hi = buf16(r, (off + 16u) | bad);
+  }
+  __device__ inline uint32_t byte(int s, int g) const {
+    const uint32_t d = s < 4 ? lo[s & 3] : hi[s & 3];
+    return (d >> (8 * g)) & 0xffu;
+  }
+};
+
+// gate_up, one token per unit: item = (assignment, 16 intermediate rows); wave w takes trips
+// [8w, 8w + 8) (K <= 4096), stages that quarter of the token's XP activation planes in its own
+// LDS region, issues all 8 trips of gate and up weights, then reduces the four partial tiles
+// in LDS in wave order.
+template <int XP, int OP, bool SV>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_single(
+    const uint16_t* __restrict__ x, int64_t x_plane, int K, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, int I, UnitSrc src, int top_k, uint16_t* __restrict__ inter,
+    int64_t inter_plane) {
+  constexpr int kPlaneBytes = kSingleQuarter * 2;  // 2 KB
+  __shared__ __attribute__((aligned(16))) uint8_t xs[kMoeWaves][XP][kPlaneBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t zero[kPlaneBytes];  // the A rows of lanes c >= 1
+  __shared__ f32x4_t red[kMoeWaves - 1][2][kWave];
+  const int ntile = I >> 4;
+  const int n_items = unit_count(src) * ntile;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int nb = K >> 5, ntrip = (nb + 3) >> 2;
+  const int tbase = wave * kSingleTrips;
+  const int64_t row_bytes = K >> 1;
+  const rsrc_t rx = make_rsrc(x, (uint32_t)(XP * x_plane * 2));
+  const uint32_t exp_bytes = (uint32_t)(2 * I) * (uint32_t)row_bytes;
+  if (tid < kPlaneBytes / 16) reinterpret_cast<u32x4_t*>(zero)[tid] = zero16();
+  __syncthreads();
+
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int u = item / ntile, nt = item - u * ntile;
+    int e, first, cnt;
+    unit_get(src, u, e, first, cnt);
+    if (cnt == 0) continue;  // uniform over the workgroup
+    const int tok = unit_member(src, first) / top_k;
+    const int eu = uniform(e);
+    const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
+    const rsrc_t rs = make_rsrc(ws + (int64_t)eu * (2 * I) * nb, (uint32_t)(2 * I * nb));
+    const uint32_t row = (uint32_t)(nt * 16 + ln.c);
+    const uint32_t og = row * (uint32_t)row_bytes, ou = og + (uint32_t)I * (uint32_t)row_bytes;
+    const uint32_t osg = row * (uint32_t)nb, osu = osg + (uint32_t)(I * nb);
+
+    // this wave's activation quarter: 16 bytes per lane per load, two loads per plane
+    u32x4_t sreg[XP][2];
+#pragma unroll
+    for (int p = 0; p < XP; ++p)
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int kel = tbase * 128 + (k * kWave + lane) * 8;
+        const uint32_t bad = (uint32_t)!(kel < K) << 31;
+        sreg[p][k] = buf16(rx, ((uint32_t)(p * x_plane + (int64_t)tok * K + kel) * 2u) | bad);
+      }
+    ScaleRow8 cg, cu;  // SV: the quarter's 32 scale bytes per row (nb a multiple of 32)
+    const uint32_t sbad = (uint32_t)!(SV && tbase < ntrip) << 31;
+    cg.load(rs, osg + 4u * (uint32_t)tbase, sbad);
+    cu.load(rs, osu + 4u * (uint32_t)tbase, sbad);
+    u32x4_t wg[kSingleTrips], wu[kSingleTrips];
+#pragma unroll
+    for (int i = 0; i < kSingleTrips; ++i) {
+      const int tr = tbase + i;
+      const int blk = moe_block(tr, ln.g);
+      const uint32_t bad = (uint32_t)!(tr < ntrip && blk < nb) << 31;
+      wg[i] = buf16(rw, (og + (uint32_t)blk * 16u) | bad);
+      wu[i] = buf16(rw, (ou + (uint32_t)blk * 16u) | bad);
+    }
+    ring_fence();
+#pragma unroll
+    for (int p = 0; p < XP; ++p)
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        *reinterpret_cast<u32x4_t*>(&xs[wave][p][(k * kWave + lane) * 16]) = sreg[p][k];
+    ring_fence();
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // this wave's LDS writes are visible to itself
+    // lane (g, c): A values of trip i, slot h at base + 256 i + 16 h (c == 0: the token row)
+    const uint8_t* abase[XP];
+#pragma unroll
+    for (int p = 0; p < XP; ++p) abase[p] = (ln.c == 0 ? &xs[wave][p][0] : zero) + ln.g * 64;
+    f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < kSingleTrips; ++i) {
+      const int tr = tbase + i, blk = moe_block(tr, ln.g);
+      uint32_t sg_, su_;
+      if (SV) {
+        sg_ = cg.byte(i, ln.g);
+        su_ = cu.byte(i, ln.g);
+      } else {
+        const uint32_t bad = (uint32_t)!(tr < ntrip && blk < nb) << 31;
+        sg_ = buf1(rs, (osg + (uint32_t)blk) | bad);
+        su_ = buf1(rs, (osu + (uint32_t)blk) | bad);
+      }
+      const float fg = e8m0_to_f32(sg_), fu = e8m0_to_f32(su_);
+#pragma unroll
+      for (int h = 0; h < 4; ++h) {
+        const bf16x8_t bg = decode8(wg[i][h], fg), bu = decode8(wu[i][h], fu);
+#pragma unroll
+        for (int p = 0; p < XP; ++p) {
+          const bf16x8_t av = as_bf16x8(*reinterpret_cast<const u32x4_t*>(abase[p] + 256 * i + 16 * h));
+          accg = mfma16x16x32(av, bg, accg);
+          accu = mfma16x16x32(av, bu, accu);
+        }
+      }
+      ring_fence();  // one trip's LDS reads and decodes at a time
+    }
+    if (wave > 0) {
+      red[wave - 1][0][lane] = accg;
+      red[wave - 1][1][lane] = accu;
+    }
+    __syncthreads();
+    if (wave == 0) {
+#pragma unroll
+      for (int w = 0; w < kMoeWaves - 1; ++w) {
+        accg += red[w][0][lane];
+        accu += red[w][1][lane];
+      }
+      if (ln.g == 0) {  // row m = 0 (the token) of column n = c
+        const float gt = accg[0];
+        store_planes<OP>(inter + (int64_t)unit_member(src, first) * I + nt * 16 + ln.c, inter_plane,
+                         gt / (1.f + __expf(-gt)) * accu[0]);
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// down + combine, one token per unit: workgroup item = (token t, 16 hidden rows), 16 waves;
+// wave w streams assignment t * top_k + j for j = w, w + 16, ... over its whole K (<= 1024:
+// all 8 trips in flight), its intermediate row staged in its own LDS region. The weighted
+// partial rows are summed in LDS in wave order.
+constexpr int kSingleDownWaves = 16;
+
+template <int IP, bool SV>
+__global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
+    const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, int H, const void* __restrict__ a_expert, int edt,
+    const void* __restrict__ a_weight, int wdt, int lo, int n_experts, int tokens, int top_k,
+    void* __restrict__ out, int odt) {
+  constexpr int kPlaneBytes = kSingleQuarter * 2;  // 2 KB: K <= 1024
+  __shared__ __attribute__((aligned(16))) uint8_t as_[kSingleDownWaves][IP][kPlaneBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t zero[kPlaneBytes];  // the A rows of lanes c >= 1
+  __shared__ float red[kSingleDownWaves][16];
+  const int rtiles = H >> 4;
+  const int n_items = tokens * rtiles;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int nb = K >> 5, ntrip = (nb + 3) >> 2;
+  const int64_t row_bytes = K >> 1;
+  const rsrc_t ra = make_rsrc(inter, (uint32_t)(IP * inter_plane * 2));
+  const uint32_t exp_bytes = (uint32_t)H * (uint32_t)row_bytes;
+  if (tid < kPlaneBytes / 16) reinterpret_cast<u32x4_t*>(zero)[tid] = zero16();
+  __syncthreads();
+
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const int t = item / rtiles, rt = item - t * rtiles;
+    float tot = 0.f;
+    for (int j = wave; j < top_k; j += kSingleDownWaves) {
+      const int64_t a = (int64_t)t * top_k + j;
+      const int64_t ex = load_index(a_expert, edt, a) - lo;
+      const float wj = load_float(a_weight, wdt, a);
+      if (!(ex >= 0 && ex < n_experts && wj != 0.f)) continue;  // uniform per wave
+      const int eu = uniform((int)ex);
+      const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
+      const rsrc_t rs = make_rsrc(ws + (int64_t)eu * H * nb, (uint32_t)(H * nb));
+      const uint32_t row = (uint32_t)(rt * 16 + ln.c);
+      const uint32_t ow = row * (uint32_t)row_bytes, os = row * (uint32_t)nb;
+      u32x4_t sreg[IP][2];
+#pragma unroll
+      for (int p = 0; p < IP; ++p)
+#pragma unroll
+        for (int k = 0; k < 2; ++k) {
+          const int kel = (k * kWave + lane) * 8;
+          const uint32_t bad = (uint32_t)!(kel < K) << 31;
+          sreg[p][k] = buf16(ra, ((uint32_t)(p * inter_plane + a * K + kel) * 2u) | bad);
+        }
+      ScaleRow8 cs;  // SV: the row's 32 scale bytes (K = 1024)
+      cs.load(rs, os, (uint32_t)!SV << 31);
+      u32x4_t w[kSingleTrips];
+#pragma unroll
+      for (int i = 0; i < kSingleTrips; ++i) {
+        const int blk = moe_block(i, ln.g);
+        const uint32_t bad = (uint32_t)!(i < ntrip && blk < nb) << 31;
+        w[i] = buf16(rw, (ow + (uint32_t)blk * 16u) | bad);
+      }
+      ring_fence();
+#pragma unroll
+      for (int p = 0; p < IP; ++p)
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+          *reinterpret_cast<u32x4_t*>(&as_[wave][p][(k * kWave + lane) * 16]) = sreg[p][k];
+      ring_fence();
+      __builtin_amdgcn_s_waitcnt(0xC07F);
+      const uint8_t* abase[IP];
+#pragma unroll
+      for (int p = 0; p < IP; ++p) abase[p] = (ln.c == 0 ? &as_[wave][p][0] : zero) + ln.g * 64;
+      f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int i = 0; i < kSingleTrips; ++i) {
+        const int blk = moe_block(i, ln.g);
+        uint32_t sb;
+        if (SV) {
+          sb = cs.byte(i, ln.g);
+        } else {
+          const uint32_t bad = (uint32_t)!(i < ntrip && blk < nb) << 31;
+          sb = buf1(rs, (os + (uint32_t)blk) | bad);
+        }
+        const float fs = e8m0_to_f32(sb);
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const bf16x8_t b = decode8(w[i][h], fs);
+#pragma unroll
+          for (int p = 0; p < IP; ++p)
+            acc = mfma16x16x32(as_bf16x8(*reinterpret_cast<const u32x4_t*>(abase[p] + 256 * i + 16 * h)), b, acc);
+        }
+        ring_fence();  // one trip's LDS reads and decodes at a time
+      }
+      tot += wj * acc[0];  // lanes 0..15 hold row m = 0 (the token) of column n = c
+    }
+    if (lane < 16) red[wave][lane] = tot;
+    __syncthreads();
+    if (wave == 0 && lane < 16) {
+      float v = red[0][lane];
+#pragma unroll
+      for (int w2 = 1; w2 < kSingleDownWaves; ++w2) v += red[w2][lane];
+      store_float(out, odt, (int64_t)t * H + rt * 16 + lane, v);
+    }
+    __syncthreads();
+  }
+}
+
 // ---------------------------------------------------------------- LDS-staged unit kernels
 //
 // Wide batches: the 4 waves of a workgroup work on one unit, each on its own weight rows, so
@@ -556,8 +803,8 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
   const int64_t row_bytes = K >> 1;
   const rsrc_t rx = make_rsrc(x, (uint32_t)(x_elems * 2));
   const uint32_t exp_bytes = (uint32_t)(2 * I) * (uint32_t)row_bytes;
-  // staging: thread -> (token row sr, 64-byte segment sseg) of a chunk
-  const int sr = tid >> 4, sseg = tid & 15;
+  // staging: load k of a chunk moves 16 bytes of token row 4k + wave at byte 16 * lane, so
+  // every wave instruction reads one row's whole 1 KB chunk (eight full 128-byte lines)
 
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int u = item / ngroup, q = item - u * ngroup;
@@ -573,18 +820,22 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
     const uint32_t row = (uint32_t)(nt * 16 + ln.c);
     const uint32_t og = row * (uint32_t)row_bytes, ou = og + (uint32_t)I * (uint32_t)row_bytes;
     const uint32_t osg = row * (uint32_t)nb, osu = osg + (uint32_t)(I * nb);
-    const uint32_t sx = sr < cnt ? (uint32_t)(unit_member(src, first + sr) / top_k) * (uint32_t)K * 2u +
-                                       (uint32_t)sseg * 64u
-                                 : kOutOfRange;
+    uint32_t sx[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 4 * k + wave;
+      sx[k] = r < cnt ? (uint32_t)(unit_member(src, first + r) / top_k) * (uint32_t)K * 2u + (uint32_t)lane * 16u
+                      : kOutOfRange;
+    }
     u32x4_t sreg[4];
     auto stage_load = [&](int c) {
       const uint32_t bad = (uint32_t)!(c < nchunk) << 31;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sreg[k] = buf16(rx, (sx + (uint32_t)c * (KC * 2) + 16u * k) | bad);
+      for (int k = 0; k < 4; ++k) sreg[k] = buf16(rx, (sx[k] + (uint32_t)c * (KC * 2)) | bad);
     };
     auto stage_store = [&](int b) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) lds16_store(&xs[b][sr * G::kRow + sseg * 64 + 16 * k], sreg[k]);
+      for (int k = 0; k < 4; ++k) lds16_store(&xs[b][(4 * k + wave) * G::kRow + lane * 16], sreg[k]);
     };
 
     auto issue = [&](u32x4_t& wg, u32x4_t& wu, int tr) {
@@ -679,8 +930,9 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
   const int64_t row_bytes = K >> 1;
   const rsrc_t ra = make_rsrc(inter, (uint32_t)(2 * inter_plane * 2));
   const uint32_t exp_bytes = (uint32_t)H * (uint32_t)row_bytes;
-  // staging: thread -> (token row sr, plane sp, 64-byte segment) of a chunk
-  const int sr = tid >> 4, sp = (tid >> 3) & 1, sseg = tid & 7;
+  // staging: load k of a chunk moves 16 bytes of (token row 2k + wave / 2, plane wave & 1) at
+  // byte 16 * (lane & 31), lanes 32..63 taking the next row: every wave instruction reads two
+  // whole 512-byte plane segments (full 128-byte lines)
 
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int u = item / ngroup, q = item - u * ngroup;
@@ -699,19 +951,26 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
       ow[r] = row * (uint32_t)row_bytes;
       os[r] = row * (uint32_t)nb;
     }
-    const uint32_t sa = sr < cnt ? (uint32_t)unit_member(src, first + sr) * (uint32_t)K * 2u +
-                                       (uint32_t)sp * (uint32_t)inter_plane * 2u + (uint32_t)sseg * 64u
-                                 : kOutOfRange;
+    // thread slot of load k: segment index k * 256 + tid over (row, plane, 16-byte column)
+    const int sp = (tid >> 5) & 1, scol = tid & 31;
+    uint32_t sa[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int r = 4 * k + (tid >> 6);
+      sa[k] = r < cnt ? (uint32_t)unit_member(src, first + r) * (uint32_t)K * 2u +
+                            (uint32_t)sp * (uint32_t)inter_plane * 2u + (uint32_t)scol * 16u
+                      : kOutOfRange;
+    }
     u32x4_t sreg[4];
     auto stage_load = [&](int c) {
       const uint32_t bad = (uint32_t)!(c < nchunk) << 31;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sreg[k] = buf16(ra, (sa + (uint32_t)c * (KC * 2) + 16u * k) | bad);
+      for (int k = 0; k < 4; ++k) sreg[k] = buf16(ra, (sa[k] + (uint32_t)c * (KC * 2)) | bad);
     };
     auto stage_store = [&](int b) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        lds16_store(&xs[b][sr * G::kRow + sp * G::kPlaneBytes + sseg * 64 + 16 * k], sreg[k]);
+        lds16_store(&xs[b][(4 * k + (tid >> 6)) * G::kRow + sp * G::kPlaneBytes + scol * 16], sreg[k]);
     };
     auto issue = [&](u32x4_t* w, int tr) {
       const int blk = moe_block(tr, ln.g);
@@ -1004,6 +1263,41 @@ int launch_down_token_t(const uint16_t* inter, int64_t inter_plane, int K, const
   return status_of(hipGetLastError());
 }
 
+// Direct mode with one token per unit: the single-token kernels when the K ranges fit their
+// fixed trip counts (gate_up K <= 4096, down K <= 1024).
+bool single_gate_up_ok(int K) { return K <= 4 * kSingleQuarter; }
+bool single_down_ok(int K) { return K <= kSingleQuarter; }
+
+template <int XP, int OP, bool SV>
+int launch_gate_up_single(const uint16_t* x, int64_t x_plane, int K, const uint8_t* wq,
+                          const uint8_t* ws, int I, const UnitSrc& src, int64_t units, int top_k,
+                          uint16_t* inter, int64_t inter_plane, hipStream_t st) {
+  static int occ = 0;
+  auto kern = k_moe_gate_up_single<XP, OP, SV>;
+  const int grid = grid_for(kern, units * (I >> 4), occ);
+  if (grid == 0) return 0;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(kMoeThreads), 0, st, x, x_plane, K, wq, ws, I, src,
+                     top_k, inter, inter_plane);
+  return status_of(hipGetLastError());
+}
+
+template <int IP, bool SV>
+int launch_down_single(const uint16_t* inter, int64_t inter_plane, int K, const uint8_t* wq,
+                       const uint8_t* ws, int H, const void* a_expert, int edt, const void* a_weight,
+                       int wdt, int lo, int n_experts, int tokens, int top_k, void* out, int odt,
+                       hipStream_t st) {
+  static int occ = 0;
+  auto kern = k_moe_down_single<IP, SV>;
+  constexpr int threads = kSingleDownWaves * kWave;
+  if (occ == 0) occ = occupancy_per_cu(kern, threads);
+  const int64_t need = (int64_t)tokens * (H >> 4), cap = (int64_t)device_cu_count() * occ;
+  const int grid = (int)(need < cap ? need : cap);
+  if (grid == 0) return 0;
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), 0, st, inter, inter_plane, K, wq, ws, H,
+                     a_expert, edt, a_weight, wdt, lo, n_experts, tokens, top_k, out, odt);
+  return status_of(hipGetLastError());
+}
+
 UnitSrc unit_list(const int32_t* units, const int32_t* sorted, const int32_t* n_units,
                   int64_t max_units) {
   UnitSrc s{};
@@ -1111,10 +1405,21 @@ int mtpk_moe_gate_up_direct(const uint16_t* x_planes, int x_nplanes, int64_t tok
     return MTPK_EINVAL;
   const int64_t a = tokens * top_k;
   if (a == 0) return 0;
-  return launch_gate_up(
-      x_nplanes, x_planes, tokens * hidden, (int)hidden, gate_up, gate_up_scale, (int)inter_dim,
-      unit_direct(a_expert, expert_dtype, a_weight, weight_dtype, expert_lo, expert_hi, a), a,
-      top_k, inter, a * inter_dim, (hipStream_t)stream);
+  const UnitSrc src =
+      unit_direct(a_expert, expert_dtype, a_weight, weight_dtype, expert_lo, expert_hi, a);
+  const hipStream_t st = (hipStream_t)stream;
+  if (single_gate_up_ok((int)hidden)) {
+#define MTPK_GS(XP_, OP_, SV_)                                                                   \
+  launch_gate_up_single<XP_, OP_, SV_>(x_planes, tokens * hidden, (int)hidden, gate_up,         \
+                                       gate_up_scale, (int)inter_dim, src, a, top_k, inter,      \
+                                       a * inter_dim, st)
+    const bool sv = (hidden / 32) % 32 == 0;
+    if (x_nplanes == 1) return sv ? MTPK_GS(1, 2, true) : MTPK_GS(1, 2, false);
+    return sv ? MTPK_GS(3, 3, true) : MTPK_GS(3, 3, false);
+#undef MTPK_GS
+  }
+  return launch_gate_up(x_nplanes, x_planes, tokens * hidden, (int)hidden, gate_up,
+                        gate_up_scale, (int)inter_dim, src, a, top_k, inter, a * inter_dim, st);
 }
 
 int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, int64_t inter_dim,
@@ -1161,6 +1466,16 @@ int mtpk_moe_down_combine(const uint16_t* inter, int inter_planes, int64_t inter
   if (tokens == 0) return 0;
   const hipStream_t st = (hipStream_t)stream;
   const int64_t ip = tokens * top_k * inter_dim;
+  if (single_down_ok((int)inter_dim) && (inter_planes == 2 || inter_planes == 3)) {
+#define MTPK_DS(IP_, SV_)                                                                     \
+  launch_down_single<IP_, SV_>(inter, ip, (int)inter_dim, down, down_scale, (int)hidden,      \
+                               a_expert, expert_dtype, a_weight, weight_dtype, expert_lo,     \
+                               (int)local_experts, (int)tokens, top_k, out, out_dtype, st)
+    const bool sv = inter_dim == 1024;
+    if (inter_planes == 2) return sv ? MTPK_DS(2, true) : MTPK_DS(2, false);
+    return sv ? MTPK_DS(3, true) : MTPK_DS(3, false);
+#undef MTPK_DS
+  }
 #define MTPK_DT(IP_, D_, SV_)                                                              \
   launch_down_token_t<IP_, D_, SV_>(inter, ip, (int)inter_dim, down, down_scale, (int)hidden, \
                                     a_expert, expert_dtype, a_weight, weight_dtype, expert_lo, \
