@@ -760,6 +760,13 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
 // activation loads off the vector memory path, where every lane of a wave costs address work
 // even when most of the unit's 16 token slots are empty.
 
+// Scalar (constant-cache) reads of the work list. An item's unit record and the member ids of
+// its staging rows are uniform over a wave, so they are read with scalar loads, outside the
+// vector-memory queue the trip ring keeps full: a vector load there would make the item's first
+// wait drain the ring. The list was written by an earlier launch and is read-only here.
+typedef const __attribute__((address_space(4))) int32_t* kc_i32_t;
+__device__ inline int32_t sload(const int32_t* p, int i) { return ((kc_i32_t)p)[i]; }
+
 // Wait for this wave's LDS operations, then workgroup barrier. Vector memory loads (the trip
 // ring) stay in flight across it.
 __device__ inline void lds_barrier() {
@@ -796,8 +803,8 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
   using G = StageGeom<KC, 1>;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][G::kBuf];
   const int ntile = I >> 4, ngroup = (ntile + kMoeWaves - 1) / kMoeWaves;
-  const int n_items = unit_count(src) * ngroup;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const int n_items = min(sload(src.n_units, 0), src.max_units) * ngroup;
+  const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
   const int nb = K >> 5, ntrip = nb >> 2, nchunk = K / KC;
   const int64_t row_bytes = K >> 1;
@@ -808,13 +815,17 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
 
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int u = item / ngroup, q = item - u * ngroup;
-    int e, first, cnt;
-    unit_get(src, u, e, first, cnt);
+    const int e = sload(src.units, 3 * u), first = sload(src.units, 3 * u + 1);
+    const int cnt = sload(src.units, 3 * u + 2);
     if (cnt == 0) continue;  // uniform over the workgroup
+    // output assignments of this lane's four token slots, read now, used after the K loop
+    int32_t om[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) om[i] = src.sorted[first + min(moe_out_slot(ln.g, i), cnt - 1)];
     const int nt_raw = q * kMoeWaves + wave;
     const bool wave_ok = nt_raw < ntile;
     const int nt = wave_ok ? nt_raw : ntile - 1;
-    const int eu = uniform(e);
+    const int eu = e;
     const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
     const rsrc_t rs = make_rsrc(ws + (int64_t)eu * (2 * I) * nb, (uint32_t)(2 * I * nb));
     const uint32_t row = (uint32_t)(nt * 16 + ln.c);
@@ -824,8 +835,8 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int r = 4 * k + wave;
-      sx[k] = r < cnt ? (uint32_t)(unit_member(src, first + r) / top_k) * (uint32_t)K * 2u + (uint32_t)lane * 16u
-                      : kOutOfRange;
+      const int tok = sload(src.sorted, first + min(r, cnt - 1)) / top_k;
+      sx[k] = r < cnt ? (uint32_t)tok * (uint32_t)K * 2u + (uint32_t)lane * 16u : kOutOfRange;
     }
     u32x4_t sreg[4];
     auto stage_load = [&](int c) {
@@ -866,26 +877,34 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
       }
     };
 
-    // prologue: chunk 0 staged, chunk 1 loading, scales and weights of the first D trips
+    // prologue: chunk 0 loads first, then the scales and weights of the first D trips, so
+    // that waiting for chunk 0 leaves the whole ring in flight; chunk 1 loads behind them
     stage_load(0);
-    stage_store(0);
-    stage_load(1);
+    ring_fence();
     issue_chunk(cg, cu, 0);
     u32x4_t rg[D], ru[D];
 #pragma unroll
-    for (int s = 0; s < D; ++s) {
-      issue(rg[s], ru[s], s);
-      ring_fence();
-    }
+    for (int s = 0; s < D; ++s) issue(rg[s], ru[s], s);
+    ring_fence();
+    stage_store(0);
+    stage_load(1);
     lds_barrier();
-    for (int c = 0; c < nchunk; ++c) {
+    // nchunk >= 1 (K is a positive multiple of KC): a bottom-tested loop keeps the ring
+    // issue above in the prologue's block instead of letting it sink past the barrier
+    int c = 0;
+    do {
       const int t = c * D;
       const uint8_t* buf = xs[c & 1];
       issue_chunk(ng, nu, t + D);
+      // trips are consumed and refilled in pairs: the two refills of a row are adjacent
+      // 64-byte segments issued back to back
 #pragma unroll
-      for (int s = 0; s < D; ++s) {
+      for (int s = 0; s < D; s += 2) {
         consume(rg[s], ru[s], s, buf);
+        consume(rg[s + 1], ru[s + 1], s + 1, buf);
+        ring_fence();
         issue(rg[s], ru[s], t + s + D);
+        issue(rg[s + 1], ru[s + 1], t + s + 1 + D);
         ring_fence();
       }
       cg = ng;
@@ -893,17 +912,15 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
       if (c + 1 < nchunk) stage_store((c + 1) & 1);
       stage_load(c + 2);
       lds_barrier();
-    }
+    } while (++c < nchunk);
 
     if (wave_ok) {
       const int n = nt * 16 + ln.c;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int m = moe_out_slot(ln.g, i);
-        if (m < cnt) {
-          const int64_t a = unit_member(src, first + m);
+        if (moe_out_slot(ln.g, i) < cnt) {
           const float gt = accg[i];
-          store_planes<2>(inter + a * I + n, inter_plane, gt / (1.f + __expf(-gt)) * accu[i]);
+          store_planes<2>(inter + (int64_t)om[i] * I + n, inter_plane, gt / (1.f + __expf(-gt)) * accu[i]);
         }
       }
     }
@@ -923,8 +940,8 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][G::kBuf];
   const int rtiles = H >> 4;
   const int ngroup = (rtiles + kMoeWaves * R - 1) / (kMoeWaves * R);
-  const int n_items = unit_count(src) * ngroup;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const int n_items = min(sload(src.n_units, 0), src.max_units) * ngroup;
+  const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
   const int nb = K >> 5, ntrip = nb >> 2, nchunk = K / KC;
   const int64_t row_bytes = K >> 1;
@@ -936,10 +953,13 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
 
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int u = item / ngroup, q = item - u * ngroup;
-    int e, first, cnt;
-    unit_get(src, u, e, first, cnt);
+    const int e = sload(src.units, 3 * u), first = sload(src.units, 3 * u + 1);
+    const int cnt = sload(src.units, 3 * u + 2);
     if (cnt == 0) continue;
-    const int eu = uniform(e);
+    int32_t om[4];  // output assignments of this lane's token slots, used after the K loop
+#pragma unroll
+    for (int i = 0; i < 4; ++i) om[i] = src.sorted[first + min(moe_out_slot(ln.g, i), cnt - 1)];
+    const int eu = e;
     const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
     const rsrc_t rs = make_rsrc(ws + (int64_t)eu * H * nb, (uint32_t)(H * nb));
     uint32_t ow[R], os[R];
@@ -956,9 +976,10 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
     uint32_t sa[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int r = 4 * k + (tid >> 6);
-      sa[k] = r < cnt ? (uint32_t)unit_member(src, first + r) * (uint32_t)K * 2u +
-                            (uint32_t)sp * (uint32_t)inter_plane * 2u + (uint32_t)scol * 16u
+      const int r = 4 * k + wave;
+      const int a = sload(src.sorted, first + min(r, cnt - 1));
+      sa[k] = r < cnt ? (uint32_t)a * (uint32_t)K * 2u + (uint32_t)sp * (uint32_t)inter_plane * 2u +
+                            (uint32_t)scol * 16u
                       : kOutOfRange;
     }
     u32x4_t sreg[4];
@@ -970,7 +991,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
     auto stage_store = [&](int b) {
 #pragma unroll
       for (int k = 0; k < 4; ++k)
-        lds16_store(&xs[b][(4 * k + (tid >> 6)) * G::kRow + sp * G::kPlaneBytes + scol * 16], sreg[k]);
+        lds16_store(&xs[b][(4 * k + wave) * G::kRow + sp * G::kPlaneBytes + scol * 16], sreg[k]);
     };
     auto issue = [&](u32x4_t* w, int tr) {
       const int blk = moe_block(tr, ln.g);
@@ -1006,18 +1027,18 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
       }
     };
 
-    stage_load(0);
-    stage_store(0);
-    stage_load(1);
+    stage_load(0);  // chunk 0 first: waiting for it leaves the ring's loads in flight
+    ring_fence();
     issue_chunk(cs, 0);
     u32x4_t ring[D][R];
 #pragma unroll
-    for (int s = 0; s < D; ++s) {
-      issue(ring[s], s);
-      ring_fence();
-    }
+    for (int s = 0; s < D; ++s) issue(ring[s], s);
+    ring_fence();
+    stage_store(0);
+    stage_load(1);
     lds_barrier();
-    for (int c = 0; c < nchunk; ++c) {
+    int c = 0;  // nchunk >= 1: bottom-tested, so the ring issue stays in the prologue
+    do {
       const int t = c * D;
       const uint8_t* buf = xs[c & 1];
       issue_chunk(ns, t + D);
@@ -1032,17 +1053,15 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
       if (c + 1 < nchunk) stage_store((c + 1) & 1);
       stage_load(c + 2);
       lds_barrier();
-    }
+    } while (++c < nchunk);
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       if (tile0 + r >= rtiles) continue;
       const int n = (tile0 + r) * 16 + ln.c;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int m = moe_out_slot(ln.g, i);
-        if (m < cnt) y[(int64_t)unit_member(src, first + m) * H + n] = acc[r][i];
-      }
+      for (int i = 0; i < 4; ++i)
+        if (moe_out_slot(ln.g, i) < cnt) y[(int64_t)om[i] * H + n] = acc[r][i];
     }
   }
 }
