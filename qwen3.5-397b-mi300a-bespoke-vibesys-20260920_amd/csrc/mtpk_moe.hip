@@ -780,6 +780,22 @@ __device__ inline u32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<con
 
 __device__ inline void lds16_store(uint8_t* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
 
+// Byte g of each of four dwords, packed low to high: one 16-byte scale segment (four trips of
+// four lane groups) reduced to the four bytes one lane group uses. sel01 / selc come from
+// lane_byte_selectors(g).
+__device__ inline uint32_t pick_lane_bytes(u32x4_t d, uint32_t sel01, uint32_t selc) {
+  const uint32_t t01 = __builtin_amdgcn_perm(d[1], d[0], sel01);
+  const uint32_t t23 = __builtin_amdgcn_perm(d[3], d[2], sel01);
+  return __builtin_amdgcn_perm(t23, t01, selc);
+}
+
+// v_perm selectors: bytes {g of the low dword, g of the high dword, zero, zero}, then the
+// low two bytes of each half.
+__device__ inline uint32_t lane_byte_sel01(int g) {
+  return (uint32_t)g | ((uint32_t)(4 + g) << 8) | 0x0c0c0000u;
+}
+constexpr uint32_t kLaneByteSelC = 0x05040100u;
+
 // K elements of the activation rows staged per chunk, and the LDS bytes of one token row
 // (NPL planes, padded by 16 bytes so the 16 token rows fall on different banks).
 template <int KC, int NPL>
@@ -856,15 +872,27 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
       wg = buf16(rw, (og + kb) | bad);
       wu = buf16(rw, (ou + kb) | bad);
     };
-    ScaleChunk<D> cg, cu, ng, nu;
-    auto issue_chunk = [&](ScaleChunk<D>& a, ScaleChunk<D>& b, int tr) {
-      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
-      a.load(rs, (osg + 4u * (uint32_t)tr) | bad);
-      b.load(rs, (osu + 4u * (uint32_t)tr) | bad);
-    };
+    // Scales: the wave's 32 scale rows (16 gate rows, then the matching 16 up rows; nb bytes
+    // each) come in with full-line loads, pass through this wave's slice of the idle chunk
+    // buffer 1, and each lane keeps the bytes of its lane group packed per turn: sdg[T] byte s
+    // is the gate scale of trip 4T + s (K <= 4096: at most 8 turns).
+    const int segs = nb >> 4, units = 32 * segs;
+    u32x4_t sload4[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int idx = k * kWave + lane;
+      const int rr = idx / segs, sg = idx - rr * segs;
+      const uint32_t grow = rr < 16 ? (uint32_t)(nt * 16 + rr) : (uint32_t)(I + nt * 16 + rr - 16);
+      const uint32_t bad = (uint32_t)!(idx < units) << 31;
+      sload4[k] = buf16(rs, (grow * (uint32_t)nb + (uint32_t)sg * 16u) | bad);
+    }
+    ring_fence();
+    uint32_t sdg[8], sdu[8];
     f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
+    uint32_t cur_g = 0u, cur_u = 0u;  // this turn's packed scales (selected per chunk)
     auto consume = [&](const u32x4_t& wg, const u32x4_t& wu, int s, const uint8_t* buf) {
-      const float fg = e8m0_to_f32(cg.byte(s, ln.g)), fu = e8m0_to_f32(cu.byte(s, ln.g));
+      const float fg = e8m0_to_f32((cur_g >> (8 * s)) & 0xffu);
+      const float fu = e8m0_to_f32((cur_u >> (8 * s)) & 0xffu);
       const uint8_t* arow = buf + ln.c * G::kRow + ((4 * s + ln.g) * 32) * 2;
       u32x4_t a[4];
 #pragma unroll
@@ -881,21 +909,50 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
     // that waiting for chunk 0 leaves the whole ring in flight; chunk 1 loads behind them
     stage_load(0);
     ring_fence();
-    issue_chunk(cg, cu, 0);
     u32x4_t rg[D], ru[D];
 #pragma unroll
     for (int s = 0; s < D; ++s) issue(rg[s], ru[s], s);
     ring_fence();
+    {
+      uint8_t* scr = xs[1] + wave * (32 * nb);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int idx = k * kWave + lane;
+        if (idx < units) lds16_store(scr + idx * 16, sload4[k]);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave reads back only its own slice
+      const uint32_t sel01 = lane_byte_sel01(ln.g);
+#pragma unroll
+      for (int T = 0; T < 8; ++T) {
+        if (T < nchunk) {
+          sdg[T] = pick_lane_bytes(lds16(scr + ln.c * nb + 16 * T), sel01, kLaneByteSelC);
+          sdu[T] = pick_lane_bytes(lds16(scr + (16 + ln.c) * nb + 16 * T), sel01, kLaneByteSelC);
+        } else {
+          sdg[T] = 0u;
+          sdu[T] = 0u;
+        }
+      }
+    }
     stage_store(0);
     stage_load(1);
-    lds_barrier();
+    lds_barrier();  // also: every wave is done with its scale slice before chunk 1 lands
     // nchunk >= 1 (K is a positive multiple of KC): a bottom-tested loop keeps the ring
     // issue above in the prologue's block instead of letting it sink past the barrier
     int c = 0;
+#pragma clang loop unroll(disable)
     do {
       const int t = c * D;
       const uint8_t* buf = xs[c & 1];
-      issue_chunk(ng, nu, t + D);
+      // turn c's scales, by selects on the uniform c (indexing a register array by c would
+      // move it to scratch, and rotating it makes every entry loop-carried)
+      cur_g = sdg[0];
+      cur_u = sdu[0];
+#pragma unroll
+      for (int T = 1; T < 8; ++T)
+        if (c == T) {
+          cur_g = sdg[T];
+          cur_u = sdu[T];
+        }
       // trips are consumed and refilled in pairs: the two refills of a row are adjacent
       // 64-byte segments issued back to back
 #pragma unroll
@@ -907,8 +964,6 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
         issue(rg[s + 1], ru[s + 1], t + s + 1 + D);
         ring_fence();
       }
-      cg = ng;
-      cu = nu;
       if (c + 1 < nchunk) stage_store((c + 1) & 1);
       stage_load(c + 2);
       lds_barrier();
@@ -999,12 +1054,23 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
 #pragma unroll
       for (int r = 0; r < R; ++r) w[r] = buf16(rw, (ow[r] + (uint32_t)blk * 16u) | bad);
     };
-    ScaleChunk<D> cs[R], ns[R];
-    auto issue_chunk = [&](ScaleChunk<D>* cc, int tr) {
-      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
+    // Scales as in gate_up: the wave's R * 16 scale rows (nb bytes, K <= 1024) come in with
+    // full-line loads, pass through its slice of the idle chunk buffer 1, and each lane keeps
+    // its lane group's bytes packed per four trips: pd[r][Q] byte s is tile r's trip 4Q + s.
+    const int segs = nb >> 4, units = R * 16 * segs;
+    u32x4_t sld[2];
 #pragma unroll
-      for (int r = 0; r < R; ++r) cc[r].load(rs, (os[r] + 4u * (uint32_t)tr) | bad);
-    };
+    for (int k = 0; k < 2; ++k) {
+      const int idx = k * kWave + lane;
+      const int rr = idx / segs, sg = idx - rr * segs;
+      const uint32_t grow = (uint32_t)(min(tile0 + rr / 16, rtiles - 1) * 16 + (rr & 15));
+      const uint32_t bad = (uint32_t)!(idx < units) << 31;
+      sld[k] = buf16(rs, (grow * (uint32_t)nb + (uint32_t)sg * 16u) | bad);
+    }
+    ring_fence();
+    uint32_t pd[R][2];
+    uint32_t cur[R];
+    int csh = 0;  // bit offset of this chunk's first trip within the packed dword
     f32x4_t acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
@@ -1017,7 +1083,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
         for (int h = 0; h < 4; ++h) a[p][h] = lds16(arow + p * G::kPlaneBytes + 16 * h);
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float fs = e8m0_to_f32(cs[r].byte(s, ln.g));
+        const float fs = e8m0_to_f32((cur[r] >> (csh + 8 * s)) & 0xffu);
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const bf16x8_t b = decode8(w[r][h], fs);
@@ -1029,27 +1095,44 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
 
     stage_load(0);  // chunk 0 first: waiting for it leaves the ring's loads in flight
     ring_fence();
-    issue_chunk(cs, 0);
     u32x4_t ring[D][R];
 #pragma unroll
     for (int s = 0; s < D; ++s) issue(ring[s], s);
     ring_fence();
+    {
+      uint8_t* scr = xs[1] + wave * (R * 16 * nb);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int idx = k * kWave + lane;
+        if (idx < units) lds16_store(scr + idx * 16, sld[k]);
+      }
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave reads back only its own slice
+      const uint32_t sel01 = lane_byte_sel01(ln.g);
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int Q = 0; Q < 2; ++Q)
+          pd[r][Q] = Q < segs ? pick_lane_bytes(lds16(scr + (r * 16 + ln.c) * nb + 16 * Q), sel01, kLaneByteSelC)
+                              : 0u;
+    }
     stage_store(0);
     stage_load(1);
     lds_barrier();
     int c = 0;  // nchunk >= 1: bottom-tested, so the ring issue stays in the prologue
+#pragma clang loop unroll(disable)
     do {
       const int t = c * D;
       const uint8_t* buf = xs[c & 1];
-      issue_chunk(ns, t + D);
+      // this chunk's two trips are bytes 2 (c & 1) .. +1 of dword c >> 1 (selects, not indexing)
+#pragma unroll
+      for (int r = 0; r < R; ++r) cur[r] = (c >> 1) ? pd[r][1] : pd[r][0];
+      csh = 16 * (c & 1);
 #pragma unroll
       for (int s = 0; s < D; ++s) {
         consume(ring[s], s, buf);
         issue(ring[s], t + s + D);
         ring_fence();
       }
-#pragma unroll
-      for (int r = 0; r < R; ++r) cs[r] = ns[r];
       if (c + 1 < nchunk) stage_store((c + 1) & 1);
       stage_load(c + 2);
       lds_barrier();
@@ -1226,7 +1309,7 @@ int launch_gate_up(int xp, const uint16_t* x, int64_t x_plane, int K, const uint
                    const uint8_t* ws, int I, const UnitSrc& src, int64_t max_units, int top_k,
                    uint16_t* inter, int64_t inter_plane, hipStream_t st) {
   const bool split = max_units * (I >> 4) < (int64_t)device_cu_count() * 16;
-  if (xp == 1 && !split && K % 512 == 0)
+  if (xp == 1 && !split && K % 512 == 0 && K <= 4096)
     return launch_gate_up_lds(x, x_plane, K, wq, ws, I, src, max_units, top_k, inter, inter_plane,
                               st);
 #define MTPK_GU(XP_, OP_, SP_, D_)                                                           \
@@ -1453,7 +1536,7 @@ int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, 
   const int64_t ip = assignments * inter_dim;
   const UnitSrc src = unit_list(units, sorted, n_units, max_units);
   const bool sv = chunked_scales((int)inter_dim, 1, 2);
-  if (inter_planes == 2 && inter_dim % 256 == 0)
+  if (inter_planes == 2 && inter_dim % 512 == 0 && inter_dim <= 1024)
     return launch_down_lds(inter, ip, (int)inter_dim, down, down_scale, (int)hidden, src,
                            max_units, y, st);
   if (inter_planes == 2)
