@@ -10,7 +10,18 @@ Weights rotate over --layers distinct copies (3.4 GB each) so no step is served 
 D_live * 6,684,672 + 2 * M * 4096 * 2, where D_live counts experts with a nonzero-weight
 assignment (the reference's definition, bench_moe_bw.py:29, :76-77).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L]
+Two more legs are reported beside `value` in the same JSON line:
+- "accept" (config 4): greedy acceptance (argmax over [48, 4, 248320] bf16 target logits, then
+  the accept kernel with every rollback index) and sampling-mode acceptance at T = 0.7
+  (rejection sampling with the target and draft logits, then the same index kernel), as us per
+  call and GB/s over one read of the logits they take;
+- "mtp_round" (config 5): full speculative rounds on the reduced-depth real-dims model (3
+  DeltaNet + 1 gated GQA layer, MXFP4 MoE on every layer, 1 MTP layer; B = 48, k = 3, 8192
+  tokens of synthetic context per sequence), as ms per round and committed tok/s. The weights
+  are random, so the draft rarely agrees with the target and a round commits about one token
+  per lane.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-accept] [--no-mtp]
 Prints one JSON line.
 """
 
@@ -97,6 +108,8 @@ def main() -> int:
     ap.add_argument("--calibrate-copy", type=int, default=0, metavar="MIB",
                     help="also run a plain device copy of this many MiB (3 launches) so a PMC "
                          "profile can scale FETCH_SIZE/WRITE_SIZE by a known byte count")
+    ap.add_argument("--no-accept", action="store_true", help="skip the acceptance leg")
+    ap.add_argument("--no-mtp", action="store_true", help="skip the MTP-round leg")
     ap.add_argument("--workloads", default="M1,M32,M192",
                     help="comma list of M1, M32, M192; `value` is measured on M192 when listed, "
                          "else on the last one listed")
@@ -223,6 +236,11 @@ def main() -> int:
     cpu = None
     if not args.no_cpu and head == "M192":
         cpu = cpu_baseline(layers[0], ins[0], dls[0], args.cpu_seconds)
+    direct = runner.direct
+    del runner, ins, outs, layers
+    torch.cuda.empty_cache()
+    accept = None if args.no_accept else accept_bench(dev)
+    mtp_round = None if args.no_mtp else mtp_round_bench(dev)
 
     line = {
         "metric": METRIC,
@@ -247,22 +265,152 @@ def main() -> int:
         "gbs_graph": {k: round(v["gbs"], 1) for k, v in results.items()},
         "d_live": {k: round(v["d_live_mean"], 1) for k, v in results.items()},
         "roofline": {
-            "kernel": "k_moe_gate_up<1,2,4,4,true> (direct)" if runner.direct else "k_moe_gate_up_lds<4>",
+            "kernel": "k_moe_gate_up_single<1,2,true> (direct)" if direct else "k_moe_gate_up_lds<4>",
             "bound": "hbm",
             "achieved": round(gu_gbs, 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_GBS, 4),
-            "traffic": None if runner.direct else profiled_traffic("mtpk::k_moe_gate_up_lds<4>"),
+            "traffic": None if direct else profiled_traffic("mtpk::k_moe_gate_up_lds<4>"),
             "traffic_source": "profiles/moe_kernels_mi355x.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
                               "copy-calibrated)",
             "avg_us": round(gu_ms * 1e3, 2),
             "algorithmic_bytes": round(gu_bytes),
         },
         "cpu_baseline": cpu,
+        "accept": accept,
+        "mtp_round": mtp_round,
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def _time_calls(fn, reps):
+    import torch
+
+    for _ in range(3):
+        fn()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(reps):
+        fn()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e3 / reps  # us
+
+
+def accept_bench(dev, b=48, k=3, vocab=248320, temperature=0.7):
+    """Config 4: greedy and rejection-sampling acceptance with the round's rollback indices."""
+    import torch
+
+    import graph_mtp
+    import mtp
+
+    t = k + 1
+    g = torch.Generator(dev).manual_seed(44)
+    target = (torch.randn(b, t, vocab, device=dev, generator=g) * 3).to(torch.bfloat16)
+    draft = (target[:, :k].float() + torch.randn(b, k, vocab, device=dev, generator=g)).to(torch.bfloat16)
+    draft_tok = mtp.sample_rows(draft, temperature, torch.rand(b * k, device=dev, generator=g)).view(b, k)
+    u_acc = torch.rand(b, k, device=dev, generator=g)
+    u_smp = torch.rand(b, device=dev, generator=g)
+    active = torch.ones(b, dtype=torch.bool, device=dev)
+    pos = torch.full((b,), 8188, dtype=torch.long, device=dev)
+    budget = torch.full((b,), 1 << 20, dtype=torch.long, device=dev)
+    stops = torch.full((b, mtp.MAX_STOP_IDS), -1, dtype=torch.long, device=dev)
+    ws = graph_mtp.rejection_workspace(b, k, vocab, dev)
+
+    def greedy():
+        sa = mtp.argmax_rows(target)
+        return graph_mtp.greedy_accept(sa, draft_tok, active, pos, budget, stops, 3)
+
+    def rejection():
+        _, _, em, _ = graph_mtp.rejection_sample(target, draft, draft_tok, u_acc, u_smp, temperature,
+                                                 workspace=ws)
+        return graph_mtp.greedy_accept(em, draft_tok, active, pos, budget, stops, 3)
+
+    us_g = _time_calls(greedy, 50)
+    us_r = _time_calls(rejection, 50)
+    acc_g = float(greedy().accept_len.float().mean())
+    acc_r = float(rejection().accept_len.float().mean())
+    logit_bytes = b * t * vocab * 2
+    log(f"accept: greedy {us_g:.1f} us, rejection {us_r:.1f} us (T={temperature}), mean accept "
+        f"{acc_g:.2f} / {acc_r:.2f}")
+    return {
+        "workload": f"C4 acceptance, target/draft bf16 [{b}, {t}, {vocab}], T={temperature}",
+        "greedy_us": round(us_g, 2),
+        "greedy_gbs": round(logit_bytes / us_g / 1e3, 1),
+        "rejection_us": round(us_r, 2),
+        "rejection_gbs": round((logit_bytes + b * k * vocab * 2) / us_r / 1e3, 1),
+        "mean_accept_greedy": round(acc_g, 3),
+        "mean_accept_rejection": round(acc_r, 3),
+    }
+
+
+def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
+    """Config 5: speculative rounds (draft k steps, verify B*(k+1) rows, accept, commit)."""
+    import torch
+
+    import graph_mtp
+    import mtp
+    import verify_model as vm
+
+    t0 = time.perf_counter()
+    model = vm.Model(vm.verify_cfg(), dev, torch.bfloat16, lanes=b, max_seq=ctx + 64, seed=0,
+                     expert_mode="bytes", moe_rows=b * (k + 1))
+    mtp.attach(model, k=k, seed=1, expert_mode="bytes")
+    start = ctx - 32
+    for lane in range(b):
+        model.blocks.grow(lane, start)
+    g = torch.Generator(device=dev).manual_seed(3)
+    for ty, pool in zip(model.cfg.layer_types, model.pool):
+        if ty == vm.ATTN:
+            pool["k"].normal_(generator=g)
+            pool["v"].normal_(generator=g)
+        else:
+            pool["conv"].normal_(generator=g)
+            pool["rec"].normal_(0, 0.05, generator=g)
+    model.mtp.pool["k"].normal_(generator=g)
+    model.mtp.pool["v"].normal_(generator=g)
+    model.hidden_cache.normal_(generator=g)
+    runner = graph_mtp.MTPVerifyRunner(model, capacity=b)
+    toks = torch.randint(0, model.cfg.vocab, (b,), generator=torch.Generator().manual_seed(4)).tolist()
+    pos = [start] * b
+    torch.cuda.synchronize()
+    log(f"mtp round: model ready in {time.perf_counter() - t0:.1f}s, "
+        f"{torch.cuda.memory_allocated() / 1e9:.1f} GB allocated")
+
+    def one_round():
+        got = runner.speculative_decode(list(range(b)), toks, pos)
+        n = 0
+        for j, c in enumerate(got):
+            pos[j] += len(c)
+            toks[j] = c[-1]
+            n += len(c)
+        return n
+
+    for _ in range(2):
+        one_round()
+    torch.cuda.synchronize()
+    w0 = time.perf_counter()
+    committed = sum(one_round() for _ in range(rounds))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - w0
+    ms = wall * 1e3 / rounds
+    log(f"mtp round: {ms:.2f} ms/round, {committed / rounds:.1f} committed/round, "
+        f"{committed / wall:.0f} tok/s")
+    res = {
+        "workload": f"C5 reduced-depth verify: 3 DeltaNet + 1 gated GQA (32q/2kv, hd 256) + MTP layer, "
+                    f"MXFP4 MoE 512 x top-10 per layer, B={b}, k={k}, {ctx}-token paged context",
+        "ms_per_round": round(ms, 3),
+        "committed_per_round": round(committed / rounds, 2),
+        "accepted_tok_s": round(committed / wall, 1),
+        "rounds": rounds,
+        "weights": "random init (draft acceptance near zero)",
+    }
+    del runner, model
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(layer, inp, dl_full, budget_s):
