@@ -37,6 +37,12 @@ __device__ inline u32x4_t buf16(rsrc_t r, uint32_t off) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
 }
 
+// The same with a wave-uniform byte offset `soff` (an SGPR operand) added to the per-lane
+// `off`. Only `off` carries kOutOfRange; `soff` itself always stays inside the buffer.
+__device__ inline u32x4_t buf16(rsrc_t r, uint32_t off, uint32_t soff) {
+  return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
+}
+
 __device__ inline uint32_t buf1(rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
 }

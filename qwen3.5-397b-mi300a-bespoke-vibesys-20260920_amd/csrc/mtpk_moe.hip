@@ -984,168 +984,203 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
 
 // down, LDS variant (hi/lo intermediate planes, chunked scales). Item = (unit, 4 x R tiles of
 // 16 hidden rows), wave w takes tiles (4q + w) R .. + R. Chunks of 256 K = 2 trips = one turn
-// of the D = 2 ring; each chunk stages both planes.
-template <int R, int D>
+// of the D = 2 ring; each chunk stages both planes. Items are software-pipelined: while an item
+// runs its last two chunks, the workgroup already issues its next grid-stride item's scale
+// rows, first two activation chunks and first D ring trips, so an item starts with its loads
+// in flight instead of waiting a full memory latency with the ring drained.
+template <int R>
 __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
     const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
     const uint8_t* __restrict__ ws, int H, UnitSrc src, float* __restrict__ y) {
-  constexpr int KC = 256, TPC = KC / 128;
-  static_assert(D == TPC, "one ring turn per staged chunk");
+  constexpr int D = 2, KC = 256;
+  constexpr int kScr = R * 16 * 32;  // a wave's scale rows (K <= 1024: at most 32 bytes each)
   using G = StageGeom<KC, 2>;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][G::kBuf];
+  __shared__ __attribute__((aligned(16))) uint8_t sscr[kMoeWaves * kScr];
   const int rtiles = H >> 4;
   const int ngroup = (rtiles + kMoeWaves * R - 1) / (kMoeWaves * R);
   const int n_items = min(sload(src.n_units, 0), src.max_units) * ngroup;
   const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
-  const int nb = K >> 5, ntrip = nb >> 2, nchunk = K / KC;
-  const int64_t row_bytes = K >> 1;
+  const int nb = K >> 5, ntrip = nb >> 2, nchunk = K / KC;  // nchunk is even (K % 512 == 0)
+  const uint32_t row_bytes = (uint32_t)(K >> 1);
   const rsrc_t ra = make_rsrc(inter, (uint32_t)(2 * inter_plane * 2));
-  const uint32_t exp_bytes = (uint32_t)H * (uint32_t)row_bytes;
-  // staging: load k of a chunk moves 16 bytes of (token row 2k + wave / 2, plane wave & 1) at
-  // byte 16 * (lane & 31), lanes 32..63 taking the next row: every wave instruction reads two
-  // whole 512-byte plane segments (full 128-byte lines)
+  const uint32_t exp_bytes = (uint32_t)H * row_bytes;
+  const int segs = nb >> 4, nscale = R * 16 * segs;  // 16-byte scale pieces of a wave's rows
+  // Offsets split into a per-lane part (voffset) and a wave-uniform per-item part (soffset).
+  // Weights: lane (g, c) reads row c of each tile. Staging: load k of a chunk moves token row
+  // 4k + wave, plane (lane >= 32), 16-byte column lane & 31, so every wave instruction reads
+  // two whole 512-byte plane segments (full 128-byte lines).
+  const uint32_t vrow = (uint32_t)ln.c * row_bytes;
+  const int sp = lane >> 5, scol = lane & 31;
+  const uint32_t vst = (uint32_t)sp * (uint32_t)inter_plane * 2u + (uint32_t)scol * 16u;
+  uint8_t* const scr = sscr + wave * kScr;
+  const uint32_t sel01 = lane_byte_sel01(ln.g);
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
-    const int u = item / ngroup, q = item - u * ngroup;
-    const int e = sload(src.units, 3 * u), first = sload(src.units, 3 * u + 1);
-    const int cnt = sload(src.units, 3 * u + 2);
-    if (cnt == 0) continue;
-    int32_t om[4];  // output assignments of this lane's token slots, used after the K loop
+  // A work item: expert, first sorted assignment, count, this wave's first tile, and the
+  // staged token rows' byte offsets (-1: no such row). cnt == 0 marks "no item".
+  struct Item {
+    int e, first, cnt, tile0;
+    int tok[4];
+  };
+  auto fetch = [&](int it) {
+    Item m{0, 0, 0, 0, {-1, -1, -1, -1}};
+    if (it < n_items) {
+      const int u = it / ngroup, q = it - u * ngroup;
+      m.e = sload(src.units, 3 * u);
+      m.first = sload(src.units, 3 * u + 1);
+      m.cnt = sload(src.units, 3 * u + 2);
+      m.tile0 = (q * kMoeWaves + wave) * R;
+      if (m.cnt > 0) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) om[i] = src.sorted[first + min(moe_out_slot(ln.g, i), cnt - 1)];
-    const int eu = e;
-    const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
-    const rsrc_t rs = make_rsrc(ws + (int64_t)eu * H * nb, (uint32_t)(H * nb));
-    uint32_t ow[R], os[R];
-    const int tile0 = (q * kMoeWaves + wave) * R;
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int rt = min(tile0 + r, rtiles - 1);
-      const uint32_t row = (uint32_t)(rt * 16 + ln.c);
-      ow[r] = row * (uint32_t)row_bytes;
-      os[r] = row * (uint32_t)nb;
+        for (int k = 0; k < 4; ++k) {
+          const int r = 4 * k + wave;
+          const int a = sload(src.sorted, m.first + min(r, m.cnt - 1));
+          m.tok[k] = r < m.cnt ? a * K * 2 : -1;
+        }
+      }
     }
-    // thread slot of load k: segment index k * 256 + tid over (row, plane, 16-byte column)
-    const int sp = (tid >> 5) & 1, scol = tid & 31;
-    uint32_t sa[4];
+    return m;
+  };
+  auto tile_off = [&](int tile0, int r) { return (uint32_t)min(tile0 + r, rtiles - 1) * 16u * row_bytes; };
+  // one ring slot: tile r (first tile tile0) of trip tr of the expert at `w`; out of range
+  // (no memory access) when !live
+  auto load_w = [&](const uint8_t* w, int tile0, int r, int tr, bool live) {
+    const uint32_t off = (vrow + (uint32_t)moe_block(tr, ln.g) * 16u) | ((uint32_t)!live << 31);
+    return buf16(make_rsrc(w, exp_bytes), off, tile_off(tile0, r));
+  };
+  u32x4_t sreg[4];
+  auto stage_load = [&](const Item& m, int c) {
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
-      const int r = 4 * k + wave;
-      const int a = sload(src.sorted, first + min(r, cnt - 1));
-      sa[k] = r < cnt ? (uint32_t)a * (uint32_t)K * 2u + (uint32_t)sp * (uint32_t)inter_plane * 2u +
-                            (uint32_t)scol * 16u
-                      : kOutOfRange;
+      const int t = m.tok[k];
+      sreg[k] = buf16(ra, vst | ((uint32_t)(t < 0) << 31), (uint32_t)max(t, 0) + (uint32_t)c * (KC * 2));
     }
-    u32x4_t sreg[4];
-    auto stage_load = [&](int c) {
-      const uint32_t bad = (uint32_t)!(c < nchunk) << 31;
+  };
+  auto stage_store = [&](int b) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sreg[k] = buf16(ra, (sa[k] + (uint32_t)c * (KC * 2)) | bad);
-    };
-    auto stage_store = [&](int b) {
-#pragma unroll
-      for (int k = 0; k < 4; ++k)
-        lds16_store(&xs[b][(4 * k + wave) * G::kRow + sp * G::kPlaneBytes + scol * 16], sreg[k]);
-    };
-    auto issue = [&](u32x4_t* w, int tr) {
-      const int blk = moe_block(tr, ln.g);
-      const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
-#pragma unroll
-      for (int r = 0; r < R; ++r) w[r] = buf16(rw, (ow[r] + (uint32_t)blk * 16u) | bad);
-    };
-    // Scales as in gate_up: the wave's R * 16 scale rows (nb bytes, K <= 1024) come in with
-    // full-line loads, pass through its slice of the idle chunk buffer 1, and each lane keeps
-    // its lane group's bytes packed per four trips: pd[r][Q] byte s is tile r's trip 4Q + s.
-    const int segs = nb >> 4, units = R * 16 * segs;
-    u32x4_t sld[2];
+    for (int k = 0; k < 4; ++k)
+      lds16_store(&xs[b][(4 * k + wave) * G::kRow + sp * G::kPlaneBytes + scol * 16], sreg[k]);
+  };
+  // The wave's R * 16 scale rows (nb bytes each) come in with full-line loads, pass through
+  // the wave's own LDS scratch, and each lane keeps its lane group's bytes packed per four
+  // trips: pd[r][Q] byte s is tile r's trip 4Q + s.
+  u32x4_t sld[2];
+  auto scale_load = [&](const Item& m) {
+    const rsrc_t rs = make_rsrc(ws + (int64_t)m.e * H * nb, (uint32_t)(H * nb));
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int idx = k * kWave + lane;
       const int rr = idx / segs, sg = idx - rr * segs;
-      const uint32_t grow = (uint32_t)(min(tile0 + rr / 16, rtiles - 1) * 16 + (rr & 15));
-      const uint32_t bad = (uint32_t)!(idx < units) << 31;
-      sld[k] = buf16(rs, (grow * (uint32_t)nb + (uint32_t)sg * 16u) | bad);
+      const uint32_t grow = (uint32_t)(min(m.tile0 + rr / 16, rtiles - 1) * 16 + (rr & 15));
+      const bool live = m.cnt > 0 && idx < nscale;
+      sld[k] = buf16(rs, (grow * (uint32_t)nb + (uint32_t)sg * 16u) | ((uint32_t)!live << 31), 0u);
     }
-    ring_fence();
-    uint32_t pd[R][2];
-    uint32_t cur[R];
-    int csh = 0;  // bit offset of this chunk's first trip within the packed dword
+  };
+  uint32_t pd[R][2];
+  auto scale_unpack = [&]() {
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int idx = k * kWave + lane;
+      if (idx < nscale) lds16_store(scr + idx * 16, sld[k]);
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave reads back only its own slice
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int Q = 0; Q < 2; ++Q)
+        pd[r][Q] = Q < segs ? pick_lane_bytes(lds16(scr + (r * 16 + ln.c) * nb + 16 * Q), sel01, kLaneByteSelC)
+                            : 0u;
+  };
+
+  // Prologue of the workgroup's first item; every later item finds the same loads issued by
+  // its predecessor's last chunks. An item with cnt == 0 (none in a prep work list) only ever
+  // issues out-of-range loads and stores nothing.
+  u32x4_t ring[D][R];
+  Item cur = fetch(blockIdx.x);
+  scale_load(cur);
+  stage_load(cur, 0);  // chunk 0 before the ring: waiting for it leaves the ring in flight
+  ring_fence();
+#pragma unroll
+  for (int s = 0; s < D; ++s)
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+      ring[s][r] = load_w(wq + (int64_t)cur.e * exp_bytes, cur.tile0, r, s, cur.cnt > 0);
+  ring_fence();
+  stage_store(0);  // waits for chunk 0, hence for the scale rows issued before it
+  scale_unpack();
+  stage_load(cur, 1);
+  lds_barrier();
+
+  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+    const Item nxt = fetch(item + gridDim.x);
+    const bool pf = nxt.cnt > 0, live = cur.cnt > 0;
+    const uint8_t* const wc = wq + (int64_t)cur.e * exp_bytes;
+    const uint8_t* const wn = wq + (int64_t)nxt.e * exp_bytes;
+    int32_t om[4];  // output assignments of this lane's token slots, used after the K loop
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      om[i] = live ? src.sorted[cur.first + min(moe_out_slot(ln.g, i), cur.cnt - 1)] : 0;
+
     f32x4_t acc[R];
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[r] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-    auto consume = [&](const u32x4_t* w, int s, const uint8_t* buf) {
+    uint32_t cs[R];
+    int csh = 0;  // bit offset of this chunk's first trip within the packed dword
+    // trip s of the chunk, tile by tile; each tile's ring slot is refilled with trip tr (of the
+    // next item once tr runs past this one's) as soon as its MFMAs are issued
+    auto consume = [&](int s, const uint8_t* buf, int tr) {
       const uint8_t* arow = buf + ln.c * G::kRow + ((4 * s + ln.g) * 32) * 2;
       u32x4_t a[2][4];
 #pragma unroll
       for (int p = 0; p < 2; ++p)
 #pragma unroll
         for (int h = 0; h < 4; ++h) a[p][h] = lds16(arow + p * G::kPlaneBytes + 16 * h);
+      const bool nx = tr >= ntrip;  // uniform
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float fs = e8m0_to_f32((cur[r] >> (csh + 8 * s)) & 0xffu);
+        const float fs = e8m0_to_f32((cs[r] >> (csh + 8 * s)) & 0xffu);
+        bf16x8_t b[4];
+#pragma unroll
+        for (int h = 0; h < 4; ++h) b[h] = decode8(ring[s][r][h], fs);
+        ring[s][r] = load_w(nx ? wn : wc, nx ? nxt.tile0 : cur.tile0, r, nx ? tr - ntrip : tr, nx ? pf : live);
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
-          const bf16x8_t b = decode8(w[r][h], fs);
-          acc[r] = mfma16x16x32(as_bf16x8(a[0][h]), b, acc[r]);
-          acc[r] = mfma16x16x32(as_bf16x8(a[1][h]), b, acc[r]);
+          acc[r] = mfma16x16x32(as_bf16x8(a[0][h]), b[h], acc[r]);
+          acc[r] = mfma16x16x32(as_bf16x8(a[1][h]), b[h], acc[r]);
         }
+        ring_fence();
       }
     };
 
-    stage_load(0);  // chunk 0 first: waiting for it leaves the ring's loads in flight
-    ring_fence();
-    u32x4_t ring[D][R];
-#pragma unroll
-    for (int s = 0; s < D; ++s) issue(ring[s], s);
-    ring_fence();
-    {
-      uint8_t* scr = xs[1] + wave * (R * 16 * nb);
-#pragma unroll
-      for (int k = 0; k < 2; ++k) {
-        const int idx = k * kWave + lane;
-        if (idx < units) lds16_store(scr + idx * 16, sld[k]);
-      }
-      __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave reads back only its own slice
-      const uint32_t sel01 = lane_byte_sel01(ln.g);
-#pragma unroll
-      for (int r = 0; r < R; ++r)
-#pragma unroll
-        for (int Q = 0; Q < 2; ++Q)
-          pd[r][Q] = Q < segs ? pick_lane_bytes(lds16(scr + (r * 16 + ln.c) * nb + 16 * Q), sel01, kLaneByteSelC)
-                              : 0u;
-    }
-    stage_store(0);
-    stage_load(1);
-    lds_barrier();
-    int c = 0;  // nchunk >= 1: bottom-tested, so the ring issue stays in the prologue
+    int c = 0;  // nchunk >= 2: bottom-tested loop
 #pragma clang loop unroll(disable)
     do {
-      const int t = c * D;
       const uint8_t* buf = xs[c & 1];
       // this chunk's two trips are bytes 2 (c & 1) .. +1 of dword c >> 1 (selects, not indexing)
 #pragma unroll
-      for (int r = 0; r < R; ++r) cur[r] = (c >> 1) ? pd[r][1] : pd[r][0];
+      for (int r = 0; r < R; ++r) cs[r] = (c >> 1) ? pd[r][1] : pd[r][0];
       csh = 16 * (c & 1);
 #pragma unroll
-      for (int s = 0; s < D; ++s) {
-        consume(ring[s], s, buf);
-        issue(ring[s], t + s + D);
-        ring_fence();
-      }
-      if (c + 1 < nchunk) stage_store((c + 1) & 1);
-      stage_load(c + 2);
+      for (int s = 0; s < D; ++s) consume(s, buf, c * D + s + D);
+      // buffer (c + 1) & 1 was last read in chunk c - 1; past the last chunk it takes the next
+      // item's chunk 0 (nchunk is even)
+      stage_store((c + 1) & 1);
+      if (c + 2 == nchunk) scale_load(nxt);
+      stage_load(c + 2 < nchunk ? cur : nxt, c + 2 < nchunk ? c + 2 : c + 2 - nchunk);
       lds_barrier();
     } while (++c < nchunk);
+    scale_unpack();  // the next item's scale rows, issued two chunks ago
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {
-      if (tile0 + r >= rtiles) continue;
-      const int n = (tile0 + r) * 16 + ln.c;
+      if (cur.tile0 + r >= rtiles) continue;
+      const int n = (cur.tile0 + r) * 16 + ln.c;
 #pragma unroll
       for (int i = 0; i < 4; ++i)
-        if (moe_out_slot(ln.g, i) < cnt) y[(int64_t)om[i] * H + n] = acc[r][i];
+        if (moe_out_slot(ln.g, i) < cur.cnt) y[(int64_t)om[i] * H + n] = acc[r][i];
     }
+    cur = nxt;
   }
 }
 
@@ -1342,7 +1377,7 @@ int launch_down_lds(const uint16_t* inter, int64_t inter_plane, int K, const uin
                     hipStream_t st) {
   static int occ = 0;
   constexpr int R = 4;
-  auto kern = k_moe_down_lds<R, 2>;
+  auto kern = k_moe_down_lds<R>;
   const int64_t items = max_units * (((H >> 4) + kMoeWaves * R - 1) / (kMoeWaves * R));
   const int grid = grid_for(kern, items, occ);
   if (grid == 0) return 0;
@@ -1536,7 +1571,8 @@ int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, 
   const int64_t ip = assignments * inter_dim;
   const UnitSrc src = unit_list(units, sorted, n_units, max_units);
   const bool sv = chunked_scales((int)inter_dim, 1, 2);
-  if (inter_planes == 2 && inter_dim % 512 == 0 && inter_dim <= 1024)
+  // the LDS kernel marks absent staging rows with an offset >= 2^31 (past the whole inter buffer)
+  if (inter_planes == 2 && inter_dim % 512 == 0 && inter_dim <= 1024 && ip * 4 < (int64_t(1) << 31))
     return launch_down_lds(inter, ip, (int)inter_dim, down, down_scale, (int)hidden, src,
                            max_units, y, st);
   if (inter_planes == 2)

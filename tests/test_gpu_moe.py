@@ -59,6 +59,42 @@ def test_small_bf16_matches_oracle(dev, tokens, experts, hidden, inter, top_k):
     assert moe_ref.rel_l2(got.float().cpu().numpy(), want) <= 2e-3
 
 
+# Many assignments per expert: hot experts span several 16-token work units (each unit
+# streams the expert's weights for its own rows), on the LDS kernels (bf16 x, K and inter
+# multiples of 512) and the register kernels (fp32 x, other widths). Zipf routing puts unit
+# counts of 1..8 in one launch, with ragged last units.
+MANY = [
+    (128, 8, 256, 96, 6, "zipf", np.float32),
+    (160, 40, 256, 64, 4, "zipf", np.float32),
+    (96, 12, 512, 512, 8, "uniform", "bf16"),
+    (160, 40, 512, 512, 4, "zipf", "bf16"),
+    (64, 24, 1024, 1024, 10, "zipf", "bf16"),
+]
+
+
+@pytest.mark.parametrize("tokens,experts,hidden,inter,top_k,routing,x_dtype", MANY)
+def test_many_units_per_expert_match_oracle(dev, tokens, experts, hidden, inter, top_k, routing, x_dtype):
+    ex = random_experts(experts, hidden, inter, seed=tokens + experts)
+    if routing == "zipf":
+        a_e, a_w = zipf_routing(tokens, experts, top_k, seed=experts, zero_frac=0.05)
+    else:
+        a_e, a_w = random_routing(tokens, experts, top_k, seed=experts)
+    x = np.random.default_rng(tokens).standard_normal((tokens, hidden)).astype(np.float32)
+    if x_dtype == "bf16":
+        x = bf16_round(x)
+        xt = torch.from_numpy(x).to(dev, torch.bfloat16)
+    else:
+        xt = torch.from_numpy(x).to(dev)
+    want = moe_ref.reference_moe(x, ex, a_e, a_w, top_k, (0, experts))
+    got = run(xt, to_dev(ex, dev), a_e, a_w, top_k, (0, experts), dev).float().cpu().numpy()
+    if x_dtype == "bf16":
+        assert moe_ref.rel_l2(got, bf16_round(want)) <= 2e-3
+    else:
+        assert moe_ref.relative_error(got, want) < 1e-5
+    zero_tok = (a_w.reshape(tokens, top_k) == 0).all(1)
+    assert not got[zero_tok].any()
+
+
 @pytest.mark.parametrize("tokens,experts,hidden,inter,top_k", SMALL)
 def test_drops_unowned_experts_and_shards_sum(dev, tokens, experts, hidden, inter, top_k):
     ex = random_experts(experts, hidden, inter, seed=7)
