@@ -215,6 +215,26 @@ int mtpk_sample_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
                      const float* u, void* workspace, int64_t workspace_bytes, int64_t* token,
                      void* stream);
 
+/* ---------------------------------------------------------------- Gated DeltaNet recurrence
+ * Gated delta-rule steps over a pool of fp32 recurrent states, replacing
+ * `deltanet_fused.delta_rule_verify_exact` (deltanet_fused.py:1090-1176, kernel :274-398) in the
+ * verify forward (`deltanet_verify_static`, graph_mtp.py:227-344) and the accepted-prefix replay
+ * (`deltanet_verify_rollback_static`, graph_mtp.py:347-437). Per step, for row j and head h:
+ *   S <- exp(g) S;  S <- S + k ((v - S^T k) beta)^T;  out = S^T q
+ * state f32 [slots_total, heads, k_dim = 128, v_dim] contiguous; row j uses state slot slot[j]
+ * (int64 [rows], NULL: slot j); rows must name distinct slots. q, k f32 [rows, t, qk_heads, 128]
+ * (q and k already l2-normalised, q scaled), head h reads q/k head h / (heads / qk_heads);
+ * v f32 [rows, t, heads, v_dim]; g (log decay) and beta f32 [rows, t, heads]; all contiguous.
+ * lengths == NULL (verify): t steps from the stored state, which is not written; out
+ * f32 [rows, t, heads, v_dim] receives every step's output. lengths int64 [rows] (commit): row j
+ * advances its slot in place by min(max(lengths[j], 0), t) steps; out may be NULL.
+ * t >= 1 (steps run in order; prefill of a prompt is one call with t = its length),
+ * k_dim 16, 32, 64 or 128, 1 <= v_dim <= 4096. */
+int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int64_t rows, int64_t t,
+                    int64_t heads, int64_t qk_heads, int64_t k_dim, int64_t v_dim, const float* q,
+                    const float* k, const float* v, const float* g, const float* beta,
+                    const int64_t* lengths, float* out, void* stream);
+
 /* ---------------------------------------------------------------- test probes
  * In-bounds probe of the compiler builtin this library's MoE relies on: one wave computes
  * d = A(16x32) * B(32x16) with v_mfma_f32_16x16x32_bf16 from per-lane operand registers

@@ -31,6 +31,7 @@ from dataclasses import dataclass, field
 import torch
 import torch.nn.functional as F
 
+import deltanet
 import mxfp4
 import mxfp4_gemv
 import router_fused
@@ -350,8 +351,8 @@ class DeltaNetRows:
     conv inputs and the per-row recurrence inputs, `[B, t, ...]`."""
 
     raw_qkv: torch.Tensor  # [B, conv_dim, t], model dtype
-    q: torch.Tensor  # [B, t, v_heads, k_dim] fp32, normalised and scaled
-    k: torch.Tensor  # [B, t, v_heads, k_dim] fp32, normalised
+    q: torch.Tensor  # [B, t, k_heads, k_dim] fp32, normalised and scaled
+    k: torch.Tensor  # [B, t, k_heads, k_dim] fp32, normalised
     v: torch.Tensor  # [B, t, v_heads, v_dim] fp32
     g: torch.Tensor  # [B, t, v_heads] fp32
     beta: torch.Tensor  # [B, t, v_heads] fp32
@@ -484,17 +485,21 @@ class Model:
         q = mixed[..., :kd].reshape(b, t, c.k_heads, c.k_dim).float()
         k = mixed[..., kd : 2 * kd].reshape(b, t, c.k_heads, c.k_dim).float()
         v = mixed[..., 2 * kd :].reshape(b, t, c.v_heads, c.v_dim).float()
-        rep = c.v_heads // c.k_heads
-        q = (l2norm(q) * c.k_dim ** -0.5).repeat_interleave(rep, dim=2)
-        k = l2norm(k).repeat_interleave(rep, dim=2)
+        q = l2norm(q) * c.k_dim ** -0.5  # [B, t, k_heads, k_dim]; v head h reads k head h // rep
+        k = l2norm(k)
         beta = torch.sigmoid(b_raw.float())
         g = -w["A_log"].float().exp() * F.softplus(a_raw.float() + w["dt_bias"].float())
-        state = pool["rec"][lanes]
-        outs = []
-        for s in range(t):
-            state, o = delta_rule_step(state, q[:, s], k[:, s], v[:, s], g[:, s], beta[:, s])
-            outs.append(o)
-        out = torch.stack(outs, dim=1)  # [B, t, vh, vd] fp32
+        if h.device.type == "cuda":
+            out = deltanet.delta_rule(pool["rec"], lanes, q, k, v, g, beta)  # [B, t, vh, vd] fp32
+        else:
+            rep = c.v_heads // c.k_heads
+            qe, ke = q.repeat_interleave(rep, dim=2), k.repeat_interleave(rep, dim=2)
+            state = pool["rec"][lanes]
+            outs = []
+            for s in range(t):
+                state, o = delta_rule_step(state, qe[:, s], ke[:, s], v[:, s], g[:, s], beta[:, s])
+                outs.append(o)
+            out = torch.stack(outs, dim=1)  # [B, t, vh, vd] fp32
         normed = gated_rmsnorm(out, z.reshape(b, t, c.v_heads, c.v_dim), w["dn_norm"], c.eps, h.dtype)
         mixer = F.linear(normed.reshape(b, t, -1), w["out_proj"])
         return mixer, DeltaNetRows(raw.contiguous(), q, k, v, g, beta)
@@ -515,9 +520,15 @@ class Model:
         else:
             idx = (n[:, None] + torch.arange(k1, device=self.device)[None, :]).clamp(max=k1 + t - 1)
         pool["conv"][lanes] = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
+        if self.device.type == "cuda":
+            deltanet.delta_rule(pool["rec"], lanes, rows.q, rows.k, rows.v, rows.g, rows.beta, n,
+                                want_out=False)
+            return
+        rep = c.v_heads // c.k_heads
+        qe, ke = rows.q.repeat_interleave(rep, dim=2), rows.k.repeat_interleave(rep, dim=2)
         state = pool["rec"][lanes]
         for s in range(t):
-            nxt, _ = delta_rule_step(state, rows.q[:, s], rows.k[:, s], rows.v[:, s], rows.g[:, s], rows.beta[:, s])
+            nxt, _ = delta_rule_step(state, qe[:, s], ke[:, s], rows.v[:, s], rows.g[:, s], rows.beta[:, s])
             state = torch.where((s < n)[:, None, None, None], nxt, state)
         pool["rec"][lanes] = state
 

@@ -68,3 +68,14 @@ def test_rejected_arguments_launch_nothing(lib):
     assert lib.mtpk_sample_rows(fake, 1, 4, 100, -1.0, fake, fake, 1 << 30, fake, None) == -1
     assert lib.mtpk_rejection_workspace_bytes(48, 3, 248320) >= 48 * 7 * 61 * 8
     assert lib.mtpk_sample_workspace_bytes(4, 100) == lib.mtpk_rejection_workspace_bytes(4, 0, 100)
+    # gated delta rule: null state, unsupported k_dim, t out of range, neither output nor commit
+    assert lib.mtpk_delta_rule(None, 4, None, 2, 2, 4, 2, 16, 16, fake, fake, fake, fake, fake,
+                               None, fake, None) == -1
+    assert lib.mtpk_delta_rule(fake, 4, None, 2, 2, 4, 2, 48, 16, fake, fake, fake, fake, fake,
+                               None, fake, None) == -1
+    assert lib.mtpk_delta_rule(fake, 4, None, 2, 0, 4, 2, 16, 16, fake, fake, fake, fake, fake,
+                               None, fake, None) == -1
+    assert lib.mtpk_delta_rule(fake, 4, None, 2, 2, 4, 2, 16, 16, fake, fake, fake, fake, fake,
+                               None, None, None) == -1
+    assert lib.mtpk_delta_rule(fake, 1, None, 2, 2, 4, 2, 16, 16, fake, fake, fake, fake, fake,
+                               None, fake, None) == -1  # 2 rows, 1 slot, no slot map

@@ -1,0 +1,116 @@
+"""The HIP gated delta rule (`deltanet.delta_rule` -> `mtpk_delta_rule`) against the float64
+oracle (`oracle/deltanet_ref.py`): verify mode (every step's output, the state pool left
+bit-identical) and commit mode (each row's slot advanced in place by its accepted prefix,
+other slots untouched), at config 1's and config 5's head dimensions. fp32 kernel vs float64
+oracle: rtol 1e-4 / atol 1e-5 on outputs and states (t <= 4 steps of 16..128-term dots)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import deltanet
+from oracle import deltanet_ref as dn
+
+pytestmark = pytest.mark.gpu
+
+RTOL, ATOL = 1e-4, 1e-5
+
+
+def _case(seed, slots_total, heads, qk_heads, dk, dv, b, t):
+    rng = np.random.default_rng(seed)
+    pool = (rng.standard_normal((slots_total, heads, dk, dv)) * 0.1).astype(np.float32)
+    q = rng.standard_normal((b, t, qk_heads, dk)).astype(np.float32)
+    q /= np.linalg.norm(q, axis=-1, keepdims=True) * np.sqrt(dk)
+    k = rng.standard_normal((b, t, qk_heads, dk)).astype(np.float32)
+    k /= np.linalg.norm(k, axis=-1, keepdims=True)
+    v = rng.standard_normal((b, t, heads, dv)).astype(np.float32)
+    g = (-rng.random((b, t, heads)) * 0.5).astype(np.float32)
+    beta = rng.random((b, t, heads)).astype(np.float32)
+    slots = rng.permutation(slots_total)[:b]
+    return pool, slots, q, k, v, g, beta
+
+
+def _dev(dev, *arrays):
+    return [torch.from_numpy(np.ascontiguousarray(a)).to(dev) for a in arrays]
+
+
+SHAPES = [
+    # slots_total, heads, qk_heads, dk, dv, rows, t
+    (5, 4, 2, 16, 16, 3, 4),  # config 1's DeltaNet heads
+    (6, 3, 3, 32, 96, 4, 2),  # ragged dv (lanes past dv idle)
+    (4, 2, 1, 64, 64, 2, 1),
+    (9, 8, 2, 128, 128, 6, 3),  # config 5's head dims
+]
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_verify_outputs_and_state_untouched(dev, shape) -> None:
+    pool, slots, q, k, v, g, beta = _case(sum(shape), *shape)
+    want_pool, want = dn.delta_rule_rows(pool, slots, q, k, v, g, beta)
+    tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, slots.astype(np.int64), q, k, v, g, beta)
+    out = deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb)
+    np.testing.assert_allclose(out.cpu().numpy(), want, rtol=RTOL, atol=ATOL)
+    assert torch.equal(tp.cpu(), torch.from_numpy(pool))
+
+
+@pytest.mark.parametrize("shape", SHAPES)
+def test_commit_advances_each_slot_by_its_prefix(dev, shape) -> None:
+    pool, slots, q, k, v, g, beta = _case(100 + sum(shape), *shape)
+    b, t = q.shape[:2]
+    lengths = np.arange(b) % (t + 2) - (1 if b > 2 else 0)  # includes -1 (clamped to 0) and > t
+    want_pool, _ = dn.delta_rule_rows(pool, slots, q, k, v, g, beta, lengths)
+    tp, ts, tq, tk, tv, tg, tb, tl = _dev(dev, pool, slots.astype(np.int64), q, k, v, g, beta,
+                                          lengths.astype(np.int64))
+    assert deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb, tl, want_out=False) is None
+    got = tp.cpu().numpy()
+    np.testing.assert_allclose(got, want_pool, rtol=RTOL, atol=ATOL)
+    for sl in range(pool.shape[0]):
+        j = np.nonzero(slots == sl)[0]
+        if len(j) == 0 or min(max(lengths[j[0]], 0), t) == 0:
+            np.testing.assert_array_equal(got[sl], pool[sl])  # bit-identical: not advanced
+
+
+def test_commit_then_verify_equals_longer_verify(dev) -> None:
+    """Committing n steps and verifying the rest from the new state gives the outputs of one
+    verify over all steps (the round's split into verify + commit is exact in structure)."""
+    pool, slots, q, k, v, g, beta = _case(7, 4, 4, 2, 128, 128, 3, 4)
+    tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, slots.astype(np.int64), q, k, v, g, beta)
+    full = deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb).cpu().numpy()
+    n = 2
+    lengths = torch.full((3,), n, dtype=torch.int64, device=dev)
+    deltanet.delta_rule(tp, ts, tq[:, :n].contiguous(), tk[:, :n].contiguous(), tv[:, :n].contiguous(),
+                        tg[:, :n].contiguous(), tb[:, :n].contiguous(), lengths, want_out=False)
+    rest = deltanet.delta_rule(tp, ts, tq[:, n:].contiguous(), tk[:, n:].contiguous(),
+                               tv[:, n:].contiguous(), tg[:, n:].contiguous(), tb[:, n:].contiguous())
+    np.testing.assert_allclose(rest.cpu().numpy(), full[:, n:], rtol=RTOL, atol=ATOL)
+
+
+def test_config5_batch_matches_oracle(dev) -> None:
+    """Config 5: 48 rows x 64 heads of 128 x 128 over a 48-slot pool, t = 4 (2 rows checked
+    against the oracle in full, every row's commit against the verify pass's own steps)."""
+    pool, slots, q, k, v, g, beta = _case(11, 48, 64, 16, 128, 128, 48, 4)
+    tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, slots.astype(np.int64), q, k, v, g, beta)
+    out = deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb).cpu().numpy()
+    pick = [0, 47]
+    _, want = dn.delta_rule_rows(pool, slots[pick], q[pick], k[pick], v[pick], g[pick], beta[pick])
+    np.testing.assert_allclose(out[pick], want, rtol=RTOL, atol=ATOL)
+    lengths = torch.from_numpy(np.arange(48) % 5).to(dev)
+    deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb, lengths, want_out=False)
+    again = deltanet.delta_rule(tp, ts, tq[:, :1].contiguous(), tk[:, :1].contiguous(),
+                                tv[:, :1].contiguous(), tg[:, :1].contiguous(), tb[:, :1].contiguous())
+    assert torch.isfinite(again).all()
+
+
+def test_rejects_bad_shapes(dev) -> None:
+    pool, slots, q, k, v, g, beta = _case(3, 4, 2, 1, 16, 16, 2, 2)
+    tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, slots.astype(np.int64), q, k, v, g, beta)
+    with pytest.raises(ValueError):
+        deltanet.delta_rule(tp, ts, tq[..., :8].contiguous(), tk[..., :8].contiguous(), tv, tg, tb)
+    with pytest.raises(ValueError):
+        deltanet.delta_rule(tp, ts, tq, tk, tv[:, :1].contiguous(), tg, tb)
+    with pytest.raises(ValueError):
+        deltanet.delta_rule(tp, ts[:1], tq, tk, tv, tg, tb)
+    with pytest.raises(ValueError):
+        deltanet.delta_rule(tp.double(), ts, tq, tk, tv, tg, tb)
