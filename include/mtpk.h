@@ -235,6 +235,27 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
                     const float* k, const float* v, const float* g, const float* beta,
                     const int64_t* lengths, float* out, void* stream);
 
+/* ---------------------------------------------------------------- paged verify attention
+ * Causal GQA attention of t query rows per lane over a paged bf16 KV cache, replacing
+ * `verify_attention_paged` (model.py:1120-1205; per row `paged_attn.decode_attention_paged`,
+ * paged_attn.py) in the verify forward and the MTP layer's attention (`mtp._attn_rows`,
+ * mtp.py:233-279, t = 1). q bf16 [batch, heads, t, head_dim] contiguous; k_pool, v_pool bf16
+ * [pool_rows, kv_heads, head_dim] contiguous, 16-row blocks; block_table int32
+ * [batch, table_stride]: lane b's position p is pool row block_table[b][p / 16] * 16 + p % 16;
+ * base_pos int64 [batch]: query row s of lane b is at base_pos[b] + s and attends to positions
+ * 0 .. base_pos[b] + s (q head h uses kv head h / (heads / kv_heads)). out bf16, q's shape.
+ * head_dim 64, 128 or 256. fp32 scores and softmax, bf16 probabilities into the PV product.
+ * n_split key splits per (lane, kv head) (mtpk_attention_splits picks one from a host bound on
+ * the context); n_split > 1 needs mtpk_attention_workspace_bytes of workspace. */
+int mtpk_attention_splits(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads, int64_t max_ctx);
+int64_t mtpk_attention_workspace_bytes(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads,
+                                       int64_t head_dim, int n_split);
+int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t heads,
+                         int64_t kv_heads, int64_t head_dim, const uint16_t* k_pool,
+                         const uint16_t* v_pool, int64_t pool_rows, const int32_t* block_table,
+                         int64_t table_stride, const int64_t* base_pos, float scale, int n_split,
+                         void* workspace, int64_t workspace_bytes, uint16_t* out, void* stream);
+
 /* ---------------------------------------------------------------- test probes
  * In-bounds probe of the compiler builtin this library's MoE relies on: one wave computes
  * d = A(16x32) * B(32x16) with v_mfma_f32_16x16x32_bf16 from per-lane operand registers

@@ -101,6 +101,13 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
+    "mtpk_attention_splits": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "mtpk_attention_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int]),
+    "mtpk_paged_attention": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
+         c_int64, c_void_p, ctypes.c_float, c_int, c_void_p, c_int64, c_void_p, c_void_p],
+    ),
 }
 
 EXPORTED = tuple(_SIGNATURES)

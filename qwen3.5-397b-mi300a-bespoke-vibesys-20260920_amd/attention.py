@@ -1,0 +1,65 @@
+"""Paged causal GQA attention of the verify rows on the device, through
+`mtpk_paged_attention` (include/mtpk.h): the role of `verify_attention_paged`
+(`model.py:1120-1205`) and, at t = 1, of the MTP draft step's attention (`mtp.py:233-279`).
+
+q bf16 `[B, heads, t, hd]`; K/V pools bf16 `[pool_rows, kv_heads, hd]` of 16-row blocks;
+`block_table` int32 `[B, blocks]` (the lanes' own tables); `base_pos` int64 `[B]`: query row s
+of lane b sits at `base_pos[b] + s` and sees every cached position up to its own. The output is
+bf16 `[B, heads, t, hd]`.
+"""
+
+from __future__ import annotations
+
+import torch
+
+import _mtpk
+
+BLOCK = 16
+HEAD_DIMS = (64, 128, 256)
+
+
+def supported(q: torch.Tensor, block_size: int) -> bool:
+    """Shapes the kernel takes: bf16 device tensors, 16-row blocks, head_dim 64/128/256."""
+    return q.device.type == "cuda" and q.dtype == torch.bfloat16 and block_size == BLOCK and \
+        q.shape[-1] in HEAD_DIMS
+
+
+def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                    block_table: torch.Tensor, base_pos: torch.Tensor, ctx_len: int,
+                    scale: float) -> torch.Tensor:
+    """`ctx_len` is a host bound on `max(base_pos) + t`; it only sizes the key splits."""
+    device = _mtpk.require_device(q, k_pool, v_pool, block_table, base_pos)
+    if q.dim() != 4 or q.dtype != torch.bfloat16:
+        raise ValueError(f"q must be bf16 [B, heads, t, hd], got {q.dtype} {tuple(q.shape)}")
+    b, heads, t, hd = q.shape
+    if k_pool.dim() != 3 or k_pool.shape != v_pool.shape or k_pool.shape[2] != hd:
+        raise ValueError(f"pools must be [rows, kv_heads, {hd}], got {tuple(k_pool.shape)}/{tuple(v_pool.shape)}")
+    if k_pool.dtype != torch.bfloat16 or v_pool.dtype != torch.bfloat16:
+        raise ValueError("pools must be bf16")
+    if not (k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous")
+    kvh = k_pool.shape[1]
+    if heads % kvh:
+        raise ValueError(f"{heads} q heads are not a multiple of {kvh} kv heads")
+    if block_table.dim() != 2 or block_table.shape[0] != b:
+        raise ValueError(f"block_table must be [{b}, blocks], got {tuple(block_table.shape)}")
+    if tuple(base_pos.shape) != (b,):
+        raise ValueError(f"base_pos must be [{b}], got {tuple(base_pos.shape)}")
+    if int(ctx_len) > block_table.shape[1] * BLOCK:
+        raise ValueError(f"context bound {ctx_len} exceeds the table's {block_table.shape[1]} blocks")
+    q = q.contiguous()
+    table = block_table.to(torch.int32).contiguous()
+    pos = base_pos.to(torch.int64).contiguous()
+    lib = _mtpk.lib()
+    n_split = int(lib.mtpk_attention_splits(b, t, heads, kvh, max(int(ctx_len), 1)))
+    ws_bytes = int(lib.mtpk_attention_workspace_bytes(b, t, heads, kvh, hd, n_split))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    out = torch.empty_like(q)
+    _mtpk.check(
+        lib.mtpk_paged_attention(q.data_ptr(), b, t, heads, kvh, hd, k_pool.data_ptr(), v_pool.data_ptr(),
+                                 k_pool.shape[0], table.data_ptr(), table.shape[1], pos.data_ptr(),
+                                 float(scale), n_split, ws.data_ptr(), ws_bytes, out.data_ptr(),
+                                 _mtpk.stream_of(device)),
+        "mtpk_paged_attention",
+    )
+    return out

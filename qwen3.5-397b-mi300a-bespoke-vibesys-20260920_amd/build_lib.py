@@ -19,7 +19,7 @@ LIB = HERE / "libmtpk.so"
 OBJ_DIR = HERE / "_build"
 ARCH = os.environ.get("MTPK_ARCH", "gfx950")
 SOURCES = ["mtpk_runtime.hip", "mtpk_moe.hip", "mtpk_router.hip", "mtpk_accept.hip", "mtpk_deltanet.hip",
-           "mtpk_rejection.hip"]
+           "mtpk_rejection.hip", "mtpk_attention.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",
@@ -53,7 +53,7 @@ def _compile(src: str) -> Path:
 
 def build(verbose: bool = False) -> Path:
     OBJ_DIR.mkdir(exist_ok=True)
-    with ThreadPoolExecutor(max_workers=min(6, len(SOURCES))) as pool:
+    with ThreadPoolExecutor(max_workers=min(7, len(SOURCES))) as pool:
         objs = list(pool.map(_compile, SOURCES))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *map(str, objs), "-o", str(tmp)]

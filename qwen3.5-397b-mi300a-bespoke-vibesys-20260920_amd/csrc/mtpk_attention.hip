@@ -1,0 +1,349 @@
+// Causal GQA attention of the verify rows over the paged bf16 KV cache (`verify_attention_paged`,
+// model.py:1120-1205, which runs `paged_attn.decode_attention_paged` per verify row; the MTP
+// layer's draft step `mtp._attn_rows`, mtp.py:233-279, is the same call with t = 1).
+//
+// Shapes: q bf16 [B, heads, t, hd]; K and V pools bf16 [pool_rows, kv_heads, hd] with 16-row
+// blocks; lane b's key position p lives in pool row table[b][p / 16] * 16 + p % 16. Query row s
+// of lane b sits at position base_pos[b] + s and sees keys 0 .. base_pos[b] + s.
+//
+// One workgroup takes one (lane, kv head, group of up to 64 query rows, key split). The query
+// rows of a kv head (group = heads / kv_heads q heads x t steps) share every key, so K and V are
+// read from HBM once per (lane, kv head, split) and staged in LDS in tiles of 32 keys: K as
+// [key][d], V transposed to [d][key] so that both MFMA B operands are 16-byte LDS reads. Each
+// wave owns 16 query rows:
+//   S = Q K^T   v_mfma_f32_16x16x32_bf16, A = Q (registers, loaded once), B = K tile
+//   online softmax over the row's keys (base-2, running max m and sum l per row)
+//   O += P V    A = P (bf16, re-laid out through a per-wave LDS patch), B = V tile
+// With n_split > 1 every workgroup writes its unnormalised O with (m, l) per row and a second
+// kernel merges the splits; with one split the workgroup writes the bf16 output directly.
+
+#include "mtpk_device.h"
+#include "mtpk_host.h"
+
+namespace mtpk {
+
+constexpr int kAttnWaves = 4;
+constexpr int kAttnThreads = kAttnWaves * kWave;
+constexpr int kAttnRows = 16 * kAttnWaves;  // query rows per workgroup
+constexpr int kAttnKeys = 32;               // keys per staged tile
+constexpr int kAttnBlock = 16;              // KV cache block size
+
+template <int HD>
+struct AttnGeom {
+  static constexpr int kDs = HD / 32;                     // d steps of the QK^T MFMA
+  static constexpr int kDt = HD / 16;                     // d tiles of the PV MFMA
+  static constexpr int kKRow = HD * 2 + 16;               // K tile row (one key), padded
+  static constexpr int kVRow = kAttnKeys * 2 + 16;        // V^T tile row (one d), padded
+  static constexpr int kPRow = kAttnKeys * 2 + 16;        // P patch row (one query row)
+  static constexpr int kKBytes = kAttnKeys * kKRow;
+  static constexpr int kVBytes = HD * kVRow;
+  static constexpr int kPBytes = 16 * kPRow;
+  static constexpr int kPieces = kAttnKeys * HD * 2 / 16;  // 16-byte pieces of one K (or V) tile
+  static constexpr int kLoads = kPieces / kAttnThreads;    // per thread and tensor
+  static_assert(kLoads >= 1 && kPieces % kAttnThreads == 0, "tile must split evenly");
+};
+
+// Key range [k0, k1) of split `sp` of a lane whose keys are [0, ctx): splits of whole tiles.
+__device__ __host__ inline void attn_split_range(int ctx, int n_split, int sp, int& k0, int& k1) {
+  const int tiles = (ctx + kAttnKeys - 1) / kAttnKeys;
+  const int per = (tiles + n_split - 1) / n_split;
+  k0 = min(sp * per * kAttnKeys, ctx);
+  k1 = min((sp + 1) * per * kAttnKeys, ctx);
+}
+
+template <int HD>
+__global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    const uint16_t* __restrict__ v_pool, int64_t pool_rows, const int32_t* __restrict__ table,
+    int table_stride, const int64_t* __restrict__ base_pos, int t, int heads, int kvh,
+    float scale_log2, int n_split, int row_groups, float* __restrict__ part_o,
+    float* __restrict__ part_ml, uint16_t* __restrict__ out) {
+  using G = AttnGeom<HD>;
+  __shared__ __attribute__((aligned(16))) uint8_t ks[G::kKBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t vs[G::kVBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t ps[kAttnWaves][G::kPBytes];
+  const int group = heads / kvh, R = group * t;
+  int id = blockIdx.x;
+  const int rg = id % row_groups;
+  id /= row_groups;
+  const int kh = id % kvh, b = id / kvh;
+  const int sp = blockIdx.y;
+  const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
+  const int g = lane >> 4, c = lane & 15;
+  const int64_t bp = base_pos[b];
+  const int ctx = (int)bp + t;
+  int k0, k1;
+  attn_split_range(ctx, n_split, sp, k0, k1);
+  if (k0 >= k1) return;  // uniform: an empty split writes nothing (the merge skips it)
+
+  // this wave's query rows r = 64 rg + 16 wave + (0..15); row r = (q head kh*group + r / t,
+  // step r % t). Lanes of A (row c) load their row; rows past R read zeros.
+  const int rbase = kAttnRows * rg + 16 * wave;
+  const int ra = rbase + c;
+  bf16x8_t qa[G::kDs];
+  {
+    const bool live = ra < R;
+    const int hq = kh * group + (live ? ra / t : 0), st = live ? ra % t : 0;
+    const uint16_t* qrow = q + (((int64_t)b * heads + hq) * t + st) * HD;
+#pragma unroll
+    for (int ds = 0; ds < G::kDs; ++ds)
+      qa[ds] = live ? as_bf16x8(ld16(qrow + 32 * ds + 8 * g)) : as_bf16x8(zero16());
+  }
+  // D-layout rows of this lane: 4g + i; their positions (rows past R are masked everywhere)
+  int qpos[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = rbase + 4 * g + i;
+    qpos[i] = r < R ? (int)bp + r % t : -1;
+  }
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.f;
+  }
+  f32x4_t o[G::kDt];
+#pragma unroll
+  for (int dt = 0; dt < G::kDt; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // staging. K: piece p = j * 256 + tid is key p / (HD / 8), 16-byte column p % (HD / 8), so a
+  // wave instruction reads whole 512-byte key rows. V: key p % 32, column p / 32, so that the
+  // transposed LDS writes of one instruction go to 32 consecutive keys of two d rows (bank
+  // spread) at the cost of 32-byte global segments.
+  constexpr int kCols = HD / 8;
+  const uint32_t pool_bytes = (uint32_t)min(pool_rows * kvh * HD * 2, (int64_t)0x7fffffff);
+  const rsrc_t rk = make_rsrc(k_pool, pool_bytes), rv = make_rsrc(v_pool, pool_bytes);
+  auto key_off = [&](int pos, int col) {
+    if (pos >= k1) return kOutOfRange;
+    const int blk = min(pos / kAttnBlock, table_stride - 1);  // never past the lane's table row
+    const int64_t row = (int64_t)table[(int64_t)b * table_stride + blk] * kAttnBlock + pos % kAttnBlock;
+    return (uint32_t)(((row * kvh + kh) * HD + col * 8) * 2);
+  };
+  u32x4_t kreg[G::kLoads], vreg[G::kLoads];
+  auto stage_load = [&](int key0) {
+#pragma unroll
+    for (int j = 0; j < G::kLoads; ++j) {
+      const int p = j * kAttnThreads + tid;
+      kreg[j] = buf16(rk, key_off(key0 + p / kCols, p % kCols));
+      vreg[j] = buf16(rv, key_off(key0 + p % kAttnKeys, p / kAttnKeys));
+    }
+  };
+  auto stage_store = [&]() {
+#pragma unroll
+    for (int j = 0; j < G::kLoads; ++j) {
+      const int p = j * kAttnThreads + tid;
+      lds16_store(ks + (p / kCols) * G::kKRow + (p % kCols) * 16, kreg[j]);
+      // V transposed: element d = 8 col + e of key kk goes to row d, column kk
+      const int kk = p % kAttnKeys, col = p / kAttnKeys;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint16_t hv = (uint16_t)(vreg[j][e >> 1] >> (16 * (e & 1)));
+        *reinterpret_cast<uint16_t*>(vs + (8 * col + e) * G::kVRow + kk * 2) = hv;
+      }
+    }
+  };
+
+  uint8_t* const pw = ps[wave];
+  stage_load(k0);
+  for (int key0 = k0; key0 < k1; key0 += kAttnKeys) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    stage_store();
+    __syncthreads();
+    if (key0 + kAttnKeys < k1) stage_load(key0 + kAttnKeys);  // next tile in flight meanwhile
+
+    // S = Q K^T for keys key0 + (0..15) and key0 + 16 + (0..15)
+    f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ds = 0; ds < G::kDs; ++ds) {
+      const bf16x8_t kb0 = as_bf16x8(lds16(ks + c * G::kKRow + (32 * ds + 8 * g) * 2));
+      const bf16x8_t kb1 = as_bf16x8(lds16(ks + (16 + c) * G::kKRow + (32 * ds + 8 * g) * 2));
+      s0 = mfma16x16x32(qa[ds], kb0, s0);
+      s1 = mfma16x16x32(qa[ds], kb1, s1);
+    }
+    // online softmax, base 2: row 4g + i, keys c and 16 + c of this lane
+    const int pa = key0 + c, pb = key0 + 16 + c;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const bool la = pa < k1 && pa <= qpos[i], lb = pb < k1 && pb <= qpos[i];
+      const float xa = la ? s0[i] * scale_log2 : -INFINITY;
+      const float xb = lb ? s1[i] * scale_log2 : -INFINITY;
+      float tm = fmaxf(xa, xb);
+#pragma unroll
+      for (int sh = 1; sh < 16; sh <<= 1) tm = fmaxf(tm, __shfl_xor(tm, sh, 16));
+      const float mn = fmaxf(m[i], tm);
+      const float alpha = mn == -INFINITY ? 1.f : exp2f(m[i] - mn);
+      const float ea = la ? exp2f(xa - mn) : 0.f;
+      const float eb = lb ? exp2f(xb - mn) : 0.f;
+      float rs = ea + eb;
+#pragma unroll
+      for (int sh = 1; sh < 16; sh <<= 1) rs += __shfl_xor(rs, sh, 16);
+      l[i] = l[i] * alpha + rs;
+      m[i] = mn;
+#pragma unroll
+      for (int dt = 0; dt < G::kDt; ++dt) o[dt][i] *= alpha;
+      // P row 4g + i, keys c and 16 + c, as bf16 into the wave's patch
+      *reinterpret_cast<__bf16*>(pw + (4 * g + i) * G::kPRow + c * 2) = (__bf16)ea;
+      *reinterpret_cast<__bf16*>(pw + (4 * g + i) * G::kPRow + (16 + c) * 2) = (__bf16)eb;
+    }
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave's own patch writes, before reading them back
+    const bf16x8_t pa8 = as_bf16x8(lds16(pw + c * G::kPRow + 8 * g * 2));
+    // O += P V: B = V[keys 8g .. 8g + 7][d = 16 dt + c] from the transposed tile
+#pragma unroll
+    for (int dt = 0; dt < G::kDt; ++dt) {
+      const bf16x8_t vb = as_bf16x8(lds16(vs + (16 * dt + c) * G::kVRow + 8 * g * 2));
+      o[dt] = mfma16x16x32(pa8, vb, o[dt]);
+    }
+  }
+
+  // rows 4g + i of this lane: o[dt][i] is d = 16 dt + c
+  const int64_t slot = ((int64_t)(b * kvh + kh) * row_groups + rg) * n_split + sp;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int rl = 16 * wave + 4 * g + i;  // row within the workgroup
+    const int r = kAttnRows * rg + rl;
+    if (r >= R) continue;
+    if (n_split == 1) {
+      const float inv = 1.f / l[i];
+      const int hq = kh * group + r / t, st = r % t;
+      uint16_t* orow = out + (((int64_t)b * heads + hq) * t + st) * HD;
+#pragma unroll
+      for (int dt = 0; dt < G::kDt; ++dt) orow[16 * dt + c] = f32_to_bf16(o[dt][i] * inv);
+    } else {
+      float* po = part_o + (slot * kAttnRows + rl) * HD;
+#pragma unroll
+      for (int dt = 0; dt < G::kDt; ++dt) po[16 * dt + c] = o[dt][i];
+      if (c == 0) {
+        part_ml[(slot * kAttnRows + rl) * 2] = m[i];
+        part_ml[(slot * kAttnRows + rl) * 2 + 1] = l[i];
+      }
+    }
+  }
+}
+
+// Merge of the key splits: out = sum_s o_s 2^(m_s - M) / sum_s l_s 2^(m_s - M), M = max_s m_s,
+// over the splits that hold keys of the row's lane. One thread per (row, 4 d values).
+template <int HD>
+__global__ __launch_bounds__(256) void k_attention_merge(
+    const float* __restrict__ part_o, const float* __restrict__ part_ml,
+    const int64_t* __restrict__ base_pos, int B, int t, int heads, int kvh, int n_split,
+    int row_groups, uint16_t* __restrict__ out) {
+  const int group = heads / kvh;
+  const int64_t rows = (int64_t)B * heads * t;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= rows * (HD / 4)) return;
+  const int64_t row = idx / (HD / 4);
+  const int d = (int)(idx % (HD / 4)) * 4;
+  const int st = (int)(row % t);
+  const int64_t bh = row / t;
+  const int hq = (int)(bh % heads), b = (int)(bh / heads);
+  const int kh = hq / group, r = (hq % group) * t + st;
+  const int rg = r / kAttnRows, rl = r % kAttnRows;
+  const int ctx = (int)base_pos[b] + t;
+  const int64_t base = ((int64_t)(b * kvh + kh) * row_groups + rg) * n_split;
+  float mx = -INFINITY;
+  for (int sp = 0; sp < n_split; ++sp) {
+    int k0, k1;
+    attn_split_range(ctx, n_split, sp, k0, k1);
+    if (k0 < k1) mx = fmaxf(mx, part_ml[((base + sp) * kAttnRows + rl) * 2]);
+  }
+  float lsum = 0.f, acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int sp = 0; sp < n_split; ++sp) {
+    int k0, k1;
+    attn_split_range(ctx, n_split, sp, k0, k1);
+    if (k0 >= k1) continue;
+    const int64_t pr = (base + sp) * kAttnRows + rl;
+    const float ms = part_ml[pr * 2];
+    const float w = ms == -INFINITY ? 0.f : exp2f(ms - mx);
+    lsum += part_ml[pr * 2 + 1] * w;
+    const float* po = part_o + pr * HD + d;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) acc[e] += po[e] * w;
+  }
+  const float inv = 1.f / lsum;
+  uint16_t* orow = out + row * HD + d;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) orow[e] = f32_to_bf16(acc[e] * inv);
+}
+
+int attention_splits(int64_t B, int64_t kvh, int row_groups, int64_t max_ctx) {
+  const int64_t wgs = B * kvh * row_groups;
+  const int64_t want = (3 * (int64_t)device_cu_count() + wgs - 1) / (wgs > 0 ? wgs : 1);
+  const int64_t tiles = (max_ctx + kAttnKeys - 1) / kAttnKeys;
+  const int64_t cap = tiles / 8 > 1 ? tiles / 8 : 1;  // at least 8 tiles per split
+  int64_t n = want < cap ? want : cap;
+  if (n > 64) n = 64;
+  return n < 1 ? 1 : (int)n;
+}
+
+template <int HD>
+int launch_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+                     int64_t pool_rows, const int32_t* table, int table_stride,
+                     const int64_t* base_pos, int B, int t, int heads, int kvh, float scale,
+                     int n_split, float* part_o, float* part_ml, uint16_t* out, hipStream_t st) {
+  const int row_groups = (heads / kvh * t + kAttnRows - 1) / kAttnRows;
+  const float scale_log2 = scale * 1.4426950408889634f;
+  hipLaunchKernelGGL(k_paged_attention<HD>, dim3(B * kvh * row_groups, n_split), dim3(kAttnThreads),
+                     0, st, q, k_pool, v_pool, pool_rows, table, table_stride, base_pos, t, heads,
+                     kvh, scale_log2, n_split, row_groups, part_o, part_ml, out);
+  int rc = status_of(hipGetLastError());
+  if (rc || n_split == 1) return rc;
+  const int64_t threads = (int64_t)B * heads * t * (HD / 4);
+  hipLaunchKernelGGL(k_attention_merge<HD>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
+                     part_o, part_ml, base_pos, B, t, heads, kvh, n_split, row_groups, out);
+  return status_of(hipGetLastError());
+}
+
+}  // namespace mtpk
+
+using namespace mtpk;
+
+extern "C" {
+
+int mtpk_attention_splits(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads, int64_t max_ctx) {
+  if (batch <= 0 || t <= 0 || kv_heads <= 0 || heads % kv_heads) return 0;
+  const int row_groups = (int)((heads / kv_heads * t + kAttnRows - 1) / kAttnRows);
+  return attention_splits(batch, kv_heads, row_groups, max_ctx);
+}
+
+int64_t mtpk_attention_workspace_bytes(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads,
+                                       int64_t head_dim, int n_split) {
+  if (batch <= 0 || t <= 0 || kv_heads <= 0 || heads % kv_heads || n_split <= 1) return 0;
+  const int64_t row_groups = (heads / kv_heads * t + kAttnRows - 1) / kAttnRows;
+  const int64_t slots = batch * kv_heads * row_groups * n_split * kAttnRows;
+  return slots * (head_dim + 2) * 4;
+}
+
+int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t heads,
+                         int64_t kv_heads, int64_t head_dim, const uint16_t* k_pool,
+                         const uint16_t* v_pool, int64_t pool_rows, const int32_t* block_table,
+                         int64_t table_stride, const int64_t* base_pos, float scale, int n_split,
+                         void* workspace, int64_t workspace_bytes, uint16_t* out, void* stream) {
+  if (!q || !k_pool || !v_pool || !block_table || !base_pos || !out) return MTPK_EINVAL;
+  if (batch < 0 || t <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return MTPK_EINVAL;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return MTPK_EINVAL;
+  if (pool_rows <= 0 || pool_rows * kv_heads * head_dim * 2 > 0x7fffffffLL) return MTPK_EINVAL;
+  if (table_stride <= 0 || n_split < 1 || n_split > 64 || !(scale > 0.f)) return MTPK_EINVAL;
+  if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool)) return MTPK_EINVAL;
+  if (batch * heads * t > INT32_MAX / 64) return MTPK_EINVAL;
+  if (n_split > 1 &&
+      (!workspace || workspace_bytes < mtpk_attention_workspace_bytes(batch, t, heads, kv_heads,
+                                                                      head_dim, n_split)))
+    return MTPK_EINVAL;
+  if (batch == 0) return 0;
+  const int64_t rg = (heads / kv_heads * t + kAttnRows - 1) / kAttnRows;
+  float* part_o = (float*)workspace;
+  float* part_ml = part_o ? part_o + batch * kv_heads * rg * n_split * kAttnRows * head_dim : nullptr;
+  const hipStream_t st = (hipStream_t)stream;
+#define MTPK_ATTN(HD_)                                                                         \
+  launch_attention<HD_>(q, k_pool, v_pool, pool_rows, block_table, (int)table_stride, base_pos, \
+                        (int)batch, (int)t, (int)heads, (int)kv_heads, scale, n_split, part_o,  \
+                        part_ml, out, st)
+  switch (head_dim) {
+    case 64: return MTPK_ATTN(64);
+    case 128: return MTPK_ATTN(128);
+    default: return MTPK_ATTN(256);
+  }
+#undef MTPK_ATTN
+}
+
+}  // extern "C"

@@ -20,6 +20,10 @@ __device__ inline u32x4_t ld16(const void* p) { return *reinterpret_cast<const u
 
 __device__ inline u32x4_t zero16() { return u32x4_t{0u, 0u, 0u, 0u}; }
 
+// 16-byte LDS read / write (ds_read_b128 / ds_write_b128; 16-byte aligned addresses).
+__device__ inline u32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
+__device__ inline void lds16_store(uint8_t* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
+
 // Raw buffer loads. A buffer resource covers [base, base + bytes); a load whose byte offset
 // lies outside returns zeros and touches no memory, so a lane that has nothing to load gets
 // the offset kOutOfRange instead of a branch around its load (branches around loads make the

@@ -776,9 +776,6 @@ __device__ inline void lds_barrier() {
   ring_fence();
 }
 
-__device__ inline u32x4_t lds16(const uint8_t* p) { return *reinterpret_cast<const u32x4_t*>(p); }
-
-__device__ inline void lds16_store(uint8_t* p, u32x4_t v) { *reinterpret_cast<u32x4_t*>(p) = v; }
 
 // Byte g of each of four dwords, packed low to high: one 16-byte scale segment (four trips of
 // four lane groups) reduced to the four bytes one lane group uses. sel01 / selc come from

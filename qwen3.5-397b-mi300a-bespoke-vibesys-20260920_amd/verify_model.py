@@ -31,6 +31,7 @@ from dataclasses import dataclass, field
 import torch
 import torch.nn.functional as F
 
+import attention
 import deltanet
 import mxfp4
 import mxfp4_gemv
@@ -177,7 +178,12 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     (`verify_attention_paged`, `model.py:1120-1205`). `q` `[B, heads, t, hd]`; pools
     `[rows, kv_heads, hd]` already hold this round's rows; query row `s` of lane `b` sits at
     `base_pos[b] + s` and sees every cached position up to its own. `ctx_blocks` bounds the
-    gather (a host value, at least every lane's block count). fp32 math, q's dtype out."""
+    gather (a host value, at least every lane's block count). fp32 math, q's dtype out. bf16
+    device tensors with 16-row blocks and head_dim 64/128/256 go to the HIP kernel
+    (`attention.paged_attention`: bf16 MFMA, bf16 probabilities, fp32 softmax)."""
+    if attention.supported(q, block_size):
+        return attention.paged_attention(q, k_pool, v_pool, block_table, base_pos, ctx_blocks * block_size,
+                                         scale)
     b, heads, t, hd = q.shape
     kvh = k_pool.shape[1]
     group = heads // kvh
