@@ -373,7 +373,7 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
     model.mtp.pool["k"].normal_(generator=g)
     model.mtp.pool["v"].normal_(generator=g)
     model.hidden_cache.normal_(generator=g)
-    runner = graph_mtp.MTPVerifyRunner(model, capacity=b)
+    runner = graph_mtp.GraphMTPRunner(model, capacity=b)
     toks = torch.randint(0, model.cfg.vocab, (b,), generator=torch.Generator().manual_seed(4)).tolist()
     pos = [start] * b
     torch.cuda.synchronize()
@@ -407,6 +407,7 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
         "accepted_tok_s": round(committed / wall, 1),
         "rounds": rounds,
         "weights": "random init (draft acceptance near zero)",
+        "runner": "GraphMTPRunner (draft + verify + accept + commit replayed as one HIP graph)",
     }
     del runner, model
     torch.cuda.empty_cache()

@@ -277,6 +277,50 @@ class MTPVerifyRunner:
         return [row[: row[-1] + 1] for row in rows]
 
 
+class GraphMTPRunner(MTPVerifyRunner):
+    """`MTPVerifyRunner` with each batch size's draft and verify steps captured in one HIP graph
+    (`GraphMTPRunner`, `graph_mtp.py:1062-1120`). A round writes the static buffers (`fill`),
+    replays the graph and reads the committed ids once. The first round of a batch size runs
+    eagerly on the capture stream (its result is that round's) and is then captured; rounds
+    with forced drafts run eagerly. The attention key splits are sized for the block tables'
+    full capacity, so one graph serves every context length."""
+
+    def __init__(self, model, capacity: int) -> None:
+        super().__init__(model, capacity)
+        self.slots = torch.zeros(capacity, dtype=torch.long, device=model.device)
+        self.ctx_bound = model.blocks.max_blocks * model.cfg.block_size
+        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
+
+    def _round(self, b: int) -> None:
+        lanes = self.slots[:b]
+        draft_round_step(self.model, self.mtp, self.buf, lanes, b)
+        verify_round_step(self.model, self.mtp, self.buf, lanes, b, self.ctx_bound)
+
+    def speculative_decode(self, slots: list[int], tokens: list[int], positions: list[int],
+                           budgets=None, stops=None, forced=None) -> list[list[int]]:
+        if forced and any(forced):
+            return super().speculative_decode(slots, tokens, positions, budgets, stops, forced)
+        b = len(slots)
+        self.fill(slots, tokens, positions, budgets, stops, None)
+        self.slots[:b] = torch.tensor(list(slots), dtype=torch.long).to(self.slots.device)
+        graph = self.graphs.get(b)
+        if graph is None:
+            side = torch.cuda.Stream(self.slots.device)
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                self._round(b)  # this round, run eagerly; also warms the allocator
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize(self.slots.device)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._round(b)
+            self.graphs[b] = graph
+        else:
+            graph.replay()
+        rows = torch.cat([self.buf.step_argmax[:b], self.buf.accept_len[:b, None]], dim=1).tolist()
+        return [row[: row[-1] + 1] for row in rows]
+
+
 # ---------------------------------------------------------------- sampling-mode acceptance
 
 

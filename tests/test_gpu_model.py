@@ -121,3 +121,48 @@ def test_config5_dims_round(dev) -> None:
     for ty, p in zip(model.cfg.layer_types, model.pool, strict=True):
         if ty != vm.ATTN:
             assert torch.isfinite(p["rec"]).all() and torch.isfinite(p["conv"].float()).all()
+
+
+def _graph_vs_eager(dev, build, prompts, rounds):
+    """Identical models, one on the eager runner and one on the captured runner: every round
+    commits the same ids (replays separated by unrelated eager work and a synchronisation)."""
+    a, b = build(), build()
+    toks, pos = [], []
+    for lane, p in enumerate(prompts):
+        toks.append(int(a.argmax(a.prefill(lane, p)[None])[0]))
+        b.prefill(lane, p)
+        pos.append(len(p))
+    lanes = list(range(len(prompts)))
+    eager = graph_mtp.MTPVerifyRunner(a, capacity=len(prompts))
+    graph = graph_mtp.GraphMTPRunner(b, capacity=len(prompts))
+    for r in range(rounds):
+        want = eager.speculative_decode(lanes, toks, pos)
+        got = graph.speculative_decode(lanes, toks, pos)
+        assert got == want, f"round {r}"
+        torch.cuda.synchronize()
+        _ = (torch.randn(256, 256, device=dev) @ torch.randn(256, 256, device=dev)).sum().item()
+        for j, c in enumerate(want):
+            pos[j] += len(c)
+            toks[j] = c[-1]
+    assert len(graph.graphs) == 1
+    return a, b, pos
+
+
+def test_config1_graph_runner_matches_eager(dev) -> None:
+    k = 3
+    a, b, pos = _graph_vs_eager(dev, lambda: mh.build(dev, k=k), mh.prompts(2), 5)
+    # the library GEMMs may pick another algorithm under capture: states agree to fp32 rounding
+    for lane in range(2):
+        mh.assert_slot_state_close(a, b, lane, pos[lane], rtol=1e-5, atol=1e-6)
+
+
+def test_config5_dims_graph_runner_matches_eager(dev) -> None:
+    def build():
+        model = vm.Model(vm.verify_cfg(), dev, torch.bfloat16, lanes=3, max_seq=96, seed=0,
+                         expert_mode="bytes", moe_rows=16)
+        mtp.attach(model, k=3, seed=1, expert_mode="bytes")
+        return model
+
+    gen = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, 248320, (4 + 5 * j,), generator=gen).tolist() for j in range(3)]
+    _graph_vs_eager(dev, build, prompts, 3)
