@@ -235,6 +235,26 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
                     const float* k, const float* v, const float* g, const float* beta,
                     const int64_t* lengths, float* out, void* stream);
 
+/* ---------------------------------------------------------------- row norms
+ * One launch per normalisation of the verify / draft forward, in place of the torch op chains
+ * of `rmsnorm` (model.py:587-604), the DeltaNet output norm (model.py:613-619), the DeltaNet
+ * q/k L2 norm and `apply_rope` (model.py:631-635). kind 0: y = x*rsqrt(mean(x^2)+eps)*(1+w);
+ * kind 1: y = x*rsqrt(mean(x^2)+eps)*w, times silu(gate) when gate is given; kind 2:
+ * y = x*rsqrt(sum(x^2)+eps)*scale (w unused). Row r (of `rows`) is head r % heads_per_token of
+ * token r / heads_per_token, read from x at token*x_token_stride + head*x_head_stride
+ * (elements; the gate likewise). res (optional, contiguous [rows, dim], heads_per_token 1,
+ * x contiguous): x is replaced by x + res in x's dtype, which is also written to sum_out.
+ * rope_cos/rope_sin (optional, f32 [positions, rot_dim]) with rope_pos (i64 [tokens]):
+ * rotate-half RoPE on the first rot_dim channels of y rounded to the output dtype (dim <= 512;
+ * rot_dim a multiple of 16, or 2, 4 or 8). out: contiguous [rows, dim]. dim a multiple of 8, <= 8192;
+ * bf16 strides multiples of 8 and pointers 16-byte aligned. */
+int mtpk_rownorm(const void* x, int x_dtype, int64_t x_token_stride, int64_t x_head_stride,
+                 const void* res, int res_dtype, void* sum_out, const void* w, int w_dtype,
+                 int kind, float eps, float scale, const void* gate, int gate_dtype,
+                 int64_t gate_token_stride, int64_t gate_head_stride, const float* rope_cos,
+                 const float* rope_sin, const int64_t* rope_pos, int rot_dim, void* out,
+                 int out_dtype, int64_t rows, int heads_per_token, int dim, void* stream);
+
 /* ---------------------------------------------------------------- paged verify attention
  * Causal GQA attention of t query rows per lane over a paged bf16 KV cache, replacing
  * `verify_attention_paged` (model.py:1120-1205; per row `paged_attn.decode_attention_paged`,

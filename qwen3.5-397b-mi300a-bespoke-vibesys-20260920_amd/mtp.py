@@ -177,11 +177,11 @@ def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: 
     c, w = model.cfg, mtp.weights
     x = _combine_rows(model, mtp, hid[:, None, :], tok)  # [B, 1, hidden]
     h = vm.rmsnorm(x, w["in_norm"], c.eps)
-    x = x + vm.gated_attention(model, w, mtp.pool, h, rope_pos, write_rows.reshape(-1, 1),
-                               block_table, block_table.shape[1])
-    hm = vm.rmsnorm(x, w["post_norm"], c.eps)
-    x = x + model.moe(w, hm[:, 0])[:, None]
-    normed = vm.rmsnorm(x, mtp.norm, c.eps)[:, 0]
+    attn = vm.gated_attention(model, w, mtp.pool, h, rope_pos, write_rows.reshape(-1, 1),
+                              block_table, block_table.shape[1])
+    x, hm = vm.add_rmsnorm(x, attn, w["post_norm"], c.eps)
+    _, normed = vm.add_rmsnorm(x, model.moe(w, hm[:, 0])[:, None], mtp.norm, c.eps)
+    normed = normed[:, 0]
     nxt = model.argmax(model.unembed(normed))[:, None]
     return normed, nxt
 

@@ -36,6 +36,7 @@ import deltanet
 import mxfp4
 import mxfp4_gemv
 import router_fused
+import rownorm
 
 ATTN = "full_attention"
 DELTANET = "linear_attention"
@@ -105,23 +106,45 @@ def verify_cfg() -> Cfg:
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """Qwen3.5 RMSNorm: normalise in fp32, scale by `1 + w` (`model.py:587-604`)."""
+    """Qwen3.5 RMSNorm: normalise in fp32, scale by `1 + w` (`model.py:587-604`). Contiguous
+    device tensors take the row-norm kernel (`rownorm.rmsnorm`)."""
+    if x.device.type == "cuda" and x.is_contiguous():
+        return rownorm.rmsnorm(x, w, eps)
     xf = x.float()
     y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps)
     return (y * (1.0 + w.float())).to(x.dtype)
 
 
+def add_rmsnorm(x: torch.Tensor, res: torch.Tensor, w: torch.Tensor,
+                eps: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """`s = x + res`, then `rmsnorm(s, w, eps)`: returns `(s, normed)`; one row-norm launch for
+    contiguous device tensors."""
+    if x.device.type == "cuda" and x.is_contiguous() and res.is_contiguous():
+        return rownorm.add_rmsnorm(x, res, w, eps)
+    s = x + res
+    return s, rmsnorm(s, w, eps)
+
+
 def gated_rmsnorm(x: torch.Tensor, gate: torch.Tensor, w: torch.Tensor, eps: float,
                   dtype: torch.dtype) -> torch.Tensor:
     """DeltaNet output norm: RMS-normalise, scale by `w` (no +1), times `silu(gate)`
-    (`model.py:613-619`)."""
+    (`model.py:613-619`). `x`, `gate` `[..., heads, dim]`; device tensors take the row-norm
+    kernel."""
+    if x.device.type == "cuda":
+        x = x if x.stride(-1) == 1 else x.contiguous()
+        gate = gate if gate.stride(-1) == 1 else gate.contiguous()
+        return rownorm.gated_rmsnorm(x, gate, w, eps, dtype)
     xf = x.float()
     y = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * w.float()
     return (y * F.silu(gate.float())).to(dtype)
 
 
-def l2norm(x: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
-    return x * torch.rsqrt((x * x).sum(-1, keepdim=True) + eps)
+def l2norm(x: torch.Tensor, eps: float = 1e-6, scale: float = 1.0) -> torch.Tensor:
+    """`x * rsqrt(sum(x^2) + eps) * scale` over the last dim of fp32 `[..., heads, dim]`."""
+    if x.device.type == "cuda":
+        return rownorm.l2norm(x if x.stride(-1) == 1 else x.contiguous(), eps, scale)
+    y = x * torch.rsqrt((x * x).sum(-1, keepdim=True) + eps)
+    return y * scale if scale != 1.0 else y
 
 
 def apply_rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
@@ -214,12 +237,17 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
     b, t, _ = h.shape
     qg = F.linear(h, w["q_proj"]).view(b, t, c.heads, 2 * c.head_dim)
     q, gate = qg[..., : c.head_dim], qg[..., c.head_dim :]
-    q = rmsnorm(q, w["q_norm"], c.eps)
-    k = rmsnorm(F.linear(h, w["k_proj"]).view(b, t, c.kv_heads, c.head_dim), w["k_norm"], c.eps)
+    kp = F.linear(h, w["k_proj"]).view(b, t, c.kv_heads, c.head_dim)
     v = F.linear(h, w["v_proj"]).view(b, t, c.kv_heads, c.head_dim)
     pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
-    cos, sin = model.cos[pos][:, :, None], model.sin[pos][:, :, None]  # [B, t, 1, rot]
-    q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
+    if h.device.type == "cuda":  # q/k norm and RoPE in one row-norm launch each
+        rope = (model.cos, model.sin, pos.reshape(-1))
+        q = rownorm.rmsnorm(q, w["q_norm"], c.eps, heads=True, rope=rope)
+        k = rownorm.rmsnorm(kp, w["k_norm"], c.eps, heads=True, rope=rope)
+    else:
+        q, k = rmsnorm(q, w["q_norm"], c.eps), rmsnorm(kp, w["k_norm"], c.eps)
+        cos, sin = model.cos[pos][:, :, None], model.sin[pos][:, :, None]  # [B, t, 1, rot]
+        q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
     rows = write_rows.reshape(-1).long()
     pool["k"][rows] = k.reshape(-1, c.kv_heads, c.head_dim)
     pool["v"][rows] = v.reshape(-1, c.kv_heads, c.head_dim)
@@ -491,7 +519,7 @@ class Model:
         q = mixed[..., :kd].reshape(b, t, c.k_heads, c.k_dim).float()
         k = mixed[..., kd : 2 * kd].reshape(b, t, c.k_heads, c.k_dim).float()
         v = mixed[..., 2 * kd :].reshape(b, t, c.v_heads, c.v_dim).float()
-        q = l2norm(q) * c.k_dim ** -0.5  # [B, t, k_heads, k_dim]; v head h reads k head h // rep
+        q = l2norm(q, scale=c.k_dim ** -0.5)  # [B, t, k_heads, k_dim]; v head h reads k head h // rep
         k = l2norm(k)
         beta = torch.sigmoid(b_raw.float())
         g = -w["A_log"].float().exp() * F.softplus(a_raw.float() + w["dt_bias"].float())
@@ -549,19 +577,22 @@ class Model:
         base_pos = base_pos.to(self.device, torch.long)
         x = self.embed[ids.to(self.device)]
         res = VerifyOut(x)
+        pending = None  # the previous layer's MoE output, added in front of the next norm
         for i, ty in enumerate(c.layer_types):
             w, pool = self.layers[i], self.pool[i]
-            h = rmsnorm(x, w["in_norm"], c.eps)
+            if pending is None:
+                h = rmsnorm(x, w["in_norm"], c.eps)
+            else:
+                x, h = add_rmsnorm(x, pending, w["in_norm"], c.eps)
             if ty == ATTN:
                 mixer = self.attention_rows(w, pool, h, lanes, base_pos, ctx_len)
             else:
                 mixer, rows = self.deltanet_verify(w, pool, h, lanes)
                 res.dn_rows[i] = rows
-            x = x + mixer
-            hm = rmsnorm(x, w["post_norm"], c.eps)
+            x, hm = add_rmsnorm(x, mixer, w["post_norm"], c.eps)
             b, t, _ = hm.shape
-            x = x + self.moe(w, hm.reshape(b * t, -1)).view(b, t, -1)
-        res.hidden = x
+            pending = self.moe(w, hm.reshape(b * t, -1)).view(b, t, -1)
+        res.hidden = x + pending
         return res
 
     def commit(self, res: VerifyOut, lanes, lengths: torch.Tensor,

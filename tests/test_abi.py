@@ -1,5 +1,6 @@
 """The C-ABI library loads and exports exactly what include/mtpk.h declares (no device calls)."""
 
+import ctypes
 import re
 from pathlib import Path
 
@@ -58,6 +59,15 @@ def test_rejected_arguments_launch_nothing(lib):
                                   None, None, None, None, None, None, None, None, None, None,
                                   None, None) == -1
     assert lib.mtpk_moe_prep(None, 3, None, 0, 10, 0, 512, None, None, 10, None, None) == -1
+    # row norm: null input, dim not a multiple of 8, unknown kind
+    assert lib.mtpk_rownorm(None, 0, 64, 64, None, 0, None, None, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
+                            None, None, None, 0, None, 0, 1, 1, 64, None) == -1
+    buf = (ctypes.c_float * 256)()
+    p = ctypes.addressof(buf)
+    assert lib.mtpk_rownorm(p, 0, 60, 60, None, 0, None, p, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
+                            None, None, None, 0, p, 0, 1, 1, 60, None) == -1
+    assert lib.mtpk_rownorm(p, 0, 64, 64, None, 0, None, p, 0, 7, 1e-6, 1.0, None, 0, 0, 0,
+                            None, None, None, 0, p, 0, 1, 1, 64, None) == -1
     # rejection sampling: null inputs, then a non-positive temperature with valid-looking
     # pointers (nothing is dereferenced before the checks)
     fake = 0x1000
