@@ -259,8 +259,9 @@ int mtpk_rownorm(const void* x, int x_dtype, int64_t x_token_stride, int64_t x_h
  * Causal GQA attention of t query rows per lane over a paged bf16 KV cache, replacing
  * `verify_attention_paged` (model.py:1120-1205; per row `paged_attn.decode_attention_paged`,
  * paged_attn.py) in the verify forward and the MTP layer's attention (`mtp._attn_rows`,
- * mtp.py:233-279, t = 1). q bf16 [batch, heads, t, head_dim] contiguous; k_pool, v_pool bf16
- * [pool_rows, kv_heads, head_dim] contiguous, 16-row blocks; block_table int32
+ * mtp.py:233-279, t = 1). q bf16 [batch, heads, t, head_dim] contiguous; k_pool bf16
+ * [pool_rows, kv_heads, head_dim] and v_pool bf16 [pool_rows / 16, kv_heads, head_dim, 16] (V
+ * transposed inside each 16-row block), both contiguous; block_table int32
  * [batch, table_stride]: lane b's position p is pool row block_table[b][p / 16] * 16 + p % 16;
  * base_pos int64 [batch]: query row s of lane b is at base_pos[b] + s and attends to positions
  * 0 .. base_pos[b] + s (q head h uses kv head h / (heads / kv_heads)). out bf16, q's shape.

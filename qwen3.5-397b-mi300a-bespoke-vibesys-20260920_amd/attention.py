@@ -2,7 +2,9 @@
 `mtpk_paged_attention` (include/mtpk.h): the role of `verify_attention_paged`
 (`model.py:1120-1205`) and, at t = 1, of the MTP draft step's attention (`mtp.py:233-279`).
 
-q bf16 `[B, heads, t, hd]`; K/V pools bf16 `[pool_rows, kv_heads, hd]` of 16-row blocks;
+q bf16 `[B, heads, t, hd]`; the K pool bf16 `[pool_rows, kv_heads, hd]` and the V pool bf16
+`[pool_rows / 16, kv_heads, hd, 16]` of 16-row blocks: V is kept transposed inside each block
+(`v_blocks`), so the kernel stages a V tile with contiguous reads and no transposition.
 `block_table` int32 `[B, blocks]` (the lanes' own tables); `base_pos` int64 `[B]`: query row s
 of lane b sits at `base_pos[b] + s` and sees every cached position up to its own. The output is
 bf16 `[B, heads, t, hd]`.
@@ -16,6 +18,30 @@ import _mtpk
 
 BLOCK = 16
 HEAD_DIMS = (64, 128, 256)
+
+
+def v_blocks(v: torch.Tensor, block: int = BLOCK) -> torch.Tensor:
+    """V rows `[rows, kv_heads, hd]` -> the V cache layout `[rows / block, kv_heads, hd, block]`."""
+    rows, kvh, hd = v.shape
+    return v.view(rows // block, block, kvh, hd).permute(0, 2, 3, 1).contiguous()
+
+
+def v_rows(vt: torch.Tensor) -> torch.Tensor:
+    """The V cache layout `[blocks, kv_heads, hd, block]` -> V rows `[blocks * block, kv_heads, hd]`."""
+    nb, kvh, hd, bs = vt.shape
+    return vt.permute(0, 3, 1, 2).reshape(nb * bs, kvh, hd)
+
+
+def write_v(vt: torch.Tensor, rows: torch.Tensor, v: torch.Tensor) -> None:
+    """Store V rows `v` `[n, kv_heads, hd]` at pool rows `rows` `[n]` of the V cache `vt`."""
+    bs = vt.shape[-1]
+    vt[rows // bs, :, :, rows % bs] = v
+
+
+def read_v(vt: torch.Tensor, rows: torch.Tensor) -> torch.Tensor:
+    """V rows at pool rows `rows` (any shape) of the V cache: `[*rows.shape, kv_heads, hd]`."""
+    bs = vt.shape[-1]
+    return vt[rows // bs, :, :, rows % bs]
 
 
 def supported(q: torch.Tensor, block_size: int) -> bool:
@@ -32,8 +58,11 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     if q.dim() != 4 or q.dtype != torch.bfloat16:
         raise ValueError(f"q must be bf16 [B, heads, t, hd], got {q.dtype} {tuple(q.shape)}")
     b, heads, t, hd = q.shape
-    if k_pool.dim() != 3 or k_pool.shape != v_pool.shape or k_pool.shape[2] != hd:
-        raise ValueError(f"pools must be [rows, kv_heads, {hd}], got {tuple(k_pool.shape)}/{tuple(v_pool.shape)}")
+    if k_pool.dim() != 3 or k_pool.shape[2] != hd or k_pool.shape[0] % BLOCK:
+        raise ValueError(f"k_pool must be [rows, kv_heads, {hd}] of {BLOCK}-row blocks, got {tuple(k_pool.shape)}")
+    if tuple(v_pool.shape) != (k_pool.shape[0] // BLOCK, k_pool.shape[1], hd, BLOCK):
+        raise ValueError(f"v_pool must be [{k_pool.shape[0] // BLOCK}, {k_pool.shape[1]}, {hd}, {BLOCK}] "
+                         f"(V transposed per block), got {tuple(v_pool.shape)}")
     if k_pool.dtype != torch.bfloat16 or v_pool.dtype != torch.bfloat16:
         raise ValueError("pools must be bf16")
     if not (k_pool.is_contiguous() and v_pool.is_contiguous()):

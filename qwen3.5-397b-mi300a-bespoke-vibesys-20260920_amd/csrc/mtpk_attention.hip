@@ -2,14 +2,16 @@
 // model.py:1120-1205, which runs `paged_attn.decode_attention_paged` per verify row; the MTP
 // layer's draft step `mtp._attn_rows`, mtp.py:233-279, is the same call with t = 1).
 //
-// Shapes: q bf16 [B, heads, t, hd]; K and V pools bf16 [pool_rows, kv_heads, hd] with 16-row
-// blocks; lane b's key position p lives in pool row table[b][p / 16] * 16 + p % 16. Query row s
-// of lane b sits at position base_pos[b] + s and sees keys 0 .. base_pos[b] + s.
+// Shapes: q bf16 [B, heads, t, hd]; K pool bf16 [pool_rows, kv_heads, hd] and V pool bf16
+// [pool_rows / 16, kv_heads, hd, 16] (V transposed inside each 16-row block, so that a V tile
+// is staged with contiguous reads and no transposition), 16-row blocks; lane b's key position p
+// lives in pool row table[b][p / 16] * 16 + p % 16, i.e. block table[b][p / 16], slot p % 16.
+// Query row s of lane b sits at position base_pos[b] + s and sees keys 0 .. base_pos[b] + s.
 //
 // One workgroup takes one (lane, kv head, group of up to 64 query rows, key split). The query
 // rows of a kv head (group = heads / kv_heads q heads x t steps) share every key, so K and V are
 // read from HBM once per (lane, kv head, split) and staged in LDS in tiles of 32 keys: K as
-// [key][d], V transposed to [d][key] so that both MFMA B operands are 16-byte LDS reads. Each
+// [key][d], V as [d][key] (its cache layout) so that both MFMA B operands are 16-byte LDS reads. Each
 // wave owns 16 query rows:
 //   S = Q K^T   v_mfma_f32_16x16x32_bf16, A = Q (registers, loaded once), B = K tile
 //   online softmax over the row's keys (base-2, running max m and sum l per row)
@@ -106,50 +108,69 @@ __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
 #pragma unroll
   for (int dt = 0; dt < G::kDt; ++dt) o[dt] = f32x4_t{0.f, 0.f, 0.f, 0.f};
 
-  // staging. K: piece p = j * 256 + tid is key p / (HD / 8), 16-byte column p % (HD / 8), so a
-  // wave instruction reads whole 512-byte key rows. V: key p % 32, column p / 32, so that the
-  // transposed LDS writes of one instruction go to 32 consecutive keys of two d rows (bank
-  // spread) at the cost of 32-byte global segments.
+  // staging of a 32-key tile = two 16-row cache blocks, whose physical ids (p0, p1) are two
+  // scalar table reads. K [rows, kvh, HD]: piece p = j * 256 + tid is key p / (HD / 8),
+  // 16-byte column p % (HD / 8), so a wave instruction reads whole key rows. V is stored
+  // transposed per block, [blocks, kvh, HD, 16]: a block's slab for this kv head is HD rows of
+  // 16 keys (HD * 32 contiguous bytes), and piece p is block p / (2 HD), channel d = (p % 2HD) / 2,
+  // keys 8 ((p % 2HD) % 2) .. + 7: 16 contiguous bytes that land unchanged in LDS row d of the
+  // [d][key] tile the PV MFMA reads. Keys at or past k1 are zero in both tiles.
   constexpr int kCols = HD / 8;
   const uint32_t pool_bytes = (uint32_t)min(pool_rows * kvh * HD * 2, (int64_t)0x7fffffff);
   const rsrc_t rk = make_rsrc(k_pool, pool_bytes), rv = make_rsrc(v_pool, pool_bytes);
-  auto key_off = [&](int pos, int col) {
-    if (pos >= k1) return kOutOfRange;
-    const int blk = min(pos / kAttnBlock, table_stride - 1);  // never past the lane's table row
-    const int64_t row = (int64_t)table[(int64_t)b * table_stride + blk] * kAttnBlock + pos % kAttnBlock;
-    return (uint32_t)(((row * kvh + kh) * HD + col * 8) * 2);
+  const int32_t* const trow = table + (int64_t)b * table_stride;
+  auto tile_blocks = [&](int key0, int& p0, int& p1) {
+    const int blk = key0 / kAttnBlock;
+    p0 = sload(trow, min(blk, table_stride - 1));  // never past the lane's table row
+    p1 = sload(trow, min(blk + 1, table_stride - 1));
   };
   u32x4_t kreg[G::kLoads], vreg[G::kLoads];
-  auto stage_load = [&](int key0) {
+  auto stage_load = [&](int key0, int p0, int p1) {
 #pragma unroll
     for (int j = 0; j < G::kLoads; ++j) {
       const int p = j * kAttnThreads + tid;
-      kreg[j] = buf16(rk, key_off(key0 + p / kCols, p % kCols));
-      vreg[j] = buf16(rv, key_off(key0 + p % kAttnKeys, p / kAttnKeys));
+      const int kk = p / kCols, col = p % kCols;
+      const int64_t krow = (int64_t)(kk < kAttnBlock ? p0 : p1) * kAttnBlock + kk % kAttnBlock;
+      kreg[j] = buf16(rk, key0 + kk < k1 ? (uint32_t)(((krow * kvh + kh) * HD + col * 8) * 2)
+                                         : kOutOfRange);
+      const int bsel = p / (2 * HD), q2 = p % (2 * HD), d = q2 >> 1, half = q2 & 1;
+      const int64_t vblk = bsel ? p1 : p0;
+      vreg[j] = buf16(rv, key0 + kAttnBlock * bsel + 8 * half < k1
+                              ? (uint32_t)((((vblk * kvh + kh) * HD + d) * kAttnBlock + 8 * half) * 2)
+                              : kOutOfRange);
     }
   };
-  auto stage_store = [&]() {
+  auto stage_store = [&](int key0) {
 #pragma unroll
     for (int j = 0; j < G::kLoads; ++j) {
       const int p = j * kAttnThreads + tid;
       lds16_store(ks + (p / kCols) * G::kKRow + (p % kCols) * 16, kreg[j]);
-      // V transposed: element d = 8 col + e of key kk goes to row d, column kk
-      const int kk = p % kAttnKeys, col = p / kAttnKeys;
+      const int bsel = p / (2 * HD), q2 = p % (2 * HD), d = q2 >> 1, half = q2 & 1;
+      const int kfirst = key0 + kAttnBlock * bsel + 8 * half;
+      u32x4_t vv = vreg[j];
+      if (kfirst + 8 > k1) {  // the piece that straddles k1: zero its keys past the end
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint16_t hv = (uint16_t)(vreg[j][e >> 1] >> (16 * (e & 1)));
-        *reinterpret_cast<uint16_t*>(vs + (8 * col + e) * G::kVRow + kk * 2) = hv;
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = kfirst + 2 * e < k1 ? 0x0000ffffu : 0u;
+          const uint32_t hi = kfirst + 2 * e + 1 < k1 ? 0xffff0000u : 0u;
+          vv[e] &= lo | hi;
+        }
       }
+      lds16_store(vs + d * G::kVRow + (kAttnBlock * bsel + 8 * half) * 2, vv);
     }
   };
 
   uint8_t* const pw = ps[wave];
-  stage_load(k0);
+  int p0, p1;
+  tile_blocks(k0, p0, p1);
+  stage_load(k0, p0, p1);
   for (int key0 = k0; key0 < k1; key0 += kAttnKeys) {
+    const int kn = key0 + kAttnKeys;
+    if (kn < k1) tile_blocks(kn, p0, p1);  // scalar reads, ready by the next stage_load
     __syncthreads();  // the previous tile's LDS reads are done
-    stage_store();
+    stage_store(key0);
     __syncthreads();
-    if (key0 + kAttnKeys < k1) stage_load(key0 + kAttnKeys);  // next tile in flight meanwhile
+    if (kn < k1) stage_load(kn, p0, p1);  // next tile in flight meanwhile
 
     // S = Q K^T for keys key0 + (0..15) and key0 + 16 + (0..15)
     f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};

@@ -53,6 +53,11 @@ __device__ inline uint32_t buf1(rsrc_t r, uint32_t off) {
 
 __device__ inline int uniform(int v) { return __builtin_amdgcn_readfirstlane(v); }
 
+// Scalar (constant-cache) load of p[i] for a wave-uniform p and i, from memory that an earlier
+// launch wrote and this one only reads.
+typedef const __attribute__((address_space(4))) int32_t* kc_i32_t;
+__device__ inline int32_t sload(const int32_t* p, int i) { return ((kc_i32_t)p)[i]; }
+
 // The e8m0 scales of D consecutive trips of one weight row: bytes [4 tr0, 4 tr0 + 4D) of the
 // row, one 8- or 16-byte load instead of D byte loads. Trip tr0 + s of lane group g reads byte
 // 4s + g, i.e. byte g of dword s.

@@ -760,12 +760,10 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
 // activation loads off the vector memory path, where every lane of a wave costs address work
 // even when most of the unit's 16 token slots are empty.
 
-// Scalar (constant-cache) reads of the work list. An item's unit record and the member ids of
-// its staging rows are uniform over a wave, so they are read with scalar loads, outside the
-// vector-memory queue the trip ring keeps full: a vector load there would make the item's first
-// wait drain the ring. The list was written by an earlier launch and is read-only here.
-typedef const __attribute__((address_space(4))) int32_t* kc_i32_t;
-__device__ inline int32_t sload(const int32_t* p, int i) { return ((kc_i32_t)p)[i]; }
+// Scalar (constant-cache) reads of the work list (`sload`). An item's unit record and the member
+// ids of its staging rows are uniform over a wave, so they are read with scalar loads, outside
+// the vector-memory queue the trip ring keeps full: a vector load there would make the item's
+// first wait drain the ring. The list was written by an earlier launch and is read-only here.
 
 // Wait for this wave's LDS operations, then workgroup barrier. Vector memory loads (the trip
 // ring) stay in flight across it.

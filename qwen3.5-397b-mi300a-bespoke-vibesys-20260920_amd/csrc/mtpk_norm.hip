@@ -9,7 +9,8 @@
 // r / heads_per_token, read at token * token_stride + head * head_stride, so head slices of a
 // projection output are read in place. fp32 arithmetic throughout.
 //
-// Layout of the work: a row of `dim` elements is split over G = min(64, dim / 8) lanes, each
+// Layout of the work (rows of a multiple of 2048 elements without RoPE: k_rownorm_row, one row
+// per workgroup): a row of `dim` elements is split over G = min(64, dim / 8) lanes, each
 // lane holding chunks of 8 consecutive elements (chunk c = lane-in-group + G * i); a wave
 // holds 64 / G rows, a workgroup 4 waves. The sum of squares is a butterfly over the G lanes.
 
@@ -181,6 +182,61 @@ __global__ __launch_bounds__(256) void k_rownorm(NormArgs a) {
     if (i < nch) store8(a.out, a.o_dt, oo + (gl + G * i) * 8, v[i]);
 }
 
+// Wide rows (dim >= 1024, no RoPE): one row per workgroup, NCH chunks of 8 per thread, so a
+// few hundred rows still fill the chip; the weight (and gate) loads are issued before the
+// reduction, which goes through the four waves' partial sums in LDS.
+template <int NCH>
+__global__ __launch_bounds__(256) void k_rownorm_row(NormArgs a) {
+  __shared__ float part[4];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
+  const int64_t r = blockIdx.x;
+  const int64_t tok = r / a.hpt, head = r - tok * a.hpt;
+  const int64_t xo = tok * a.x_ts + head * a.x_hs, oo = r * a.dim, go = tok * a.g_ts + head * a.g_hs;
+  float v[NCH][8], wv[NCH][8], gv[NCH][8];
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int e = (tid + 256 * i) * 8;
+    load8(a.x, a.x_dt, xo + e, v[i]);
+    if (a.kind != 2) load8(a.w, a.w_dt, e, wv[i]);
+    if (a.gate) load8(a.gate, a.g_dt, go + e, gv[i]);
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    const int e = (tid + 256 * i) * 8;
+    if (a.res) {
+      float rv[8];
+      load8(a.res, a.res_dt, oo + e, rv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        v[i][j] = a.x_dt == MTPK_BF16 ? round_bf16(v[i][j] + rv[j]) : v[i][j] + rv[j];
+      store8(a.sum_out, a.x_dt, oo + e, v[i]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) ss += v[i][j] * v[i][j];
+  }
+  ss = wave_sum(ss);
+  if (lane == 0) part[wave] = ss;
+  __syncthreads();
+  ss = (part[0] + part[1]) + (part[2] + part[3]);
+  const float inv = a.kind == 2 ? rsqrtf(ss + a.eps) : rsqrtf(ss / (float)a.dim + a.eps);
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    float y[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      if (a.kind == 2)
+        y[j] = v[i][j] * inv * a.scale;
+      else if (a.kind == 0)
+        y[j] = (v[i][j] * inv) * (1.f + wv[i][j]);
+      else
+        y[j] = a.gate ? (v[i][j] * inv * wv[i][j]) * (gv[i][j] / (1.f + __expf(-gv[i][j])))
+                      : v[i][j] * inv * wv[i][j];
+    }
+    store8(a.out, a.o_dt, oo + (tid + 256 * i) * 8, y);
+  }
+}
+
 }  // namespace mtpk
 
 using namespace mtpk;
@@ -223,10 +279,21 @@ int mtpk_rownorm(const void* x, int x_dtype, int64_t x_token_stride, int64_t x_h
              w,        w_dtype,  kind,           eps,           scale, gate,       gate_dtype,
              gate_token_stride, gate_head_stride, rope_cos,     rope_sin, rope_pos, rot_dim,
              out,      out_dtype, rows,          heads_per_token, dim};
+  const hipStream_t st = (hipStream_t)stream;
+  if (!rope_cos && dim % 2048 == 0 && dim <= 8192) {  // one row per workgroup
+    if (rows > INT32_MAX) return MTPK_EINVAL;
+    const dim3 grid((unsigned)rows);
+    switch (dim / 2048) {
+      case 1: hipLaunchKernelGGL(k_rownorm_row<1>, grid, dim3(256), 0, st, a); break;
+      case 2: hipLaunchKernelGGL(k_rownorm_row<2>, grid, dim3(256), 0, st, a); break;
+      case 3: hipLaunchKernelGGL(k_rownorm_row<3>, grid, dim3(256), 0, st, a); break;
+      default: hipLaunchKernelGGL(k_rownorm_row<4>, grid, dim3(256), 0, st, a); break;
+    }
+    return status_of(hipGetLastError());
+  }
   const int rpw = 64 / g;
   const int64_t wgs = (rows + 4 * rpw - 1) / (4 * rpw);
   if (wgs > INT32_MAX) return MTPK_EINVAL;
-  const hipStream_t st = (hipStream_t)stream;
   switch (g) {
     case 64: hipLaunchKernelGGL(k_rownorm<64>, dim3((unsigned)wgs), dim3(256), 0, st, a); break;
     case 32: hipLaunchKernelGGL(k_rownorm<32>, dim3((unsigned)wgs), dim3(256), 0, st, a); break;

@@ -21,6 +21,7 @@ from dataclasses import dataclass
 import torch
 
 import _mtpk
+import attention
 
 MAX_STOP_IDS = 8
 """Widest per-lane stop-id set a speculative round accepts (`mtp.py:80`)."""
@@ -138,7 +139,9 @@ def attach(model, k: int | None = None, seed: int = 1, expert_mode: str = "quant
         pre_fc_norm_embedding=vm._normal((c.hidden,), 0.02, dt, dev, gen),
         pre_fc_norm_hidden=vm._normal((c.hidden,), 0.02, dt, dev, gen),
         norm=vm._normal((c.hidden,), 0.02, dt, dev, gen),
-        pool={"k": torch.zeros(shape, dtype=dt, device=dev), "v": torch.zeros(shape, dtype=dt, device=dev)},
+        pool={"k": torch.zeros(shape, dtype=dt, device=dev),
+              "v": torch.zeros(model.blocks.rows // c.block_size, c.kv_heads, c.head_dim, c.block_size,
+                               dtype=dt, device=dev)},
     )
     model.mtp = m
     return m
@@ -230,9 +233,9 @@ def cache_target_rows(model, mtp: MTP, tokens: torch.Tensor, raw_previous_hidden
     if keep is not None:
         live = keep.reshape(-1)
         k = torch.where(live[:, None, None], k, mtp.pool["k"][rows])
-        v = torch.where(live[:, None, None], v, mtp.pool["v"][rows])
+        v = torch.where(live[:, None, None], v, attention.read_v(mtp.pool["v"], rows))
     mtp.pool["k"][rows] = k
-    mtp.pool["v"][rows] = v
+    attention.write_v(mtp.pool["v"], rows, v)
 
 
 def verify_and_commit(model, mtp: MTP, slots: list[int], base_tokens: list[int],

@@ -198,8 +198,9 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                     block_table: torch.Tensor, base_pos: torch.Tensor, ctx_blocks: int,
                     block_size: int, scale: float) -> torch.Tensor:
     """Causal attention of `t` new query rows per lane over the paged cache
-    (`verify_attention_paged`, `model.py:1120-1205`). `q` `[B, heads, t, hd]`; pools
-    `[rows, kv_heads, hd]` already hold this round's rows; query row `s` of lane `b` sits at
+    (`verify_attention_paged`, `model.py:1120-1205`). `q` `[B, heads, t, hd]`; the pools (K
+    `[rows, kv_heads, hd]`, V `[rows / block, kv_heads, hd, block]`, see `attention.v_blocks`)
+    already hold this round's rows; query row `s` of lane `b` sits at
     `base_pos[b] + s` and sees every cached position up to its own. `ctx_blocks` bounds the
     gather (a host value, at least every lane's block count). fp32 math, q's dtype out. bf16
     device tensors with 16-row blocks and head_dim 64/128/256 go to the HIP kernel
@@ -215,7 +216,7 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     rows = (blocks[:, :, None] * block_size + tok).reshape(b, -1)  # [B, S]
     s_len = rows.shape[1]
     keys = k_pool[rows].float().permute(0, 2, 3, 1).contiguous()  # [B, kvh, hd, S]
-    vals = v_pool[rows].float().permute(0, 2, 1, 3).contiguous()  # [B, kvh, S, hd]
+    vals = attention.read_v(v_pool, rows).float().permute(0, 2, 1, 3).contiguous()  # [B, kvh, S, hd]
     qg = q.float().reshape(b, kvh, group * t, hd)
     scores = torch.matmul(qg, keys) * scale  # [B, kvh, group*t, S]
     qpos = base_pos.long()[:, None] + torch.arange(t, device=q.device)[None, :]  # [B, t]
@@ -250,7 +251,7 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
     rows = write_rows.reshape(-1).long()
     pool["k"][rows] = k.reshape(-1, c.kv_heads, c.head_dim)
-    pool["v"][rows] = v.reshape(-1, c.kv_heads, c.head_dim)
+    attention.write_v(pool["v"], rows, v.reshape(-1, c.kv_heads, c.head_dim))
     out = paged_attention(q.transpose(1, 2), pool["k"], pool["v"], block_table, base_pos, ctx_blocks,
                           c.block_size, c.head_dim ** -0.5)
     out = out.transpose(1, 2).reshape(b, t, -1)
@@ -432,10 +433,11 @@ class Model:
         self.blocks = BlockTables(lanes, max_seq, cfg.block_size, dev, seed)
         self.pool: list[dict] = []
         for ty in cfg.layer_types:
-            if ty == ATTN:
+            if ty == ATTN:  # V transposed inside each block (attention.v_blocks)
                 shape = (self.blocks.rows, cfg.kv_heads, cfg.head_dim)
+                vshape = (self.blocks.rows // cfg.block_size, cfg.kv_heads, cfg.head_dim, cfg.block_size)
                 self.pool.append({"k": torch.zeros(shape, dtype=dtype, device=dev),
-                                  "v": torch.zeros(shape, dtype=dtype, device=dev)})
+                                  "v": torch.zeros(vshape, dtype=dtype, device=dev)})
             else:
                 self.pool.append({
                     "conv": torch.zeros(lanes, cfg.conv_dim, cfg.conv_k - 1, dtype=dtype, device=dev),

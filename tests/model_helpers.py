@@ -4,6 +4,7 @@ from __future__ import annotations
 
 import torch
 
+import attention
 import mtp
 import verify_model as vm
 
@@ -48,14 +49,16 @@ def assert_slot_state_close(a: vm.Model, b: vm.Model, lane: int, length: int,
     pos = torch.arange(length, device=a.device)[None, :]
     rows_a = a.blocks.physical_rows(lanes, pos).reshape(-1)
     rows_b = b.blocks.physical_rows(lanes.to(b.device), pos.to(b.device)).reshape(-1)
+    def kv(pool, rows):  # K rows and V rows (V is kept transposed per block)
+        return pool["k"][rows], attention.read_v(pool["v"], rows)
+
     for ty, pa, pb in zip(a.cfg.layer_types, a.pool, b.pool, strict=True):
         if ty == vm.ATTN:
-            for name in ("k", "v"):
-                torch.testing.assert_close(pa[name][rows_a].cpu(), pb[name][rows_b].cpu(), rtol=rtol, atol=atol)
+            for ta, tb in zip(kv(pa, rows_a), kv(pb, rows_b), strict=True):
+                torch.testing.assert_close(ta.cpu(), tb.cpu(), rtol=rtol, atol=atol)
         else:
             for name in ("conv", "rec"):
                 torch.testing.assert_close(pa[name][lane].cpu(), pb[name][lane].cpu(), rtol=rtol, atol=atol)
-    for name in ("k", "v"):
-        torch.testing.assert_close(a.mtp.pool[name][rows_a].cpu(), b.mtp.pool[name][rows_b].cpu(),
-                                   rtol=rtol, atol=atol)
+    for ta, tb in zip(kv(a.mtp.pool, rows_a), kv(b.mtp.pool, rows_b), strict=True):
+        torch.testing.assert_close(ta.cpu(), tb.cpu(), rtol=rtol, atol=atol)
     torch.testing.assert_close(a.cached_hidden(lane).cpu(), b.cached_hidden(lane).cpu(), rtol=rtol, atol=atol)

@@ -36,7 +36,8 @@ def _case(seed, b, heads, kvh, hd, t, base, max_blocks):
 def _check(dev, q, k, v, table, base, scale):
     t = q.shape[2]
     ctx = int(base.max()) + t
-    got = attention.paged_attention(q.to(dev), k.to(dev), v.to(dev), torch.from_numpy(table).to(dev),
+    got = attention.paged_attention(q.to(dev), k.to(dev), attention.v_blocks(v).to(dev),
+                                    torch.from_numpy(table).to(dev),
                                     torch.from_numpy(base).to(dev), ctx, scale)
     want = ar.paged_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), table, base, scale)
     got = got.float().cpu().numpy()

@@ -14,6 +14,7 @@ import pytest
 import torch
 import torch.nn.functional as F
 
+import attention
 import mtp
 import verify_model as vm
 from tests import model_helpers as mh
@@ -132,7 +133,9 @@ def test_paged_attention_matches_dense_per_lane() -> None:
     k_pool = torch.randn(tables.rows, kvh, hd, generator=gen)
     v_pool = torch.randn(tables.rows, kvh, hd, generator=gen)
     q = torch.randn(lanes, heads, t, hd, generator=gen)
-    got = vm.paged_attention(q, k_pool, v_pool, tables.table, torch.tensor(base), tables.max_blocks, bs, 0.3)
+    v_cache = attention.v_blocks(v_pool, bs)
+    assert torch.equal(attention.v_rows(v_cache), v_pool)
+    got = vm.paged_attention(q, k_pool, v_cache, tables.table, torch.tensor(base), tables.max_blocks, bs, 0.3)
     for j, p in enumerate(base):
         rows = tables.physical_rows(torch.tensor([j]), torch.arange(p + t)[None])[0]
         for hh in range(heads):
