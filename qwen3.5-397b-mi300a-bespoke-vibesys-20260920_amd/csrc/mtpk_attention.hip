@@ -53,6 +53,31 @@ __device__ __host__ inline void attn_split_range(int ctx, int n_split, int sp, i
   k1 = min((sp + 1) * per * kAttnKeys, ctx);
 }
 
+// Max / sum over the 16 lanes of a DPP row (lanes 16r .. 16r + 15), every lane getting the
+// result: quad_perm swaps (xor 1, xor 2) combine each quad, row_half_mirror (lane i with 7 - i
+// inside each 8) the two quads of a half, row_mirror (i with 15 - i) the two halves. Register
+// moves, no LDS round trip.
+template <int CTRL>
+__device__ inline float dpp_mov(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+
+__device__ inline float row16_max(float v) {
+  v = fmaxf(v, dpp_mov<0xB1>(v));   // quad_perm [1, 0, 3, 2]
+  v = fmaxf(v, dpp_mov<0x4E>(v));   // quad_perm [2, 3, 0, 1]
+  v = fmaxf(v, dpp_mov<0x141>(v));  // row_half_mirror
+  v = fmaxf(v, dpp_mov<0x140>(v));  // row_mirror
+  return v;
+}
+
+__device__ inline float row16_sum(float v) {
+  v += dpp_mov<0xB1>(v);
+  v += dpp_mov<0x4E>(v);
+  v += dpp_mov<0x141>(v);
+  v += dpp_mov<0x140>(v);
+  return v;
+}
+
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
     const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
@@ -181,24 +206,21 @@ __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
       s0 = mfma16x16x32(qa[ds], kb0, s0);
       s1 = mfma16x16x32(qa[ds], kb1, s1);
     }
-    // online softmax, base 2: row 4g + i, keys c and 16 + c of this lane
+    // online softmax, base 2: row 4g + i, keys c and 16 + c of this lane. m is the row max
+    // (uniform over the row's 16 lanes); l is this lane's own share of the row sum, reduced
+    // over the 16 lanes once, after the last tile.
     const int pa = key0 + c, pb = key0 + 16 + c;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const bool la = pa < k1 && pa <= qpos[i], lb = pb < k1 && pb <= qpos[i];
       const float xa = la ? s0[i] * scale_log2 : -INFINITY;
       const float xb = lb ? s1[i] * scale_log2 : -INFINITY;
-      float tm = fmaxf(xa, xb);
-#pragma unroll
-      for (int sh = 1; sh < 16; sh <<= 1) tm = fmaxf(tm, __shfl_xor(tm, sh, 16));
+      const float tm = row16_max(fmaxf(xa, xb));
       const float mn = fmaxf(m[i], tm);
       const float alpha = mn == -INFINITY ? 1.f : exp2f(m[i] - mn);
       const float ea = la ? exp2f(xa - mn) : 0.f;
       const float eb = lb ? exp2f(xb - mn) : 0.f;
-      float rs = ea + eb;
-#pragma unroll
-      for (int sh = 1; sh < 16; sh <<= 1) rs += __shfl_xor(rs, sh, 16);
-      l[i] = l[i] * alpha + rs;
+      l[i] = l[i] * alpha + (ea + eb);
       m[i] = mn;
 #pragma unroll
       for (int dt = 0; dt < G::kDt; ++dt) o[dt][i] *= alpha;
@@ -216,6 +238,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
     }
   }
 
+#pragma unroll
+  for (int i = 0; i < 4; ++i) l[i] = row16_sum(l[i]);
   // rows 4g + i of this lane: o[dt][i] is d = 16 dt + c
   const int64_t slot = ((int64_t)(b * kvh + kh) * row_groups + rg) * n_split + sp;
 #pragma unroll
