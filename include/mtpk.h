@@ -235,6 +235,24 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
                     const float* k, const float* v, const float* g, const float* beta,
                     const int64_t* lengths, float* out, void* stream);
 
+/* ---------------------------------------------------------------- skinny bf16 GEMM
+ * y[M, N] = x[M, K] . w[N, K]^T for M <= 64 token rows, bf16 in, fp32 accumulation: the
+ * weight-bandwidth-bound linears of the MTP draft step (fc, q/k/v/o projections), the shared
+ * expert and router of a decode or draft MoE layer (`swiglu_mlp`, model.py:638-649;
+ * model.py:2811-2873) and the LM head (`greedy_token`, mtp.py:640-658). x, w contiguous,
+ * 16-byte aligned; K a multiple of 256; N * K * 2 < 2^31.
+ * epilogue 0: out = y, f32 or bf16 [M, N].
+ * epilogue 1: rows [0, N/2) are gate and [N/2, N) up (the `load_experts` gate_up order):
+ *             out[m, j] = silu(y[m, j]) * y[m, N/2 + j], [M, N/2]; N/2 a multiple of 16.
+ * epilogue 2: out int64 [M] = first-occurrence argmax over n of bf16(y[m, n]) (the argmax of
+ *             the bf16 logits epilogue 0 would store).
+ * workspace: mtpk_gemm_workspace_bytes(m, n, k, epilogue) bytes (split-K partials or argmax
+ * keys; 0 means none is needed). */
+int64_t mtpk_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epilogue);
+int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
+                   int epilogue, void* out, int out_dtype, void* workspace,
+                   int64_t workspace_bytes, void* stream);
+
 /* ---------------------------------------------------------------- row norms
  * One launch per normalisation of the verify / draft forward, in place of the torch op chains
  * of `rmsnorm` (model.py:587-604), the DeltaNet output norm (model.py:613-619), the DeltaNet

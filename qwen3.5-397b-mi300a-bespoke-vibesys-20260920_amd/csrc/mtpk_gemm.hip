@@ -1,0 +1,321 @@
+// bf16 weight-streaming GEMM for few token rows on gfx950: Y[M, N] = X[M, K] . W[N, K]^T with
+// M <= 64, the shape of the MTP draft step's projections (M = B = 48), the LM head
+// (`greedy_token`, mtp.py:640-658; N = vocab) and the shared expert / router of a decode or
+// draft MoE layer (model.py:2811-2873). These are weight-bandwidth bound: every weight byte is
+// read once, and the token rows are the MFMA's other operand.
+//
+// Workgroup = 4 waves, tile = 64 weight rows (wave w: rows 16 w .. + 15; with the paired SiLU
+// epilogue also the matching 16 "up" rows N/2 + ...) x all M tokens (TT = ceil(M / 16) MFMA token
+// tiles). v_mfma_f32_16x16x32_bf16 with the lane layout of the MoE kernels: lane (g, c) supplies
+// K positions 8 g .. 8 g + 7 of each 32-K step, for weight row c (B) and token row c of a tile (A).
+// The token rows are staged in LDS in chunks of 256 K (double-buffered, one barrier per chunk);
+// the weights stream through a ring of D = 8 steps (16 bytes per lane per step) per wave. Chunk
+// c + 2 is loaded at the end of chunk c after that point's ring refills and stored at the end of
+// chunk c + 1, when every ring load issued before it has been consumed (vmcnt retires in order).
+//
+// Split-K: grid.y = KS workgroups share a tile's K range; with KS > 1 each writes fp32 partials
+// [KS, M, cols] and k_gemm_reduce sums them in split order and applies the epilogue, so the
+// result does not depend on scheduling.
+// Epilogues: 0 store, 1 out[m, j] = silu(y[m, j]) * y[m, N/2 + j] (j < N/2), 2 argmax over n of
+// bf16(y[m, n]) with the first-occurrence rule (one key per row and tile, then a max over tiles),
+// i.e. the argmax of the bf16 logits this kernel would store.
+
+#include "mtpk_device.h"
+#include "mtpk_host.h"
+
+namespace mtpk {
+
+constexpr int kGemmKC = 256;                 // K per staged chunk
+constexpr int kGemmSteps = kGemmKC / 32;     // MFMA steps per chunk
+constexpr int kGemmRing = 8;                 // ring depth in steps
+constexpr int kGemmRow = kGemmKC * 2 + 16;   // LDS bytes of one token row (padded)
+enum { kEpiStore = 0, kEpiSilu = 1, kEpiArgmax = 2 };
+
+struct GemmArgs {
+  const uint16_t* x;
+  const uint16_t* w;
+  int M, N, K, KS, epi, odt, cols;  // cols: output columns (N, or N / 2 for the SiLU epilogue)
+  void* out;
+  float* part;
+  uint64_t* keys;  // argmax: [M, tiles]
+};
+
+template <int TT, int S>
+__global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t xs[2][TT * 16 * kGemmRow];
+  __shared__ uint64_t kred[4][TT * 16];
+  const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int tile = blockIdx.x, ks = blockIdx.y;
+  const int kc_per = a.K / kGemmKC / a.KS;  // chunks of this split
+  const int k0 = ks * kc_per * kGemmKC;
+  const int nchunk = kc_per;
+  // weight rows of this wave: stream 0 at n0 + 16 wave + c, stream 1 at N/2 + the same
+  const int r0 = tile * 64 + 16 * wave + ln.c;
+  int wrow[S];
+  bool wok[S];
+#pragma unroll
+  for (int s = 0; s < S; ++s) {
+    const int r = r0 + s * (a.N / 2);
+    wok[s] = S == 1 ? r < a.N : r0 < a.cols;
+    wrow[s] = wok[s] ? r : 0;
+  }
+  const rsrc_t rw = make_rsrc(a.w, 0x7fffffff);
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2));
+  // ring step st of this split: K = k0 + 32 st + 8 g .. + 7 of each stream's row
+  auto issue = [&](u32x4_t* v, int st) {
+    const bool in = st < nchunk * kGemmSteps;
+#pragma unroll
+    for (int s = 0; s < S; ++s) {
+      const uint32_t off = (uint32_t)(((int64_t)wrow[s] * a.K + k0 + 32 * st + 8 * ln.g) * 2);
+      v[s] = buf16(rw, (wok[s] && in) ? off : kOutOfRange);
+    }
+  };
+  // staging: load j moves 16 bytes of token row (256 j + tid) / 32, column (tid % 32) * 16
+  constexpr int kSL = TT * 2;  // 16-byte loads per thread per chunk
+  u32x4_t sreg[kSL];
+  auto stage_load = [&](int c) {
+#pragma unroll
+    for (int j = 0; j < kSL; ++j) {
+      const int p = j * 256 + tid, row = p >> 5, col = p & 31;
+      const bool ok = c < nchunk && row < a.M;
+      sreg[j] = buf16(rx, ok ? (uint32_t)(((int64_t)row * a.K + k0 + c * kGemmKC + col * 8) * 2)
+                             : kOutOfRange);
+    }
+  };
+  auto stage_store = [&](int b) {
+#pragma unroll
+    for (int j = 0; j < kSL; ++j) {
+      const int p = j * 256 + tid, row = p >> 5, col = p & 31;
+      lds16_store(&xs[b][row * kGemmRow + col * 16], sreg[j]);
+    }
+  };
+
+  f32x4_t acc[S][TT];
+#pragma unroll
+  for (int s = 0; s < S; ++s)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[s][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  stage_load(0);
+  ring_fence();
+  u32x4_t ring[kGemmRing][S];
+#pragma unroll
+  for (int st = 0; st < kGemmRing; ++st) issue(ring[st], st);
+  ring_fence();
+  stage_store(0);
+  stage_load(1);
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __syncthreads();
+  int c = 0;
+#pragma clang loop unroll(disable)
+  do {
+    const uint8_t* buf = xs[c & 1];
+#pragma unroll
+    for (int st = 0; st < kGemmSteps; ++st) {
+      const uint8_t* arow = buf + ln.c * kGemmRow + (32 * st + 8 * ln.g) * 2;
+      u32x4_t av[TT];
+#pragma unroll
+      for (int t = 0; t < TT; ++t) av[t] = lds16(arow + t * 16 * kGemmRow);
+#pragma unroll
+      for (int s = 0; s < S; ++s)
+#pragma unroll
+        for (int t = 0; t < TT; ++t)
+          acc[s][t] = mfma16x16x32(as_bf16x8(av[t]), as_bf16x8(ring[st][s]), acc[s][t]);
+      ring_fence();
+      issue(ring[st], c * kGemmSteps + st + kGemmRing);
+      ring_fence();
+    }
+    if (c + 1 < nchunk) stage_store((c + 1) & 1);
+    stage_load(c + 2);
+    __builtin_amdgcn_s_waitcnt(0xC07F);
+    __syncthreads();
+  } while (++c < nchunk);
+
+  // lane (g, c): acc[s][t][i] is token m = 16 t + 4 g + i, column r0 (stream s)
+  if (a.KS > 1) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int m = 16 * t + 4 * ln.g + i;
+        if (m >= a.M) continue;
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          const int col = S == 1 ? r0 : r0 + s * a.cols;  // partial columns: gate, then up
+          if (!wok[s]) continue;
+          a.part[((int64_t)ks * a.M + m) * (int64_t)(S * a.cols) + col] = acc[s][t][i];
+        }
+      }
+    return;
+  }
+  if (a.epi == kEpiArgmax) {
+    // first-occurrence argmax of the bf16 values: the max key over this wave's 16 columns,
+    // then over the 4 waves
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = bf16_to_f32(f32_to_bf16(acc[0][t][i]));
+        uint64_t key = wok[0] ? argmax_key(v, (uint32_t)r0) : 0;
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          const uint32_t lo = __shfl_xor((uint32_t)key, o, kWave);
+          const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), o, kWave);
+          const uint64_t k2 = ((uint64_t)hi << 32) | lo;
+          key = k2 > key ? k2 : key;
+        }
+        if (ln.c == 0) kred[wave][16 * t + 4 * ln.g + i] = key;
+      }
+    __syncthreads();
+    for (int m = tid; m < a.M; m += 256) {
+      uint64_t b = kred[0][m];
+      for (int w2 = 1; w2 < 4; ++w2) b = kred[w2][m] > b ? kred[w2][m] : b;
+      a.keys[(int64_t)m * gridDim.x + tile] = b;
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * t + 4 * ln.g + i;
+      if (m >= a.M || !wok[0]) continue;
+      float v = acc[0][t][i];
+      if (S == 2) v = v / (1.f + __expf(-v)) * acc[1][t][i];
+      store_float(a.out, a.odt, (int64_t)m * a.cols + r0, v);
+    }
+}
+
+// Split-K reduction: out[m, col] = epilogue(sum over ks of part[ks, m, .]) in split order.
+__global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int KS, int M,
+                                                     int cols, int epi, void* __restrict__ out,
+                                                     int odt) {
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= (int64_t)M * cols) return;
+  const int64_t m = idx / cols, col = idx - m * cols;
+  const int pc = epi == kEpiSilu ? 2 * cols : cols;
+  float g = 0.f, u = 0.f;
+  for (int ks = 0; ks < KS; ++ks) {
+    const float* p = part + ((int64_t)ks * M + m) * pc;
+    g += p[col];
+    if (epi == kEpiSilu) u += p[cols + col];
+  }
+  const float v = epi == kEpiSilu ? g / (1.f + __expf(-g)) * u : g;
+  store_float(out, odt, m * cols + col, v);
+}
+
+// One workgroup per row: the max over the row's tile keys (thousands for an LM head), strided
+// over the threads, then over the waves.
+__global__ __launch_bounds__(256) void k_gemm_argmax_final(const uint64_t* __restrict__ keys,
+                                                           int M, int tiles,
+                                                           int64_t* __restrict__ out) {
+  __shared__ uint64_t red[4];
+  const int m = blockIdx.x, tid = threadIdx.x;
+  uint64_t b = 0;
+  for (int t = tid; t < tiles; t += 256) {
+    const uint64_t k = keys[(int64_t)m * tiles + t];
+    b = k > b ? k : b;
+  }
+  b = wave_max_u64(b);
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = b;
+  __syncthreads();
+  if (tid == 0) {
+    uint64_t r = red[0];
+    for (int w = 1; w < 4; ++w) r = red[w] > r ? red[w] : r;
+    out[m] = (int64_t)argmax_key_index(r);
+  }
+}
+
+namespace {
+
+int gemm_cols(int64_t n, int epi) { return (int)(epi == kEpiSilu ? n / 2 : n); }
+
+// Split count: a power of two dividing K / 256, enough workgroups for ~3 per CU, at least 4
+// chunks per split; argmax takes no split.
+int gemm_splits(int64_t m, int64_t n, int64_t k, int epi) {
+  if (epi == kEpiArgmax) return 1;
+  const int64_t tiles = (gemm_cols(n, epi) + 63) / 64;
+  const int64_t chunks = k / kGemmKC;
+  const int64_t want = (3 * (int64_t)device_cu_count() + tiles - 1) / tiles;
+  int ks = 1;
+  while (ks * 2 <= want && chunks % (ks * 2) == 0 && chunks / (ks * 2) >= 4) ks *= 2;
+  return ks;
+}
+
+template <int TT, int S>
+void launch_gemm(const GemmArgs& a, int tiles, hipStream_t st) {
+  hipLaunchKernelGGL((k_gemm_skinny<TT, S>), dim3((unsigned)tiles, (unsigned)a.KS), dim3(256), 0,
+                     st, a);
+}
+
+}  // namespace
+
+}  // namespace mtpk
+
+using namespace mtpk;
+
+extern "C" {
+
+int64_t mtpk_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epilogue) {
+  if (m <= 0 || m > 64 || n <= 0 || k <= 0 || k % kGemmKC || epilogue < 0 || epilogue > 2) return 0;
+  const int ks = gemm_splits(m, n, k, epilogue);
+  const int64_t tiles = (gemm_cols(n, epilogue) + 63) / 64;
+  if (epilogue == kEpiArgmax) return m * tiles * 8;
+  if (ks == 1) return 0;
+  return (int64_t)ks * m * (epilogue == kEpiSilu ? n : gemm_cols(n, epilogue)) * 4;
+}
+
+int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, int64_t n,
+                   int epilogue, void* out, int out_dtype, void* workspace,
+                   int64_t workspace_bytes, void* stream) {
+  if (!x || !w || !out) return MTPK_EINVAL;
+  if (m < 0 || m > 64 || n <= 0 || k <= 0 || k % kGemmKC || epilogue < 0 || epilogue > 2)
+    return MTPK_EINVAL;
+  if (epilogue == kEpiSilu && (n % 2 || (n / 2) % 16)) return MTPK_EINVAL;
+  if (epilogue != kEpiArgmax && out_dtype != MTPK_F32 && out_dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (!aligned16(x) || !aligned16(w)) return MTPK_EINVAL;
+  if (n * k * 2 > 0x7fffffffLL || m * k * 2 > 0x7fffffffLL || n > INT32_MAX / 2) return MTPK_EINVAL;
+  if (workspace_bytes < mtpk_gemm_workspace_bytes(m > 0 ? m : 1, n, k, epilogue)) return MTPK_EINVAL;
+  if (m == 0) return 0;
+  const int ks = gemm_splits(m, n, k, epilogue);
+  if ((ks > 1 || epilogue == kEpiArgmax) && !workspace) return MTPK_EINVAL;
+  const int cols = gemm_cols(n, epilogue);
+  const int tiles = (cols + 63) / 64;
+  GemmArgs a{x, w, (int)m, (int)n, (int)k, ks, epilogue, out_dtype, cols, out,
+             ks > 1 ? static_cast<float*>(workspace) : nullptr,
+             epilogue == kEpiArgmax ? static_cast<uint64_t*>(workspace) : nullptr};
+  const hipStream_t st = (hipStream_t)stream;
+  const int tt = (int)((m + 15) / 16);
+  if (epilogue == kEpiSilu) {
+    switch (tt) {
+      case 1: launch_gemm<1, 2>(a, tiles, st); break;
+      case 2: launch_gemm<2, 2>(a, tiles, st); break;
+      case 3: launch_gemm<3, 2>(a, tiles, st); break;
+      default: launch_gemm<4, 2>(a, tiles, st); break;
+    }
+  } else {
+    switch (tt) {
+      case 1: launch_gemm<1, 1>(a, tiles, st); break;
+      case 2: launch_gemm<2, 1>(a, tiles, st); break;
+      case 3: launch_gemm<3, 1>(a, tiles, st); break;
+      default: launch_gemm<4, 1>(a, tiles, st); break;
+    }
+  }
+  int rc = status_of(hipGetLastError());
+  if (rc) return rc;
+  if (epilogue == kEpiArgmax) {
+    hipLaunchKernelGGL(k_gemm_argmax_final, dim3((unsigned)m), dim3(256), 0, st,
+                       a.keys, (int)m, tiles, static_cast<int64_t*>(out));
+    return status_of(hipGetLastError());
+  }
+  if (ks > 1) {
+    const int64_t total = m * cols;
+    hipLaunchKernelGGL(k_gemm_reduce, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, st,
+                       a.part, ks, (int)m, cols, epilogue, out, out_dtype);
+    return status_of(hipGetLastError());
+  }
+  return 0;
+}
+
+}  // extern "C"

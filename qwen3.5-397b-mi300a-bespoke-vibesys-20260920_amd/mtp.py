@@ -94,12 +94,11 @@ def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
 
 def greedy_token(model, normed: torch.Tensor) -> torch.Tensor:
     """`model.unembed(normed).float().argmax(-1, keepdim=True)` for `[B, hidden]` rows, `[B, 1]`
-    long. On a device the argmax is the HIP kernel; the fp32 cast is not needed because the
-    kernel compares bf16 logits exactly."""
-    logits = model.unembed(normed)
-    if logits.device.type == "cuda":
-        return argmax_rows(logits)[..., None]
-    return logits.float().argmax(-1, keepdim=True)
+    long. On a device this is `model.next_tokens` (the HIP argmax compares the bf16 logits
+    exactly, so the fp32 cast is not needed)."""
+    if normed.device.type == "cuda":
+        return model.next_tokens(normed)[..., None]
+    return model.unembed(normed).float().argmax(-1, keepdim=True)
 
 
 # ---------------------------------------------------------------- the MTP head
@@ -185,7 +184,7 @@ def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: 
     x, hm = vm.add_rmsnorm(x, attn, w["post_norm"], c.eps)
     _, normed = vm.add_rmsnorm(x, model.moe(w, hm[:, 0])[:, None], mtp.norm, c.eps)
     normed = normed[:, 0]
-    nxt = model.argmax(model.unembed(normed))[:, None]
+    nxt = model.next_tokens(normed)[:, None]
     return normed, nxt
 
 
@@ -222,9 +221,9 @@ def cache_target_rows(model, mtp: MTP, tokens: torch.Tensor, raw_previous_hidden
     x = _combine_rows(model, mtp, draft_seed(model, raw_previous_hidden), tokens)
     x = vm.rmsnorm(x, w["in_norm"], c.eps)
     lead = tokens.shape
-    k = vm.rmsnorm(torch.nn.functional.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim),
+    k = vm.rmsnorm(vm.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim),
                    w["k_norm"], c.eps)
-    v = torch.nn.functional.linear(x, w["v_proj"]).view(*lead, c.kv_heads, c.head_dim)
+    v = vm.linear(x, w["v_proj"]).view(*lead, c.kv_heads, c.head_dim)
     pos = positions.long()
     k = vm.apply_rope(k, model.cos[pos][..., None, :], model.sin[pos][..., None, :])
     rows = write_rows.reshape(-1).long()

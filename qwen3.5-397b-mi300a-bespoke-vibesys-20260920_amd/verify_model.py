@@ -33,6 +33,7 @@ import torch.nn.functional as F
 
 import attention
 import deltanet
+import dense
 import mxfp4
 import mxfp4_gemv
 import router_fused
@@ -103,6 +104,29 @@ def verify_cfg() -> Cfg:
 
 
 # ---------------------------------------------------------------- layer math
+
+SMALL_WEIGHT_BYTES = 32 << 20
+"""Linears of at most this many weight bytes and <= 64 rows take the skinny HIP GEMM
+(`dense`): they are launch-latency bound, where it beats the library GEMM by 4-15 us per call on
+MI355X; larger ones are bandwidth bound and stay on the library GEMM, which is as fast there."""
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """`F.linear(x, w)`; small weights at few rows run on `dense.linear`."""
+    if w.numel() * w.element_size() <= SMALL_WEIGHT_BYTES and dense.fits(x, w):
+        return dense.linear(x, w)
+    return F.linear(x, w)
+
+
+def swiglu(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor) -> torch.Tensor:
+    """`down(silu(gate(x)) * up(x))` with `w_gate_up = cat([gate; up])` (`model.py:638-649`); the
+    gate/up GEMM and its SiLU product are one launch when the skinny GEMM takes the shapes."""
+    if w_gate_up.numel() * w_gate_up.element_size() <= SMALL_WEIGHT_BYTES and dense.fits(x, w_gate_up):
+        act = dense.silu_linear(x, w_gate_up)
+    else:
+        gate, up = F.linear(x, w_gate_up).chunk(2, dim=-1)
+        act = F.silu(gate) * up
+    return linear(act, w_down)
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
@@ -238,8 +262,8 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
     b, t, _ = h.shape
     qg = F.linear(h, w["q_proj"]).view(b, t, c.heads, 2 * c.head_dim)
     q, gate = qg[..., : c.head_dim], qg[..., c.head_dim :]
-    kp = F.linear(h, w["k_proj"]).view(b, t, c.kv_heads, c.head_dim)
-    v = F.linear(h, w["v_proj"]).view(b, t, c.kv_heads, c.head_dim)
+    kp = linear(h, w["k_proj"]).view(b, t, c.kv_heads, c.head_dim)
+    v = linear(h, w["v_proj"]).view(b, t, c.kv_heads, c.head_dim)
     pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
     if h.device.type == "cuda":  # q/k norm and RoPE in one row-norm launch each
         rope = (model.cos, model.sin, pos.reshape(-1))
@@ -474,7 +498,7 @@ class Model:
         """Routed MXFP4 experts + gated shared expert over rows `h` `[N, hidden]`
         (`model.py:2811-2873`)."""
         c = self.cfg
-        routing = F.linear(h, w["router_gate"])
+        routing = linear(h, w["router_gate"])
         if h.device.type == "cuda":
             top_w, top_i = router_fused.route(routing, c.experts, c.top_k, index_dtype=torch.int32)
         else:
@@ -490,8 +514,7 @@ class Model:
         else:
             routed = mxfp4_gemv.reference_moe(h, w["experts"], assign, c.top_k, (0, c.experts),
                                               mxfp4.dequant_mxfp4)
-        gate, up = F.linear(h, w["shared_gate_up"]).chunk(2, dim=-1)
-        shared = F.linear(F.silu(gate) * up, w["shared_down"])
+        shared = swiglu(h, w["shared_gate_up"], w["shared_down"])
         return routed + torch.sigmoid(routing[:, c.experts :]) * shared
 
     def attention_rows(self, w: dict, pool: dict, h: torch.Tensor, lanes: torch.Tensor,
@@ -609,6 +632,15 @@ class Model:
 
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return self.unembed(rmsnorm(hidden, self.final_norm, self.cfg.eps))
+
+    def next_tokens(self, normed: torch.Tensor) -> torch.Tensor:
+        """Greedy next token of final-normed rows `[..., hidden]`: `argmax(unembed(normed))`.
+        Up to 16 bf16 device rows take the skinny GEMM with its argmax epilogue (the logits never
+        reach memory; same first-occurrence rule over the bf16 logits, `mtp.py:640-658`)."""
+        rows = normed.numel() // normed.shape[-1]
+        if rows <= 16 and dense.fits(normed, self.lm_head):
+            return dense.argmax_linear(normed, self.lm_head)
+        return self.argmax(self.unembed(normed))
 
     def argmax(self, logits: torch.Tensor) -> torch.Tensor:
         """First-occurrence argmax over the vocab (the HIP kernel on a device)."""

@@ -53,12 +53,18 @@ def test_host_only_entry_points(lib):
 
 def test_rejected_arguments_launch_nothing(lib):
     """Argument checks run before any HIP call, so they are exercised without a device."""
+    buf0 = (ctypes.c_float * 64)()
     assert lib.mtpk_route_topk(None, 1, 1, 8, 8, 2, None, None, 3, None) == -1
     assert lib.mtpk_dequant_mxfp4(None, None, 1, 33, 0, None, None) == -1
     assert lib.mtpk_greedy_accept(None, 4, None, 3, None, None, None, None, 0, 1, 4, 3,
                                   None, None, None, None, None, None, None, None, None, None,
                                   None, None) == -1
     assert lib.mtpk_moe_prep(None, 3, None, 0, 10, 0, 512, None, None, 10, None, None) == -1
+    # skinny GEMM: rows over 64, K not a multiple of 256, null pointers
+    assert lib.mtpk_gemm_workspace_bytes(65, 64, 256, 0) == 0
+    assert lib.mtpk_gemm_bf16(None, 4, 256, None, 64, 0, None, 1, None, 0, None) == -1
+    assert lib.mtpk_gemm_bf16(p0 := ctypes.addressof(buf0), 4, 300, p0, 64, 0, p0, 1, None, 0, None) == -1
+    assert lib.mtpk_gemm_bf16(p0, 65, 256, p0, 64, 0, p0, 1, None, 0, None) == -1
     # row norm: null input, dim not a multiple of 8, unknown kind
     assert lib.mtpk_rownorm(None, 0, 64, 64, None, 0, None, None, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
                             None, None, None, 0, None, 0, 1, 1, 64, None) == -1
