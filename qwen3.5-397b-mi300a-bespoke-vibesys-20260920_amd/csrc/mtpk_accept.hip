@@ -24,24 +24,64 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
   const int tid = threadIdx.x;
   uint64_t best = 0;
   if (vec && dt == MTPK_BF16) {
+    // Four 16-byte loads in flight per thread. A chunk of 8 values updates the thread's best
+    // only if its float max beats it strictly (an equal value has a later index, so the earlier
+    // one stays: the key order), and then at the chunk's first index holding that max; +0 and
+    // -0 compare equal as the keys fold them. A chunk holding a NaN takes the key path.
     const uint16_t* base = reinterpret_cast<const uint16_t*>(logits) + row * stride;
-    for (int64_t i = begin + (int64_t)tid * 8; i < end; i += (int64_t)kArgmaxThreads * 8) {
-      if (i + 8 <= end) {
-        const u32x4_t v = ld16(base + i);
+    float bv = -INFINITY;
+    int64_t bi = -1;
+    auto chunk8 = [&](const u32x4_t& v, int64_t i0) {
+      float f[8];
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          const uint32_t w = v[q];
-          const uint64_t k0 = argmax_key(bf16_to_f32((uint16_t)(w & 0xffffu)), (uint32_t)(i + 2 * q));
-          const uint64_t k1 = argmax_key(bf16_to_f32((uint16_t)(w >> 16)), (uint32_t)(i + 2 * q + 1));
-          best = k0 > best ? k0 : best;
-          best = k1 > best ? k1 : best;
+      for (int q = 0; q < 4; ++q) {
+        f[2 * q] = bits_f32(v[q] << 16);
+        f[2 * q + 1] = bits_f32(v[q] & 0xffff0000u);
+      }
+      bool nan = false;
+      float m8 = f[0];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        nan |= f[j] != f[j];
+        m8 = fmaxf(m8, f[j]);
+      }
+      if (nan) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint64_t k = argmax_key(f[j], (uint32_t)(i0 + j));
+          best = k > best ? k : best;
         }
+      } else if (m8 > bv || bi < 0) {
+        int first = 7;
+#pragma unroll
+        for (int j = 7; j >= 0; --j)
+          if (f[j] == m8) first = j;
+        bv = m8;
+        bi = i0 + first;
+      }
+    };
+    const int64_t step = (int64_t)kArgmaxThreads * 8;
+    int64_t i = begin + (int64_t)tid * 8;
+    for (; i + 3 * step + 8 <= end; i += 4 * step) {
+      u32x4_t v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = ld16(base + i + u * step);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) chunk8(v[u], i + u * step);
+    }
+    for (; i < end; i += step) {
+      if (i + 8 <= end) {
+        chunk8(ld16(base + i), i);
       } else {
         for (int64_t q = i; q < end; ++q) {
           const uint64_t k = argmax_key(bf16_to_f32(base[q]), (uint32_t)q);
           best = k > best ? k : best;
         }
       }
+    }
+    if (bi >= 0) {
+      const uint64_t k = argmax_key(bv, (uint32_t)bi);
+      best = k > best ? k : best;
     }
   } else if (vec && dt == MTPK_F32) {
     const float* base = reinterpret_cast<const float*>(logits) + row * stride;
