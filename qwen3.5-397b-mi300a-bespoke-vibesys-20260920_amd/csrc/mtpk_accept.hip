@@ -14,6 +14,13 @@
 namespace mtpk {
 
 constexpr int kArgmaxThreads = 256;
+// 16-byte loads in flight per thread, and the workgroup count the chunking aims at. Measured
+// over [192 | 48, 248320] bf16: 4 loads and about 1024 workgroups beat 2/8/16 loads and
+// 512/2048/4096 workgroups (fewer, longer workgroups win at 48 rows; no setting gains at 192);
+// a 1024-thread workgroup per row, which would drop the second launch, streams at only about
+// 40 GB/s per CU and lost at every row count.
+constexpr int kArgmaxLoads = 4;
+constexpr int64_t kArgmaxWorkgroups = 1024;
 
 __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
     const void* __restrict__ logits, int dt, int64_t stride, int64_t vocab, int64_t chunk,
@@ -24,7 +31,7 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
   const int tid = threadIdx.x;
   uint64_t best = 0;
   if (vec && dt == MTPK_BF16) {
-    // Four 16-byte loads in flight per thread. A chunk of 8 values updates the thread's best
+    // kArgmaxLoads 16-byte loads in flight per thread. A chunk of 8 values updates the thread's best
     // only if its float max beats it strictly (an equal value has a later index, so the earlier
     // one stays: the key order), and then at the chunk's first index holding that max; +0 and
     // -0 compare equal as the keys fold them. A chunk holding a NaN takes the key path.
@@ -61,21 +68,21 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
       }
     };
     const int64_t step = (int64_t)kArgmaxThreads * 8;
-    int64_t i = begin + (int64_t)tid * 8;
-    for (; i + 3 * step + 8 <= end; i += 4 * step) {
-      u32x4_t v[4];
+    for (int64_t i = begin + (int64_t)tid * 8; i < end; i += kArgmaxLoads * step) {
+      u32x4_t v[kArgmaxLoads];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = ld16(base + i + u * step);
+      for (int u = 0; u < kArgmaxLoads; ++u)
+        if (i + u * step + 8 <= end) v[u] = ld16(base + i + u * step);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) chunk8(v[u], i + u * step);
-    }
-    for (; i < end; i += step) {
-      if (i + 8 <= end) {
-        chunk8(ld16(base + i), i);
-      } else {
-        for (int64_t q = i; q < end; ++q) {
-          const uint64_t k = argmax_key(bf16_to_f32(base[q]), (uint32_t)q);
-          best = k > best ? k : best;
+      for (int u = 0; u < kArgmaxLoads; ++u) {
+        const int64_t i0 = i + u * step;
+        if (i0 + 8 <= end) {
+          chunk8(v[u], i0);
+        } else {
+          for (int64_t q = i0; q < end; ++q) {
+            const uint64_t k = argmax_key(bf16_to_f32(base[q]), (uint32_t)q);
+            best = k > best ? k : best;
+          }
         }
       }
     }
@@ -131,6 +138,7 @@ __global__ __launch_bounds__(256) void k_argmax_final(const uint64_t* __restrict
 }
 
 constexpr int kAcceptThreads = 1024;
+constexpr int kPre = 8;
 
 __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
     const int64_t* __restrict__ sa, int64_t ss, const int64_t* __restrict__ draft, int64_t ds,
@@ -148,34 +156,61 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
   int len = 0;
   if (j < B) {
     const int64_t* row = sa + (int64_t)j * ss;
-    int acc = 0;
-    while (acc < k && draft[(int64_t)j * ds + acc] == row[acc]) ++acc;
-    int first_stop = t;
-    for (int s = 0; s < t && first_stop == t; ++s)
-      for (int q = 0; q < n_stops; ++q)
-        if (stops[(int64_t)j * n_stops + q] == row[s]) {
-          first_stop = s;
-          break;
-        }
+    const int64_t* drow = draft + (int64_t)j * ds;
+    const int64_t* srow = stops + (int64_t)j * n_stops;
+    // Every load of the row is issued at once, the first kPre verify columns, drafts and stop
+    // ids into registers: compared one after another they cost an HBM round trip each.
+    int64_t rv[kPre], dv[kPre], sv[kPre];
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      rv[u] = u < t ? row[u] : 0;
+      dv[u] = u < k ? drow[u] : 0;
+      sv[u] = u < n_stops ? srow[u] : 0;
+    }
     const int64_t bud = budget[j];
+    const bool act = active[j] != 0;
+    const int64_t p0 = next_pos ? pos[j] : 0;
+    auto column = [&](int s) {
+      int64_t v = 0;
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) v = u == s ? rv[u] : v;
+      return s < kPre ? v : row[s];
+    };
+    auto is_stop = [&](int64_t tok) {
+      bool hit = false;
+#pragma unroll
+      for (int u = 0; u < kPre; ++u) hit |= u < n_stops && sv[u] == tok;
+      for (int q = kPre; q < n_stops; ++q) hit |= srow[q] == tok;
+      return hit;
+    };
+    int acc = 0;
+    bool same = true;
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      same = same && u < k && dv[u] == rv[u];
+      acc = same ? u + 1 : acc;
+    }
+    if (same)
+      while (acc < k && drow[acc] == row[acc]) ++acc;
+    int first_stop = t;
+#pragma unroll
+    for (int s = kPre - 1; s >= 0; --s)
+      if (s < t && is_stop(rv[s])) first_stop = s;
+    for (int s = kPre; s < t && first_stop == t; ++s)
+      if (is_stop(row[s])) first_stop = s;
     int64_t lim = acc < first_stop ? acc : first_stop;
     if (bud - 1 < lim) lim = bud - 1;
     if (lim < 0) lim = 0;
     const int a = (int)lim;
-    const bool act = active[j] != 0;
     len = act ? a + 1 : 1;
     accept_len[j] = a;
     if (lengths) lengths[j] = len;
-    const int64_t bn = row[a];
+    const int64_t bn = column(a);
     if (bonus) bonus[j] = bn;
-    if (next_pos) next_pos[j] = pos[j] + a + 1;
+    if (next_pos) next_pos[j] = p0 + a + 1;
     const int64_t left = bud - (a + 1);
     if (budget_left) budget_left[j] = left;
-    if (live) {
-      bool stopped = false;
-      for (int q = 0; q < n_stops; ++q) stopped |= stops[(int64_t)j * n_stops + q] == bn;
-      live[j] = (!stopped && left > 0) ? 1 : 0;
-    }
+    if (live) live[j] = (!is_stop(bn) && left > 0) ? 1 : 0;
     if (hidden_src) hidden_src[j] = (int64_t)j * t + a;
     if (keep)
       for (int s = 0; s < t; ++s) keep[(int64_t)j * t + s] = (act && s <= a) ? 1 : 0;
@@ -226,8 +261,8 @@ extern "C" {
 
 int64_t mtpk_argmax_partials(int64_t rows, int64_t vocab) {
   if (rows <= 0 || vocab <= 0) return 0;
-  // Enough workgroups to stream at HBM rate (about 8 per CU on 256 CUs), chunks of >= 2048.
-  int64_t chunks = (2048 + rows - 1) / rows;
+  // About kArgmaxWorkgroups workgroups over all rows, chunks of >= 2048 values.
+  int64_t chunks = (kArgmaxWorkgroups + rows - 1) / rows;
   const int64_t by_len = (vocab + 2047) / 2048;
   if (chunks > by_len) chunks = by_len;
   if (chunks < 1) chunks = 1;
@@ -242,12 +277,12 @@ int mtpk_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
   if (rows < 0 || rows > 65535 || vocab <= 0 || vocab > INT32_MAX || row_stride < vocab)
     return MTPK_EINVAL;
   if (rows == 0) return 0;
-  const int64_t chunks = mtpk_argmax_partials(rows, vocab) / rows;
   const int per_vec = dtype == MTPK_BF16 ? 8 : 4;
-  int64_t chunk = (vocab + chunks - 1) / chunks;
-  chunk = (chunk + per_vec - 1) / per_vec * per_vec;
   const int vec = aligned16(logits) && (row_stride % per_vec) == 0;
   const hipStream_t st = (hipStream_t)stream;
+  const int64_t chunks = mtpk_argmax_partials(rows, vocab) / rows;
+  int64_t chunk = (vocab + chunks - 1) / chunks;
+  chunk = (chunk + per_vec - 1) / per_vec * per_vec;
   hipLaunchKernelGGL(k_argmax_partial, dim3((unsigned)chunks, (unsigned)rows),
                      dim3(kArgmaxThreads), 0, st, logits, dtype, row_stride, vocab, chunk, vec,
                      partials);

@@ -10,10 +10,12 @@
 //
 // Four launches, all streaming the logits at HBM rate with 16-byte loads:
 //   stats : (chunk, row) workgroups -> per-chunk (max, sum exp(z - max)) of z = logit / T
-//   decide: one wave per item -> row softmax constants; for rejection, the accept length
+//   decide: one workgroup per lane, a wave per verify row -> row softmax constants and
+//           margins; for rejection, the accept length (one wave per row when plain sampling)
 //   mass  : (chunk, item) workgroups -> per-chunk sums of the item's draw weights
-//   pick  : one workgroup per item -> the chunk where the cumulative mass crosses r * total,
-//           then a block scan inside it; writes the token (and the emitted row)
+//   pick  : one workgroup per item -> the chunk where the cumulative mass crosses r * total
+//           (one wave: scan and ballot over the chunk masses), then a block scan inside it;
+//           writes the token (and the emitted row)
 // Every sum runs in a fixed order, so results are deterministic for fixed shapes.
 
 #include "mtpk_device.h"
@@ -117,67 +119,80 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_stats(RsRows rr, int64_t n_ta
 // Combine a row's chunk partials (one wave): max M and sum S of exp(z - M).
 __device__ inline float2 rs_row_stats(const float2* part, int64_t r, int nchunk) {
   const int lane = threadIdx.x & (kWave - 1);
-  float m = -INFINITY;
-  for (int c = lane; c < nchunk; c += kWave) m = fmaxf(m, part[r * nchunk + c].x);
+  const float2 v0 = lane < nchunk ? part[r * nchunk + lane] : make_float2(-INFINITY, 0.f);
+  float m = v0.x;
+  for (int c = lane + kWave; c < nchunk; c += kWave) m = fmaxf(m, part[r * nchunk + c].x);
   m = wave_max(m);
-  float s = 0.f;
-  for (int c = lane; c < nchunk; c += kWave) {
+  float s = lane < nchunk ? v0.y * __expf(v0.x - m) : 0.f;
+  for (int c = lane + kWave; c < nchunk; c += kWave) {
     const float2 v = part[r * nchunk + c];
     s += v.y * __expf(v.x - m);
   }
   return make_float2(m, wave_sum(s));
 }
 
-// Rejection decision, one wave per lane b: accept length, margins, and the item to draw.
-__global__ __launch_bounds__(kWave) void k_rs_decide(RsRows rr, const float2* __restrict__ part,
-                                                    int nchunk, int B, int k, float inv_t,
-                                                    const int64_t* __restrict__ draft_tokens,
-                                                    const float* __restrict__ u_accept,
-                                                    RsItem* __restrict__ items,
-                                                    int64_t* __restrict__ accept_len,
-                                                    float* __restrict__ margin) {
+// Rejection decision for lane b: one workgroup, its waves take the t verify rows in parallel
+// (row softmax constants and the margin p(x) - u q(x)), then the first negative margin is the
+// accept length.
+constexpr int kDecideWaves = 4;
+constexpr int kMaxT = 64;
+
+__global__ __launch_bounds__(kWave * kDecideWaves) void k_rs_decide(
+    RsRows rr, const float2* __restrict__ part, int nchunk, int B, int k, float inv_t,
+    const int64_t* __restrict__ draft_tokens, const float* __restrict__ u_accept,
+    RsItem* __restrict__ items, int64_t* __restrict__ accept_len, float* __restrict__ margin) {
+  __shared__ float s_mg[kMaxT];
+  __shared__ float4 s_st[kMaxT];
   const int b = blockIdx.x;
   const int t = k + 1;
+  const int wv = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int64_t n_target = (int64_t)B * t;
-  int a = k;
-  float2 sa_t = make_float2(0.f, 1.f), sa_q = make_float2(0.f, 1.f);
-  for (int i = 0; i < t; ++i) {
+  for (int i = wv; i < t; i += kDecideWaves) {
+    // The token and its two logits first (their loads overlap the partials' below).
+    const int64_t x = i < k ? draft_tokens[(int64_t)b * k + i] : -1;
+    const float ua = i < k ? u_accept[(int64_t)b * k + i] : 0.f;
+    const bool in_vocab = x >= 0 && x < rr.vocab;
+    float lt = 0.f, lq = 0.f;
+    if (in_vocab) {
+      lt = load_float(rr.target, rr.dt, ((int64_t)b * t + i) * rr.vocab + x) * inv_t;
+      lq = load_float(rr.draft, rr.dt, ((int64_t)b * k + i) * rr.vocab + x) * inv_t;
+    }
     const float2 st = rs_row_stats(part, (int64_t)b * t + i, nchunk);
     float2 sq = make_float2(0.f, 1.f);
     float mg = 0.f;
     if (i < k) {
       sq = rs_row_stats(part, n_target + (int64_t)b * k + i, nchunk);
-      const int64_t x = draft_tokens[(int64_t)b * k + i];
-      if (x >= 0 && x < rr.vocab) {
-        const float lt = load_float(rr.target, rr.dt, ((int64_t)b * t + i) * rr.vocab + x) * inv_t;
-        const float lq = load_float(rr.draft, rr.dt, ((int64_t)b * k + i) * rr.vocab + x) * inv_t;
+      if (in_vocab) {
         const float p = __expf(lt - st.x) / st.y, q = __expf(lq - sq.x) / sq.y;
-        mg = p - u_accept[(int64_t)b * k + i] * q;
+        mg = p - ua * q;
       } else {
         mg = -1.f;  // a token outside the vocabulary is never accepted
       }
-      if (margin && threadIdx.x == 0) margin[(int64_t)b * k + i] = mg;
     }
-    if (i == a) {
-      sa_t = st;
-      sa_q = sq;
-    }
-    if (i < k && a == k && mg < 0.f) {
-      a = i;
-      sa_t = st;
-      sa_q = sq;
+    if (lane == 0) {
+      s_mg[i] = mg;
+      s_st[i] = make_float4(st.x, st.y, sq.x, sq.y);
+      if (margin && i < k) margin[(int64_t)b * k + i] = mg;
     }
   }
+  __syncthreads();
   if (threadIdx.x == 0) {
+    int a = k;
+    for (int i = 0; i < k; ++i)
+      if (s_mg[i] < 0.f) {
+        a = i;
+        break;
+      }
+    const float4 sa = s_st[a];
     RsItem it;
     it.trow = b * t + a;
     it.drow = a < k ? b * k + a : -1;
     it.a = a;
     it.pad = 0;
-    it.mt = sa_t.x;
-    it.st = sa_t.y;
-    it.mq = sa_q.x;
-    it.sq = sa_q.y;
+    it.mt = sa.x;
+    it.st = sa.y;
+    it.mq = sa.z;
+    it.sq = sa.w;
     items[b] = it;
     accept_len[b] = a;
   }
@@ -202,27 +217,36 @@ __global__ __launch_bounds__(kWave) void k_rs_rows(const float2* __restrict__ pa
   }
 }
 
-// Draw weights of this thread's 16 slots: residual max(0, p - q) and target p.
-__device__ inline void rs_weights(const RsRows& rr, const RsItem& it, int c, float inv_t,
-                                  float (&wr)[kRsPerThread], float (&wp)[kRsPerThread]) {
-  float z[kRsPerThread];
-  rs_load(rr.target, rr.dt, rr.vec, it.trow, rr.vocab, c, threadIdx.x, inv_t, z);
+// Draw weights of this thread's 16 slots from the logits z (target) and zq (draft): target p,
+// and the residual max(0, p - q) when the item has a draft row.
+__device__ inline void rs_weights_of(const RsItem& it, const float (&z)[kRsPerThread],
+                                     const float (&zq)[kRsPerThread], float (&wr)[kRsPerThread],
+                                     float (&wp)[kRsPerThread]) {
 #pragma unroll
   for (int e = 0; e < kRsPerThread; ++e) wp[e] = __expf(z[e] - it.mt) / it.st;
   if (it.drow >= 0) {
-    rs_load(rr.draft, rr.dt, rr.vec, it.drow, rr.vocab, c, threadIdx.x, inv_t, z);
 #pragma unroll
-    for (int e = 0; e < kRsPerThread; ++e) wr[e] = fmaxf(wp[e] - __expf(z[e] - it.mq) / it.sq, 0.f);
+    for (int e = 0; e < kRsPerThread; ++e) wr[e] = fmaxf(wp[e] - __expf(zq[e] - it.mq) / it.sq, 0.f);
   } else {
 #pragma unroll
     for (int e = 0; e < kRsPerThread; ++e) wr[e] = 0.f;
   }
 }
 
+__device__ inline void rs_weights(const RsRows& rr, const RsItem& it, int c, float inv_t,
+                                  float (&wr)[kRsPerThread], float (&wp)[kRsPerThread]) {
+  float z[kRsPerThread], zq[kRsPerThread];
+  rs_load(rr.target, rr.dt, rr.vec, it.trow, rr.vocab, c, threadIdx.x, inv_t, z);
+  if (it.drow >= 0) rs_load(rr.draft, rr.dt, rr.vec, it.drow, rr.vocab, c, threadIdx.x, inv_t, zq);
+  rs_weights_of(it, z, zq, wr, wp);
+}
+
+// Per-chunk sums of an item's draw weights, one workgroup per (chunk, item).
 __global__ __launch_bounds__(kRsThreads) void k_rs_mass(RsRows rr, const RsItem* __restrict__ items,
-                                                       float inv_t, float2* __restrict__ mass) {
-  __shared__ float red[kRsThreads / kWave];
-  const int c = blockIdx.x, nchunk = gridDim.x;
+                                                       int nchunk, float inv_t,
+                                                       float2* __restrict__ mass) {
+  __shared__ float2 red[kRsThreads / kWave];
+  const int c = blockIdx.x;
   const int item = blockIdx.y;
   const RsItem it = items[item];
   float wr[kRsPerThread], wp[kRsPerThread];
@@ -233,9 +257,16 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_mass(RsRows rr, const RsItem*
     sr += wr[e];
     sp += wp[e];
   }
-  sr = block_sum(sr, red);
-  sp = block_sum(sp, red);
-  if (threadIdx.x == 0) mass[(int64_t)item * nchunk + c] = make_float2(sr, sp);
+  sr = wave_sum(sr);
+  sp = wave_sum(sp);
+  const int tid = threadIdx.x;
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = make_float2(sr, sp);
+  __syncthreads();
+  if (tid == 0) {
+    const float2 a = red[0], b = red[1], d = red[2], e = red[3];
+    mass[(int64_t)item * nchunk + c] =
+        make_float2((a.x + b.x) + (d.x + e.x), (a.y + b.y) + (d.y + e.y));
+  }
 }
 
 __device__ inline float wave_incl_scan_f(float v, int lane) {
@@ -257,34 +288,49 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_pick(
   const int item = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
   const RsItem it = items[item];
-  if (tid == 0) {
-    float tr = 0.f, tp = 0.f;
-    for (int c = 0; c < nchunk; ++c) {
-      const float2 m = mass[(int64_t)item * nchunk + c];
+  if (wv == 0) {
+    // One wave finds the chunk where the cumulative mass crosses r * total: totals by a wave
+    // sum, then 64 chunks at a time by an inclusive scan and a ballot.
+    const float u = u_sample[item];
+    const float2* row_mass = mass + (int64_t)item * nchunk;
+    const float2 m0 = lane < nchunk ? row_mass[lane] : make_float2(0.f, 0.f);
+    float tr = m0.x, tp = m0.y;
+    for (int c = lane + kWave; c < nchunk; c += kWave) {
+      const float2 m = row_mass[c];
       tr += m.x;
       tp += m.y;
     }
+    tr = wave_sum(tr);
+    tp = wave_sum(tp);
     const int use_r = it.drow >= 0 && tr > 0.f;
-    const float total = use_r ? tr : tp;
-    const float target = u_sample[item] * total;
+    const float target = u * (use_r ? tr : tp);
     float cum = 0.f;
     int chunk = -1, last_pos = 0;
-    for (int c = 0; c < nchunk; ++c) {
-      const float2 m = mass[(int64_t)item * nchunk + c];
+    for (int g0 = 0; g0 < nchunk; g0 += kWave) {
+      const int c = g0 + lane;
+      float2 m = m0;
+      if (g0 > 0) m = c < nchunk ? row_mass[c] : make_float2(0.f, 0.f);
       const float w = use_r ? m.x : m.y;
-      if (w > 0.f) last_pos = c;
-      if (cum + w > target) {
-        chunk = c;
+      const float inc = wave_incl_scan_f(w, lane);
+      const uint64_t hit = __ballot(c < nchunk && cum + inc > target);
+      if (hit) {
+        const int f = __ffsll((long long)hit) - 1;
+        chunk = g0 + f;
+        cum += __shfl(inc - w, f, kWave);
         break;
       }
-      cum += w;
+      const uint64_t positive = __ballot(w > 0.f);
+      if (positive) last_pos = g0 + 63 - __clzll((long long)positive);
+      cum += __shfl(inc, kWave - 1, kWave);
     }
-    s_fallback = chunk < 0;
-    s_chunk = chunk < 0 ? last_pos : chunk;
-    s_use_r = use_r;
-    s_before = cum;
-    s_target = target;
-    s_best = INT32_MAX;
+    if (lane == 0) {
+      s_fallback = chunk < 0;
+      s_chunk = chunk < 0 ? last_pos : chunk;
+      s_use_r = use_r;
+      s_before = cum;
+      s_target = target;
+      s_best = INT32_MAX;
+    }
   }
   __syncthreads();
   const int c = s_chunk;
@@ -382,11 +428,11 @@ int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int6
                      rr, batch * t, inv_t, part);
   int rc = status_of(hipGetLastError());
   if (rc) return rc;
-  hipLaunchKernelGGL(k_rs_decide, dim3((unsigned)batch), dim3(kWave), 0, st, rr, part, (int)nchunk,
+  hipLaunchKernelGGL(k_rs_decide, dim3((unsigned)batch), dim3(kWave * kDecideWaves), 0, st, rr, part, (int)nchunk,
                      (int)batch, k, inv_t, draft_tokens, u_accept, items, accept_len, margin);
   if ((rc = status_of(hipGetLastError()))) return rc;
-  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)batch), dim3(kRsThreads), 0, st,
-                     rr, items, inv_t, mass);
+  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)batch),
+                     dim3(kRsThreads), 0, st, rr, items, (int)nchunk, inv_t, mass);
   if ((rc = status_of(hipGetLastError()))) return rc;
   hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, items, mass,
                      (int)nchunk, inv_t, u_sample, token, draft_tokens, k, emitted);
@@ -424,8 +470,8 @@ int mtpk_sample_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
   if (rc) return rc;
   hipLaunchKernelGGL(k_rs_rows, dim3((unsigned)rows), dim3(kWave), 0, st, part, (int)nchunk, items);
   if ((rc = status_of(hipGetLastError()))) return rc;
-  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)rows), dim3(kRsThreads), 0, st,
-                     rr, items, inv_t, mass);
+  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)rows),
+                     dim3(kRsThreads), 0, st, rr, items, (int)nchunk, inv_t, mass);
   if ((rc = status_of(hipGetLastError()))) return rc;
   hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)rows), dim3(kRsThreads), 0, st, rr, items, mass,
                      (int)nchunk, inv_t, u, token, nullptr, 0, nullptr);
