@@ -4,8 +4,8 @@
 // draft MoE layer (model.py:2811-2873). These are weight-bandwidth bound: every weight byte is
 // read once, and the token rows are the MFMA's other operand.
 //
-// Workgroup = 4 waves, tile = 64 weight rows (wave w: rows 16 w .. + 15; with the paired SiLU
-// epilogue also the matching 16 "up" rows N/2 + ...) x all M tokens (TT = ceil(M / 16) MFMA token
+// Workgroup = NW = 4 or 8 waves, tile = 16 NW weight rows (wave w: rows 16 w .. + 15; with the
+// paired SiLU epilogue also the matching 16 "up" rows N/2 + ...) x all M tokens (TT = ceil(M / 16) MFMA token
 // tiles). v_mfma_f32_16x16x32_bf16 with the lane layout of the MoE kernels: lane (g, c) supplies
 // K positions 8 g .. 8 g + 7 of each 32-K step, for weight row c (B) and token row c of a tile (A).
 // The token rows are staged in LDS in chunks of 256 K (double-buffered, one barrier per chunk);
@@ -27,7 +27,10 @@ namespace mtpk {
 
 constexpr int kGemmKC = 256;                 // K per staged chunk
 constexpr int kGemmSteps = kGemmKC / 32;     // MFMA steps per chunk
-constexpr int kGemmRing = 8;                 // ring depth in steps
+// Ring depth in steps. The chunk-end wait for the staged token rows also waits for every ring
+// load issued before them (vmcnt retires in order), so a deeper ring than one chunk's steps + 1
+// would be drained at each chunk boundary.
+constexpr int kGemmRing = 8;
 constexpr int kGemmRow = kGemmKC * 2 + 16;   // LDS bytes of one token row (padded)
 enum { kEpiStore = 0, kEpiSilu = 1, kEpiArgmax = 2 };
 
@@ -40,10 +43,12 @@ struct GemmArgs {
   uint64_t* keys;  // argmax: [M, tiles]
 };
 
-template <int TT, int S>
-__global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
+template <int TT, int S, int NW>
+__global__ __launch_bounds__(NW * kWave, 16 / NW) void k_gemm_skinny(GemmArgs a) {
+  constexpr int NT = NW * kWave;
+  constexpr int kRing = kGemmRing;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][TT * 16 * kGemmRow];
-  __shared__ uint64_t kred[4][TT * 16];
+  __shared__ uint64_t kred[NW][TT * 16];
   const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
   const int tile = blockIdx.x, ks = blockIdx.y;
@@ -51,7 +56,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
   const int k0 = ks * kc_per * kGemmKC;
   const int nchunk = kc_per;
   // weight rows of this wave: stream 0 at n0 + 16 wave + c, stream 1 at N/2 + the same
-  const int r0 = tile * 64 + 16 * wave + ln.c;
+  const int r0 = tile * 16 * NW + 16 * wave + ln.c;
   int wrow[S];
   bool wok[S];
 #pragma unroll
@@ -71,13 +76,15 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
       v[s] = buf16(rw, (wok[s] && in) ? off : kOutOfRange);
     }
   };
-  // staging: load j moves 16 bytes of token row (256 j + tid) / 32, column (tid % 32) * 16
-  constexpr int kSL = TT * 2;  // 16-byte loads per thread per chunk
+  // staging: load j moves 16 bytes of token row (NT j + tid) / 32, column (tid % 32) * 16
+  constexpr int kSL = TT * 16 * 32 / NT;  // 16-byte loads per thread per chunk
+  static_assert(kSL * NT == TT * 16 * 32, "staging split");
+  static_assert(kRing == kGemmSteps, "one ring slot per step of a chunk");
   u32x4_t sreg[kSL];
   auto stage_load = [&](int c) {
 #pragma unroll
     for (int j = 0; j < kSL; ++j) {
-      const int p = j * 256 + tid, row = p >> 5, col = p & 31;
+      const int p = j * NT + tid, row = p >> 5, col = p & 31;
       const bool ok = c < nchunk && row < a.M;
       sreg[j] = buf16(rx, ok ? (uint32_t)(((int64_t)row * a.K + k0 + c * kGemmKC + col * 8) * 2)
                              : kOutOfRange);
@@ -86,7 +93,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
   auto stage_store = [&](int b) {
 #pragma unroll
     for (int j = 0; j < kSL; ++j) {
-      const int p = j * 256 + tid, row = p >> 5, col = p & 31;
+      const int p = j * NT + tid, row = p >> 5, col = p & 31;
       lds16_store(&xs[b][row * kGemmRow + col * 16], sreg[j]);
     }
   };
@@ -99,9 +106,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
 
   stage_load(0);
   ring_fence();
-  u32x4_t ring[kGemmRing][S];
+  u32x4_t ring[kRing][S];
 #pragma unroll
-  for (int st = 0; st < kGemmRing; ++st) issue(ring[st], st);
+  for (int st = 0; st < kRing; ++st) issue(ring[st], st);
   ring_fence();
   stage_store(0);
   stage_load(1);
@@ -113,6 +120,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
     const uint8_t* buf = xs[c & 1];
 #pragma unroll
     for (int st = 0; st < kGemmSteps; ++st) {
+      u32x4_t* slot = ring[st];
       const uint8_t* arow = buf + ln.c * kGemmRow + (32 * st + 8 * ln.g) * 2;
       u32x4_t av[TT];
 #pragma unroll
@@ -121,9 +129,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
       for (int s = 0; s < S; ++s)
 #pragma unroll
         for (int t = 0; t < TT; ++t)
-          acc[s][t] = mfma16x16x32(as_bf16x8(av[t]), as_bf16x8(ring[st][s]), acc[s][t]);
+          acc[s][t] = mfma16x16x32(as_bf16x8(av[t]), as_bf16x8(slot[s]), acc[s][t]);
       ring_fence();
-      issue(ring[st], c * kGemmSteps + st + kGemmRing);
+      issue(slot, c * kGemmSteps + st + kRing);
       ring_fence();
     }
     if (c + 1 < nchunk) stage_store((c + 1) & 1);
@@ -151,7 +159,7 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
   }
   if (a.epi == kEpiArgmax) {
     // first-occurrence argmax of the bf16 values: the max key over this wave's 16 columns,
-    // then over the 4 waves
+    // then over the NW waves
 #pragma unroll
     for (int t = 0; t < TT; ++t)
 #pragma unroll
@@ -168,9 +176,9 @@ __global__ __launch_bounds__(256, 2) void k_gemm_skinny(GemmArgs a) {
         if (ln.c == 0) kred[wave][16 * t + 4 * ln.g + i] = key;
       }
     __syncthreads();
-    for (int m = tid; m < a.M; m += 256) {
+    for (int m = tid; m < a.M; m += NT) {
       uint64_t b = kred[0][m];
-      for (int w2 = 1; w2 < 4; ++w2) b = kred[w2][m] > b ? kred[w2][m] : b;
+      for (int w2 = 1; w2 < NW; ++w2) b = kred[w2][m] > b ? kred[w2][m] : b;
       a.keys[(int64_t)m * gridDim.x + tile] = b;
     }
     return;
@@ -231,22 +239,47 @@ namespace {
 
 int gemm_cols(int64_t n, int epi) { return (int)(epi == kEpiSilu ? n / 2 : n); }
 
+// Waves per workgroup. At TT >= 3 token tiles the 2 x TT x 8 KiB staged token rows hold a CU to
+// three 4-wave workgroups; 8 waves sharing one staged copy double the resident waves, which
+// measured 4% faster on [48 | 64, 4096] x [248320, 4096] (the LM head) but slower wherever the
+// 128-row tiles leave fewer than two workgroups per CU (N = 4096: 8.8 -> 12.4 us).
+int gemm_waves(int64_t m, int64_t n, int epi) {
+  const int64_t cols = gemm_cols(n, epi);
+  return (m + 15) / 16 >= 3 && cols / 128 >= 2 * (int64_t)device_cu_count() ? 8 : 4;
+}
+
+int64_t gemm_tiles(int64_t m, int64_t n, int epi) {
+  const int64_t rows = 16 * gemm_waves(m, n, epi);
+  return (gemm_cols(n, epi) + rows - 1) / rows;
+}
+
 // Split count: a power of two dividing K / 256, enough workgroups for ~3 per CU, at least 4
 // chunks per split; argmax takes no split.
 int gemm_splits(int64_t m, int64_t n, int64_t k, int epi) {
   if (epi == kEpiArgmax) return 1;
-  const int64_t tiles = (gemm_cols(n, epi) + 63) / 64;
+  const int64_t tiles = gemm_tiles(m, n, epi);
   const int64_t chunks = k / kGemmKC;
-  const int64_t want = (3 * (int64_t)device_cu_count() + tiles - 1) / tiles;
+  const int64_t want = (3 * (int64_t)device_cu_count() * 4 / gemm_waves(m, n, epi) + tiles - 1) / tiles;
   int ks = 1;
   while (ks * 2 <= want && chunks % (ks * 2) == 0 && chunks / (ks * 2) >= 4) ks *= 2;
   return ks;
 }
 
-template <int TT, int S>
+template <int TT, int S, int NW>
 void launch_gemm(const GemmArgs& a, int tiles, hipStream_t st) {
-  hipLaunchKernelGGL((k_gemm_skinny<TT, S>), dim3((unsigned)tiles, (unsigned)a.KS), dim3(256), 0,
-                     st, a);
+  hipLaunchKernelGGL((k_gemm_skinny<TT, S, NW>), dim3((unsigned)tiles, (unsigned)a.KS),
+                     dim3(NW * kWave), 0, st, a);
+}
+
+template <int S>
+void launch_gemm_tt(const GemmArgs& a, int tt, int tiles, hipStream_t st) {
+  const bool wide = gemm_waves(a.M, a.N, a.epi) == 8;
+  switch (tt) {
+    case 1: wide ? launch_gemm<1, S, 8>(a, tiles, st) : launch_gemm<1, S, 4>(a, tiles, st); break;
+    case 2: wide ? launch_gemm<2, S, 8>(a, tiles, st) : launch_gemm<2, S, 4>(a, tiles, st); break;
+    case 3: wide ? launch_gemm<3, S, 8>(a, tiles, st) : launch_gemm<3, S, 4>(a, tiles, st); break;
+    default: wide ? launch_gemm<4, S, 8>(a, tiles, st) : launch_gemm<4, S, 4>(a, tiles, st); break;
+  }
 }
 
 }  // namespace
@@ -260,7 +293,7 @@ extern "C" {
 int64_t mtpk_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epilogue) {
   if (m <= 0 || m > 64 || n <= 0 || k <= 0 || k % kGemmKC || epilogue < 0 || epilogue > 2) return 0;
   const int ks = gemm_splits(m, n, k, epilogue);
-  const int64_t tiles = (gemm_cols(n, epilogue) + 63) / 64;
+  const int64_t tiles = gemm_tiles(m, n, epilogue);
   if (epilogue == kEpiArgmax) return m * tiles * 8;
   if (ks == 1) return 0;
   return (int64_t)ks * m * (epilogue == kEpiSilu ? n : gemm_cols(n, epilogue)) * 4;
@@ -281,27 +314,16 @@ int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, i
   const int ks = gemm_splits(m, n, k, epilogue);
   if ((ks > 1 || epilogue == kEpiArgmax) && !workspace) return MTPK_EINVAL;
   const int cols = gemm_cols(n, epilogue);
-  const int tiles = (cols + 63) / 64;
+  const int tiles = (int)gemm_tiles(m, n, epilogue);
   GemmArgs a{x, w, (int)m, (int)n, (int)k, ks, epilogue, out_dtype, cols, out,
              ks > 1 ? static_cast<float*>(workspace) : nullptr,
              epilogue == kEpiArgmax ? static_cast<uint64_t*>(workspace) : nullptr};
   const hipStream_t st = (hipStream_t)stream;
   const int tt = (int)((m + 15) / 16);
-  if (epilogue == kEpiSilu) {
-    switch (tt) {
-      case 1: launch_gemm<1, 2>(a, tiles, st); break;
-      case 2: launch_gemm<2, 2>(a, tiles, st); break;
-      case 3: launch_gemm<3, 2>(a, tiles, st); break;
-      default: launch_gemm<4, 2>(a, tiles, st); break;
-    }
-  } else {
-    switch (tt) {
-      case 1: launch_gemm<1, 1>(a, tiles, st); break;
-      case 2: launch_gemm<2, 1>(a, tiles, st); break;
-      case 3: launch_gemm<3, 1>(a, tiles, st); break;
-      default: launch_gemm<4, 1>(a, tiles, st); break;
-    }
-  }
+  if (epilogue == kEpiSilu)
+    launch_gemm_tt<2>(a, tt, tiles, st);
+  else
+    launch_gemm_tt<1>(a, tt, tiles, st);
   int rc = status_of(hipGetLastError());
   if (rc) return rc;
   if (epilogue == kEpiArgmax) {

@@ -29,7 +29,8 @@ def _close(got, want):
 
 
 @pytest.mark.parametrize("m,k,n", [(48, 8192, 4096), (48, 4096, 16384), (48, 4096, 512), (1, 4096, 513),
-                                   (4, 1024, 4096), (64, 256, 64), (17, 512, 100), (33, 4096, 20608)])
+                                   (4, 1024, 4096), (64, 256, 64), (17, 512, 100), (33, 4096, 20608),
+                                   (40, 512, 70000), (64, 256, 66000)])  # 8-wave tiles, ragged N
 def test_linear_matches_fp32(dev, m, k, n):
     x, w = _inputs(dev, m, k, n, m + n)
     assert dense.fits(x, w)
@@ -38,7 +39,7 @@ def test_linear_matches_fp32(dev, m, k, n):
     _close(got, x.float() @ w.float().T)
 
 
-@pytest.mark.parametrize("m,k,inter", [(48, 4096, 1024), (1, 4096, 1024), (5, 1024, 48)])
+@pytest.mark.parametrize("m,k,inter", [(48, 4096, 1024), (1, 4096, 1024), (5, 1024, 48), (48, 256, 65552)])
 def test_silu_linear_matches_swiglu(dev, m, k, inter):
     x, w = _inputs(dev, m, k, 2 * inter, 7 + m)
     got = dense.silu_linear(x, w)
