@@ -142,6 +142,25 @@ int mtpk_fused_moe(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
                    int top_k, int expert_lo, int expert_hi, void* workspace,
                    int64_t workspace_bytes, void* out, void* stream);
 
+/* ---------------------------------------------------------------- routed bf16 experts
+ * The MTP draft layer's routed experts in the real checkpoint, which are dense bf16 while the
+ * target layers' are MXFP4: replaces `mtp_dense_moe.grouped_moe` / `fused_moe`
+ * (mtp_dense_moe.py:359-745). Same contract as mtpk_fused_moe with bf16 weights: gate_up
+ * bf16 [local_experts, 2 I, H] (gate rows, then up rows), down bf16 [local_experts, H, I], x
+ * bf16 [tokens, H] contiguous, a_expert / a_weight [tokens * top_k] (live: expert in
+ * [expert_lo, expert_hi) and weight != 0), out bf16 [tokens, H] = sum over a token's live
+ * assignments in j order of w * down(silu(gate x) * (up x)); tokens with none get zeros.
+ * fp32 accumulation; the intermediate is kept as two bf16 planes (16 significant bits).
+ * H and I multiples of 256, one expert's gate_up < 2^31 bytes. workspace: 256-byte aligned,
+ * mtpk_moe_dense_workspace_bytes(...) bytes. */
+int64_t mtpk_moe_dense_workspace_bytes(int64_t tokens, int64_t top_k, int64_t local_experts,
+                                       int64_t inter, int64_t hidden);
+int mtpk_moe_dense(const uint16_t* x, int64_t tokens, int64_t hidden, const uint16_t* gate_up,
+                   const uint16_t* down, int64_t local_experts, int64_t inter_dim,
+                   const void* a_expert, int expert_dtype, const void* a_weight, int weight_dtype,
+                   int top_k, int expert_lo, int expert_hi, void* workspace,
+                   int64_t workspace_bytes, uint16_t* out, void* stream);
+
 /* ---------------------------------------------------------------- router top-k
  * Replaces `router_fused.route` / `_fused_route_kernel` (router_fused.py:56-151) and the torch
  * chain in `Model.moe` (model.py:2840-2843). routing [tokens, >= experts_out] f32|bf16 with

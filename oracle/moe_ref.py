@@ -10,12 +10,17 @@ activation dtype at the end (`mxfp4_gemv.py:1651`). Assignment `a` belongs to to
 Accumulation is float64, so this is the exact answer up to the final rounding; the north-star
 bar (rel-L2 <= 2e-3) and the reference's own bars are measured against it.
 
+`dense_moe` is the same arithmetic over dense bf16 experts (the MTP layer of the real
+checkpoint, `mtp_dense_moe.py:359-745`).
+
 Pinning (tests/test_oracle_moe.py):
 - against a brute-force per-element triple loop on tiny shapes (no matmul, no vectorised
   dequant), so a transposed operand or a swapped gate/up half fails;
 - the invariants the reference tests state: zero-weight tokens give exact zeros
   (`test_mxfp4_fused_gemv.py:293-316`), shards sum to the whole (`:261-290`), assignments
-  outside `expert_range` are dropped.
+  outside `expert_range` are dropped;
+- `dense_moe`: against its own element-by-element loop, and equal to `reference_moe` when its
+  dense experts are the dequantised MXFP4 experts; inactive tokens give exact zeros.
 """
 
 from __future__ import annotations
@@ -81,6 +86,60 @@ def reference_moe(
             y = act @ dn.T  # [n, H]
             np.add.at(out, tok, y * a_weight[sel, None])
     return out.astype(np.float32)
+
+
+def dense_moe(
+    x: np.ndarray,
+    experts: dict,
+    a_expert: np.ndarray,
+    a_weight: np.ndarray,
+    top_k: int,
+    expert_range: tuple[int, int],
+    active: np.ndarray | None = None,
+) -> np.ndarray:
+    """The routed MoE over dense (bf16-valued) experts, fp64-accumulated, float32 `[T, H]`:
+    the contract of the MTP layer's `mtp_dense_moe.fused_moe` / `grouped_moe`
+    (`mtp_dense_moe.py:359-745`). `experts` holds `gate_up [E, 2I, H]` (gate rows, then up)
+    and `down [E, H, I]` for the local experts `[lo, hi)`. Live assignments are owned, have a
+    nonzero weight and, when `active` `[T]` is given, an active token
+    (`mtp_dense_moe.py:600-610`); out[t] = sum over live j of w_j * down(silu(g) * u)."""
+    lo, hi = expert_range
+    x = np.asarray(x, dtype=np.float64)
+    a_expert = np.asarray(a_expert).reshape(-1).astype(np.int64)
+    a_weight = np.asarray(a_weight, dtype=np.float64).reshape(-1)
+    if active is not None:
+        a_weight = a_weight * np.repeat(np.asarray(active, dtype=bool), top_k)
+    inter = experts["gate_up"].shape[1] // 2
+    out = np.zeros((x.shape[0], experts["down"].shape[1]), dtype=np.float64)
+    keep = np.nonzero(live_mask(a_expert, a_weight, lo, hi))[0]
+    for e in np.unique(a_expert[keep] - lo):
+        sel = keep[a_expert[keep] - lo == e]
+        tok = sel // top_k
+        h = x[tok] @ np.asarray(experts["gate_up"][e], dtype=np.float64).T
+        act = silu(h[:, :inter]) * h[:, inter:]
+        y = act @ np.asarray(experts["down"][e], dtype=np.float64).T
+        np.add.at(out, tok, y * a_weight[sel, None])
+    return out.astype(np.float32)
+
+
+def brute_force_dense_moe(x, experts, a_expert, a_weight, top_k, expert_range) -> np.ndarray:
+    """`dense_moe` element by element, for tiny shapes only."""
+    lo, hi = expert_range
+    inter = experts["gate_up"].shape[1] // 2
+    out = np.zeros((x.shape[0], experts["down"].shape[1]))
+    for a in range(len(a_expert)):
+        e, w = int(a_expert[a]), float(a_weight[a])
+        if not (lo <= e < hi) or w == 0.0:
+            continue
+        t, gu, dn = a // top_k, experts["gate_up"][e - lo], experts["down"][e - lo]
+        act = []
+        for n in range(inter):
+            g = sum(float(gu[n, k]) * float(x[t, k]) for k in range(x.shape[1]))
+            u = sum(float(gu[inter + n, k]) * float(x[t, k]) for k in range(x.shape[1]))
+            act.append(g / (1.0 + np.exp(-g)) * u)
+        for n in range(out.shape[1]):
+            out[t, n] += w * sum(float(dn[n, k]) * act[k] for k in range(inter))
+    return out
 
 
 def brute_force_moe(x, experts, a_expert, a_weight, top_k, expert_range) -> np.ndarray:

@@ -35,6 +35,7 @@ import attention
 import deltanet
 import dense
 import mxfp4
+import mtp_dense_moe
 import mxfp4_gemv
 import router_fused
 import rownorm
@@ -345,8 +346,13 @@ def random_experts(cfg: Cfg, device: torch.device, gen: torch.Generator, mode: s
 
     `mode="quantized"`: fp32 N(0, 0.02) weights quantised with `mxfp4.quantize_mxfp4`.
     `mode="bytes"`: packed bytes uniform over 0..255 and scale bytes uniform over 118..130.
+    `mode="dense"`: bf16 N(0, 0.02) `gate_up` `[E, 2I, H]` and `down` `[E, H, I]`, the layout of
+    the real checkpoint's MTP layer (its experts are not quantised).
     """
     e, i, h = cfg.experts, cfg.inter, cfg.hidden
+    if mode == "dense":
+        return {"gate_up": _normal((e, 2 * i, h), 0.02, torch.bfloat16, device, gen),
+                "down": _normal((e, h, i), 0.02, torch.bfloat16, device, gen)}
     if mode == "quantized":
         gu = _normal((e * 2 * i, h), 0.02, torch.float32, gen.device, gen)
         dn = _normal((e * h, i), 0.02, torch.float32, gen.device, gen)
@@ -506,7 +512,9 @@ class Model:
             top_w, top_i = probs.topk(c.top_k, dim=-1)
             top_w = top_w / top_w.sum(-1, keepdim=True)
         assign = (top_i.reshape(-1), top_w.reshape(-1))
-        if mxfp4_gemv.available(h.device):
+        if "gate_up_scale" not in w["experts"]:
+            routed = self._dense_moe(w["experts"], h, top_i, top_w)
+        elif mxfp4_gemv.available(h.device):
             routed = mxfp4_gemv.fused_moe(h.contiguous(), w["experts"], assign, c.top_k, (0, c.experts),
                                           inter=self.moe_ws)
         elif h.device.type == "cuda":
@@ -516,6 +524,24 @@ class Model:
                                               mxfp4.dequant_mxfp4)
         shared = swiglu(h, w["shared_gate_up"], w["shared_down"])
         return routed + torch.sigmoid(routing[:, c.experts :]) * shared
+
+    def _dense_moe(self, ex: dict, h: torch.Tensor, top_i: torch.Tensor,
+                   top_w: torch.Tensor) -> torch.Tensor:
+        """Routed dense (bf16) experts: `mtp_dense_moe.fused_moe` on a device, the per-expert
+        torch form of `mtp._routed_grouped` (`mtp.py:347-388`) on the CPU."""
+        c = self.cfg
+        if h.device.type == "cuda":
+            return mtp_dense_moe.fused_moe(h.to(torch.bfloat16).contiguous(), ex, (top_i, top_w),
+                                           c.top_k, (0, c.experts)).to(h.dtype)
+        out = torch.zeros(h.shape[0], ex["down"].shape[1], dtype=torch.float32)
+        flat_i, flat_w = top_i.reshape(-1), top_w.reshape(-1).float()
+        tok = torch.arange(flat_i.numel()) // c.top_k
+        for e in flat_i.unique().tolist():
+            sel = (flat_i == e).nonzero()[:, 0]
+            gate, up = (h[tok[sel]].float() @ ex["gate_up"][e].float().T).chunk(2, dim=-1)
+            y = (F.silu(gate) * up) @ ex["down"][e].float().T
+            out.index_add_(0, tok[sel], y * flat_w[sel, None])
+        return out.to(h.dtype)
 
     def attention_rows(self, w: dict, pool: dict, h: torch.Tensor, lanes: torch.Tensor,
                        base_pos: torch.Tensor, ctx_len: int) -> torch.Tensor:

@@ -12,10 +12,12 @@ PROMPT_LEN = 16
 GEN_TOKENS = 32
 
 
-def build(device: str = "cpu", k: int = 1, lanes: int = 2, max_seq: int = 96) -> vm.Model:
-    """Config 1's model: same weights on every device (drawn on the CPU from fixed seeds)."""
+def build(device: str = "cpu", k: int = 1, lanes: int = 2, max_seq: int = 96,
+          mtp_experts: str = "quantized") -> vm.Model:
+    """Config 1's model: same weights on every device (drawn on the CPU from fixed seeds).
+    `mtp_experts="dense"` gives the MTP layer bf16 experts, as in the real checkpoint."""
     model = vm.Model(vm.tiny_cfg(), device, torch.float32, lanes=lanes, max_seq=max_seq, seed=0)
-    mtp.attach(model, k=k, seed=1)
+    mtp.attach(model, k=k, seed=1, expert_mode=mtp_experts)
     return model
 
 

@@ -49,6 +49,9 @@ def test_host_only_entry_points(lib):
     b = lib.mtpk_moe_workspace_bytes(192, 10, 512, 1024, 4096, 0)
     assert a > 1920 * 4096 * 4 and b > a  # f32 x carries three planes
     assert lib.mtpk_argmax_partials(192, 248320) >= 192
+    # bf16 experts: ids + units + n_units + two intermediate planes + f32 y
+    w = lib.mtpk_moe_dense_workspace_bytes(48, 10, 512, 1024, 4096)
+    assert w >= 480 * 4 + 3 * lib.mtpk_moe_max_units(480, 512) * 4 + 2 * 480 * 1024 * 2 + 480 * 4096 * 4
 
 
 def test_rejected_arguments_launch_nothing(lib):
@@ -65,6 +68,15 @@ def test_rejected_arguments_launch_nothing(lib):
     assert lib.mtpk_gemm_bf16(None, 4, 256, None, 64, 0, None, 1, None, 0, None) == -1
     assert lib.mtpk_gemm_bf16(p0 := ctypes.addressof(buf0), 4, 300, p0, 64, 0, p0, 1, None, 0, None) == -1
     assert lib.mtpk_gemm_bf16(p0, 65, 256, p0, 64, 0, p0, 1, None, 0, None) == -1
+    # bf16 experts: null weights, H not a multiple of 256, an expert range that is not the
+    # local expert count, a workspace that is not 256-byte aligned
+    f = 0x1000
+    args = lambda **kw: [kw.get("x", f), 4, kw.get("h", 256), kw.get("gu", f), f, 8, 256, f, 2, f, 0,
+                         2, 0, kw.get("hi", 8), kw.get("ws", f), 1 << 30, f, None]
+    assert lib.mtpk_moe_dense(*args(gu=None)) == -1
+    assert lib.mtpk_moe_dense(*args(h=320)) == -1
+    assert lib.mtpk_moe_dense(*args(hi=9)) == -1
+    assert lib.mtpk_moe_dense(*args(ws=f + 16)) == -1
     # row norm: null input, dim not a multiple of 8, unknown kind
     assert lib.mtpk_rownorm(None, 0, 64, 64, None, 0, None, None, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
                             None, None, None, 0, None, 0, 1, 1, 64, None) == -1

@@ -20,12 +20,13 @@ import verify_model as vm
 from tests import model_helpers as mh
 
 
-@pytest.mark.parametrize("k", [1, 3])
-def test_speculative_decode_matches_greedy(k: int) -> None:
-    """2 prompts of 16 ids, 32 generated tokens (config 1 is k = 1)."""
+@pytest.mark.parametrize("k,mtp_experts", [(1, "quantized"), (3, "quantized"), (3, "dense")])
+def test_speculative_decode_matches_greedy(k: int, mtp_experts: str) -> None:
+    """2 prompts of 16 ids, 32 generated tokens (config 1 is k = 1); with "dense" the MTP
+    layer's experts are bf16, as in the real checkpoint."""
     ids = mh.prompts()
     truth = mh.greedy_truth(mh.build(k=k), ids, mh.GEN_TOKENS)
-    spec = mh.build(k=k)
+    spec = mh.build(k=k, mtp_experts=mtp_experts)
     got, toks, pos = [], [], []
     for lane, p in enumerate(ids):
         base = int(spec.argmax(spec.prefill(lane, p)[None])[0])
@@ -192,3 +193,21 @@ def test_quantize_mxfp4_round_trips_grid_values() -> None:
     packed, scale = mxfp4.quantize_mxfp4(w)
     torch.testing.assert_close(mxfp4.dequant_mxfp4(packed, scale, torch.float32), w, rtol=0, atol=0)
     assert scale[:, 0].tolist() == [124, 127, 129, 132]
+
+
+def test_dense_expert_moe_matches_the_oracle() -> None:
+    """The CPU form of the routed bf16 experts (the MTP layer of the real checkpoint) against
+    the float64 restatement of the same contract."""
+    from oracle import moe_ref
+
+    model = mh.build(k=1, mtp_experts="dense")
+    ex = model.mtp.weights["experts"]
+    c = model.cfg
+    gen = torch.Generator().manual_seed(3)
+    h = torch.randn(5, c.hidden, generator=gen)
+    top_w, top_i = torch.rand(5, c.top_k, generator=gen).softmax(-1), torch.stack(
+        [torch.randperm(c.experts, generator=gen)[: c.top_k] for _ in range(5)])
+    got = model._dense_moe(ex, h, top_i, top_w)
+    dense = {k: v.float().numpy() for k, v in ex.items()}
+    want = moe_ref.dense_moe(h.numpy(), dense, top_i.numpy(), top_w.numpy(), c.top_k, (0, c.experts))
+    np.testing.assert_allclose(got.numpy(), want, rtol=1e-4, atol=1e-5 * np.abs(want).max())
