@@ -10,11 +10,14 @@ Weights rotate over --layers distinct copies (3.4 GB each) so no step is served 
 D_live * 6,684,672 + 2 * M * 4096 * 2, where D_live counts experts with a nonzero-weight
 assignment (the reference's definition, bench_moe_bw.py:29, :76-77).
 
-Two more legs are reported beside `value` in the same JSON line:
+More legs are reported beside `value` in the same JSON line:
 - "accept" (config 4): greedy acceptance (argmax over [48, 4, 248320] bf16 target logits, then
   the accept kernel with every rollback index) and sampling-mode acceptance at T = 0.7
   (rejection sampling with the target and draft logits, then the same index kernel), as us per
   call and GB/s over one read of the logits they take;
+- "dense_moe": the real checkpoint's MTP-layer MoE, whose 512 experts are bf16 (12.9 GB), at the
+  draft step's 48 rows with Zipf(1.1) and uniform routing, as us per call and GB/s over
+  D_live * 25,165,824 + 2 * 48 * 4096 * 2 bytes;
 - "mtp_round" (config 5): full speculative rounds on the reduced-depth real-dims model (3
   DeltaNet + 1 gated GQA layer, MXFP4 MoE on every layer, 1 MTP layer; B = 48, k = 3, 8192
   tokens of synthetic context per sequence), as ms per round and committed tok/s. The weights
@@ -22,6 +25,7 @@ Two more legs are reported beside `value` in the same JSON line:
   per lane.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--layers L] [--no-accept] [--no-mtp]
+                       [--no-dense]
 Prints one JSON line.
 """
 
@@ -110,6 +114,8 @@ def main() -> int:
                          "profile can scale FETCH_SIZE/WRITE_SIZE by a known byte count")
     ap.add_argument("--no-accept", action="store_true", help="skip the acceptance leg")
     ap.add_argument("--no-mtp", action="store_true", help="skip the MTP-round leg")
+    ap.add_argument("--no-dense", action="store_true",
+                    help="skip the bf16-expert leg (the real checkpoint's MTP-layer MoE)")
     ap.add_argument("--workloads", default="M1,M32,M192",
                     help="comma list of M1, M32, M192; `value` is measured on M192 when listed, "
                          "else on the last one listed")
@@ -240,6 +246,7 @@ def main() -> int:
     del runner, ins, outs, layers
     torch.cuda.empty_cache()
     accept = None if args.no_accept else accept_bench(dev)
+    dense_moe = None if args.no_dense else dense_moe_bench(dev)
     mtp_round = None if args.no_mtp else mtp_round_bench(dev)
 
     line = {
@@ -279,6 +286,7 @@ def main() -> int:
         },
         "cpu_baseline": cpu,
         "accept": accept,
+        "dense_moe": dense_moe,
         "mtp_round": mtp_round,
     }
     print(json.dumps(line), flush=True)
@@ -377,6 +385,58 @@ def accept_bench(dev, b=48, k=3, vocab=248320, temperature=0.7):
         "mean_accept_greedy": round(acc_g, 3),
         "mean_accept_rejection": round(acc_r, 3),
     }
+
+
+DENSE_EXPERT_BYTES = (2 * I * H + H * I) * 2  # bf16 gate_up + down of one expert
+
+
+def uniform_routing(tokens, seed):
+    """Top-10 of 512 uniformly without replacement, softmax weights of N(0,1) logits."""
+    rng = np.random.default_rng(seed)
+    picks = np.stack([rng.permutation(E)[:TOP_K] for _ in range(tokens)])
+    z = rng.standard_normal((tokens, TOP_K))
+    w = np.exp(z - z.max(-1, keepdims=True))
+    return picks.astype(np.int32).reshape(-1), (w / w.sum(-1, keepdims=True)).astype(np.float32).reshape(-1)
+
+
+def dense_moe_bench(dev, b=48, copies=2, calls=20):
+    """The real checkpoint's MTP-layer MoE: 512 bf16 experts (12.9 GB a copy) at the draft
+    step's B = 48 rows, top-10, Zipf(1.1) and uniform routing, timed by graph replay over
+    rotating copies so repeats are not served from the last-level cache."""
+    import torch
+
+    import mtp_dense_moe as dm
+
+    g = torch.Generator(device=dev).manual_seed(17)
+    layers = []
+    for _ in range(copies):
+        ex = {"gate_up": torch.empty(E, 2 * I, H, dtype=torch.bfloat16, device=dev),
+              "down": torch.empty(E, H, I, dtype=torch.bfloat16, device=dev)}
+        for ten in ex.values():
+            for e0 in range(0, E, 64):
+                ten[e0 : e0 + 64] = torch.randn(ten[e0 : e0 + 64].shape, generator=g, device=dev) * 0.02
+        layers.append(ex)
+    x = (torch.randn(b, H, generator=g, device=dev)).to(torch.bfloat16)
+    res = {"workload": f"MTP-layer routed bf16 experts, B={b}, top-{TOP_K} of {E}, H={H} I={I}",
+           "timing": f"HIP-graph replay of {calls} calls over {copies} rotating expert copies"}
+    for name, (a_e, a_w) in (("zipf", zipf_routing(b, seed=71)), ("uniform", uniform_routing(b, seed=72))):
+        route = (torch.from_numpy(a_e).view(b, TOP_K).to(dev), torch.from_numpy(a_w).view(b, TOP_K).to(dev))
+        scratch = dm.grouped_scratch(b, TOP_K, E, H, dev, intermediate=I)
+        inter = torch.empty(b * TOP_K, I, dtype=torch.bfloat16, device=dev)
+        out = torch.empty(b, H, dtype=torch.bfloat16, device=dev)
+
+        def call(c):
+            dm.grouped_moe(x, layers[c], route, TOP_K, (0, E), inter, out, scratch)
+
+        us = _time_graph(call, copies, calls)
+        dl = d_live(a_e, a_w)
+        byts = dl * DENSE_EXPERT_BYTES + 2 * b * H * 2
+        res[name] = {"us": round(us, 1), "d_live": dl, "gbs": round(byts / us / 1e3, 1),
+                     "frac_of_peak": round(byts / us / 1e3 / PEAK_GBS, 4)}
+        log(f"dense MoE ({name}): {us:.1f} us, D_live {dl}, {byts / us / 1e3:.0f} GB/s")
+    del layers
+    torch.cuda.empty_cache()
+    return res
 
 
 def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
