@@ -254,6 +254,31 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
                     const float* k, const float* v, const float* g, const float* beta,
                     const int64_t* lengths, float* out, void* stream);
 
+/* Verify-row preparation of a Gated DeltaNet layer, replacing the torch chain of
+ * `deltanet_verify` (model.py:3738-3905) between the in-projection and the recurrence: proj
+ * [batch * t, proj_stride] (model dtype f32|bf16; per row qkv [C], z [v_heads * v_dim],
+ * b [v_heads], a [v_heads], C = 2 k_heads k_dim + v_heads v_dim); conv_state [slots, C,
+ * conv_k - 1] and conv_w [C, conv_k] of the model dtype; slot i64 [batch]; a_log, dt_bias f32
+ * [v_heads]. Step s of row b: x = silu(sum_j win[s + j] conv_w[c][j]) over the window [stored
+ * columns | the t new qkv columns], rounded to the model dtype; q = l2norm(x_q) * q_scale,
+ * k = l2norm(x_k) (l2norm(x) = x rsqrt(sum x^2 + eps)), v = x_v, all f32 [batch, t, heads,
+ * dim]; beta = sigmoid(b), g = -exp(a_log) softplus(a + dt_bias), f32 [batch, t, v_heads].
+ * Head dims <= 256, conv_k <= 9. */
+int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const void* conv_state,
+                       const int64_t* slot, const void* conv_w, const float* a_log,
+                       const float* dt_bias, int64_t batch, int64_t t, int64_t k_heads,
+                       int64_t k_dim, int64_t v_heads, int64_t v_dim, int64_t conv_k, float eps,
+                       float q_scale, float* q, float* k, float* v, float* g, float* beta,
+                       void* stream);
+
+/* The commit's conv-window update (`deltanet_verify_rollback`, model.py:3907-3972): the window
+ * of slot[b], conv_state[slot[b]] [channels, k1], becomes columns idx[b][0 .. k1) (i64, clamped
+ * to [0, k1 + t - 1]) of [stored window | the t new raw columns proj[b * t + s][0 .. channels)].
+ * In place; slots distinct. */
+int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, const void* proj,
+                     int64_t proj_stride, const int64_t* idx, int64_t batch, int64_t channels,
+                     int64_t k1, int64_t t, void* stream);
+
 /* ---------------------------------------------------------------- skinny bf16 GEMM
  * y[M, N] = x[M, K] . w[N, K]^T for M <= 64 token rows, bf16 in, fp32 accumulation: the
  * weight-bandwidth-bound linears of the MTP draft step (fc, q/k/v/o projections), the shared

@@ -69,6 +69,17 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_int64, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int64,
          c_void_p, c_void_p],
     ),
+    "mtpk_deltanet_prep": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+         c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, ctypes.c_float, ctypes.c_float, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "mtpk_conv_commit": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64,
+         c_int64, c_void_p],
+    ),
     "mtpk_moe_dense_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "mtpk_moe_dense": (
         c_int,

@@ -101,6 +101,117 @@ int launch_delta_rule_mode(float* state, const int64_t* slot, int rows, int t, i
                                             lengths, nullptr, st);
 }
 
+// ---------------------------------------------------------------- verify-row preparation
+// Everything between the DeltaNet in-projection and the delta rule for the verify rows, in one
+// launch (`deltanet_verify`, model.py:3738-3905, up to `delta_rule_verify_exact`): the depthwise
+// causal conv over the stored window and the new raw columns, SiLU, rounding to the model dtype
+// (the conv output is a model-dtype tensor), the q / k / v split, the q and k L2 norms (q also
+// scaled by k_dim^-1/2), beta = sigmoid(b) and g = -exp(A_log) softplus(a + dt_bias). One
+// workgroup per verify row (b, s); its waves take 128-channel head units in turn (q heads, then
+// k heads, then v heads), lane l holding channels l, l + 64, ...
+//
+// Conv taps run in order j = 0 .. conv_k - 1 as separate products and sums (no fused
+// multiply-add), as the torch form does them.
+constexpr int kPrepThreadsDn = 256;
+constexpr int kPrepMaxPerLane = 4;  // head dims up to 256
+
+struct DnPrepArgs {
+  const void* proj;       // [B * t, proj_stride] model dtype: qkv (C), z, b (vh), a (vh)
+  int64_t proj_stride;
+  const void* conv;       // conv state [slots, C, k1] model dtype
+  const int64_t* slot;    // [B]
+  const void* conv_w;     // [C, conv_k] model dtype
+  const float* a_log;     // [vh] f32
+  const float* dt_bias;   // [vh] f32
+  int dt, t, kh, kd, vh, vd, conv_k;
+  float eps, q_scale;
+  float *q, *k, *v, *g, *beta;
+};
+
+__global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) {
+  const int rs = blockIdx.x;  // b * t + s
+  const int b = rs / a.t, s = rs - b * a.t;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
+  const int k1 = a.conv_k - 1;
+  const int C = 2 * a.kh * a.kd + a.vh * a.vd;
+  const int64_t slot = a.slot[b];
+  const int units = 2 * a.kh + a.vh;
+  for (int u = wave; u < units; u += kPrepThreadsDn / kWave) {
+    const bool is_v = u >= 2 * a.kh;
+    const int dim = is_v ? a.vd : a.kd;
+    const int c0 = is_v ? 2 * a.kh * a.kd + (u - 2 * a.kh) * a.vd : u * a.kd;
+    float x[kPrepMaxPerLane];
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kPrepMaxPerLane; ++i) {
+      const int ch = lane + kWave * i;
+      x[i] = 0.f;
+      if (ch >= dim) continue;
+      const int c = c0 + ch;
+      float acc = 0.f;
+      for (int j = 0; j < a.conv_k; ++j) {
+        const int p = s + j;  // window column: the stored k1, then the t new ones
+        const float win = p < k1 ? load_float(a.conv, a.dt, (slot * C + c) * k1 + p)
+                                 : load_float(a.proj, a.dt, ((int64_t)b * a.t + p - k1) * a.proj_stride + c);
+        const float prod = __fmul_rn(win, load_float(a.conv_w, a.dt, (int64_t)c * a.conv_k + j));
+        acc = j == 0 ? prod : __fadd_rn(acc, prod);
+      }
+      float y = acc / (1.f + expf(-acc));
+      if (a.dt == MTPK_BF16) y = bf16_to_f32(f32_to_bf16(y));
+      x[i] = y;
+      ss += y * y;
+    }
+    if (is_v) {
+      float* dst = a.v + ((int64_t)rs * a.vh + (u - 2 * a.kh)) * a.vd;
+#pragma unroll
+      for (int i = 0; i < kPrepMaxPerLane; ++i)
+        if (lane + kWave * i < dim) dst[lane + kWave * i] = x[i];
+    } else {
+      const bool is_q = u < a.kh;
+      const float inv = rsqrtf(wave_sum(ss) + a.eps);
+      const float sc = is_q ? a.q_scale : 1.f;
+      float* dst = (is_q ? a.q : a.k) + ((int64_t)rs * a.kh + (is_q ? u : u - a.kh)) * a.kd;
+#pragma unroll
+      for (int i = 0; i < kPrepMaxPerLane; ++i)
+        if (lane + kWave * i < dim) dst[lane + kWave * i] = x[i] * inv * sc;
+    }
+  }
+  for (int h = tid; h < a.vh; h += kPrepThreadsDn) {
+    const int64_t base = (int64_t)rs * a.proj_stride + C + a.vh * a.vd;
+    const float braw = load_float(a.proj, a.dt, base + h);
+    const float araw = load_float(a.proj, a.dt, base + a.vh + h);
+    const float x = __fadd_rn(araw, a.dt_bias[h]);
+    const float sp = x > 20.f ? x : log1pf(expf(x));
+    a.beta[(int64_t)rs * a.vh + h] = 1.f / (1.f + expf(-braw));
+    a.g[(int64_t)rs * a.vh + h] = -expf(a.a_log[h]) * sp;
+  }
+}
+
+// The commit's conv-window update (`deltanet_verify_rollback`, model.py:3907-3972): slot b's
+// window becomes columns idx[b][0 .. k1) of [stored window | the t new raw columns]. A thread
+// owns one (row, channel) and reads all of its sources before it writes, so the in-place update
+// cannot read a value it has already replaced.
+constexpr int kConvMaxK1 = 8;
+
+__global__ __launch_bounds__(256) void k_conv_commit(void* __restrict__ conv, int dt,
+                                                     const int64_t* __restrict__ slot,
+                                                     const void* __restrict__ proj,
+                                                     int64_t proj_stride, const int64_t* __restrict__ idx,
+                                                     int B, int C, int k1, int t) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)B * C) return;
+  const int b = (int)(i / C), c = (int)(i - (int64_t)b * C);
+  const int64_t base = (slot[b] * C + c) * k1;
+  float v[kConvMaxK1];
+  for (int w = 0; w < k1; ++w) {
+    int64_t p = idx[(int64_t)b * k1 + w];
+    p = p < 0 ? 0 : (p > k1 + t - 1 ? k1 + t - 1 : p);
+    v[w] = p < k1 ? load_float(conv, dt, base + p)
+                  : load_float(proj, dt, ((int64_t)b * t + p - k1) * proj_stride + c);
+  }
+  for (int w = 0; w < k1; ++w) store_float(conv, dt, base + w, v[w]);
+}
+
 }  // namespace mtpk
 
 using namespace mtpk;
@@ -132,6 +243,46 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
     default: return MTPK_DN(128);
   }
 #undef MTPK_DN
+}
+
+int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const void* conv_state,
+                       const int64_t* slot, const void* conv_w, const float* a_log,
+                       const float* dt_bias, int64_t batch, int64_t t, int64_t k_heads,
+                       int64_t k_dim, int64_t v_heads, int64_t v_dim, int64_t conv_k, float eps,
+                       float q_scale, float* q, float* k, float* v, float* g, float* beta,
+                       void* stream) {
+  if (!proj || !conv_state || !slot || !conv_w || !a_log || !dt_bias || !q || !k || !v || !g || !beta)
+    return MTPK_EINVAL;
+  if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (batch < 0 || t < 1 || k_heads < 1 || v_heads < 1 || conv_k < 2 || conv_k > kConvMaxK1 + 1)
+    return MTPK_EINVAL;
+  if (k_dim < 1 || k_dim > kWave * kPrepMaxPerLane || v_dim < 1 || v_dim > kWave * kPrepMaxPerLane)
+    return MTPK_EINVAL;
+  const int64_t C = 2 * k_heads * k_dim + v_heads * v_dim;
+  if (proj_stride < C + v_heads * v_dim + 2 * v_heads || batch * t > INT32_MAX) return MTPK_EINVAL;
+  if (batch == 0) return 0;
+  DnPrepArgs a{proj, proj_stride, conv_state, slot, conv_w, a_log, dt_bias, dtype, (int)t,
+               (int)k_heads, (int)k_dim, (int)v_heads, (int)v_dim, (int)conv_k, eps, q_scale,
+               q, k, v, g, beta};
+  hipLaunchKernelGGL(k_deltanet_prep, dim3((unsigned)(batch * t)), dim3(kPrepThreadsDn), 0,
+                     (hipStream_t)stream, a);
+  return status_of(hipGetLastError());
+}
+
+int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, const void* proj,
+                     int64_t proj_stride, const int64_t* idx, int64_t batch, int64_t channels,
+                     int64_t k1, int64_t t, void* stream) {
+  if (!conv_state || !slot || !proj || !idx) return MTPK_EINVAL;
+  if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (batch < 0 || channels < 1 || k1 < 1 || k1 > kConvMaxK1 || t < 1 || proj_stride < channels)
+    return MTPK_EINVAL;
+  if (batch * channels > INT32_MAX) return MTPK_EINVAL;
+  if (batch == 0) return 0;
+  const int64_t n = batch * channels;
+  hipLaunchKernelGGL(k_conv_commit, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, conv_state, dtype, slot, proj, proj_stride, idx,
+                     (int)batch, (int)channels, (int)k1, (int)t);
+  return status_of(hipGetLastError());
 }
 
 }  // extern "C"

@@ -66,3 +66,59 @@ def delta_rule(state: torch.Tensor, slots: torch.Tensor | None, q: torch.Tensor,
         "mtpk_delta_rule",
     )
     return out
+
+
+def prep(proj: torch.Tensor, conv_state: torch.Tensor, slots: torch.Tensor, conv_w: torch.Tensor,
+         a_log: torch.Tensor, dt_bias: torch.Tensor, k_heads: int, k_dim: int, v_heads: int,
+         v_dim: int, eps: float = 1e-6) -> tuple[torch.Tensor, ...]:
+    """The verify rows' recurrence inputs from the in-projection in one launch
+    (`mtpk_deltanet_prep`): `proj` `[B, t, P]` (last dim contiguous: qkv, z, b, a), the stored
+    conv windows `conv_state` `[slots_total, C, conv_k - 1]` read at `slots` `[B]`, `conv_w`
+    `[C, conv_k]` of the model dtype, `a_log` / `dt_bias` `[v_heads]` (taken in fp32). Returns fp32
+    `q`, `k` `[B, t, k_heads, k_dim]` (L2-normalised, q scaled by k_dim^-1/2), `v`
+    `[B, t, v_heads, v_dim]`, `g`, `beta` `[B, t, v_heads]`."""
+    device = _mtpk.require_device(proj, conv_state, slots, conv_w, a_log, dt_bias)
+    b, t, width = proj.shape
+    if proj.stride(2) != 1 or proj.stride(0) != t * proj.stride(1):
+        raise ValueError("proj must be [B, t, P] with contiguous rows")
+    dt = proj.dtype
+    for name, ten in (("conv_state", conv_state), ("conv_w", conv_w)):
+        if ten.dtype != dt or not ten.is_contiguous():
+            raise ValueError(f"{name} must be contiguous {dt}")
+    a_log = a_log.float().contiguous()
+    dt_bias = dt_bias.float().contiguous()
+    f32 = dict(dtype=torch.float32, device=device)
+    q = torch.empty(b, t, k_heads, k_dim, **f32)
+    k = torch.empty(b, t, k_heads, k_dim, **f32)
+    v = torch.empty(b, t, v_heads, v_dim, **f32)
+    g = torch.empty(b, t, v_heads, **f32)
+    beta = torch.empty(b, t, v_heads, **f32)
+    sl = slots.to(torch.int64).contiguous()
+    _mtpk.check(_mtpk.lib().mtpk_deltanet_prep(
+        proj.data_ptr(), _mtpk.float_code(dt), proj.stride(1), conv_state.data_ptr(), sl.data_ptr(),
+        conv_w.data_ptr(), a_log.data_ptr(), dt_bias.data_ptr(), b, t, k_heads, k_dim, v_heads, v_dim,
+        conv_w.shape[1], float(eps), float(k_dim) ** -0.5, q.data_ptr(), k.data_ptr(), v.data_ptr(),
+        g.data_ptr(), beta.data_ptr(), _mtpk.stream_of(device)), "mtpk_deltanet_prep")  # fmt: skip
+    return q, k, v, g, beta
+
+
+def conv_commit(conv_state: torch.Tensor, slots: torch.Tensor, proj: torch.Tensor,
+                idx: torch.Tensor, channels: int) -> None:
+    """Slot `slots[b]`'s conv window `conv_state[slot]` `[C, k1]` becomes columns `idx[b]`
+    `[k1]` of [stored window | the t new raw columns], the raw columns being `proj[b, :, :C]`
+    (`mtpk_conv_commit`)."""
+    device = _mtpk.require_device(conv_state, slots, proj, idx)
+    b, t, _ = proj.shape
+    if proj.stride(2) != 1 or proj.stride(0) != t * proj.stride(1):
+        raise ValueError("proj must be [B, t, P] with contiguous rows")
+    if proj.dtype != conv_state.dtype or not conv_state.is_contiguous():
+        raise ValueError("conv_state must be contiguous and of proj's dtype")
+    k1 = conv_state.shape[-1]
+    ix = idx.to(torch.int64).contiguous()
+    if ix.shape != (b, k1):
+        raise ValueError(f"idx must be [{b}, {k1}]")
+    sl = slots.to(torch.int64).contiguous()
+    _mtpk.check(_mtpk.lib().mtpk_conv_commit(
+        conv_state.data_ptr(), _mtpk.float_code(conv_state.dtype), sl.data_ptr(), proj.data_ptr(),
+        proj.stride(1), ix.data_ptr(), b, channels, k1, t, _mtpk.stream_of(device)),
+        "mtpk_conv_commit")  # fmt: skip

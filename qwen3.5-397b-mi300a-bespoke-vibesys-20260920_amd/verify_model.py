@@ -415,12 +415,13 @@ class DeltaNetRows:
     """What `deltanet_commit` needs from a verify forward of one DeltaNet layer: the raw
     conv inputs and the per-row recurrence inputs, `[B, t, ...]`."""
 
-    raw_qkv: torch.Tensor  # [B, conv_dim, t], model dtype
+    raw_qkv: torch.Tensor  # [B, conv_dim, t], model dtype (a view of `proj` on a device)
     q: torch.Tensor  # [B, t, k_heads, k_dim] fp32, normalised and scaled
     k: torch.Tensor  # [B, t, k_heads, k_dim] fp32, normalised
     v: torch.Tensor  # [B, t, v_heads, v_dim] fp32
     g: torch.Tensor  # [B, t, v_heads] fp32
     beta: torch.Tensor  # [B, t, v_heads] fp32
+    proj: torch.Tensor | None = None  # [B, t, P] in-projection output (device path)
 
 
 @dataclass
@@ -564,6 +565,14 @@ class Model:
         proj = F.linear(h, w["in_proj_all"])
         qkv, z, b_raw, a_raw = proj.split(c.in_proj_sizes, dim=-1)
         raw = qkv.transpose(1, 2)  # [B, C, t]
+        if h.device.type == "cuda":
+            # conv, SiLU, split, q/k norms, g and beta in one launch; then the recurrence
+            q, k, v, g, beta = deltanet.prep(proj, pool["conv"], lanes, w["conv"], w["A_log"],
+                                             w["dt_bias"], c.k_heads, c.k_dim, c.v_heads, c.v_dim)
+            out = deltanet.delta_rule(pool["rec"], lanes, q, k, v, g, beta)  # [B, t, vh, vd] fp32
+            normed = gated_rmsnorm(out, z.reshape(b, t, c.v_heads, c.v_dim), w["dn_norm"], c.eps, h.dtype)
+            mixer = F.linear(normed.reshape(b, t, -1), w["out_proj"])
+            return mixer, DeltaNetRows(raw, q, k, v, g, beta, proj)
         window = torch.cat([pool["conv"][lanes], raw], dim=-1)
         mixed = causal_conv_rows(window, w["conv"], t).to(h.dtype).transpose(1, 2)  # [B, t, C]
         kd = c.k_heads * c.k_dim
@@ -574,17 +583,14 @@ class Model:
         k = l2norm(k)
         beta = torch.sigmoid(b_raw.float())
         g = -w["A_log"].float().exp() * F.softplus(a_raw.float() + w["dt_bias"].float())
-        if h.device.type == "cuda":
-            out = deltanet.delta_rule(pool["rec"], lanes, q, k, v, g, beta)  # [B, t, vh, vd] fp32
-        else:
-            rep = c.v_heads // c.k_heads
-            qe, ke = q.repeat_interleave(rep, dim=2), k.repeat_interleave(rep, dim=2)
-            state = pool["rec"][lanes]
-            outs = []
-            for s in range(t):
-                state, o = delta_rule_step(state, qe[:, s], ke[:, s], v[:, s], g[:, s], beta[:, s])
-                outs.append(o)
-            out = torch.stack(outs, dim=1)  # [B, t, vh, vd] fp32
+        rep = c.v_heads // c.k_heads
+        qe, ke = q.repeat_interleave(rep, dim=2), k.repeat_interleave(rep, dim=2)
+        state = pool["rec"][lanes]
+        outs = []
+        for s in range(t):
+            state, o = delta_rule_step(state, qe[:, s], ke[:, s], v[:, s], g[:, s], beta[:, s])
+            outs.append(o)
+        out = torch.stack(outs, dim=1)  # [B, t, vh, vd] fp32
         normed = gated_rmsnorm(out, z.reshape(b, t, c.v_heads, c.v_dim), w["dn_norm"], c.eps, h.dtype)
         mixer = F.linear(normed.reshape(b, t, -1), w["out_proj"])
         return mixer, DeltaNetRows(raw.contiguous(), q, k, v, g, beta)
@@ -599,11 +605,16 @@ class Model:
         k1 = c.conv_k - 1
         t = rows.q.shape[1]
         n = lengths.to(self.device, torch.long)
-        window = torch.cat([pool["conv"][lanes], rows.raw_qkv], dim=-1)  # [B, C, k1 + t]
         if conv_idx is not None:
             idx = conv_idx.long()
         else:
             idx = (n[:, None] + torch.arange(k1, device=self.device)[None, :]).clamp(max=k1 + t - 1)
+        if self.device.type == "cuda" and rows.proj is not None:
+            deltanet.conv_commit(pool["conv"], lanes, rows.proj, idx, c.conv_dim)
+            deltanet.delta_rule(pool["rec"], lanes, rows.q, rows.k, rows.v, rows.g, rows.beta, n,
+                                want_out=False)
+            return
+        window = torch.cat([pool["conv"][lanes], rows.raw_qkv], dim=-1)  # [B, C, k1 + t]
         pool["conv"][lanes] = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
         if self.device.type == "cuda":
             deltanet.delta_rule(pool["rec"], lanes, rows.q, rows.k, rows.v, rows.g, rows.beta, n,

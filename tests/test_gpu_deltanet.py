@@ -114,3 +114,73 @@ def test_rejects_bad_shapes(dev) -> None:
         deltanet.delta_rule(tp, ts[:1], tq, tk, tv, tg, tb)
     with pytest.raises(ValueError):
         deltanet.delta_rule(tp.double(), ts, tq, tk, tv, tg, tb)
+
+
+# ---------------------------------------------------------------- verify-row preparation
+
+
+def _torch_prep(proj, conv_state, slots, conv_w, a_log, dt_bias, kh, kd, vh, vd):
+    """The torch chain `deltanet.prep` replaces (verify_model's CPU form of deltanet_verify)."""
+    import torch.nn.functional as F
+
+    import verify_model as vm
+
+    b, t, _ = proj.shape
+    c = 2 * kh * kd + vh * vd
+    qkv, z, b_raw, a_raw = proj.split([c, vh * vd, vh, vh], dim=-1)
+    window = torch.cat([conv_state[slots], qkv.transpose(1, 2)], dim=-1)
+    mixed = vm.causal_conv_rows(window, conv_w, t).to(proj.dtype).transpose(1, 2)
+    q = mixed[..., : kh * kd].reshape(b, t, kh, kd).float()
+    k = mixed[..., kh * kd : 2 * kh * kd].reshape(b, t, kh, kd).float()
+    v = mixed[..., 2 * kh * kd :].reshape(b, t, vh, vd).float()
+    q = q * torch.rsqrt((q * q).sum(-1, keepdim=True) + 1e-6) * kd ** -0.5
+    k = k * torch.rsqrt((k * k).sum(-1, keepdim=True) + 1e-6)
+    beta = torch.sigmoid(b_raw.float())
+    g = -a_log.float().exp() * F.softplus(a_raw.float() + dt_bias.float())
+    return q, k, v, g, beta
+
+
+@pytest.mark.parametrize("dtype,b,t,kh,kd,vh,vd,slots_total", [
+    (torch.bfloat16, 48, 4, 16, 128, 64, 128, 50),  # config 5's DeltaNet at 192 verify rows
+    (torch.float32, 2, 4, 2, 16, 4, 16, 3),         # config 1
+    (torch.bfloat16, 3, 1, 2, 256, 4, 192, 4),      # one step, wide heads
+])
+def test_prep_matches_the_torch_chain(dev, dtype, b, t, kh, kd, vh, vd, slots_total) -> None:
+    g = torch.Generator(device="cpu").manual_seed(b + t)
+    c = 2 * kh * kd + vh * vd
+    width = c + vh * vd + 2 * vh + 8  # padded rows: the kernel takes a row stride
+    proj = (torch.randn(b, t, width, generator=g) * 2).to(dtype).to(dev)[..., : width - 8]
+    conv_state = torch.randn(slots_total, c, 3, generator=g).to(dtype).to(dev)
+    conv_w = (torch.randn(c, 4, generator=g) * 0.3).to(dtype).to(dev)
+    a_log = torch.log(torch.rand(vh, generator=g) * 15 + 1).to(dev)
+    dt_bias = torch.rand(vh, generator=g).to(dev)
+    slots = torch.randperm(slots_total, generator=g)[:b].to(dev)
+    got = deltanet.prep(proj, conv_state, slots, conv_w, a_log, dt_bias, kh, kd, vh, vd)
+    want = _torch_prep(proj, conv_state, slots, conv_w, a_log, dt_bias, kh, kd, vh, vd)
+    for name, x, y in zip(("q", "k", "v", "g", "beta"), got, want, strict=True):
+        assert x.shape == y.shape and x.dtype == torch.float32, name
+        if dtype == torch.bfloat16 and name in ("q", "k", "v"):
+            # a conv output may round to the neighbouring bf16 value (the sums are the same, the
+            # exp inside SiLU is not): every element within one bf16 step, and elements beyond
+            # fp32 rounding (the norm's sum order) rare
+            assert torch.allclose(x, y, rtol=2 ** -7, atol=1e-6), name
+            far = (x - y).abs() > 1e-5 * y.abs() + 1e-7
+            assert float(far.float().mean()) < 1e-3, name
+        else:
+            torch.testing.assert_close(x, y, rtol=1e-5, atol=1e-6, msg=name)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_conv_commit_matches_the_gather(dev, dtype) -> None:
+    b, t, c, k1, slots_total = 5, 4, 300, 3, 7
+    g = torch.Generator(device="cpu").manual_seed(11)
+    proj = torch.randn(b, t, c + 20, generator=g).to(dtype).to(dev)
+    conv = torch.randn(slots_total, c, k1, generator=g).to(dtype).to(dev)
+    slots = torch.tensor([6, 0, 3, 2, 5], device=dev)
+    lengths = torch.tensor([1, 4, 2, 3, 1], device=dev)
+    idx = (lengths[:, None] + torch.arange(k1, device=dev)[None, :]).clamp(max=k1 + t - 1)
+    window = torch.cat([conv[slots], proj[..., :c].transpose(1, 2)], dim=-1)
+    want = conv.clone()
+    want[slots] = torch.gather(window, 2, idx[:, None, :].expand(-1, c, -1))
+    deltanet.conv_commit(conv, slots, proj, idx, c)
+    assert torch.equal(conv, want)  # untouched slots 1 and 4 included
