@@ -161,6 +161,21 @@ int mtpk_moe_dense(const uint16_t* x, int64_t tokens, int64_t hidden, const uint
                    int top_k, int expert_lo, int expert_hi, void* workspace,
                    int64_t workspace_bytes, uint16_t* out, void* stream);
 
+/* mtpk_fused_moe plus the shared expert's term of the layer (`Model.moe`, model.py:2871-2872;
+ * the reference's `bw_combine_glue`, mxfp4_gemv.py:2266-2312): out = routed + sigmoid(g_t) *
+ * shared[t], with g_t = shared_gate[t * gate_stride] (the shared-gate column of the router
+ * GEMM output) and shared [tokens, hidden] of shared_dtype. The routed sum, the sigmoid and the
+ * product are each rounded to the output dtype before the add, as the unfused torch ops round
+ * them, so both spellings give the same values. shared = NULL is mtpk_fused_moe. */
+int mtpk_fused_moe_shared(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                          const uint8_t* gate_up, const uint8_t* gate_up_scale, const uint8_t* down,
+                          const uint8_t* down_scale, int64_t local_experts, int64_t inter_dim,
+                          const void* a_expert, int expert_dtype, const void* a_weight,
+                          int weight_dtype, int top_k, int expert_lo, int expert_hi,
+                          const void* shared, int shared_dtype, const void* shared_gate,
+                          int gate_dtype, int64_t gate_stride, void* workspace,
+                          int64_t workspace_bytes, void* out, void* stream);
+
 /* ---------------------------------------------------------------- router top-k
  * Replaces `router_fused.route` / `_fused_route_kernel` (router_fused.py:56-151) and the torch
  * chain in `Model.moe` (model.py:2840-2843). routing [tokens, >= experts_out] f32|bf16 with

@@ -69,6 +69,12 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_int64, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int64,
          c_void_p, c_void_p],
     ),
+    "mtpk_fused_moe_shared": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+         c_int64, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int,
+         c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p],
+    ),
     "mtpk_deltanet_prep": (
         c_int,
         [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,

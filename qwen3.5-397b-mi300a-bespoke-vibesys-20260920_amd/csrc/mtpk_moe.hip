@@ -1184,10 +1184,36 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
 // out[t, n..n+3] = sum_j w_j * y[t*top_k + j, n..n+3] over live assignments, in j order. The
 // routing of a group of four j is loaded before their y rows so the loads overlap.
 
+// The shared expert's term of a MoE layer, out = routed + sigmoid(gate) * shared, with the
+// torch chain's rounding points (`Model.moe`, model.py:2871-2872): the routed sum, the sigmoid
+// and the product are each rounded to the output dtype before the final add, so the fused
+// layer gives the same values as the three separate elementwise ops.
+struct SharedTerm {
+  const void* shared;  // [T, H] of dtype sdt, or null
+  int sdt;
+  const void* gate;  // pre-sigmoid logit of token t at gate[t * gate_stride]
+  int gdt;
+  int64_t gate_stride;
+};
+
+__device__ inline float round_to(int dt, float v) {
+  return dt == MTPK_BF16 ? bf16_to_f32(f32_to_bf16(v)) : v;
+}
+
+__device__ inline float shared_gate(const SharedTerm& st, int t, int odt) {
+  const float g = load_float(st.gate, st.gdt, (int64_t)t * st.gate_stride);
+  return round_to(odt, 1.f / (1.f + expf(-g)));
+}
+
+__device__ inline float add_shared(const SharedTerm& st, float gs, float routed, int64_t i, int odt) {
+  const float prod = round_to(odt, gs * load_float(st.shared, st.sdt, i));
+  return round_to(odt, routed) + prod;
+}
+
 __global__ __launch_bounds__(256) void k_moe_combine(
     const float* __restrict__ y, const void* __restrict__ a_expert, int edt,
     const void* __restrict__ a_weight, int wdt, int top_k, int H, int lo, int hi,
-    void* __restrict__ out, int odt) {
+    void* __restrict__ out, int odt, SharedTerm st) {
   const int t = blockIdx.y;
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
@@ -1215,8 +1241,24 @@ __global__ __launch_bounds__(256) void k_moe_combine(
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] += w[q] * bits_f32(yv[q][c]);
   }
+  if (st.shared) {
+    const float gs = shared_gate(st, t, odt);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = add_shared(st, gs, acc[c], (int64_t)t * H + n + c, odt);
+  }
 #pragma unroll
   for (int c = 0; c < 4; ++c) store_float(out, odt, (int64_t)t * H + n + c, acc[c]);
+}
+
+// The shared term over a routed output already in `out` (the direct path, whose down kernel
+// writes the routed sum itself).
+__global__ __launch_bounds__(256) void k_moe_shared_glue(void* __restrict__ out, int odt, int H,
+                                                         SharedTerm st) {
+  const int t = blockIdx.y;
+  const int n = blockIdx.x * blockDim.x + threadIdx.x;
+  if (n >= H) return;
+  const int64_t i = (int64_t)t * H + n;
+  store_float(out, odt, i, add_shared(st, shared_gate(st, t, odt), load_float(out, odt, i), i, odt));
 }
 
 // ---------------------------------------------------------------- plane split
@@ -1633,7 +1675,7 @@ int mtpk_moe_combine(const float* y, const void* a_expert, int expert_dtype, con
   const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
   hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
-                     expert_hi, out, out_dtype);
+                     expert_hi, out, out_dtype, SharedTerm{nullptr, 0, nullptr, 0, 0});
   return status_of(hipGetLastError());
 }
 
@@ -1653,7 +1695,26 @@ int mtpk_fused_moe(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
                    const void* a_expert, int expert_dtype, const void* a_weight, int weight_dtype,
                    int top_k, int expert_lo, int expert_hi, void* workspace,
                    int64_t workspace_bytes, void* out, void* stream) {
+  return mtpk_fused_moe_shared(x, x_dtype, tokens, hidden, gate_up, gate_up_scale, down,
+                               down_scale, local_experts, inter_dim, a_expert, expert_dtype,
+                               a_weight, weight_dtype, top_k, expert_lo, expert_hi, nullptr, 0,
+                               nullptr, 0, 0, workspace, workspace_bytes, out, stream);
+}
+
+int mtpk_fused_moe_shared(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                          const uint8_t* gate_up, const uint8_t* gate_up_scale, const uint8_t* down,
+                          const uint8_t* down_scale, int64_t local_experts, int64_t inter_dim,
+                          const void* a_expert, int expert_dtype, const void* a_weight,
+                          int weight_dtype, int top_k, int expert_lo, int expert_hi,
+                          const void* shared, int shared_dtype, const void* shared_gate,
+                          int gate_dtype, int64_t gate_stride, void* workspace,
+                          int64_t workspace_bytes, void* out, void* stream) {
   if (!x || !out || !workspace || !dtype_float_ok(x_dtype)) return MTPK_EINVAL;
+  if (shared && (!shared_gate || !dtype_float_ok(shared_dtype) || !dtype_float_ok(gate_dtype) ||
+                 gate_stride < 0))
+    return MTPK_EINVAL;
+  if (tokens > 65535 || hidden <= 0 || hidden % 4) return MTPK_EINVAL;  // the combine's grid
+  const SharedTerm st{shared, shared_dtype, shared_gate, gate_dtype, gate_stride};
   if (tokens < 0 || top_k <= 0 || top_k > MTPK_MAX_TOP_K) return MTPK_EINVAL;
   if ((int64_t)expert_hi - expert_lo != local_experts) return MTPK_EINVAL;
   if (workspace_bytes <
@@ -1690,9 +1751,13 @@ int mtpk_fused_moe(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
                                  local_experts, inter_dim, a_expert, expert_dtype, a_weight,
                                  weight_dtype, top_k, expert_lo, expert_hi, inter, ip, stream);
     if (rc) return rc;
-    return mtpk_moe_down_combine(inter, ip, inter_dim, down, down_scale, local_experts, hidden,
-                                 a_expert, expert_dtype, a_weight, weight_dtype, tokens, top_k,
-                                 expert_lo, expert_hi, out, x_dtype, stream);
+    rc = mtpk_moe_down_combine(inter, ip, inter_dim, down, down_scale, local_experts, hidden,
+                               a_expert, expert_dtype, a_weight, weight_dtype, tokens, top_k,
+                               expert_lo, expert_hi, out, x_dtype, stream);
+    if (rc || !shared) return rc;
+    hipLaunchKernelGGL(k_moe_shared_glue, dim3((unsigned)((hidden + 255) / 256), (unsigned)tokens),
+                       dim3(256), 0, (hipStream_t)stream, out, x_dtype, (int)hidden, st);
+    return status_of(hipGetLastError());
   }
   rc = mtpk_moe_prep(a_expert, expert_dtype, a_weight, weight_dtype, a, expert_lo, expert_hi,
                      sorted, units, mu, n_units, stream);
@@ -1703,8 +1768,11 @@ int mtpk_fused_moe(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
   rc = mtpk_moe_down(inter, ip, a, inter_dim, down, down_scale, local_experts, hidden, sorted,
                      units, n_units, mu, y, stream);
   if (rc) return rc;
-  return mtpk_moe_combine(y, a_expert, expert_dtype, a_weight, weight_dtype, tokens, top_k,
-                          hidden, expert_lo, expert_hi, out, x_dtype, stream);
+  const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
+  hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
+                     expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
+                     expert_hi, out, x_dtype, st);
+  return status_of(hipGetLastError());
 }
 
 int mtpk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,

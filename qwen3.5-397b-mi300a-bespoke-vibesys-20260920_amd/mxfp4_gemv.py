@@ -108,8 +108,15 @@ def fused_moe(
     order: torch.Tensor | None = None,
     grouped: bool | None = None,
     total_experts: int | None = None,
+    shared: torch.Tensor | None = None,
+    shared_gate: torch.Tensor | None = None,
 ) -> torch.Tensor:
     """Routed-expert output `[T, hidden]` for tokens `x` `[T, hidden]`, never dequantising to HBM.
+
+    With `shared` `[T, hidden]` and `shared_gate` `[T, 1]` (the shared-gate column of the
+    router GEMM output, any row stride) the layer's shared-expert term is added in the same
+    launch: `out = routed + sigmoid(shared_gate) * shared` (`model.py:2871-2872`,
+    `bw_combine_glue` `mxfp4_gemv.py:2266-2312`), with the unfused ops' rounding points.
 
     `inter` is optional caller scratch: used as the kernels' workspace when it is at least
     `workspace_bytes(...)` bytes, contiguous and 256-byte aligned (the reference sizes it
@@ -137,17 +144,27 @@ def fused_moe(
     xcode = _mtpk.float_code(x.dtype)
     nbytes = lib.mtpk_moe_workspace_bytes(tokens, top_k, local, intermediate, hidden, xcode)
     ws = _workspace(device, nbytes, inter)
+    sh_ptr = gate_ptr = None
+    sh_code = gate_code = gate_stride = 0
+    if shared is not None:
+        if shared_gate is None or shared.shape != (tokens, hidden) or not shared.is_contiguous():
+            raise ValueError("shared must be a contiguous [T, hidden] tensor, with shared_gate")
+        if shared_gate.dim() != 2 or shared_gate.shape[0] != tokens:
+            raise ValueError("shared_gate must be [T, 1] (any row stride)")
+        sh_ptr, sh_code = shared.data_ptr(), _mtpk.float_code(shared.dtype)
+        gate_ptr, gate_code, gate_stride = (shared_gate.data_ptr(), _mtpk.float_code(shared_gate.dtype),
+                                            shared_gate.stride(0))
     _mtpk.check(
-        lib.mtpk_fused_moe(
+        lib.mtpk_fused_moe_shared(
             x.data_ptr(), xcode, tokens, hidden,
             gate_up.data_ptr(), experts["gate_up_scale"].data_ptr(),
             down.data_ptr(), experts["down_scale"].data_ptr(), local, intermediate,
             a_expert.data_ptr(), _mtpk.index_code(a_expert.dtype),
             a_weight.data_ptr(), _mtpk.float_code(a_weight.dtype),
-            top_k, lo, hi, ws.data_ptr(), ws.numel() * ws.element_size(),
-            out.data_ptr(), _mtpk.stream_of(device),
+            top_k, lo, hi, sh_ptr, sh_code, gate_ptr, gate_code, gate_stride,
+            ws.data_ptr(), ws.numel() * ws.element_size(), out.data_ptr(), _mtpk.stream_of(device),
         ),
-        "mtpk_fused_moe",
+        "mtpk_fused_moe_shared",
     )  # fmt: skip
     return out
 

@@ -513,17 +513,19 @@ class Model:
             top_w, top_i = probs.topk(c.top_k, dim=-1)
             top_w = top_w / top_w.sum(-1, keepdim=True)
         assign = (top_i.reshape(-1), top_w.reshape(-1))
+        shared = swiglu(h, w["shared_gate_up"], w["shared_down"])
         if "gate_up_scale" not in w["experts"]:
             routed = self._dense_moe(w["experts"], h, top_i, top_w)
         elif mxfp4_gemv.available(h.device):
-            routed = mxfp4_gemv.fused_moe(h.contiguous(), w["experts"], assign, c.top_k, (0, c.experts),
-                                          inter=self.moe_ws)
+            # the shared expert's gated term is added inside the routed layer's combine
+            return mxfp4_gemv.fused_moe(h.contiguous(), w["experts"], assign, c.top_k, (0, c.experts),
+                                        inter=self.moe_ws, shared=shared.contiguous(),
+                                        shared_gate=routing[:, c.experts :])
         elif h.device.type == "cuda":
             raise RuntimeError("SEED_FUSED_MOE=0 has no device path in this build")
         else:
             routed = mxfp4_gemv.reference_moe(h, w["experts"], assign, c.top_k, (0, c.experts),
                                               mxfp4.dequant_mxfp4)
-        shared = swiglu(h, w["shared_gate_up"], w["shared_down"])
         return routed + torch.sigmoid(routing[:, c.experts :]) * shared
 
     def _dense_moe(self, ex: dict, h: torch.Tensor, top_i: torch.Tensor,

@@ -243,3 +243,32 @@ def test_real_dims_repeat_is_bit_identical(real_layer):
     a = mxfp4_gemv.fused_moe(x, real_layer, r, TOP_K, (0, E)).clone()
     b = mxfp4_gemv.fused_moe(x, real_layer, r, TOP_K, (0, E))
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("tokens", [1, 4, 48, 192])
+def test_shared_term_in_the_combine_equals_the_unfused_ops(real_layer, tokens):
+    """`fused_moe(..., shared=, shared_gate=)` (direct path at <= 4 tokens, combine kernel
+    above) is bit-identical to `routed + sigmoid(gate) * shared` as separate bf16 torch ops."""
+    dev = torch.device("cuda:0")
+    a_e, a_w = zipf_routing(tokens, E, TOP_K, seed=tokens, zero_frac=0.05)
+    g = torch.Generator(dev).manual_seed(tokens)
+    x = torch.randn(tokens, H, device=dev, generator=g).to(torch.bfloat16)
+    routing = torch.randn(tokens, E + 1, device=dev, generator=g).to(torch.bfloat16)
+    shared = (torch.randn(tokens, H, device=dev, generator=g) * 100).to(torch.bfloat16)
+    ae, aw = torch.from_numpy(a_e).to(dev), torch.from_numpy(a_w).to(dev)
+    routed = mxfp4_gemv.fused_moe(x, real_layer, (ae, aw), TOP_K, (0, E))
+    want = routed + torch.sigmoid(routing[:, E:]) * shared
+    got = mxfp4_gemv.fused_moe(x, real_layer, (ae, aw), TOP_K, (0, E), shared=shared,
+                               shared_gate=routing[:, E:])
+    assert torch.equal(got, want)
+
+
+def test_shared_term_fp32(dev):
+    ex = to_dev(random_experts(8, 64, 32, seed=70), dev)
+    a_e, a_w = random_routing(6, 8, 2, seed=71)
+    x = torch.randn(6, 64, device=dev)
+    gate = torch.randn(6, 3, device=dev)[:, 1:2]  # a column view with row stride 3
+    shared = torch.randn(6, 64, device=dev)
+    routed = run(x, ex, a_e, a_w, 2, (0, 8), dev)
+    got = run(x, ex, a_e, a_w, 2, (0, 8), dev, shared=shared, shared_gate=gate)
+    torch.testing.assert_close(got, routed + torch.sigmoid(gate) * shared, rtol=1e-6, atol=1e-6)
