@@ -354,6 +354,18 @@ int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t he
                          int64_t table_stride, const int64_t* base_pos, float scale, int n_split,
                          void* workspace, int64_t workspace_bytes, uint16_t* out, void* stream);
 
+/* This round's K and V rows into the paged caches (the cache writes of `attn_verify`,
+ * model.py:3519-3577, graph_mtp.py:857-860, and `mtp.cache_target_rows`, mtp.py:440-485):
+ * k, v bf16 rows (b, s) of kv_heads * head_dim values at row strides k_row_stride /
+ * v_row_stride (elements, row = b * t + s), position base_pos[b] + s, pool row
+ * block_table[b][pos / 16] * 16 + pos % 16 of k_pool [pool_rows, kv_heads, head_dim] and of
+ * v_pool [pool_rows / 16, kv_heads, head_dim, 16] (the layout mtpk_paged_attention reads).
+ * keep (optional, u8 [batch * t]): rows with 0 are not written. head_dim a multiple of 8. */
+int mtpk_kv_write(const uint16_t* k, int64_t k_row_stride, const uint16_t* v, int64_t v_row_stride,
+                  uint16_t* k_pool, uint16_t* v_pool, int64_t pool_rows, const int32_t* block_table,
+                  int64_t table_stride, const int64_t* base_pos, const uint8_t* keep, int64_t batch,
+                  int64_t t, int64_t kv_heads, int64_t head_dim, void* stream);
+
 /* ---------------------------------------------------------------- test probes
  * In-bounds probe of the compiler builtin this library's MoE relies on: one wave computes
  * d = A(16x32) * B(32x16) with v_mfma_f32_16x16x32_bf16 from per-lane operand registers

@@ -92,3 +92,30 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
         "mtpk_paged_attention",
     )
     return out
+
+
+def kv_write(k_pool: torch.Tensor, v_pool: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+             block_table: torch.Tensor, base_pos: torch.Tensor, keep: torch.Tensor | None = None) -> None:
+    """Store K/V rows `k`, `v` `[B, t, kv_heads, hd]` (inner two dims contiguous, rows at any
+    stride) at positions `base_pos[b] + s` through the lanes' `block_table` `[B, blocks]` into
+    the K pool and the block-transposed V pool (`mtpk_kv_write`); rows with `keep[b, s]` False
+    are left as they are."""
+    device = _mtpk.require_device(k_pool, v_pool, k, v, block_table, base_pos)
+    b, t, kvh, hd = k.shape
+    for name, x in (("k", k), ("v", v)):
+        if x.dtype != torch.bfloat16 or x.shape != (b, t, kvh, hd) or x.stride(3) != 1 or x.stride(2) != hd \
+                or x.stride(0) != t * x.stride(1):
+            raise ValueError(f"{name} must be bf16 [B, t, kv_heads, hd] with contiguous rows")
+    if k_pool.shape[1:] != (kvh, hd) or v_pool.shape[1:] != (kvh, hd, BLOCK):
+        raise ValueError("pools do not match the rows' kv_heads / head_dim")
+    table = block_table.to(torch.int32).contiguous()
+    pos = base_pos.to(torch.int64).contiguous()
+    kp = None
+    if keep is not None:
+        kp = keep.reshape(-1).to(torch.uint8).contiguous()
+        if kp.numel() != b * t:
+            raise ValueError("keep must have B * t entries")
+    _mtpk.check(_mtpk.lib().mtpk_kv_write(
+        k.data_ptr(), k.stride(1), v.data_ptr(), v.stride(1), k_pool.data_ptr(), v_pool.data_ptr(),
+        k_pool.shape[0], table.data_ptr(), table.shape[1], pos.data_ptr(), _mtpk.ptr(kp), b, t, kvh,
+        hd, _mtpk.stream_of(device)), "mtpk_kv_write")  # fmt: skip

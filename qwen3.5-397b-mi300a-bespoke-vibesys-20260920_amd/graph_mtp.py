@@ -17,6 +17,7 @@ import torch
 
 import _mtpk
 import mtp as mtp_mod
+import verify_model as vm
 
 
 def _fixed_prefix_pack_index(lengths: torch.Tensor, width: int) -> tuple[torch.Tensor, torch.Tensor]:
@@ -176,9 +177,10 @@ def draft_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: in
     hid = mtp_mod.draft_seed(model, model.hidden_cache[lanes])
     tok = buf.token_matrix[:b, :1]
     table = model.blocks.table[lanes]
+    on_device = vm.kv_write_in_kernel(model)
     for s in range(m.k):
         pos = buf.pos[:b] + s
-        rows = model.blocks.physical_rows(lanes, pos[:, None])[:, 0]
+        rows = None if on_device else model.blocks.physical_rows(lanes, pos[:, None])[:, 0]
         hid, tok = mtp_mod.draft_step(model, m, hid, tok, pos, rows, table)
         if forced is not None:
             tok = torch.where((forced_n > s)[:, None], forced[:, s : s + 1], tok)
@@ -214,8 +216,12 @@ def verify_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: i
     grid = pos[:, None] + torch.arange(t, device=dev)[None, :]
     raw_seed = model.hidden_cache[lanes]
     previous = torch.cat([raw_seed[:, None], res.hidden[:, :-1]], dim=1)
-    mtp_mod.cache_target_rows(model, m, buf.token_matrix[:b], previous, grid,
-                              model.blocks.physical_rows(lanes, grid), out.keep)
+    if vm.kv_write_in_kernel(model):
+        mtp_mod.cache_target_rows(model, m, buf.token_matrix[:b], previous, grid, None, out.keep,
+                                  block_table=model.blocks.table[lanes], base_pos=pos)
+    else:
+        mtp_mod.cache_target_rows(model, m, buf.token_matrix[:b], previous, grid,
+                                  model.blocks.physical_rows(lanes, grid), out.keep)
     model.hidden_cache[lanes] = res.hidden.reshape(b * t, -1)[out.hidden_src]
 
 

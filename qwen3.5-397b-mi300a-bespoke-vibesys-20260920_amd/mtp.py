@@ -22,6 +22,7 @@ import torch
 
 import _mtpk
 import attention
+import rownorm
 
 MAX_STOP_IDS = 8
 """Widest per-lane stop-id set a speculative round accepts (`mtp.py:80`)."""
@@ -166,12 +167,14 @@ def _combine_rows(model, mtp: MTP, hidden: torch.Tensor, tokens: torch.Tensor) -
 
 
 def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: torch.Tensor,
-               write_rows: torch.Tensor, block_table: torch.Tensor,
+               write_rows: torch.Tensor | None, block_table: torch.Tensor,
                block_valid: torch.Tensor | None = None,
                active: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
     """One MTP decoder-layer step on device-resident tensors (`mtp.py:506-549`):
     `(hid [B, hidden], tok [B, 1])` -> the next pair. `rope_pos` `[B]` is the fed token's
-    position, `write_rows` `[B]` its MTP pool row, `block_table` `[B, blocks]` the lanes' tables.
+    position, `write_rows` `[B]` its MTP pool row (None when `verify_model.kv_write_in_kernel`:
+    the K/V write maps the position through the table), `block_table` `[B, blocks]` the lanes'
+    tables.
     `block_valid` and `active` are accepted for signature compatibility: the attention reads
     the table up to its width and masks by position, and inactive lanes write their own rows."""
     import verify_model as vm
@@ -179,7 +182,8 @@ def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: 
     c, w = model.cfg, mtp.weights
     x = _combine_rows(model, mtp, hid[:, None, :], tok)  # [B, 1, hidden]
     h = vm.rmsnorm(x, w["in_norm"], c.eps)
-    attn = vm.gated_attention(model, w, mtp.pool, h, rope_pos, write_rows.reshape(-1, 1),
+    attn = vm.gated_attention(model, w, mtp.pool, h, rope_pos,
+                              None if write_rows is None else write_rows.reshape(-1, 1),
                               block_table, block_table.shape[1])
     x, hm = vm.add_rmsnorm(x, attn, w["post_norm"], c.eps)
     _, normed = vm.add_rmsnorm(x, model.moe(w, hm[:, 0])[:, None], mtp.norm, c.eps)
@@ -210,17 +214,28 @@ def draft(model, mtp: MTP, hidden: torch.Tensor, tokens: list[int], slots: list[
 
 
 def cache_target_rows(model, mtp: MTP, tokens: torch.Tensor, raw_previous_hidden: torch.Tensor,
-                      positions: torch.Tensor, write_rows: torch.Tensor,
-                      keep: torch.Tensor | None = None) -> None:
+                      positions: torch.Tensor, write_rows: torch.Tensor | None,
+                      keep: torch.Tensor | None = None, *, block_table: torch.Tensor | None = None,
+                      base_pos: torch.Tensor | None = None) -> None:
     """Write the MTP layer's canonical K/V for fed tokens from the target's hidden stream
     (`mtp.py:440-485`): token `tokens[b, s]` at `positions[b, s]` paired with the target's raw
-    hidden state of the previous position. Rows with `keep` False are left as they are."""
+    hidden state of the previous position. Rows with `keep` False are left as they are.
+    When `verify_model.kv_write_in_kernel(model)`, `block_table` `[B, blocks]` with `base_pos`
+    `[B]` (`positions[b, s] = base_pos[b] + s`) replace `write_rows`: RoPE rides on the k norm
+    and one kernel writes the K/V rows through the table."""
     import verify_model as vm
 
     c, w = model.cfg, mtp.weights
     x = _combine_rows(model, mtp, draft_seed(model, raw_previous_hidden), tokens)
     x = vm.rmsnorm(x, w["in_norm"], c.eps)
     lead = tokens.shape
+    if vm.kv_write_in_kernel(model) and block_table is not None and base_pos is not None:
+        rope = (model.cos, model.sin, positions.reshape(-1))
+        k = rownorm.rmsnorm(vm.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim),
+                            w["k_norm"], c.eps, heads=True, rope=rope)
+        v = vm.linear(x, w["v_proj"]).view(*lead, c.kv_heads, c.head_dim)
+        attention.kv_write(mtp.pool["k"], mtp.pool["v"], k, v, block_table, base_pos, keep)
+        return
     k = vm.rmsnorm(vm.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim),
                    w["k_norm"], c.eps)
     v = vm.linear(x, w["v_proj"]).view(*lead, c.kv_heads, c.head_dim)

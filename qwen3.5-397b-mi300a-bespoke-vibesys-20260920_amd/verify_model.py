@@ -252,13 +252,20 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     return out.reshape(b, heads, t, hd).to(q.dtype)
 
 
+def kv_write_in_kernel(model: "Model") -> bool:
+    """Whether this round's K/V rows go to the caches through `attention.kv_write` (a bf16
+    model on a device), so that callers need not compute the rows' physical pool rows."""
+    return model.device.type == "cuda" and model.dtype == torch.bfloat16
+
+
 def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_pos: torch.Tensor,
                     write_rows: torch.Tensor, block_table: torch.Tensor, ctx_blocks: int) -> torch.Tensor:
     """Gated GQA attention of `t` rows per lane (`h` `[B, t, hidden]`, normed): q/gate
     projection, q/k RMSNorm, partial RoPE at `base_pos + s`, this round's K/V written at
     `write_rows` `[B, t]` of `pool`, causal paged attention, `o_proj(out * sigmoid(gate))`
     (`model.py:2158-2290`, `model.py:3519-3577`; the MTP layer's `_attn_rows`, `mtp.py:233-279`,
-    is the same call on its own pool)."""
+    is the same call on its own pool). When `kv_write_in_kernel(model)`, `write_rows` may be
+    None: the K/V write maps positions to pool rows through `block_table` itself."""
     c = model.cfg
     b, t, _ = h.shape
     qg = F.linear(h, w["q_proj"]).view(b, t, c.heads, 2 * c.head_dim)
@@ -274,9 +281,12 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
         q, k = rmsnorm(q, w["q_norm"], c.eps), rmsnorm(kp, w["k_norm"], c.eps)
         cos, sin = model.cos[pos][:, :, None], model.sin[pos][:, :, None]  # [B, t, 1, rot]
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
-    rows = write_rows.reshape(-1).long()
-    pool["k"][rows] = k.reshape(-1, c.kv_heads, c.head_dim)
-    attention.write_v(pool["v"], rows, v.reshape(-1, c.kv_heads, c.head_dim))
+    if kv_write_in_kernel(model):  # positions -> pool rows through the table, inside the kernel
+        attention.kv_write(pool["k"], pool["v"], k, v, block_table, base_pos)
+    else:
+        rows = write_rows.reshape(-1).long()
+        pool["k"][rows] = k.reshape(-1, c.kv_heads, c.head_dim)
+        attention.write_v(pool["v"], rows, v.reshape(-1, c.kv_heads, c.head_dim))
     out = paged_attention(q.transpose(1, 2), pool["k"], pool["v"], block_table, base_pos, ctx_blocks,
                           c.block_size, c.head_dim ** -0.5)
     out = out.transpose(1, 2).reshape(b, t, -1)
@@ -553,8 +563,10 @@ class Model:
         bound on `base_pos + t`."""
         c = self.cfg
         t = h.shape[1]
-        pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
-        rows = self.blocks.physical_rows(lanes, pos)
+        rows = None
+        if not kv_write_in_kernel(self):
+            pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
+            rows = self.blocks.physical_rows(lanes, pos)
         ctx_blocks = (ctx_len + c.block_size - 1) // c.block_size
         return gated_attention(self, w, pool, h, base_pos, rows, self.blocks.table[lanes], ctx_blocks)
 

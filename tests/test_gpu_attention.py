@@ -82,3 +82,34 @@ def test_rejects_bad_arguments(dev) -> None:
     with pytest.raises(ValueError):
         attention.paged_attention(q.to(dev)[..., :32].contiguous(), k.to(dev)[..., :32].contiguous(),
                                   v.to(dev)[..., :32].contiguous(), **args)
+
+
+@pytest.mark.parametrize("keep_some", [False, True])
+def test_kv_write_matches_the_indexed_writes(dev, keep_some) -> None:
+    """`attention.kv_write` (positions mapped through the block tables in the kernel) stores
+    exactly what the indexed K write and `write_v` store, and nothing else."""
+    import verify_model as vm
+
+    b, t, kvh, hd, lanes_total = 3, 4, 2, 256, 5
+    blocks = vm.BlockTables(lanes_total, 64, 16, dev, seed=3)
+    lanes = torch.tensor([4, 0, 2], device=dev)
+    base = torch.tensor([13, 0, 30], device=dev)  # block crossings inside the round
+    for lane, p in zip(lanes.tolist(), base.tolist(), strict=True):
+        blocks.grow(lane, p + t)
+    g = torch.Generator(device="cpu").manual_seed(5)
+    k = torch.randn(b, t, kvh, hd, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(b, t, kvh, hd, generator=g).to(torch.bfloat16).to(dev)
+    kp = torch.randn(blocks.rows, kvh, hd, generator=g).to(torch.bfloat16).to(dev)
+    vp = torch.randn(blocks.rows // 16, kvh, hd, 16, generator=g).to(torch.bfloat16).to(dev)
+    keep = None
+    if keep_some:
+        keep = torch.arange(t, device=dev)[None, :] <= torch.tensor([0, 3, 1], device=dev)[:, None]
+    want_k, want_v = kp.clone(), vp.clone()
+    pos = base[:, None] + torch.arange(t, device=dev)[None, :]
+    rows = blocks.physical_rows(lanes, pos).reshape(-1)
+    sel = torch.ones(b * t, dtype=torch.bool, device=dev) if keep is None else keep.reshape(-1)
+    want_k[rows[sel]] = k.reshape(-1, kvh, hd)[sel]
+    attention.write_v(want_v, rows[sel], v.reshape(-1, kvh, hd)[sel])
+    attention.kv_write(kp, vp, k, v, blocks.table[lanes], base, keep)
+    assert torch.equal(kp, want_k)
+    assert torch.equal(vp, want_v)
