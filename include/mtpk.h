@@ -354,6 +354,21 @@ int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t he
                          int64_t table_stride, const int64_t* base_pos, float scale, int n_split,
                          void* workspace, int64_t workspace_bytes, uint16_t* out, void* stream);
 
+/* mtpk_paged_attention with the query rows read, and the output rows written, at any row
+ * strides, and the attention output gate applied in the epilogue (`model.py:2158-2290`:
+ * `o_proj(out * sigmoid(gate))`). Element d of (lane b, q head h, step s) is at
+ * b * strides[0] + h * strides[1] + s * strides[2] + d of q, gate and out (three int64 strides
+ * each, multiples of 8 for q). gate may be NULL; with it, out = bf16(bf16(o) *
+ * bf16(sigmoid(gate))), the rounding of the unfused bf16 torch ops. */
+int mtpk_paged_attention_gated(const uint16_t* q, const int64_t* q_strides, const uint16_t* gate,
+                               const int64_t* gate_strides, int64_t batch, int64_t t,
+                               int64_t heads, int64_t kv_heads, int64_t head_dim,
+                               const uint16_t* k_pool, const uint16_t* v_pool, int64_t pool_rows,
+                               const int32_t* block_table, int64_t table_stride,
+                               const int64_t* base_pos, float scale, int n_split, void* workspace,
+                               int64_t workspace_bytes, uint16_t* out, const int64_t* out_strides,
+                               void* stream);
+
 /* This round's K and V rows into the paged caches (the cache writes of `attn_verify`,
  * model.py:3519-3577, graph_mtp.py:857-860, and `mtp.cache_target_rows`, mtp.py:440-485):
  * k, v bf16 rows (b, s) of kv_heads * head_dim values at row strides k_row_stride /

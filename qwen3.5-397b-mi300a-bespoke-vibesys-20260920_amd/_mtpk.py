@@ -75,6 +75,12 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_int64, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int,
          c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p],
     ),
+    "mtpk_paged_attention_gated": (
+        c_int,
+        [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
+         c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_void_p, ctypes.c_float, c_int,
+         c_void_p, c_int64, c_void_p, c_void_p, c_void_p],
+    ),
     "mtpk_kv_write": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64,

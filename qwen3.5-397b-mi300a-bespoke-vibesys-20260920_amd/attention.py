@@ -12,6 +12,8 @@ bf16 `[B, heads, t, hd]`.
 
 from __future__ import annotations
 
+import ctypes
+
 import torch
 
 import _mtpk
@@ -91,6 +93,59 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
                                  _mtpk.stream_of(device)),
         "mtpk_paged_attention",
     )
+    return out
+
+
+def _strides(x: torch.Tensor) -> ctypes.Array:
+    """(lane, head, step) element strides of a `[B, t, heads, hd]` tensor, as int64[3]."""
+    return (ctypes.c_int64 * 3)(x.stride(0), x.stride(2), x.stride(1))
+
+
+def paged_attention_gated(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+                          block_table: torch.Tensor, base_pos: torch.Tensor, ctx_len: int,
+                          scale: float, gate: torch.Tensor | None = None) -> torch.Tensor:
+    """`paged_attention` on q `[B, t, heads, hd]` (the q-norm output's layout: any strides,
+    unit stride over hd), output `[B, t, heads, hd]` contiguous, times `sigmoid(gate)` when
+    `gate` `[B, t, heads, hd]` is given (`mtpk_paged_attention_gated`), with the unfused bf16
+    ops' rounding."""
+    device = _mtpk.require_device(q, k_pool, v_pool, block_table, base_pos)
+    if q.dim() != 4 or q.dtype != torch.bfloat16 or q.stride(3) != 1:
+        raise ValueError(f"q must be bf16 [B, t, heads, hd] with unit stride over hd, got {tuple(q.shape)}")
+    b, t, heads, hd = q.shape
+    if gate is not None and (gate.shape != q.shape or gate.dtype != torch.bfloat16 or gate.stride(3) != 1):
+        raise ValueError("gate must be bf16 of q's shape with unit stride over hd")
+    if k_pool.dim() != 3 or k_pool.shape[2] != hd or k_pool.shape[0] % BLOCK:
+        raise ValueError(f"k_pool must be [rows, kv_heads, {hd}] of {BLOCK}-row blocks, got {tuple(k_pool.shape)}")
+    if tuple(v_pool.shape) != (k_pool.shape[0] // BLOCK, k_pool.shape[1], hd, BLOCK):
+        raise ValueError(f"v_pool must be [{k_pool.shape[0] // BLOCK}, {k_pool.shape[1]}, {hd}, {BLOCK}] "
+                         f"(V transposed per block), got {tuple(v_pool.shape)}")
+    if k_pool.dtype != torch.bfloat16 or v_pool.dtype != torch.bfloat16 or not (
+            k_pool.is_contiguous() and v_pool.is_contiguous()):
+        raise ValueError("pools must be contiguous bf16")
+    kvh = k_pool.shape[1]
+    if heads % kvh:
+        raise ValueError(f"{heads} q heads are not a multiple of {kvh} kv heads")
+    if block_table.dim() != 2 or block_table.shape[0] != b or tuple(base_pos.shape) != (b,):
+        raise ValueError("block_table must be [B, blocks] and base_pos [B]")
+    if int(ctx_len) > block_table.shape[1] * BLOCK:
+        raise ValueError(f"context bound {ctx_len} exceeds the table's {block_table.shape[1]} blocks")
+    table = block_table.to(torch.int32).contiguous()
+    pos = base_pos.to(torch.int64).contiguous()
+    lib = _mtpk.lib()
+    n_split = int(lib.mtpk_attention_splits(b, t, heads, kvh, max(int(ctx_len), 1)))
+    ws_bytes = int(lib.mtpk_attention_workspace_bytes(b, t, heads, kvh, hd, n_split))
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    out = torch.empty(b, t, heads, hd, dtype=torch.bfloat16, device=device)
+    qs, os_ = _strides(q), _strides(out)
+    gs = _strides(gate) if gate is not None else None
+    _mtpk.check(
+        lib.mtpk_paged_attention_gated(
+            q.data_ptr(), ctypes.addressof(qs), _mtpk.ptr(gate), ctypes.addressof(gs) if gs else None,
+            b, t, heads, kvh, hd, k_pool.data_ptr(), v_pool.data_ptr(), k_pool.shape[0], table.data_ptr(),
+            table.shape[1], pos.data_ptr(), float(scale), n_split, ws.data_ptr(), ws_bytes,
+            out.data_ptr(), ctypes.addressof(os_), _mtpk.stream_of(device)),
+        "mtpk_paged_attention_gated",
+    )  # fmt: skip
     return out
 
 

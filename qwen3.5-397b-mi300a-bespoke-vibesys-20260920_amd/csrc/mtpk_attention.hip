@@ -78,13 +78,37 @@ __device__ inline float row16_sum(float v) {
   return v;
 }
 
+// Where the query rows come from and the output rows go: element d of (lane b, q head h, step s)
+// is at b * sb + h * sh + s * st + d of each tensor (unit stride over d). With `gate`, the stored
+// output is bf16(bf16(o) * bf16(sigmoid(gate))), the rounding of the torch chain
+// `out * torch.sigmoid(gate)` on bf16 tensors (`model.py:2158-2290`).
+struct AttnRows {
+  int64_t sb, sh, st;
+  __device__ inline int64_t at(int b, int h, int s) const { return b * sb + h * sh + s * st; }
+};
+struct AttnIO {
+  const uint16_t* q;
+  AttnRows qr;
+  uint16_t* out;
+  AttnRows orow;
+  const uint16_t* gate;  // may be null
+  AttnRows gr;
+};
+
+__device__ inline uint16_t attn_out_value(const AttnIO& io, float v, int b, int h, int s, int d) {
+  if (!io.gate) return f32_to_bf16(v);
+  const float g = bf16_to_f32(io.gate[io.gr.at(b, h, s) + d]);
+  const float sg = bf16_to_f32(f32_to_bf16(1.f / (1.f + expf(-g))));
+  return f32_to_bf16(bf16_to_f32(f32_to_bf16(v)) * sg);
+}
+
 template <int HD>
 __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
-    const uint16_t* __restrict__ q, const uint16_t* __restrict__ k_pool,
+    AttnIO io, const uint16_t* __restrict__ k_pool,
     const uint16_t* __restrict__ v_pool, int64_t pool_rows, const int32_t* __restrict__ table,
     int table_stride, const int64_t* __restrict__ base_pos, int t, int heads, int kvh,
     float scale_log2, int n_split, int row_groups, float* __restrict__ part_o,
-    float* __restrict__ part_ml, uint16_t* __restrict__ out) {
+    float* __restrict__ part_ml) {
   using G = AttnGeom<HD>;
   __shared__ __attribute__((aligned(16))) uint8_t ks[G::kKBytes];
   __shared__ __attribute__((aligned(16))) uint8_t vs[G::kVBytes];
@@ -111,7 +135,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
   {
     const bool live = ra < R;
     const int hq = kh * group + (live ? ra / t : 0), st = live ? ra % t : 0;
-    const uint16_t* qrow = q + (((int64_t)b * heads + hq) * t + st) * HD;
+    const uint16_t* qrow = io.q + io.qr.at(b, hq, st);
 #pragma unroll
     for (int ds = 0; ds < G::kDs; ++ds)
       qa[ds] = live ? as_bf16x8(ld16(qrow + 32 * ds + 8 * g)) : as_bf16x8(zero16());
@@ -250,9 +274,10 @@ __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
     if (n_split == 1) {
       const float inv = 1.f / l[i];
       const int hq = kh * group + r / t, st = r % t;
-      uint16_t* orow = out + (((int64_t)b * heads + hq) * t + st) * HD;
+      uint16_t* orow = io.out + io.orow.at(b, hq, st);
 #pragma unroll
-      for (int dt = 0; dt < G::kDt; ++dt) orow[16 * dt + c] = f32_to_bf16(o[dt][i] * inv);
+      for (int dt = 0; dt < G::kDt; ++dt)
+        orow[16 * dt + c] = attn_out_value(io, o[dt][i] * inv, b, hq, st, 16 * dt + c);
     } else {
       float* po = part_o + (slot * kAttnRows + rl) * HD;
 #pragma unroll
@@ -271,7 +296,7 @@ template <int HD>
 __global__ __launch_bounds__(256) void k_attention_merge(
     const float* __restrict__ part_o, const float* __restrict__ part_ml,
     const int64_t* __restrict__ base_pos, int B, int t, int heads, int kvh, int n_split,
-    int row_groups, uint16_t* __restrict__ out) {
+    int row_groups, AttnIO io) {
   const int group = heads / kvh;
   const int64_t rows = (int64_t)B * heads * t;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -305,9 +330,9 @@ __global__ __launch_bounds__(256) void k_attention_merge(
     for (int e = 0; e < 4; ++e) acc[e] += po[e] * w;
   }
   const float inv = 1.f / lsum;
-  uint16_t* orow = out + row * HD + d;
+  uint16_t* orow = io.out + io.orow.at(b, hq, st) + d;
 #pragma unroll
-  for (int e = 0; e < 4; ++e) orow[e] = f32_to_bf16(acc[e] * inv);
+  for (int e = 0; e < 4; ++e) orow[e] = attn_out_value(io, acc[e] * inv, b, hq, st, d + e);
 }
 
 int attention_splits(int64_t B, int64_t kvh, int row_groups, int64_t max_ctx) {
@@ -321,20 +346,20 @@ int attention_splits(int64_t B, int64_t kvh, int row_groups, int64_t max_ctx) {
 }
 
 template <int HD>
-int launch_attention(const uint16_t* q, const uint16_t* k_pool, const uint16_t* v_pool,
+int launch_attention(const AttnIO& io, const uint16_t* k_pool, const uint16_t* v_pool,
                      int64_t pool_rows, const int32_t* table, int table_stride,
                      const int64_t* base_pos, int B, int t, int heads, int kvh, float scale,
-                     int n_split, float* part_o, float* part_ml, uint16_t* out, hipStream_t st) {
+                     int n_split, float* part_o, float* part_ml, hipStream_t st) {
   const int row_groups = (heads / kvh * t + kAttnRows - 1) / kAttnRows;
   const float scale_log2 = scale * 1.4426950408889634f;
   hipLaunchKernelGGL(k_paged_attention<HD>, dim3(B * kvh * row_groups, n_split), dim3(kAttnThreads),
-                     0, st, q, k_pool, v_pool, pool_rows, table, table_stride, base_pos, t, heads,
-                     kvh, scale_log2, n_split, row_groups, part_o, part_ml, out);
+                     0, st, io, k_pool, v_pool, pool_rows, table, table_stride, base_pos, t, heads,
+                     kvh, scale_log2, n_split, row_groups, part_o, part_ml);
   int rc = status_of(hipGetLastError());
   if (rc || n_split == 1) return rc;
   const int64_t threads = (int64_t)B * heads * t * (HD / 4);
   hipLaunchKernelGGL(k_attention_merge<HD>, dim3((unsigned)((threads + 255) / 256)), dim3(256), 0, st,
-                     part_o, part_ml, base_pos, B, t, heads, kvh, n_split, row_groups, out);
+                     part_o, part_ml, base_pos, B, t, heads, kvh, n_split, row_groups, io);
   return status_of(hipGetLastError());
 }
 
@@ -398,17 +423,21 @@ int64_t mtpk_attention_workspace_bytes(int64_t batch, int64_t t, int64_t heads, 
   return slots * (head_dim + 2) * 4;
 }
 
-int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t heads,
-                         int64_t kv_heads, int64_t head_dim, const uint16_t* k_pool,
-                         const uint16_t* v_pool, int64_t pool_rows, const int32_t* block_table,
-                         int64_t table_stride, const int64_t* base_pos, float scale, int n_split,
-                         void* workspace, int64_t workspace_bytes, uint16_t* out, void* stream) {
-  if (!q || !k_pool || !v_pool || !block_table || !base_pos || !out) return MTPK_EINVAL;
+namespace {
+
+int paged_attention_io(const AttnIO& io, int64_t batch, int64_t t, int64_t heads, int64_t kv_heads,
+                       int64_t head_dim, const uint16_t* k_pool, const uint16_t* v_pool,
+                       int64_t pool_rows, const int32_t* block_table, int64_t table_stride,
+                       const int64_t* base_pos, float scale, int n_split, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  if (!io.q || !k_pool || !v_pool || !block_table || !base_pos || !io.out) return MTPK_EINVAL;
   if (batch < 0 || t <= 0 || heads <= 0 || kv_heads <= 0 || heads % kv_heads) return MTPK_EINVAL;
   if (head_dim != 64 && head_dim != 128 && head_dim != 256) return MTPK_EINVAL;
   if (pool_rows <= 0 || pool_rows * kv_heads * head_dim * 2 > 0x7fffffffLL) return MTPK_EINVAL;
   if (table_stride <= 0 || n_split < 1 || n_split > 64 || !(scale > 0.f)) return MTPK_EINVAL;
-  if (!aligned16(q) || !aligned16(k_pool) || !aligned16(v_pool)) return MTPK_EINVAL;
+  if (!aligned16(io.q) || !aligned16(k_pool) || !aligned16(v_pool)) return MTPK_EINVAL;
+  // 16-byte q loads: every q row starts on a 16-byte boundary
+  if (io.qr.sb % 8 || io.qr.sh % 8 || io.qr.st % 8) return MTPK_EINVAL;
   if (batch * heads * t > INT32_MAX / 64) return MTPK_EINVAL;
   if (n_split > 1 &&
       (!workspace || workspace_bytes < mtpk_attention_workspace_bytes(batch, t, heads, kv_heads,
@@ -419,16 +448,48 @@ int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t he
   float* part_o = (float*)workspace;
   float* part_ml = part_o ? part_o + batch * kv_heads * rg * n_split * kAttnRows * head_dim : nullptr;
   const hipStream_t st = (hipStream_t)stream;
-#define MTPK_ATTN(HD_)                                                                         \
-  launch_attention<HD_>(q, k_pool, v_pool, pool_rows, block_table, (int)table_stride, base_pos, \
-                        (int)batch, (int)t, (int)heads, (int)kv_heads, scale, n_split, part_o,  \
-                        part_ml, out, st)
+#define MTPK_ATTN(HD_)                                                                          \
+  launch_attention<HD_>(io, k_pool, v_pool, pool_rows, block_table, (int)table_stride, base_pos, \
+                        (int)batch, (int)t, (int)heads, (int)kv_heads, scale, n_split, part_o,   \
+                        part_ml, st)
   switch (head_dim) {
     case 64: return MTPK_ATTN(64);
     case 128: return MTPK_ATTN(128);
     default: return MTPK_ATTN(256);
   }
 #undef MTPK_ATTN
+}
+
+}  // namespace
+
+int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t heads,
+                         int64_t kv_heads, int64_t head_dim, const uint16_t* k_pool,
+                         const uint16_t* v_pool, int64_t pool_rows, const int32_t* block_table,
+                         int64_t table_stride, const int64_t* base_pos, float scale, int n_split,
+                         void* workspace, int64_t workspace_bytes, uint16_t* out, void* stream) {
+  const AttnRows dense{heads * t * head_dim, t * head_dim, head_dim};  // [B, heads, t, HD]
+  const AttnIO io{q, dense, out, dense, nullptr, dense};
+  return paged_attention_io(io, batch, t, heads, kv_heads, head_dim, k_pool, v_pool, pool_rows,
+                            block_table, table_stride, base_pos, scale, n_split, workspace,
+                            workspace_bytes, stream);
+}
+
+int mtpk_paged_attention_gated(const uint16_t* q, const int64_t* q_strides, const uint16_t* gate,
+                               const int64_t* gate_strides, int64_t batch, int64_t t,
+                               int64_t heads, int64_t kv_heads, int64_t head_dim,
+                               const uint16_t* k_pool, const uint16_t* v_pool, int64_t pool_rows,
+                               const int32_t* block_table, int64_t table_stride,
+                               const int64_t* base_pos, float scale, int n_split, void* workspace,
+                               int64_t workspace_bytes, uint16_t* out, const int64_t* out_strides,
+                               void* stream) {
+  if (!q_strides || !out_strides || (gate && !gate_strides)) return MTPK_EINVAL;
+  const AttnRows qr{q_strides[0], q_strides[1], q_strides[2]};
+  const AttnRows orow{out_strides[0], out_strides[1], out_strides[2]};
+  const AttnRows gr = gate ? AttnRows{gate_strides[0], gate_strides[1], gate_strides[2]} : orow;
+  const AttnIO io{q, qr, out, orow, gate, gr};
+  return paged_attention_io(io, batch, t, heads, kv_heads, head_dim, k_pool, v_pool, pool_rows,
+                            block_table, table_stride, base_pos, scale, n_split, workspace,
+                            workspace_bytes, stream);
 }
 
 int mtpk_kv_write(const uint16_t* k, int64_t k_row_stride, const uint16_t* v, int64_t v_row_stride,

@@ -287,6 +287,11 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
         rows = write_rows.reshape(-1).long()
         pool["k"][rows] = k.reshape(-1, c.kv_heads, c.head_dim)
         attention.write_v(pool["v"], rows, v.reshape(-1, c.kv_heads, c.head_dim))
+    if attention.supported(q, c.block_size):
+        # q read in its [B, t, heads, hd] layout, the sigmoid gate applied in the epilogue
+        out = attention.paged_attention_gated(q, pool["k"], pool["v"], block_table, base_pos,
+                                              ctx_blocks * c.block_size, c.head_dim ** -0.5, gate)
+        return F.linear(out.reshape(b, t, -1), w["o_proj"])
     out = paged_attention(q.transpose(1, 2), pool["k"], pool["v"], block_table, base_pos, ctx_blocks,
                           c.block_size, c.head_dim ** -0.5)
     out = out.transpose(1, 2).reshape(b, t, -1)

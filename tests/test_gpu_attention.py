@@ -113,3 +113,30 @@ def test_kv_write_matches_the_indexed_writes(dev, keep_some) -> None:
     attention.kv_write(kp, vp, k, v, blocks.table[lanes], base, keep)
     assert torch.equal(kp, want_k)
     assert torch.equal(vp, want_v)
+
+
+@pytest.mark.parametrize("t,ctx", [(4, 200), (1, 8192), (4, 8192)])
+def test_gated_layout_equals_the_unfused_ops(dev, t, ctx) -> None:
+    """`paged_attention_gated` on the q-norm layout with the gate in the epilogue equals the
+    transposes + `paged_attention` + `out * sigmoid(gate)` as bf16 torch ops, bit for bit (one
+    key split and several)."""
+    import verify_model as vm
+
+    b, heads, kvh, hd = 3, 32, 2, 256
+    blocks = vm.BlockTables(b, ctx + t, 16, dev, seed=2)
+    base = torch.tensor([ctx - t, ctx // 3, 7], device=dev)
+    for lane in range(b):
+        blocks.grow(lane, int(base[lane]) + t)
+    g = torch.Generator(device="cpu").manual_seed(t)
+    kp = torch.randn(blocks.rows, kvh, hd, generator=g).to(torch.bfloat16).to(dev)
+    vp = torch.randn(blocks.rows // 16, kvh, hd, 16, generator=g).to(torch.bfloat16).to(dev)
+    qg = torch.randn(b, t, heads, 2 * hd, generator=g).to(torch.bfloat16).to(dev)
+    q, gate = qg[..., :hd], qg[..., hd:]  # strided views, as the model holds them
+    table, lanes = blocks.table, torch.arange(b, device=dev)
+    want = attention.paged_attention(q.transpose(1, 2), kp, vp, table[lanes], base, ctx + t, hd ** -0.5)
+    want = want.transpose(1, 2) * torch.sigmoid(gate)
+    got = attention.paged_attention_gated(q, kp, vp, table[lanes], base, ctx + t, hd ** -0.5, gate)
+    assert got.is_contiguous() and torch.equal(got, want)
+    plain = attention.paged_attention_gated(q, kp, vp, table[lanes], base, ctx + t, hd ** -0.5)
+    ref = attention.paged_attention(q.transpose(1, 2), kp, vp, table[lanes], base, ctx + t, hd ** -0.5)
+    assert torch.equal(plain, ref.transpose(1, 2))
