@@ -106,13 +106,16 @@ int launch_delta_rule_mode(float* state, const int64_t* slot, int rows, int t, i
 // launch (`deltanet_verify`, model.py:3738-3905, up to `delta_rule_verify_exact`): the depthwise
 // causal conv over the stored window and the new raw columns, SiLU, rounding to the model dtype
 // (the conv output is a model-dtype tensor), the q / k / v split, the q and k L2 norms (q also
-// scaled by k_dim^-1/2), beta = sigmoid(b) and g = -exp(A_log) softplus(a + dt_bias). One
-// workgroup per verify row (b, s); its waves take 128-channel head units in turn (q heads, then
-// k heads, then v heads), lane l holding channels l, l + 64, ...
+// scaled by k_dim^-1/2), beta = sigmoid(b) and g = -exp(A_log) softplus(a + dt_bias). One wave
+// per (verify row (b, s), head unit), the units being the q heads, then the k heads, then the v
+// heads; lane l holds channels l, l + 64, ... A workgroup is 4 units of one row (grid: rows x
+// units / 4), so the launch has thousands of workgroups and every wave issues all of its loads
+// at once; the workgroups of unit group 0 also write the row's g and beta.
 //
 // Conv taps run in order j = 0 .. conv_k - 1 as separate products and sums (no fused
 // multiply-add), as the torch form does them.
 constexpr int kPrepThreadsDn = 256;
+constexpr int kConvMaxK1 = 8;  // conv_k - 1 at most
 constexpr int kPrepMaxPerLane = 4;  // head dims up to 256
 
 struct DnPrepArgs {
@@ -136,7 +139,8 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
   const int C = 2 * a.kh * a.kd + a.vh * a.vd;
   const int64_t slot = a.slot[b];
   const int units = 2 * a.kh + a.vh;
-  for (int u = wave; u < units; u += kPrepThreadsDn / kWave) {
+  const int u = blockIdx.y * (kPrepThreadsDn / kWave) + wave;
+  if (u < units) {
     const bool is_v = u >= 2 * a.kh;
     const int dim = is_v ? a.vd : a.kd;
     const int c0 = is_v ? 2 * a.kh * a.kd + (u - 2 * a.kh) * a.vd : u * a.kd;
@@ -149,7 +153,9 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
       if (ch >= dim) continue;
       const int c = c0 + ch;
       float acc = 0.f;
-      for (int j = 0; j < a.conv_k; ++j) {
+#pragma unroll
+      for (int j = 0; j < kConvMaxK1 + 1; ++j) {  // all taps' loads issued together
+        if (j >= a.conv_k) break;
         const int p = s + j;  // window column: the stored k1, then the t new ones
         const float win = p < k1 ? load_float(a.conv, a.dt, (slot * C + c) * k1 + p)
                                  : load_float(a.proj, a.dt, ((int64_t)b * a.t + p - k1) * a.proj_stride + c);
@@ -176,7 +182,7 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
         if (lane + kWave * i < dim) dst[lane + kWave * i] = x[i] * inv * sc;
     }
   }
-  for (int h = tid; h < a.vh; h += kPrepThreadsDn) {
+  for (int h = tid; blockIdx.y == 0 && h < a.vh; h += kPrepThreadsDn) {
     const int64_t base = (int64_t)rs * a.proj_stride + C + a.vh * a.vd;
     const float braw = load_float(a.proj, a.dt, base + h);
     const float araw = load_float(a.proj, a.dt, base + a.vh + h);
@@ -191,8 +197,6 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
 // window becomes columns idx[b][0 .. k1) of [stored window | the t new raw columns]. A thread
 // owns one (row, channel) and reads all of its sources before it writes, so the in-place update
 // cannot read a value it has already replaced.
-constexpr int kConvMaxK1 = 8;
-
 __global__ __launch_bounds__(256) void k_conv_commit(void* __restrict__ conv, int dt,
                                                      const int64_t* __restrict__ slot,
                                                      const void* __restrict__ proj,
@@ -264,8 +268,11 @@ int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const v
   DnPrepArgs a{proj, proj_stride, conv_state, slot, conv_w, a_log, dt_bias, dtype, (int)t,
                (int)k_heads, (int)k_dim, (int)v_heads, (int)v_dim, (int)conv_k, eps, q_scale,
                q, k, v, g, beta};
-  hipLaunchKernelGGL(k_deltanet_prep, dim3((unsigned)(batch * t)), dim3(kPrepThreadsDn), 0,
-                     (hipStream_t)stream, a);
+  const int64_t units = 2 * k_heads + v_heads;
+  const int64_t groups = (units + kPrepThreadsDn / kWave - 1) / (kPrepThreadsDn / kWave);
+  if (groups > 65535) return MTPK_EINVAL;
+  hipLaunchKernelGGL(k_deltanet_prep, dim3((unsigned)(batch * t), (unsigned)groups),
+                     dim3(kPrepThreadsDn), 0, (hipStream_t)stream, a);
   return status_of(hipGetLastError());
 }
 
