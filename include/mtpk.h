@@ -295,8 +295,9 @@ int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, const voi
                      int64_t k1, int64_t t, void* stream);
 
 /* ---------------------------------------------------------------- skinny bf16 GEMM
- * y[M, N] = x[M, K] . w[N, K]^T for M <= 64 token rows, bf16 in, fp32 accumulation: the
- * weight-bandwidth-bound linears of the MTP draft step (fc, q/k/v/o projections), the shared
+ * y[M, N] = x[M, K] . w[N, K]^T for M <= 256 token rows, bf16 in, fp32 accumulation: the
+ * weight-bandwidth-bound linears of the MTP draft and verify steps (fc, q/k/v/o and DeltaNet
+ * projections), the shared
  * expert and router of a decode or draft MoE layer (`swiglu_mlp`, model.py:638-649;
  * model.py:2811-2873) and the LM head (`greedy_token`, mtp.py:640-658). x, w contiguous,
  * 16-byte aligned; K a multiple of 256; N * K * 2 < 2^31.

@@ -1,8 +1,10 @@
 // bf16 weight-streaming GEMM for few token rows on gfx950: Y[M, N] = X[M, K] . W[N, K]^T with
-// M <= 64, the shape of the MTP draft step's projections (M = B = 48), the LM head
-// (`greedy_token`, mtp.py:640-658; N = vocab) and the shared expert / router of a decode or
-// draft MoE layer (model.py:2811-2873). These are weight-bandwidth bound: every weight byte is
-// read once, and the token rows are the MFMA's other operand.
+// M <= 256, the shape of the MTP draft step's projections (M = B = 48), the verify step's
+// (M = B (k + 1) = 192), the LM head (`greedy_token`, mtp.py:640-658; N = vocab) and the shared
+// expert / router of a decode or draft MoE layer (model.py:2811-2873). These are weight-
+// bandwidth bound: every weight byte is read from HBM once, and the token rows are the MFMA's
+// other operand. Above 64 rows the rows are split into groups of 64, one workgroup per
+// (weight tile, row group).
 //
 // Workgroup = NW = 4 or 8 waves, tile = 16 NW weight rows (wave w: rows 16 w .. + 15; with the
 // paired SiLU epilogue also the matching 16 "up" rows N/2 + ...) x all M tokens (TT = ceil(M / 16) MFMA token
@@ -41,6 +43,8 @@ struct GemmArgs {
   void* out;
   float* part;
   uint64_t* keys;  // argmax: [M, tiles]
+  int tiles;       // weight tiles of 16 NW rows
+  int RG;          // row groups of 16 TT token rows (M > 64: RG = ceil(M / 64), TT = 4)
 };
 
 template <int TT, int S, int NW>
@@ -51,7 +55,21 @@ __global__ __launch_bounds__(NW * kWave, 16 / NW) void k_gemm_skinny(GemmArgs a)
   __shared__ uint64_t kred[NW][TT * 16];
   const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
-  const int tile = blockIdx.x, ks = blockIdx.y;
+  // Workgroup -> (weight tile, row group). With several row groups, the groups of one tile
+  // get ids 8 apart (the XCD round-robin), so that they run on one XCD close in time and can
+  // share its L2. Measured at 192 rows, this pays where the weight tiles are few (N = 4096:
+  // 47 us against the library GEMM's 61) but not on wide N (the LM head re-reads its weights
+  // about 2.6 times, 2.3 TB/s), where callers keep the library GEMM.
+  int tile = blockIdx.x, rg = 0;
+  if (a.RG > 1) {
+    const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
+    tile = (slot / a.RG) * 8 + xcd;
+    rg = slot % a.RG;
+    if (tile >= a.tiles) return;  // grid padding, before any barrier
+  }
+  const int ks = blockIdx.y;
+  const int m0 = rg * 16 * TT;                             // first token row of this group
+  const int Mg = a.M - m0 < 16 * TT ? a.M - m0 : 16 * TT;  // its rows
   const int kc_per = a.K / kGemmKC / a.KS;  // chunks of this split
   const int k0 = ks * kc_per * kGemmKC;
   const int nchunk = kc_per;
@@ -85,8 +103,8 @@ __global__ __launch_bounds__(NW * kWave, 16 / NW) void k_gemm_skinny(GemmArgs a)
 #pragma unroll
     for (int j = 0; j < kSL; ++j) {
       const int p = j * NT + tid, row = p >> 5, col = p & 31;
-      const bool ok = c < nchunk && row < a.M;
-      sreg[j] = buf16(rx, ok ? (uint32_t)(((int64_t)row * a.K + k0 + c * kGemmKC + col * 8) * 2)
+      const bool ok = c < nchunk && row < Mg;
+      sreg[j] = buf16(rx, ok ? (uint32_t)(((int64_t)(m0 + row) * a.K + k0 + c * kGemmKC + col * 8) * 2)
                              : kOutOfRange);
     }
   };
@@ -147,12 +165,12 @@ __global__ __launch_bounds__(NW * kWave, 16 / NW) void k_gemm_skinny(GemmArgs a)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int m = 16 * t + 4 * ln.g + i;
-        if (m >= a.M) continue;
+        if (m >= Mg) continue;
 #pragma unroll
         for (int s = 0; s < S; ++s) {
           const int col = S == 1 ? r0 : r0 + s * a.cols;  // partial columns: gate, then up
           if (!wok[s]) continue;
-          a.part[((int64_t)ks * a.M + m) * (int64_t)(S * a.cols) + col] = acc[s][t][i];
+          a.part[((int64_t)ks * a.M + m0 + m) * (int64_t)(S * a.cols) + col] = acc[s][t][i];
         }
       }
     return;
@@ -176,10 +194,10 @@ __global__ __launch_bounds__(NW * kWave, 16 / NW) void k_gemm_skinny(GemmArgs a)
         if (ln.c == 0) kred[wave][16 * t + 4 * ln.g + i] = key;
       }
     __syncthreads();
-    for (int m = tid; m < a.M; m += NT) {
+    for (int m = tid; m < Mg; m += NT) {
       uint64_t b = kred[0][m];
       for (int w2 = 1; w2 < NW; ++w2) b = kred[w2][m] > b ? kred[w2][m] : b;
-      a.keys[(int64_t)m * gridDim.x + tile] = b;
+      a.keys[(int64_t)(m0 + m) * a.tiles + tile] = b;
     }
     return;
   }
@@ -188,10 +206,10 @@ __global__ __launch_bounds__(NW * kWave, 16 / NW) void k_gemm_skinny(GemmArgs a)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int m = 16 * t + 4 * ln.g + i;
-      if (m >= a.M || !wok[0]) continue;
+      if (m >= Mg || !wok[0]) continue;
       float v = acc[0][t][i];
       if (S == 2) v = v / (1.f + __expf(-v)) * acc[1][t][i];
-      store_float(a.out, a.odt, (int64_t)m * a.cols + r0, v);
+      store_float(a.out, a.odt, (int64_t)(m0 + m) * a.cols + r0, v);
     }
 }
 
@@ -239,6 +257,13 @@ namespace {
 
 int gemm_cols(int64_t n, int epi) { return (int)(epi == kEpiSilu ? n / 2 : n); }
 
+constexpr int64_t kGemmMaxRows = 256;  // 4 row groups of 64
+
+// Row groups of 64 token rows: one below 65 rows (then TT = ceil(M / 16)), else ceil(M / 64)
+// with TT = 4.
+int gemm_groups(int64_t m) { return m <= 64 ? 1 : (int)((m + 63) / 64); }
+int gemm_tt(int64_t m) { return m <= 64 ? (int)((m + 15) / 16) : 4; }
+
 // Waves per workgroup. At TT >= 3 token tiles the 2 x TT x 8 KiB staged token rows hold a CU to
 // three 4-wave workgroups; 8 waves sharing one staged copy double the resident waves, which
 // measured 4% faster on [48 | 64, 4096] x [248320, 4096] (the LM head) but slower wherever the
@@ -259,7 +284,8 @@ int gemm_splits(int64_t m, int64_t n, int64_t k, int epi) {
   if (epi == kEpiArgmax) return 1;
   const int64_t tiles = gemm_tiles(m, n, epi);
   const int64_t chunks = k / kGemmKC;
-  const int64_t want = (3 * (int64_t)device_cu_count() * 4 / gemm_waves(m, n, epi) + tiles - 1) / tiles;
+  const int64_t wgs = tiles * gemm_groups(m);
+  const int64_t want = (3 * (int64_t)device_cu_count() * 4 / gemm_waves(m, n, epi) + wgs - 1) / wgs;
   int ks = 1;
   while (ks * 2 <= want && chunks % (ks * 2) == 0 && chunks / (ks * 2) >= 4) ks *= 2;
   return ks;
@@ -267,7 +293,10 @@ int gemm_splits(int64_t m, int64_t n, int64_t k, int epi) {
 
 template <int TT, int S, int NW>
 void launch_gemm(const GemmArgs& a, int tiles, hipStream_t st) {
-  hipLaunchKernelGGL((k_gemm_skinny<TT, S, NW>), dim3((unsigned)tiles, (unsigned)a.KS),
+  // several row groups: tiles padded to a multiple of 8 (the XCD count) so that a tile's
+  // groups share an XCD; the padding workgroups exit at once
+  const int64_t grid = a.RG > 1 ? (int64_t)((tiles + 7) / 8) * 8 * a.RG : tiles;
+  hipLaunchKernelGGL((k_gemm_skinny<TT, S, NW>), dim3((unsigned)grid, (unsigned)a.KS),
                      dim3(NW * kWave), 0, st, a);
 }
 
@@ -291,7 +320,8 @@ using namespace mtpk;
 extern "C" {
 
 int64_t mtpk_gemm_workspace_bytes(int64_t m, int64_t n, int64_t k, int epilogue) {
-  if (m <= 0 || m > 64 || n <= 0 || k <= 0 || k % kGemmKC || epilogue < 0 || epilogue > 2) return 0;
+  if (m <= 0 || m > kGemmMaxRows || n <= 0 || k <= 0 || k % kGemmKC || epilogue < 0 || epilogue > 2)
+    return 0;
   const int ks = gemm_splits(m, n, k, epilogue);
   const int64_t tiles = gemm_tiles(m, n, epilogue);
   if (epilogue == kEpiArgmax) return m * tiles * 8;
@@ -303,7 +333,7 @@ int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, i
                    int epilogue, void* out, int out_dtype, void* workspace,
                    int64_t workspace_bytes, void* stream) {
   if (!x || !w || !out) return MTPK_EINVAL;
-  if (m < 0 || m > 64 || n <= 0 || k <= 0 || k % kGemmKC || epilogue < 0 || epilogue > 2)
+  if (m < 0 || m > kGemmMaxRows || n <= 0 || k <= 0 || k % kGemmKC || epilogue < 0 || epilogue > 2)
     return MTPK_EINVAL;
   if (epilogue == kEpiSilu && (n % 2 || (n / 2) % 16)) return MTPK_EINVAL;
   if (epilogue != kEpiArgmax && out_dtype != MTPK_F32 && out_dtype != MTPK_BF16) return MTPK_EINVAL;
@@ -317,9 +347,11 @@ int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, i
   const int tiles = (int)gemm_tiles(m, n, epilogue);
   GemmArgs a{x, w, (int)m, (int)n, (int)k, ks, epilogue, out_dtype, cols, out,
              ks > 1 ? static_cast<float*>(workspace) : nullptr,
-             epilogue == kEpiArgmax ? static_cast<uint64_t*>(workspace) : nullptr};
+             epilogue == kEpiArgmax ? static_cast<uint64_t*>(workspace) : nullptr, tiles,
+             gemm_groups(m)};
+  if ((int64_t)(tiles + 7) / 8 * 8 * a.RG > INT32_MAX) return MTPK_EINVAL;
   const hipStream_t st = (hipStream_t)stream;
-  const int tt = (int)((m + 15) / 16);
+  const int tt = gemm_tt(m);
   if (epilogue == kEpiSilu)
     launch_gemm_tt<2>(a, tt, tiles, st);
   else

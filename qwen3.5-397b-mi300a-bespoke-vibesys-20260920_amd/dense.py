@@ -1,6 +1,6 @@
 """bf16 linears of a few token rows on the device (`mtpk_gemm_bf16`).
 
-`linear(x, w)` is `F.linear(x, w)` for `x` `[..., K]` with at most 64 rows; `silu_linear` is
+`linear(x, w)` is `F.linear(x, w)` for `x` `[..., K]` with at most 256 rows; `silu_linear` is
 the shared expert's gate_up with its `silu(gate) * up` (`swiglu_mlp`, `model.py:638-649`) in the
 same launch; `argmax_linear` the LM head with its first-occurrence argmax
 (`greedy_token`, `mtp.py:640-658`) in the same launch, so the logits never reach memory.
@@ -13,12 +13,12 @@ import torch
 
 import _mtpk
 
-MAX_ROWS = 64
+MAX_ROWS = 256
 STORE, SILU, ARGMAX = 0, 1, 2
 
 
 def fits(x: torch.Tensor, w: torch.Tensor) -> bool:
-    """bf16 device tensors, at most 64 rows, K a multiple of 256, contiguous rows."""
+    """bf16 device tensors, at most 256 rows, K a multiple of 256, contiguous rows."""
     if x.device.type != "cuda" or x.dtype != torch.bfloat16 or w.dtype != torch.bfloat16:
         return False
     rows = x.numel() // x.shape[-1] if x.dim() else 0

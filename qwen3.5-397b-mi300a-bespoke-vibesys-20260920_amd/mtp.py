@@ -163,7 +163,7 @@ def _combine_rows(model, mtp: MTP, hidden: torch.Tensor, tokens: torch.Tensor) -
     eps = model.cfg.eps
     emb = vm.rmsnorm(model.embed[tokens], mtp.pre_fc_norm_embedding, eps)
     hid = vm.rmsnorm(hidden, mtp.pre_fc_norm_hidden, eps)
-    return torch.nn.functional.linear(torch.cat([emb, hid], dim=-1), mtp.fc)
+    return vm.linear(torch.cat([emb, hid], dim=-1), mtp.fc)
 
 
 def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: torch.Tensor,

@@ -109,13 +109,26 @@ def verify_cfg() -> Cfg:
 SMALL_WEIGHT_BYTES = 32 << 20
 """Linears of at most this many weight bytes and <= 64 rows take the skinny HIP GEMM
 (`dense`): they are launch-latency bound, where it beats the library GEMM by 4-15 us per call on
-MI355X; larger ones are bandwidth bound and stay on the library GEMM, which is as fast there."""
+MI355X; larger ones at <= 64 rows are bandwidth bound and the library GEMM is as fast there."""
+
+
+def _dense_wide_rows(rows: int, w: torch.Tensor) -> bool:
+    """65..256 rows: the skinny GEMM's row groups beat the library GEMM on 2048..4096 output
+    rows with K >= 1024 (measured at 192 rows: [4096, 8192] 47 against 61 us, [4096, 1024] 10.2
+    against 11.4 us), where the library's tiles leave most of the GPU idle; wider N stays on the
+    library GEMM (the 192-row LM head: 881 against 494 us)."""
+    n, k = w.shape
+    return 64 < rows <= dense.MAX_ROWS and 2048 <= n <= 4096 and k >= 1024
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """`F.linear(x, w)`; small weights at few rows run on `dense.linear`."""
-    if w.numel() * w.element_size() <= SMALL_WEIGHT_BYTES and dense.fits(x, w):
-        return dense.linear(x, w)
+    """`F.linear(x, w)`; the shapes the skinny GEMM streams faster run on `dense.linear`."""
+    if dense.fits(x, w):
+        rows = x.numel() // x.shape[-1]
+        if rows <= 64 and w.numel() * w.element_size() <= SMALL_WEIGHT_BYTES:
+            return dense.linear(x, w)
+        if _dense_wide_rows(rows, w):
+            return dense.linear(x, w)
     return F.linear(x, w)
 
 
@@ -123,7 +136,7 @@ def swiglu(x: torch.Tensor, w_gate_up: torch.Tensor, w_down: torch.Tensor) -> to
     """`down(silu(gate(x)) * up(x))` with `w_gate_up = cat([gate; up])` (`model.py:638-649`); the
     gate/up GEMM and its SiLU product are one launch when the skinny GEMM takes the shapes."""
     if w_gate_up.numel() * w_gate_up.element_size() <= SMALL_WEIGHT_BYTES and dense.fits(x, w_gate_up):
-        act = dense.silu_linear(x, w_gate_up)
+        act = dense.silu_linear(x, w_gate_up)  # at 192 rows 19 us against 16 us + the SiLU product
     else:
         gate, up = F.linear(x, w_gate_up).chunk(2, dim=-1)
         act = F.silu(gate) * up
@@ -291,7 +304,7 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
         # q read in its [B, t, heads, hd] layout, the sigmoid gate applied in the epilogue
         out = attention.paged_attention_gated(q, pool["k"], pool["v"], block_table, base_pos,
                                               ctx_blocks * c.block_size, c.head_dim ** -0.5, gate)
-        return F.linear(out.reshape(b, t, -1), w["o_proj"])
+        return linear(out.reshape(b, t, -1), w["o_proj"])
     out = paged_attention(q.transpose(1, 2), pool["k"], pool["v"], block_table, base_pos, ctx_blocks,
                           c.block_size, c.head_dim ** -0.5)
     out = out.transpose(1, 2).reshape(b, t, -1)
@@ -590,7 +603,7 @@ class Model:
                                              w["dt_bias"], c.k_heads, c.k_dim, c.v_heads, c.v_dim)
             out = deltanet.delta_rule(pool["rec"], lanes, q, k, v, g, beta)  # [B, t, vh, vd] fp32
             normed = gated_rmsnorm(out, z.reshape(b, t, c.v_heads, c.v_dim), w["dn_norm"], c.eps, h.dtype)
-            mixer = F.linear(normed.reshape(b, t, -1), w["out_proj"])
+            mixer = linear(normed.reshape(b, t, -1), w["out_proj"])
             return mixer, DeltaNetRows(raw, q, k, v, g, beta, proj)
         window = torch.cat([pool["conv"][lanes], raw], dim=-1)
         mixed = causal_conv_rows(window, w["conv"], t).to(h.dtype).transpose(1, 2)  # [B, t, C]

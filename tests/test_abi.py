@@ -63,11 +63,11 @@ def test_rejected_arguments_launch_nothing(lib):
                                   None, None, None, None, None, None, None, None, None, None,
                                   None, None) == -1
     assert lib.mtpk_moe_prep(None, 3, None, 0, 10, 0, 512, None, None, 10, None, None) == -1
-    # skinny GEMM: rows over 64, K not a multiple of 256, null pointers
-    assert lib.mtpk_gemm_workspace_bytes(65, 64, 256, 0) == 0
+    # skinny GEMM: rows over 256, K not a multiple of 256, null pointers
+    assert lib.mtpk_gemm_workspace_bytes(257, 64, 256, 0) == 0
     assert lib.mtpk_gemm_bf16(None, 4, 256, None, 64, 0, None, 1, None, 0, None) == -1
     assert lib.mtpk_gemm_bf16(p0 := ctypes.addressof(buf0), 4, 300, p0, 64, 0, p0, 1, None, 0, None) == -1
-    assert lib.mtpk_gemm_bf16(p0, 65, 256, p0, 64, 0, p0, 1, None, 0, None) == -1
+    assert lib.mtpk_gemm_bf16(p0, 257, 256, p0, 64, 0, p0, 1, None, 0, None) == -1
     # bf16 experts: null weights, H not a multiple of 256, an expert range that is not the
     # local expert count, a workspace that is not 256-byte aligned
     f = 0x1000

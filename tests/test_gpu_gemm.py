@@ -30,7 +30,10 @@ def _close(got, want):
 
 @pytest.mark.parametrize("m,k,n", [(48, 8192, 4096), (48, 4096, 16384), (48, 4096, 512), (1, 4096, 513),
                                    (4, 1024, 4096), (64, 256, 64), (17, 512, 100), (33, 4096, 20608),
-                                   (40, 512, 70000), (64, 256, 66000)])  # 8-wave tiles, ragged N
+                                   (40, 512, 70000), (64, 256, 66000),  # 8-wave tiles, ragged N
+                                   # row groups of 64 (ragged last group, split K, 8-wave tiles)
+                                   (192, 4096, 20608), (192, 8192, 4096), (100, 1024, 513),
+                                   (256, 256, 66000), (130, 4096, 512)])
 def test_linear_matches_fp32(dev, m, k, n):
     x, w = _inputs(dev, m, k, n, m + n)
     assert dense.fits(x, w)
@@ -39,7 +42,8 @@ def test_linear_matches_fp32(dev, m, k, n):
     _close(got, x.float() @ w.float().T)
 
 
-@pytest.mark.parametrize("m,k,inter", [(48, 4096, 1024), (1, 4096, 1024), (5, 1024, 48), (48, 256, 65552)])
+@pytest.mark.parametrize("m,k,inter", [(48, 4096, 1024), (1, 4096, 1024), (5, 1024, 48), (48, 256, 65552),
+                                       (192, 4096, 1024), (77, 512, 96)])
 def test_silu_linear_matches_swiglu(dev, m, k, inter):
     x, w = _inputs(dev, m, k, 2 * inter, 7 + m)
     got = dense.silu_linear(x, w)
@@ -48,7 +52,7 @@ def test_silu_linear_matches_swiglu(dev, m, k, inter):
     _close(got, want)
 
 
-@pytest.mark.parametrize("m,n", [(48, 248320), (1, 248320), (7, 1000)])
+@pytest.mark.parametrize("m,n", [(48, 248320), (1, 248320), (7, 1000), (192, 248320), (70, 5000)])
 def test_argmax_linear_is_the_argmax_of_its_bf16_logits(dev, m, n):
     x, w = _inputs(dev, m, 4096, n, 3 + m)
     idx = dense.argmax_linear(x, w)
@@ -71,7 +75,7 @@ def test_ties_pick_the_lowest_column(dev):
 def test_rejects_unsupported(dev):
     x, w = _inputs(dev, 4, 300, 64, 1)
     assert not dense.fits(x, w)  # K not a multiple of 256
-    x, w = _inputs(dev, 65, 256, 64, 1)
-    assert not dense.fits(x, w)  # more than 64 rows
+    x, w = _inputs(dev, 257, 256, 64, 1)
+    assert not dense.fits(x, w)  # more than 256 rows
     with pytest.raises(ValueError):
         dense.linear(x, w)
