@@ -56,10 +56,11 @@ __global__ __launch_bounds__(NW * kWave, 16 / NW) void k_gemm_skinny(GemmArgs a)
   const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
   // Workgroup -> (weight tile, row group). With several row groups, the groups of one tile
-  // get ids 8 apart (the XCD round-robin), so that they run on one XCD close in time and can
-  // share its L2. Measured at 192 rows, this pays where the weight tiles are few (N = 4096:
-  // 47 us against the library GEMM's 61) but not on wide N (the LM head re-reads its weights
-  // about 2.6 times, 2.3 TB/s), where callers keep the library GEMM.
+  // get ids 8 apart: workgroup i runs on XCD i % 8 (checked on MI355X for 4096 workgroups), so
+  // they run on one XCD close in time and can share its L2. Each group still does the tile's
+  // full load and MFMA work. Measured at 192 rows this pays where the weight tiles are few
+  // (N = 4096: 47 us against the library GEMM's 61) but not on wide N (the LM head: 881 against
+  // 494 us), where callers keep the library GEMM.
   int tile = blockIdx.x, rg = 0;
   if (a.RG > 1) {
     const int xcd = blockIdx.x & 7, slot = blockIdx.x >> 3;
