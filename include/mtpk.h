@@ -219,6 +219,23 @@ int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int6
                        int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                        int64_t* hidden_src, void* stream);
 
+/* The verify step's argmax and acceptance in two launches instead of three: mtpk_argmax_keys
+ * writes the first-occurrence (value, index) keys of each row's vocabulary chunks, keys u64
+ * [rows, chunks] with chunks = mtpk_argmax_partials(rows, vocab) / rows (the first kernel of
+ * mtpk_argmax_rows); mtpk_greedy_accept_keys reduces row (b, s)'s keys (rows = batch * t, row
+ * b * t + s), writes step_argmax[b * sa_stride + s] and then does what mtpk_greedy_accept does,
+ * with the same outputs. batch * t <= 4096 (MTPK_EINVAL beyond). */
+int mtpk_argmax_keys(const void* logits, int dtype, int64_t rows, int64_t vocab,
+                     int64_t row_stride, uint64_t* keys, void* stream);
+int mtpk_greedy_accept_keys(const uint64_t* keys, int64_t chunks, int64_t* step_argmax,
+                            int64_t sa_stride, const int64_t* draft, int64_t draft_stride,
+                            const uint8_t* active, const int64_t* pos, const int64_t* budget,
+                            const int64_t* stops, int n_stops, int batch, int t, int conv_k1,
+                            int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                            int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                            int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                            int64_t* hidden_src, void* stream);
+
 /* ---------------------------------------------------------------- rejection sampling
  * Sampling-mode acceptance for an MTP round at temperature T > 0. The reference engine has no
  * counterpart: it runs MTP rounds only for all-greedy batches (scheduler.py:1775-1793,

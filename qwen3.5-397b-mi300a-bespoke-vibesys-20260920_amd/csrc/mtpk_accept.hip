@@ -139,9 +139,15 @@ __global__ __launch_bounds__(256) void k_argmax_final(const uint64_t* __restrict
 
 constexpr int kAcceptThreads = 1024;
 constexpr int kPre = 8;
+constexpr int kKeyRows = 4096;  // B * t bound of the keys path: one u64 of LDS per verify row
 
+// keys (optional): the argmax chunk keys [B * t, chunks] of k_argmax_partial. The workgroup
+// then first folds them into one key per verify row (LDS max, so any key order gives the same
+// first-occurrence winner), writes the indices to sa_out and reads the verify columns from
+// LDS: the argmax needs no second launch.
 __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
-    const int64_t* __restrict__ sa, int64_t ss, const int64_t* __restrict__ draft, int64_t ds,
+    const uint64_t* __restrict__ keys, int chunks, int64_t* sa_out,
+    const int64_t* sa, int64_t ss, const int64_t* __restrict__ draft, int64_t ds,
     const uint8_t* __restrict__ active, const int64_t* __restrict__ pos,
     const int64_t* __restrict__ budget, const int64_t* __restrict__ stops, int n_stops, int B,
     int t, int conv_k1, int64_t* __restrict__ accept_len, int64_t* __restrict__ lengths,
@@ -153,9 +159,26 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
   __shared__ int wtot[kAcceptThreads / kWave];
   const int j = threadIdx.x, lane = j & (kWave - 1), wv = j / kWave;
   const int k = t - 1;
+  __shared__ unsigned long long s_key[kKeyRows];
   int len = 0;
+  if (keys) {
+    const int rows = B * t;
+    for (int r = j; r < rows; r += kAcceptThreads) s_key[r] = 0;
+    __syncthreads();
+    const int64_t n = (int64_t)rows * chunks;
+    for (int64_t i = j; i < n; i += kAcceptThreads)
+      atomicMax(&s_key[i / chunks], (unsigned long long)keys[i]);
+    __syncthreads();
+    for (int r = j; r < rows; r += kAcceptThreads) {
+      const int64_t tok = (int64_t)argmax_key_index(s_key[r]);
+      s_key[r] = (unsigned long long)tok;
+      sa_out[(int64_t)(r / t) * ss + r % t] = tok;
+    }
+    __syncthreads();
+  }
   if (j < B) {
-    const int64_t* row = sa + (int64_t)j * ss;
+    const int64_t* row = keys ? reinterpret_cast<const int64_t*>(s_key) + (int64_t)j * t
+                              : sa + (int64_t)j * ss;
     const int64_t* drow = draft + (int64_t)j * ds;
     const int64_t* srow = stops + (int64_t)j * n_stops;
     // Every load of the row is issued at once, the first kPre verify columns, drafts and stop
@@ -293,13 +316,16 @@ int mtpk_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
   return status_of(hipGetLastError());
 }
 
-int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
-                       int64_t draft_stride, const uint8_t* active, const int64_t* pos,
-                       const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
-                       int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
-                       int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
-                       int64_t* next_pos, int64_t* budget_left, uint8_t* live,
-                       int64_t* hidden_src, void* stream) {
+namespace {
+
+int greedy_accept_launch(const uint64_t* keys, int chunks, int64_t* sa_out,
+                         const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
+                         int64_t draft_stride, const uint8_t* active, const int64_t* pos,
+                         const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
+                         int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                         int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                         int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                         int64_t* hidden_src, void* stream) {
   if (!step_argmax || !active || !budget || !accept_len) return MTPK_EINVAL;
   if (batch <= 0 || batch > kAcceptThreads || t < 1 || t > 64) return MTPK_EINVAL;
   if (t > 1 && !draft) return MTPK_EINVAL;
@@ -307,9 +333,58 @@ int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int6
   if (next_pos && !pos) return MTPK_EINVAL;
   if (sa_stride < t || (t > 1 && draft_stride < t - 1)) return MTPK_EINVAL;
   hipLaunchKernelGGL(k_greedy_accept, dim3(1), dim3(kAcceptThreads), 0, (hipStream_t)stream,
-                     step_argmax, sa_stride, draft, draft_stride, active, pos, budget, stops,
-                     n_stops, batch, t, conv_k1, accept_len, lengths, packed_src, packed_cu,
-                     conv_idx, keep, bonus, next_pos, budget_left, live, hidden_src);
+                     keys, chunks, sa_out, step_argmax, sa_stride, draft, draft_stride, active, pos,
+                     budget, stops, n_stops, batch, t, conv_k1, accept_len, lengths, packed_src,
+                     packed_cu, conv_idx, keep, bonus, next_pos, budget_left, live, hidden_src);
+  return status_of(hipGetLastError());
+}
+
+}  // namespace
+
+int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
+                       int64_t draft_stride, const uint8_t* active, const int64_t* pos,
+                       const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
+                       int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                       int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                       int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                       int64_t* hidden_src, void* stream) {
+  return greedy_accept_launch(nullptr, 0, nullptr, step_argmax, sa_stride, draft, draft_stride,
+                              active, pos, budget, stops, n_stops, batch, t, conv_k1, accept_len,
+                              lengths, packed_src, packed_cu, conv_idx, keep, bonus, next_pos,
+                              budget_left, live, hidden_src, stream);
+}
+
+int mtpk_greedy_accept_keys(const uint64_t* keys, int64_t chunks, int64_t* step_argmax,
+                            int64_t sa_stride, const int64_t* draft, int64_t draft_stride,
+                            const uint8_t* active, const int64_t* pos, const int64_t* budget,
+                            const int64_t* stops, int n_stops, int batch, int t, int conv_k1,
+                            int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                            int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                            int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                            int64_t* hidden_src, void* stream) {
+  if (!keys || chunks < 1 || chunks > 65535) return MTPK_EINVAL;
+  if ((int64_t)batch * t > kKeyRows) return MTPK_EINVAL;
+  return greedy_accept_launch(keys, (int)chunks, step_argmax, step_argmax, sa_stride, draft,
+                              draft_stride, active, pos, budget, stops, n_stops, batch, t, conv_k1,
+                              accept_len, lengths, packed_src, packed_cu, conv_idx, keep, bonus,
+                              next_pos, budget_left, live, hidden_src, stream);
+}
+
+int mtpk_argmax_keys(const void* logits, int dtype, int64_t rows, int64_t vocab,
+                     int64_t row_stride, uint64_t* keys, void* stream) {
+  if (!logits || !keys) return MTPK_EINVAL;
+  if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (rows < 0 || rows > 65535 || vocab <= 0 || vocab > INT32_MAX || row_stride < vocab)
+    return MTPK_EINVAL;
+  if (rows == 0) return 0;
+  const int per_vec = dtype == MTPK_BF16 ? 8 : 4;
+  const int vec = aligned16(logits) && (row_stride % per_vec) == 0;
+  const int64_t chunks = mtpk_argmax_partials(rows, vocab) / rows;
+  int64_t chunk = (vocab + chunks - 1) / chunks;
+  chunk = (chunk + per_vec - 1) / per_vec * per_vec;
+  hipLaunchKernelGGL(k_argmax_partial, dim3((unsigned)chunks, (unsigned)rows),
+                     dim3(kArgmaxThreads), 0, (hipStream_t)stream, logits, dtype, row_stride, vocab,
+                     chunk, vec, keys);
   return status_of(hipGetLastError());
 }
 

@@ -119,11 +119,18 @@ def accept_round(buf: MTPVerifyBuffers, step_argmax: torch.Tensor | None = None)
     )
 
 
+KEY_ROWS = 4096
+"""Verify rows (B * t) up to which `greedy_accept(..., keys=)` takes the argmax keys."""
+
+
 def greedy_accept(step_argmax: torch.Tensor, draft: torch.Tensor, active: torch.Tensor,
                   pos: torch.Tensor, budget: torch.Tensor, stops: torch.Tensor, conv_k1: int,
-                  *, out: AcceptResult | None = None) -> AcceptResult:
+                  *, out: AcceptResult | None = None,
+                  keys: tuple[torch.Tensor, int] | None = None) -> AcceptResult:
     """`mtpk_greedy_accept` on device tensors: step_argmax i64 [B, t], draft i64 [B, t-1] (row
-    stride free, unit column stride), active bool [B], pos/budget i64 [B], stops i64 [B, S]."""
+    stride free, unit column stride), active bool [B], pos/budget i64 [B], stops i64 [B, S].
+    With `keys` (`mtp.argmax_keys` of the [B * t, vocab] verify logits) the same launch first
+    finishes the argmax and writes it into `step_argmax` (`mtpk_greedy_accept_keys`)."""
     device = _mtpk.require_device(step_argmax, draft, active, pos, budget, stops)
     b, t = step_argmax.shape
     if draft.shape != (b, t - 1) or (t > 1 and draft.stride(1) != 1) or step_argmax.stride(1) != 1:
@@ -143,8 +150,13 @@ def greedy_accept(step_argmax: torch.Tensor, draft: torch.Tensor, active: torch.
             torch.empty(b, **long), torch.empty(b, **long), torch.empty(b, **long),
             torch.empty(b, dtype=torch.bool, device=device), torch.empty(b, **long),
         )
+    if keys is not None:
+        key_t, chunks = keys
+        if key_t.shape != (b * t, chunks) or not key_t.is_contiguous():
+            raise ValueError(f"keys must be contiguous [{b * t}, {chunks}]")
     _mtpk.check(
-        _mtpk.lib().mtpk_greedy_accept(
+        (_mtpk.lib().mtpk_greedy_accept_keys if keys is not None else _mtpk.lib().mtpk_greedy_accept)(
+            *((keys[0].data_ptr(), keys[1]) if keys is not None else ()),
             step_argmax.data_ptr(), step_argmax.stride(0), draft.data_ptr(),
             draft.stride(0) if t > 1 else 0, active.contiguous().data_ptr(),
             pos.contiguous().data_ptr(), budget.contiguous().data_ptr(), stops.data_ptr(),
@@ -196,12 +208,17 @@ def verify_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: i
     dev = buf.pos.device
     pos = buf.pos[:b]
     res = model.forward_rows(buf.token_matrix[:b], lanes, pos, ctx_len)
-    buf.step_argmax[:b] = model.argmax(model.logits(res.hidden)).view(b, t)
+    logits = model.logits(res.hidden)
+    keys = None
+    if dev.type == "cuda" and b * t <= KEY_ROWS:  # the accept launch finishes the argmax
+        keys = mtp_mod.argmax_keys(logits.reshape(b * t, -1))
+    else:
+        buf.step_argmax[:b] = model.argmax(logits).view(b, t)
     out = AcceptResult(buf.accept_len[:b], buf.lengths[:b], buf.packed_src[: b * t],
                        buf.packed_cu[: b + 1], buf.conv_idx[:b], buf.keep[:b], buf.bonus[:b],
                        buf.next_pos[:b], buf.budget_left[:b], buf.live[:b], buf.hidden_src[:b])
     greedy_accept(buf.step_argmax[:b], buf.token_matrix[:b, 1:], buf.active[:b], pos,
-                  buf.budget[:b], buf.stops[:b], buf.conv_k1, out=out)
+                  buf.budget[:b], buf.stops[:b], buf.conv_k1, out=out, keys=keys)
     if forced_n is not None:
         # A forced lane commits its forced tokens plus one target token; stop ids and the
         # budget do not apply to forced tokens (`graph_verify_wide.py:196-200`).

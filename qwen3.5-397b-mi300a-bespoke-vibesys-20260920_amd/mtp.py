@@ -93,6 +93,25 @@ def argmax_rows(logits: torch.Tensor) -> torch.Tensor:
     return out.reshape(lead)
 
 
+def argmax_keys(logits: torch.Tensor) -> tuple[torch.Tensor, int]:
+    """The first launch of `argmax_rows` alone (`mtpk_argmax_keys`): the first-occurrence
+    (value, index) keys of each row's vocabulary chunks, `(keys u64-as-int64 [rows, chunks],
+    chunks)` for `graph_mtp.greedy_accept(..., keys=)`, which finishes the argmax."""
+    device = _mtpk.require_device(logits)
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    vocab = logits.shape[-1]
+    flat = logits.reshape(-1, vocab) if logits.dim() != 2 else logits
+    rows = flat.shape[0]
+    lib = _mtpk.lib()
+    chunks = max(int(lib.mtpk_argmax_partials(rows, vocab)) // max(rows, 1), 1)
+    keys = torch.empty(rows, chunks, dtype=torch.int64, device=device)
+    _mtpk.check(lib.mtpk_argmax_keys(flat.data_ptr(), _mtpk.float_code(flat.dtype), rows, vocab,
+                                     flat.stride(0), keys.data_ptr(), _mtpk.stream_of(device)),
+                "mtpk_argmax_keys")
+    return keys, chunks
+
+
 def greedy_token(model, normed: torch.Tensor) -> torch.Tensor:
     """`model.unembed(normed).float().argmax(-1, keepdim=True)` for `[B, hidden]` rows, `[B, 1]`
     long. On a device this is `model.next_tokens` (the HIP argmax compares the bf16 logits

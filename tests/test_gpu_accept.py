@@ -123,6 +123,48 @@ def test_config4_greedy_full_vocab(dev):
         assert np.array_equal(getattr(r, name).cpu().numpy().astype(w.dtype), w), name
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("b,t,v", [(1, 4, 248320), (48, 4, 248320), (3, 2, 1003), (1024, 4, 600)])
+def test_keys_path_finishes_the_argmax(dev, dt, b, t, v):
+    """`mtpk_argmax_keys` + `mtpk_greedy_accept_keys` against numpy: the written step_argmax is
+    the first-occurrence argmax (coarse logits, so ties across vocabulary chunks are common) and
+    every acceptance output equals the oracle's on it."""
+    g = torch.Generator(dev).manual_seed(b + t)
+    logits = torch.randint(-6, 6, (b * t, v), device=dev, generator=g).to(dt)
+    rng = np.random.default_rng(b * 7 + v)
+    want_sa = ar.argmax_first(logits.float().cpu().numpy()).reshape(b, t)
+    draft = np.where(rng.random((b, t - 1)) < 0.7, want_sa[:, : t - 1], rng.integers(0, v, (b, t - 1)))
+    active = rng.random(b) < 0.9
+    pos = rng.integers(0, 8000, b)
+    budget = rng.integers(1, 8, b)
+    stops = np.where(rng.random((b, 8)) < 0.1, rng.integers(0, v, (b, 8)), -1)
+    step_argmax = torch.full((b, t), -7, dtype=torch.long, device=dev)
+    r = graph_mtp.greedy_accept(
+        step_argmax, dev_long(draft, dev), torch.from_numpy(active).to(dev), dev_long(pos, dev),
+        dev_long(budget, dev), dev_long(stops, dev), 3, keys=mtp.argmax_keys(logits))
+    assert np.array_equal(step_argmax.cpu().numpy(), want_sa)
+    want = ar.round_indices(draft, want_sa, active, pos, budget, stops, 3)
+    for name, w in want.items():
+        assert np.array_equal(getattr(r, name).cpu().numpy().astype(w.dtype), w), name
+
+
+def test_keys_path_limits(dev):
+    """batch * t above 4096 verify rows is refused by the C check; a keys tensor of another
+    row count by the wrapper."""
+    b, t = 1024, 5
+    keys = mtp.argmax_keys(torch.zeros(b * t, 16, device=dev))
+    ones = torch.ones(b, dtype=torch.bool, device=dev)
+    z = torch.zeros(b, dtype=torch.long, device=dev)
+    stops = torch.full((b, 1), -1, dtype=torch.long, device=dev)
+    draft = torch.zeros(b, t - 1, dtype=torch.long, device=dev)
+    with pytest.raises(ValueError, match="mtpk_greedy_accept"):
+        graph_mtp.greedy_accept(torch.zeros(b, t, dtype=torch.long, device=dev), draft, ones, z,
+                                z + 1, stops, 0, keys=keys)
+    with pytest.raises(ValueError, match="keys must be"):
+        graph_mtp.greedy_accept(torch.zeros(2, 2, dtype=torch.long, device=dev), draft[:2, :1],
+                                ones[:2], z[:2], z[:2] + 1, stops[:2], 0, keys=keys)
+
+
 def test_accept_round_writes_buffers(dev):
     buf = graph_mtp.MTPVerifyBuffers(8, 4, 64, 4, dev)
     rng = np.random.default_rng(3)
