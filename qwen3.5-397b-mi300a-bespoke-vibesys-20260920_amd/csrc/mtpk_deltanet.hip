@@ -8,7 +8,7 @@
 // Every column v of S evolves on its own (its update needs only k . s_v), so a lane owns one
 // column: its dk (16..128) values stay in registers for all t steps, and one 64-lane wave
 // covers 64 columns of one (row, head). q and k are the same for the whole wave and come in through
-// scalar loads; the state is read once (dword loads, 256 contiguous bytes per wave
+// LDS; the state is read once (dword loads, 256 contiguous bytes per wave
 // instruction) and, in commit mode, written back once in place.
 //
 // Verify mode (lengths == NULL): t steps from the committed state, outputs for every step, the
@@ -21,19 +21,20 @@
 namespace mtpk {
 
 
-// Wave-uniform fp32 reads of data an earlier launch wrote and this one only reads.
-typedef const __attribute__((address_space(4))) float* kc_f32_t;
-__device__ inline float sloadf(const float* p, int64_t i) { return ((kc_f32_t)p)[i]; }
-
 template <int DK, bool OUT, bool COMMIT>
 __global__ __launch_bounds__(kWave) void k_delta_rule(
     float* __restrict__ state, const int64_t* __restrict__ slot, int t, int heads, int rep, int dv,
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta,
     const int64_t* __restrict__ lengths, float* __restrict__ out) {
-  const int bh = blockIdx.x;  // row * heads + head
+  static_assert(DK % 4 == 0, "k and q are read back four values at a time");
+  // Workgroup (bh, c) is id bh * nblk + c: the column blocks of one matrix are dispatched
+  // together, so the matrix's rows are read whole (its 64-column blocks interleave every
+  // 256 bytes) while they are still open in the memory's row buffers.
+  const int nblk = (dv + kWave - 1) / kWave;
+  const int bh = blockIdx.x / nblk;  // row * heads + head
   const int row = bh / heads, head = bh - row * heads;
-  const int col = blockIdx.y * kWave + threadIdx.x;
+  const int col = (blockIdx.x - bh * nblk) * kWave + threadIdx.x;
   const bool live = col < dv;
   const int64_t s_idx = slot ? slot[row] : row;
   // the (slot, head) matrix as one buffer: element (i, col) at byte 4 col + 4 dv i, the
@@ -48,27 +49,77 @@ __global__ __launch_bounds__(kWave) void k_delta_rule(
   int n = t;
   if (COMMIT) n = (int)min(max(lengths[row], (int64_t)0), (int64_t)t);
   const int qk_heads = heads / rep, kh = head / rep;
+  // A step's k and q (the same for the whole wave) pass through LDS: each lane loads one or two
+  // of their values, and the product loops read them back four at a time as broadcasts. Step
+  // st + 1's k, q, v, g and beta are loaded while step st runs, so no step waits for its
+  // inputs after the first.
+  constexpr int kPer = (DK + kWave - 1) / kWave;
+  __shared__ __attribute__((aligned(16))) float kq[2][2][DK];
+  const int lane = threadIdx.x;
+  float nk[kPer], nq[kPer], nv = 0.f, ng = 0.f, nbt = 0.f;
+  auto step_load = [&](int st) {
+    const int64_t rs = (int64_t)row * t + (st < n ? st : 0);
+    const int64_t qk_off = (rs * qk_heads + kh) * DK, hv = rs * heads + head;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int i = p * kWave + lane;
+      nk[p] = i < DK ? k[qk_off + i] : 0.f;
+      nq[p] = OUT && i < DK ? q[qk_off + i] : 0.f;
+    }
+    nv = live ? v[hv * dv + col] : 0.f;
+    ng = g[hv];
+    nbt = beta[hv];
+  };
+  if (n > 0) step_load(0);
   for (int st = 0; st < n; ++st) {
-    const int64_t rs = (int64_t)row * t + st;
-    const int64_t qk_off = (rs * qk_heads + kh) * DK;
-    const int64_t hv = rs * heads + head;
-    const float decay = __expf(sloadf(g, hv));
-    const float bt = sloadf(beta, hv);
-    const float vv = live ? v[hv * dv + col] : 0.f;
+    const int b = st & 1;
+#pragma unroll
+    for (int p = 0; p < kPer; ++p) {
+      const int i = p * kWave + lane;
+      if (i < DK) {
+        kq[b][0][i] = nk[p];
+        if (OUT) kq[b][1][i] = nq[p];
+      }
+    }
+    const float decay = __expf(ng), bt = nbt, vv = nv;
+    __syncthreads();  // this step's k and q are in LDS (a one-wave workgroup)
+    if (st + 1 < n) step_load(st + 1);
+    const float4* kk = reinterpret_cast<const float4*>(kq[b][0]);
+    const float4* qq = reinterpret_cast<const float4*>(kq[b][1]);
     float mem = 0.f;
 #pragma unroll
-    for (int i = 0; i < DK; ++i) {
-      s[i] *= decay;
-      mem = fmaf(s[i], sloadf(k, qk_off + i), mem);
+    for (int i4 = 0; i4 < DK / 4; ++i4) {
+      const float4 kv = kk[i4];
+      s[4 * i4] *= decay;
+      s[4 * i4 + 1] *= decay;
+      s[4 * i4 + 2] *= decay;
+      s[4 * i4 + 3] *= decay;
+      mem = fmaf(s[4 * i4], kv.x, mem);
+      mem = fmaf(s[4 * i4 + 1], kv.y, mem);
+      mem = fmaf(s[4 * i4 + 2], kv.z, mem);
+      mem = fmaf(s[4 * i4 + 3], kv.w, mem);
     }
     const float delta = (vv - mem) * bt;
+    // read k again rather than keep all DK values live across both loops: the state already
+    // takes DK registers
+    asm volatile("" ::: "memory");
     float o = 0.f;
 #pragma unroll
-    for (int i = 0; i < DK; ++i) {
-      s[i] = fmaf(sloadf(k, qk_off + i), delta, s[i]);
-      if (OUT) o = fmaf(s[i], sloadf(q, qk_off + i), o);
+    for (int i4 = 0; i4 < DK / 4; ++i4) {
+      const float4 kv = kk[i4];
+      s[4 * i4] = fmaf(kv.x, delta, s[4 * i4]);
+      s[4 * i4 + 1] = fmaf(kv.y, delta, s[4 * i4 + 1]);
+      s[4 * i4 + 2] = fmaf(kv.z, delta, s[4 * i4 + 2]);
+      s[4 * i4 + 3] = fmaf(kv.w, delta, s[4 * i4 + 3]);
+      if (OUT) {
+        const float4 qv = qq[i4];
+        o = fmaf(s[4 * i4], qv.x, o);
+        o = fmaf(s[4 * i4 + 1], qv.y, o);
+        o = fmaf(s[4 * i4 + 2], qv.z, o);
+        o = fmaf(s[4 * i4 + 3], qv.w, o);
+      }
     }
-    if (OUT && live) out[hv * dv + col] = o;
+    if (OUT && live) out[((int64_t)row * t + st) * heads * dv + (int64_t)head * dv + col] = o;
   }
   if (COMMIT) {
 #pragma unroll
@@ -82,8 +133,9 @@ template <int DK, bool OUT, bool COMMIT>
 int launch_delta_rule(float* state, const int64_t* slot, int rows, int t, int heads, int rep,
                       int dv, const float* q, const float* k, const float* v, const float* g,
                       const float* beta, const int64_t* lengths, float* out, hipStream_t st) {
-  hipLaunchKernelGGL((k_delta_rule<DK, OUT, COMMIT>), dim3(rows * heads, (dv + kWave - 1) / kWave),
-                     dim3(kWave), 0, st, state, slot, t, heads, rep, dv, q, k, v, g, beta, lengths, out);
+  const int64_t grid = (int64_t)rows * heads * ((dv + kWave - 1) / kWave);
+  if (grid > INT32_MAX) return MTPK_EINVAL;
+  hipLaunchKernelGGL((k_delta_rule<DK, OUT, COMMIT>), dim3((unsigned)grid), dim3(kWave), 0, st, state, slot, t, heads, rep, dv, q, k, v, g, beta, lengths, out);
   return status_of(hipGetLastError());
 }
 
