@@ -124,7 +124,8 @@ def test_config4_greedy_full_vocab(dev):
 
 
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
-@pytest.mark.parametrize("b,t,v", [(1, 4, 248320), (48, 4, 248320), (3, 2, 1003), (1024, 4, 600)])
+@pytest.mark.parametrize("b,t,v", [(1, 4, 248320), (48, 4, 248320), (3, 2, 1003), (1024, 4, 600),
+                                   (5, 1, 3000), (64, 64, 40)])
 def test_keys_path_finishes_the_argmax(dev, dt, b, t, v):
     """`mtpk_argmax_keys` + `mtpk_greedy_accept_keys` against numpy: the written step_argmax is
     the first-occurrence argmax (coarse logits, so ties across vocabulary chunks are common) and
