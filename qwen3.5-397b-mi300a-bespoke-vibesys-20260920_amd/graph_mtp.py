@@ -166,7 +166,7 @@ def greedy_accept(step_argmax: torch.Tensor, draft: torch.Tensor, active: torch.
             out.bonus.data_ptr(), out.next_pos.data_ptr(), out.budget_left.data_ptr(),
             out.live.data_ptr(), out.hidden_src.data_ptr(), _mtpk.stream_of(device),
         ),
-        "mtpk_greedy_accept",
+        "mtpk_greedy_accept_keys" if keys is not None else "mtpk_greedy_accept",
     )  # fmt: skip
     return out
 
