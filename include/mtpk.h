@@ -46,9 +46,20 @@ int mtpk_abi_version(void);
  * out f32 [rows, k]. k % 32 == 0.
  * mode 0: exact fp32, fp4 * 2^(s-127), scale byte 0 -> +0.0, 255 -> +inf.
  * mode 1: the MoE kernels' in-register decode (hardware fp4 -> bf16 convert with the block
- *         scale folded in), widened to fp32; exact for scale bytes 2..252. */
+ *         scale folded in, `decode8`), widened to fp32; equal to mode 0 bit for bit for scale
+ *         bytes 0..254 (byte 0 as +-0.0); byte 255 gives NaN for every code. */
 int mtpk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,
                        int mode, float* out, void* stream);
+
+/* Load-time precondition of the in-register decode: replaces `mxfp4_gemv.bw_scales_ok` /
+ * `moe_hip.supports` (mxfp4_gemv.py:1761-1776, moe_hip.py:204-215). Counts, into *bad_count
+ * (device int32, cleared by the call), the threads that found a 32-element block whose e8m0
+ * scale is 255 and whose 16 packed bytes hold a nonzero-magnitude code: the one case where the
+ * hardware convert (NaN) differs from the pinned decode (+-inf). Block b is packed bytes
+ * [16 b, 16 b + 16) and scale byte b, so a whole [E, N, K/2] / [E, N, K/32] pair is scanned
+ * as blocks = E * N * K / 32. Zero means every block decodes exactly. */
+int mtpk_scale_scan(const uint8_t* packed, const uint8_t* scale, int64_t blocks,
+                    int32_t* bad_count, void* stream);
 
 /* ---------------------------------------------------------------- routed MXFP4 MoE
  * Weights in the `load_experts` layout (model.py:758-804): gate_up u8 [E, 2I, H/2] (rows
@@ -71,7 +82,9 @@ int64_t mtpk_moe_workspace_bytes(int64_t tokens, int64_t top_k, int64_t local_ex
  * :2320-2376) and `moe_hip.prep` (moe_hip.py:268-285). Counting sort of live assignments by
  * local expert into sorted i32 [assignments] (expert-grouped; order inside one expert's run
  * is unspecified), units i32 [3*max_units] = (local expert, first position in sorted,
- * count <= MTPK_MOE_UNIT_TOKENS), n_units i32 [1]. One workgroup. */
+ * count <= MTPK_MOE_UNIT_TOKENS), n_units i32 [1]. One workgroup. max_units below
+ * mtpk_moe_max_units(assignments, expert_hi - expert_lo) is MTPK_EINVAL (a shorter list would
+ * drop live assignments); the same bound holds for `mtpk_moe_gate_up` and `mtpk_moe_down`. */
 int mtpk_moe_prep(const void* a_expert, int expert_dtype, const void* a_weight, int weight_dtype,
                   int64_t assignments, int expert_lo, int expert_hi, int32_t* sorted,
                   int32_t* units, int64_t max_units, int32_t* n_units, void* stream);
@@ -273,7 +286,8 @@ int mtpk_sample_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
  * (`deltanet_verify_rollback_static`, graph_mtp.py:347-437). Per step, for row j and head h:
  *   S <- exp(g) S;  S <- S + k ((v - S^T k) beta)^T;  out = S^T q
  * state f32 [slots_total, heads, k_dim = 128, v_dim] contiguous; row j uses state slot slot[j]
- * (int64 [rows], NULL: slot j); rows must name distinct slots. q, k f32 [rows, t, qk_heads, 128]
+ * (int64 [rows], NULL: slot j); rows must name distinct slots. A row whose slot lies outside
+ * [0, slots_total) touches no state: its outputs are zeros and a commit leaves the pool as is. q, k f32 [rows, t, qk_heads, 128]
  * (q and k already l2-normalised, q scaled), head h reads q/k head h / (heads / qk_heads);
  * v f32 [rows, t, heads, v_dim]; g (log decay) and beta f32 [rows, t, heads]; all contiguous.
  * lengths == NULL (verify): t steps from the stored state, which is not written; out
@@ -295,9 +309,10 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
  * columns | the t new qkv columns], rounded to the model dtype; q = l2norm(x_q) * q_scale,
  * k = l2norm(x_k) (l2norm(x) = x rsqrt(sum x^2 + eps)), v = x_v, all f32 [batch, t, heads,
  * dim]; beta = sigmoid(b), g = -exp(a_log) softplus(a + dt_bias), f32 [batch, t, v_heads].
- * Head dims <= 256, conv_k <= 9. */
+ * Head dims <= 256, conv_k <= 9. conv_state has slots_total slots; a row whose slot lies
+ * outside [0, slots_total) reads a zero window instead. */
 int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const void* conv_state,
-                       const int64_t* slot, const void* conv_w, const float* a_log,
+                       const int64_t* slot, int64_t slots_total, const void* conv_w, const float* a_log,
                        const float* dt_bias, int64_t batch, int64_t t, int64_t k_heads,
                        int64_t k_dim, int64_t v_heads, int64_t v_dim, int64_t conv_k, float eps,
                        float q_scale, float* q, float* k, float* v, float* g, float* beta,
@@ -306,8 +321,10 @@ int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const v
 /* The commit's conv-window update (`deltanet_verify_rollback`, model.py:3907-3972): the window
  * of slot[b], conv_state[slot[b]] [channels, k1], becomes columns idx[b][0 .. k1) (i64, clamped
  * to [0, k1 + t - 1]) of [stored window | the t new raw columns proj[b * t + s][0 .. channels)].
- * In place; slots distinct. */
-int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, const void* proj,
+ * In place; slots distinct; conv_state has slots_total slots, and a row whose slot lies
+ * outside [0, slots_total) is skipped. */
+int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, int64_t slots_total,
+                     const void* proj,
                      int64_t proj_stride, const int64_t* idx, int64_t batch, int64_t channels,
                      int64_t k1, int64_t t, void* stream);
 

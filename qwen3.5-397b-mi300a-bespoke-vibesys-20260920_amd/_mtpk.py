@@ -29,6 +29,7 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
     "mtpk_status_string": (ctypes.c_char_p, [c_int]),
     "mtpk_abi_version": (c_int, []),
     "mtpk_dequant_mxfp4": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
+    "mtpk_scale_scan": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "mtpk_moe_max_units": (c_int64, [c_int64, c_int64]),
     "mtpk_moe_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int]),
     "mtpk_moe_prep": (
@@ -88,13 +89,13 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
     ),
     "mtpk_deltanet_prep": (
         c_int,
-        [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+        [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int64,
          c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, ctypes.c_float, ctypes.c_float, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
     "mtpk_conv_commit": (
         c_int,
-        [c_void_p, c_int, c_void_p, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64,
+        [c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64,
          c_int64, c_void_p],
     ),
     "mtpk_moe_dense_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),

@@ -23,8 +23,8 @@ namespace mtpk {
 
 template <int DK, bool OUT, bool COMMIT>
 __global__ __launch_bounds__(kWave) void k_delta_rule(
-    float* __restrict__ state, const int64_t* __restrict__ slot, int t, int heads, int rep, int dv,
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
+    float* __restrict__ state, int64_t slots_total, const int64_t* __restrict__ slot, int t,
+    int heads, int rep, int dv, const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ v,
     const float* __restrict__ g, const float* __restrict__ beta,
     const int64_t* __restrict__ lengths, float* __restrict__ out) {
   static_assert(DK % 4 == 0, "k and q are read back four values at a time");
@@ -37,6 +37,11 @@ __global__ __launch_bounds__(kWave) void k_delta_rule(
   const int col = (blockIdx.x - bh * nblk) * kWave + threadIdx.x;
   const bool live = col < dv;
   const int64_t s_idx = slot ? slot[row] : row;
+  if (s_idx < 0 || s_idx >= slots_total) {  // no such slot: zero outputs, no state access
+    if (OUT && live)
+      for (int st = 0; st < t; ++st) out[((int64_t)row * t + st) * heads * dv + (int64_t)head * dv + col] = 0.f;
+    return;  // uniform over the one-wave workgroup
+  }
   // the (slot, head) matrix as one buffer: element (i, col) at byte 4 col + 4 dv i, the
   // per-lane part in voffset (out of range for lanes past dv) and the row offset in soffset
   const rsrc_t rsm = make_rsrc(state + ((s_idx * heads + head) * DK) * (int64_t)dv,
@@ -130,26 +135,26 @@ __global__ __launch_bounds__(kWave) void k_delta_rule(
 }
 
 template <int DK, bool OUT, bool COMMIT>
-int launch_delta_rule(float* state, const int64_t* slot, int rows, int t, int heads, int rep,
+int launch_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int rows, int t, int heads, int rep,
                       int dv, const float* q, const float* k, const float* v, const float* g,
                       const float* beta, const int64_t* lengths, float* out, hipStream_t st) {
   const int64_t grid = (int64_t)rows * heads * ((dv + kWave - 1) / kWave);
   if (grid > INT32_MAX) return MTPK_EINVAL;
-  hipLaunchKernelGGL((k_delta_rule<DK, OUT, COMMIT>), dim3((unsigned)grid), dim3(kWave), 0, st, state, slot, t, heads, rep, dv, q, k, v, g, beta, lengths, out);
+  hipLaunchKernelGGL((k_delta_rule<DK, OUT, COMMIT>), dim3((unsigned)grid), dim3(kWave), 0, st, state, slots_total, slot, t, heads, rep, dv, q, k, v, g, beta, lengths, out);
   return status_of(hipGetLastError());
 }
 
 template <int DK>
-int launch_delta_rule_mode(float* state, const int64_t* slot, int rows, int t, int heads, int rep,
+int launch_delta_rule_mode(float* state, int64_t slots_total, const int64_t* slot, int rows, int t, int heads, int rep,
                            int dv, const float* q, const float* k, const float* v, const float* g,
                            const float* beta, const int64_t* lengths, float* out, hipStream_t st) {
   if (!lengths)
-    return launch_delta_rule<DK, true, false>(state, slot, rows, t, heads, rep, dv, q, k, v, g, beta,
+    return launch_delta_rule<DK, true, false>(state, slots_total, slot, rows, t, heads, rep, dv, q, k, v, g, beta,
                                               nullptr, out, st);
   if (out)
-    return launch_delta_rule<DK, true, true>(state, slot, rows, t, heads, rep, dv, q, k, v, g, beta,
+    return launch_delta_rule<DK, true, true>(state, slots_total, slot, rows, t, heads, rep, dv, q, k, v, g, beta,
                                              lengths, out, st);
-  return launch_delta_rule<DK, false, true>(state, slot, rows, t, heads, rep, dv, q, k, v, g, beta,
+  return launch_delta_rule<DK, false, true>(state, slots_total, slot, rows, t, heads, rep, dv, q, k, v, g, beta,
                                             lengths, nullptr, st);
 }
 
@@ -175,6 +180,7 @@ struct DnPrepArgs {
   int64_t proj_stride;
   const void* conv;       // conv state [slots, C, k1] model dtype
   const int64_t* slot;    // [B]
+  int64_t slots_total;    // conv_state slots; a row whose slot is outside reads a zero window
   const void* conv_w;     // [C, conv_k] model dtype
   const float* a_log;     // [vh] f32
   const float* dt_bias;   // [vh] f32
@@ -190,6 +196,7 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
   const int k1 = a.conv_k - 1;
   const int C = 2 * a.kh * a.kd + a.vh * a.vd;
   const int64_t slot = a.slot[b];
+  const bool slot_ok = slot >= 0 && slot < a.slots_total;
   const int units = 2 * a.kh + a.vh;
   const int u = blockIdx.y * (kPrepThreadsDn / kWave) + wave;
   if (u < units) {
@@ -209,7 +216,7 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
       for (int j = 0; j < kConvMaxK1 + 1; ++j) {  // all taps' loads issued together
         if (j >= a.conv_k) break;
         const int p = s + j;  // window column: the stored k1, then the t new ones
-        const float win = p < k1 ? load_float(a.conv, a.dt, (slot * C + c) * k1 + p)
+        const float win = p < k1 ? (slot_ok ? load_float(a.conv, a.dt, (slot * C + c) * k1 + p) : 0.f)
                                  : load_float(a.proj, a.dt, ((int64_t)b * a.t + p - k1) * a.proj_stride + c);
         const float prod = __fmul_rn(win, load_float(a.conv_w, a.dt, (int64_t)c * a.conv_k + j));
         acc = j == 0 ? prod : __fadd_rn(acc, prod);
@@ -251,12 +258,14 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
 // cannot read a value it has already replaced.
 __global__ __launch_bounds__(256) void k_conv_commit(void* __restrict__ conv, int dt,
                                                      const int64_t* __restrict__ slot,
+                                                     int64_t slots_total,
                                                      const void* __restrict__ proj,
                                                      int64_t proj_stride, const int64_t* __restrict__ idx,
                                                      int B, int C, int k1, int t) {
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)B * C) return;
   const int b = (int)(i / C), c = (int)(i - (int64_t)b * C);
+  if (slot[b] < 0 || slot[b] >= slots_total) return;  // no such slot: nothing to update
   const int64_t base = (slot[b] * C + c) * k1;
   float v[kConvMaxK1];
   for (int w = 0; w < k1; ++w) {
@@ -291,7 +300,7 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
   const hipStream_t st = (hipStream_t)stream;
   const int r = (int)rows, tt = (int)t, h = (int)heads, rep = (int)(heads / qk_heads), dv = (int)v_dim;
 #define MTPK_DN(DK_) \
-  launch_delta_rule_mode<DK_>(state, slot, r, tt, h, rep, dv, q, k, v, g, beta, lengths, out, st)
+  launch_delta_rule_mode<DK_>(state, slots_total, slot, r, tt, h, rep, dv, q, k, v, g, beta, lengths, out, st)
   switch (k_dim) {
     case 16: return MTPK_DN(16);
     case 32: return MTPK_DN(32);
@@ -302,7 +311,7 @@ int mtpk_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int6
 }
 
 int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const void* conv_state,
-                       const int64_t* slot, const void* conv_w, const float* a_log,
+                       const int64_t* slot, int64_t slots_total, const void* conv_w, const float* a_log,
                        const float* dt_bias, int64_t batch, int64_t t, int64_t k_heads,
                        int64_t k_dim, int64_t v_heads, int64_t v_dim, int64_t conv_k, float eps,
                        float q_scale, float* q, float* k, float* v, float* g, float* beta,
@@ -310,14 +319,15 @@ int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const v
   if (!proj || !conv_state || !slot || !conv_w || !a_log || !dt_bias || !q || !k || !v || !g || !beta)
     return MTPK_EINVAL;
   if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
-  if (batch < 0 || t < 1 || k_heads < 1 || v_heads < 1 || conv_k < 2 || conv_k > kConvMaxK1 + 1)
+  if (batch < 0 || t < 1 || k_heads < 1 || v_heads < 1 || conv_k < 2 || conv_k > kConvMaxK1 + 1 ||
+      slots_total < 1)
     return MTPK_EINVAL;
   if (k_dim < 1 || k_dim > kWave * kPrepMaxPerLane || v_dim < 1 || v_dim > kWave * kPrepMaxPerLane)
     return MTPK_EINVAL;
   const int64_t C = 2 * k_heads * k_dim + v_heads * v_dim;
   if (proj_stride < C + v_heads * v_dim + 2 * v_heads || batch * t > INT32_MAX) return MTPK_EINVAL;
   if (batch == 0) return 0;
-  DnPrepArgs a{proj, proj_stride, conv_state, slot, conv_w, a_log, dt_bias, dtype, (int)t,
+  DnPrepArgs a{proj, proj_stride, conv_state, slot, slots_total, conv_w, a_log, dt_bias, dtype, (int)t,
                (int)k_heads, (int)k_dim, (int)v_heads, (int)v_dim, (int)conv_k, eps, q_scale,
                q, k, v, g, beta};
   const int64_t units = 2 * k_heads + v_heads;
@@ -328,18 +338,20 @@ int mtpk_deltanet_prep(const void* proj, int dtype, int64_t proj_stride, const v
   return status_of(hipGetLastError());
 }
 
-int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, const void* proj,
+int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, int64_t slots_total,
+                     const void* proj,
                      int64_t proj_stride, const int64_t* idx, int64_t batch, int64_t channels,
                      int64_t k1, int64_t t, void* stream) {
   if (!conv_state || !slot || !proj || !idx) return MTPK_EINVAL;
   if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
-  if (batch < 0 || channels < 1 || k1 < 1 || k1 > kConvMaxK1 || t < 1 || proj_stride < channels)
+  if (batch < 0 || channels < 1 || k1 < 1 || k1 > kConvMaxK1 || t < 1 || proj_stride < channels ||
+      slots_total < 1)
     return MTPK_EINVAL;
   if (batch * channels > INT32_MAX) return MTPK_EINVAL;
   if (batch == 0) return 0;
   const int64_t n = batch * channels;
   hipLaunchKernelGGL(k_conv_commit, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, conv_state, dtype, slot, proj, proj_stride, idx,
+                     (hipStream_t)stream, conv_state, dtype, slot, slots_total, proj, proj_stride, idx,
                      (int)batch, (int)channels, (int)k1, (int)t);
   return status_of(hipGetLastError());
 }

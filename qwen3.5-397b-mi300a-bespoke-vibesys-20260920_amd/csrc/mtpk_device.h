@@ -94,10 +94,32 @@ struct ScaleChunk<4> {
 // next are always the oldest outstanding ones (the wait before them leaves D-1 trips in flight).
 __device__ inline void ring_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Decode parameters of one 32-element block with e8m0 scale byte s: the fp32 scale operand of
+// the hardware convert, and the mask applied to the packed codes first.
+// The convert takes only the exponent field of its fp32 scale, so s = 0 (fp32 +0.0) acts as
+// 2^-127, the OCP reading of that byte, where the pinned kernel decode gives +-0.0. For such a
+// block only the codes' sign bits are kept: +-0 * 2^-127 is exactly +-0.0, the sign from the
+// code as in the pinned decode. Bytes 1..254 are exact as they are (bf16 has fp32's exponent
+// range, so the subnormal products of byte 1 and the overflow to +-inf at 253..254 come out as
+// in fp32; checked bit for bit on the GPU). Byte 255, the OCP NaN scale, gives NaN for every
+// code, where the pinned decode gives +-inf for nonzero codes: experts holding such a block
+// are refused at load (`mtpk_scales_ok`).
+struct BlockScale {
+  float f;
+  uint32_t keep;
+};
+
+__device__ inline BlockScale block_scale(uint32_t s) {
+  s &= 0xffu;
+  return BlockScale{e8m0_to_f32(s), s ? 0xffffffffu : 0x88888888u};
+}
+
 // Eight e2m1 codes of one packed dword (code j = nibble j, low nibble first) times the block
 // scale, as eight bf16 in element order: the hardware fp4 -> bf16 convert with the e8m0 scale
-// applied (one instruction per byte). `scale` is the fp32 2^(s-127).
-__device__ inline bf16x8_t decode8(uint32_t w, float scale) {
+// applied (one instruction per byte).
+__device__ inline bf16x8_t decode8(uint32_t w, const BlockScale& b) {
+  w &= b.keep;
+  const float scale = b.f;
   const bf16x2_t p0 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 0);
   const bf16x2_t p1 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 1);
   const bf16x2_t p2 = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(w, scale, 2);

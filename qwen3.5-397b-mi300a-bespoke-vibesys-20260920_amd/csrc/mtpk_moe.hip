@@ -231,8 +231,8 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up(
     };
     f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
     auto consume = [&](const GuTrip<XP>& r, int s) {
-      const float fg = e8m0_to_f32(SV ? cg.byte(s, ln.g) : r.sg);
-      const float fu = e8m0_to_f32(SV ? cu.byte(s, ln.g) : r.su);
+      const BlockScale fg = block_scale(SV ? cg.byte(s, ln.g) : r.sg);
+      const BlockScale fu = block_scale(SV ? cu.byte(s, ln.g) : r.su);
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
         const bf16x8_t bg = decode8(r.wg[h], fg), bu = decode8(r.wu[h], fu);
@@ -369,7 +369,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down(
     auto consume = [&](const DnTrip<IP, R>& t, int s) {
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float fs = e8m0_to_f32(SV ? cs[r].byte(s, ln.g) : t.s[r]);
+        const BlockScale fs = block_scale(SV ? cs[r].byte(s, ln.g) : t.s[r]);
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const bf16x8_t b = decode8(t.w[r][h], fs);
@@ -465,7 +465,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_token(
       };
       f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
       auto consume = [&](const DnTrip<IP, 1>& r, int s) {
-        const float fs = e8m0_to_f32(SV ? cs.byte(s, ln.g) : r.s[0]);
+        const BlockScale fs = block_scale(SV ? cs.byte(s, ln.g) : r.s[0]);
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const bf16x8_t b = decode8(r.w[0][h], fs);
@@ -613,7 +613,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_single(
         sg_ = buf1(rs, (osg + (uint32_t)blk) | bad);
         su_ = buf1(rs, (osu + (uint32_t)blk) | bad);
       }
-      const float fg = e8m0_to_f32(sg_), fu = e8m0_to_f32(su_);
+      const BlockScale fg = block_scale(sg_), fu = block_scale(su_);
 #pragma unroll
       for (int h = 0; h < 4; ++h) {
         const bf16x8_t bg = decode8(wg[i][h], fg), bu = decode8(wu[i][h], fu);
@@ -727,7 +727,7 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
           const uint32_t bad = (uint32_t)!(i < ntrip && blk < nb) << 31;
           sb = buf1(rs, (os + (uint32_t)blk) | bad);
         }
-        const float fs = e8m0_to_f32(sb);
+        const BlockScale fs = block_scale(sb);
 #pragma unroll
         for (int h = 0; h < 4; ++h) {
           const bf16x8_t b = decode8(w[i][h], fs);
@@ -886,8 +886,8 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
     f32x4_t accg = {0.f, 0.f, 0.f, 0.f}, accu = {0.f, 0.f, 0.f, 0.f};
     uint32_t cur_g = 0u, cur_u = 0u;  // this turn's packed scales (selected per chunk)
     auto consume = [&](const u32x4_t& wg, const u32x4_t& wu, int s, const uint8_t* buf) {
-      const float fg = e8m0_to_f32((cur_g >> (8 * s)) & 0xffu);
-      const float fu = e8m0_to_f32((cur_u >> (8 * s)) & 0xffu);
+      const BlockScale fg = block_scale(cur_g >> (8 * s));
+      const BlockScale fu = block_scale(cur_u >> (8 * s));
       const uint8_t* arow = buf + ln.c * G::kRow + ((4 * s + ln.g) * 32) * 2;
       u32x4_t a[4];
 #pragma unroll
@@ -1134,7 +1134,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
       const bool nx = tr >= ntrip;  // uniform
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        const float fs = e8m0_to_f32((cs[r] >> (csh + 8 * s)) & 0xffu);
+        const BlockScale fs = block_scale(cs[r] >> (csh + 8 * s));
         bf16x8_t b[4];
 #pragma unroll
         for (int h = 0; h < 4; ++h) b[h] = decode8(ring[s][r][h], fs);
@@ -1288,27 +1288,70 @@ __global__ __launch_bounds__(256) void k_dequant(const uint8_t* __restrict__ pac
                                                  const uint8_t* __restrict__ scale, int64_t rows,
                                                  int K, int mode, float* __restrict__ out) {
   const int64_t half = K >> 1, nb = K >> 5;
-  const int64_t total = rows * half;
-  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t r = i / half, col = i - r * half;
-    const uint32_t b = packed[i];
-    const uint32_t s = scale[r * nb + (2 * col) / 32];
-    float v0, v1;
-    if (mode == 0) {
-      const float f = e8m0_to_f32(s);
-      v0 = fp4_to_f32(b & 15u) * f;
-      v1 = fp4_to_f32(b >> 4) * f;
-    } else {
-      const bf16x2_t p = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp4(b, e8m0_to_f32(s), 0);
-      const uint32_t bits = __builtin_bit_cast(uint32_t, p);
-      v0 = bf16_to_f32((uint16_t)(bits & 0xffffu));
-      v1 = bf16_to_f32((uint16_t)(bits >> 16));
+  if (mode == 0) {
+    const int64_t total = rows * half;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+      const int64_t r = i / half, col = i - r * half;
+      const uint32_t b = packed[i];
+      const float f = e8m0_to_f32(scale[r * nb + (2 * col) / 32]);
+      out[r * K + 2 * col] = fp4_to_f32(b & 15u) * f;
+      out[r * K + 2 * col + 1] = fp4_to_f32(b >> 4) * f;
     }
-    out[r * K + 2 * col] = v0;
-    out[r * K + 2 * col + 1] = v1;
+    return;
+  }
+  // mode 1: the MoE kernels' decode8 on each packed dword (K % 32 == 0, so a dword never
+  // straddles a row or a scale block)
+  const int64_t words = rows * (half >> 2), wpr = half >> 2;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < words;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / wpr, wc = i - r * wpr;
+    const uint8_t* pb = packed + r * half + 4 * wc;
+    const uint32_t w = (uint32_t)pb[0] | ((uint32_t)pb[1] << 8) | ((uint32_t)pb[2] << 16) |
+                       ((uint32_t)pb[3] << 24);
+    const bf16x8_t v = decode8(w, block_scale(scale[r * nb + (8 * wc) / 32]));
+    const u32x4_t bits = __builtin_bit_cast(u32x4_t, v);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      out[r * K + 8 * wc + 2 * j] = bf16_to_f32((uint16_t)(bits[j] & 0xffffu));
+      out[r * K + 8 * wc + 2 * j + 1] = bf16_to_f32((uint16_t)(bits[j] >> 16));
+    }
   }
 }
+
+// Blocks the in-register decode cannot reproduce: scale byte 255 (the OCP NaN scale, where the
+// pinned decode gives +-inf for nonzero codes and the hardware convert NaN) over a block that
+// holds a nonzero-magnitude code. Block b is packed bytes [16 b, 16 b + 16) and scale byte b.
+// Each thread tests 16 scale bytes with one load when `vec` (16-byte aligned scales) and reads
+// packed bytes only for the blocks that carry scale 255; *bad counts the threads that found one.
+__global__ __launch_bounds__(256) void k_scale_scan(const uint8_t* __restrict__ packed,
+                                                    const uint8_t* __restrict__ scale,
+                                                    int64_t blocks, int vec,
+                                                    int32_t* __restrict__ bad) {
+  int found = 0;
+  auto check = [&](int64_t b) {
+    if (scale[b] != 0xffu) return;
+    const uint8_t* p = packed + 16 * b;
+    uint32_t any = 0;
+    for (int i = 0; i < 16; ++i) any |= p[i];
+    if (any & 0x77u) found = 1;
+  };
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t groups = vec ? blocks / 16 : 0;
+  for (int64_t gi = tid; gi < groups; gi += stride) {
+    const u32x4_t s = ld16(scale + 16 * gi);
+    uint32_t ff = 0;  // nonzero when some byte of s is 0xff (zero-byte test on ~s)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) ff |= (~s[j] - 0x01010101u) & s[j] & 0x80808080u;
+    if (ff)
+      for (int i = 0; i < 16; ++i) check(16 * gi + i);
+  }
+  for (int64_t b = groups * 16 + tid; b < blocks; b += stride) check(b);
+  if (found) atomicAdd(bad, 1);
+}
+
+__global__ void k_zero_i32(int32_t* p) { *p = 0; }
 
 __global__ __launch_bounds__(64) void k_probe_mfma(const uint16_t* __restrict__ a,
                                                    const uint16_t* __restrict__ b,
@@ -1538,7 +1581,8 @@ int mtpk_moe_prep(const void* a_expert, int expert_dtype, const void* a_weight, 
   if (!dtype_index_ok(expert_dtype) || !dtype_float_ok(weight_dtype)) return MTPK_EINVAL;
   if (ne <= 0 || ne > MTPK_MAX_EXPERTS || assignments < 0 || assignments > INT32_MAX)
     return MTPK_EINVAL;
-  if (max_units < 0 || max_units > INT32_MAX / 3) return MTPK_EINVAL;
+  // fewer units than the bound would drop assignments that down and combine still expect
+  if (max_units < mtpk_moe_max_units(assignments, ne) || max_units > INT32_MAX / 3) return MTPK_EINVAL;
   hipLaunchKernelGGL(k_moe_prep, dim3(1), dim3(kPrepThreads), 0, (hipStream_t)stream, a_expert,
                      expert_dtype, a_weight, weight_dtype, (int)assignments, expert_lo, (int)ne,
                      sorted, units, (int)max_units, n_units);
@@ -1554,7 +1598,9 @@ int mtpk_moe_gate_up(const uint16_t* x_planes, int x_nplanes, int64_t tokens, in
     return MTPK_EINVAL;
   if (!gemm_shapes_ok(hidden, inter_dim, local_experts) || top_k <= 0) return MTPK_EINVAL;
   if (!aligned16(x_planes) || !aligned16(gate_up) || !aligned16(inter)) return MTPK_EINVAL;
-  if (max_units <= 0 || max_units > INT32_MAX / inter_dim) return MTPK_EINVAL;
+  if (max_units <= 0 || max_units > INT32_MAX / inter_dim ||
+      max_units < mtpk_moe_max_units(assignments, local_experts))
+    return MTPK_EINVAL;
   if (!((x_nplanes == 1 && inter_planes == 2) || (x_nplanes == 3 && inter_planes == 3)))
     return MTPK_EINVAL;
   return launch_gate_up(x_nplanes, x_planes, tokens * hidden, (int)hidden, gate_up, gate_up_scale,
@@ -1603,7 +1649,9 @@ int mtpk_moe_down(const uint16_t* inter, int inter_planes, int64_t assignments, 
   if (!inter || !down || !down_scale || !sorted || !units || !n_units || !y) return MTPK_EINVAL;
   if (!gemm_shapes_ok(hidden, inter_dim, local_experts)) return MTPK_EINVAL;
   if (!aligned16(inter) || !aligned16(down)) return MTPK_EINVAL;
-  if (max_units <= 0 || max_units > INT32_MAX / hidden) return MTPK_EINVAL;
+  if (max_units <= 0 || max_units > INT32_MAX / hidden ||
+      max_units < mtpk_moe_max_units(assignments, local_experts))
+    return MTPK_EINVAL;
   const hipStream_t st = (hipStream_t)stream;
   const int64_t ip = assignments * inter_dim;
   const UnitSrc src = unit_list(units, sorted, n_units, max_units);
@@ -1786,6 +1834,22 @@ int mtpk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows
   const int grid = (int)(blocks < 16384 ? blocks : 16384);
   hipLaunchKernelGGL(k_dequant, dim3(grid), dim3(256), 0, (hipStream_t)stream, packed, scale,
                      rows, (int)k, mode, out);
+  return status_of(hipGetLastError());
+}
+
+int mtpk_scale_scan(const uint8_t* packed, const uint8_t* scale, int64_t blocks,
+                    int32_t* bad_count, void* stream) {
+  if (!packed || !scale || !bad_count || blocks < 0) return MTPK_EINVAL;
+  const hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(k_zero_i32, dim3(1), dim3(1), 0, st, bad_count);
+  if (blocks > 0) {
+    const int vec = aligned16(scale) ? 1 : 0;
+    const int64_t work = vec ? blocks / 16 + 16 : blocks;
+    const int64_t wgs = (work + 255) / 256;
+    const int grid = (int)(wgs < 8192 ? wgs : 8192);
+    hipLaunchKernelGGL(k_scale_scan, dim3(grid), dim3(256), 0, st, packed, scale, blocks, vec,
+                       bad_count);
+  }
   return status_of(hipGetLastError());
 }
 

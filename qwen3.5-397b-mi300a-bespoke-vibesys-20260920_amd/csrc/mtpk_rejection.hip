@@ -109,12 +109,19 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_stats(RsRows rr, int64_t n_ta
 #pragma unroll
   for (int e = 0; e < kRsPerThread; ++e) m = fmaxf(m, z[e]);
   m = block_max(m, red);
+  // A chunk of -inf logits (a masked stretch of the vocabulary) has no mass: (-inf, 0), not the
+  // NaN of exp(-inf - -inf). m is uniform over the workgroup, so is the branch.
   float s = 0.f;
+  if (m > -INFINITY) {
 #pragma unroll
-  for (int e = 0; e < kRsPerThread; ++e) s += __expf(z[e] - m);
+    for (int e = 0; e < kRsPerThread; ++e) s += __expf(z[e] - m);
+  }
   s = block_sum(s, red);
   if (threadIdx.x == 0) part[r * nchunk + c] = make_float2(m, s);
 }
+
+// A chunk partial's share of a row sum with row max m; a massless (-inf) chunk adds nothing.
+__device__ inline float rs_share(float2 v, float m) { return v.x > -INFINITY ? v.y * __expf(v.x - m) : 0.f; }
 
 // Combine a row's chunk partials (one wave): max M and sum S of exp(z - M).
 __device__ inline float2 rs_row_stats(const float2* part, int64_t r, int nchunk) {
@@ -123,11 +130,8 @@ __device__ inline float2 rs_row_stats(const float2* part, int64_t r, int nchunk)
   float m = v0.x;
   for (int c = lane + kWave; c < nchunk; c += kWave) m = fmaxf(m, part[r * nchunk + c].x);
   m = wave_max(m);
-  float s = lane < nchunk ? v0.y * __expf(v0.x - m) : 0.f;
-  for (int c = lane + kWave; c < nchunk; c += kWave) {
-    const float2 v = part[r * nchunk + c];
-    s += v.y * __expf(v.x - m);
-  }
+  float s = rs_share(v0, m);
+  for (int c = lane + kWave; c < nchunk; c += kWave) s += rs_share(part[r * nchunk + c], m);
   return make_float2(m, wave_sum(s));
 }
 
@@ -179,7 +183,7 @@ __global__ __launch_bounds__(kWave * kDecideWaves) void k_rs_decide(
   if (threadIdx.x == 0) {
     int a = k;
     for (int i = 0; i < k; ++i)
-      if (s_mg[i] < 0.f) {
+      if (!(s_mg[i] >= 0.f)) {  // a NaN margin (a fully masked row) rejects too
         a = i;
         break;
       }

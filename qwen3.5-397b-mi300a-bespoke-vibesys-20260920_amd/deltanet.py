@@ -96,7 +96,7 @@ def prep(proj: torch.Tensor, conv_state: torch.Tensor, slots: torch.Tensor, conv
     sl = slots.to(torch.int64).contiguous()
     _mtpk.check(_mtpk.lib().mtpk_deltanet_prep(
         proj.data_ptr(), _mtpk.float_code(dt), proj.stride(1), conv_state.data_ptr(), sl.data_ptr(),
-        conv_w.data_ptr(), a_log.data_ptr(), dt_bias.data_ptr(), b, t, k_heads, k_dim, v_heads, v_dim,
+        conv_state.shape[0], conv_w.data_ptr(), a_log.data_ptr(), dt_bias.data_ptr(), b, t, k_heads, k_dim, v_heads, v_dim,
         conv_w.shape[1], float(eps), float(k_dim) ** -0.5, q.data_ptr(), k.data_ptr(), v.data_ptr(),
         g.data_ptr(), beta.data_ptr(), _mtpk.stream_of(device)), "mtpk_deltanet_prep")  # fmt: skip
     return q, k, v, g, beta
@@ -119,6 +119,7 @@ def conv_commit(conv_state: torch.Tensor, slots: torch.Tensor, proj: torch.Tenso
         raise ValueError(f"idx must be [{b}, {k1}]")
     sl = slots.to(torch.int64).contiguous()
     _mtpk.check(_mtpk.lib().mtpk_conv_commit(
-        conv_state.data_ptr(), _mtpk.float_code(conv_state.dtype), sl.data_ptr(), proj.data_ptr(),
+        conv_state.data_ptr(), _mtpk.float_code(conv_state.dtype), sl.data_ptr(), conv_state.shape[0],
+        proj.data_ptr(),
         proj.stride(1), ix.data_ptr(), b, channels, k1, t, _mtpk.stream_of(device)),
         "mtpk_conv_commit")  # fmt: skip

@@ -63,6 +63,56 @@ def use_grouped(assignments: int, experts: int) -> bool:
     return assignments >= GROUPED_MIN_PER_EXPERT * max(experts, 1)
 
 
+_REFUSED: set[tuple[int, int]] = set()
+"""(gate_up_scale, down_scale) data pointers of expert payloads `supports` refused."""
+
+
+def bw_scales_ok(experts: dict) -> bool:
+    """Precondition of the in-register decode (interface of `mxfp4_gemv.py:1761-1776`): no
+    32-element block with e8m0 scale 255 holds a nonzero-magnitude code.
+
+    The hardware fp4 converter the kernels decode with reproduces the pinned decode bit for bit
+    at every other scale (byte 0 as +-0.0 through the code mask, 1..254 as they are). At 255,
+    the OCP NaN scale, it returns NaN where the pinned decode gives +-inf for nonzero codes
+    (zero codes are NaN in both). One device scan of the scales (the packed bytes are read only
+    under scale 255) and one host sync: call at load time, never inside graph capture.
+    """
+    lib = _mtpk.lib()
+    device = _mtpk.require_device(experts["gate_up"], experts["down"])
+    bad = torch.zeros(2, dtype=torch.int32, device=device)
+    st = _mtpk.stream_of(device)
+    for i, (w, s) in enumerate((("gate_up", "gate_up_scale"), ("down", "down_scale"))):
+        packed, scale = experts[w], experts[s]
+        if not (packed.is_contiguous() and scale.is_contiguous()) or packed.numel() != 16 * scale.numel():
+            raise ValueError(f"experts[{w!r}] / [{s!r}] are not a contiguous MXFP4 pair")
+        _mtpk.check(lib.mtpk_scale_scan(packed.data_ptr(), scale.data_ptr(), scale.numel(),
+                                        bad[i:].data_ptr(), st), "mtpk_scale_scan")
+    return not bool(bad.any().item())
+
+
+def supports(experts: dict) -> bool:
+    """Load-time check that `fused_moe` computes these experts exactly (the role of
+    `moe_hip.supports`, `moe_hip.py:204-215`): contiguous MXFP4 payloads of matching shapes
+    and `bw_scales_ok`. A refusal is remembered, and `fused_moe` then raises `ValueError` for
+    these tensors instead of decoding them. One host sync."""
+    gu, gus, dn, dns = (experts[k] for k in ("gate_up", "gate_up_scale", "down", "down_scale"))
+    shapes = (
+        gu.dim() == 3 and dn.dim() == 3 and gu.shape[1] % 2 == 0
+        and gus.shape == (*gu.shape[:2], gu.shape[2] * 2 // BLOCK_SCALE)
+        and dns.shape == (*dn.shape[:2], dn.shape[2] * 2 // BLOCK_SCALE)
+        and dn.shape[0] == gu.shape[0] and dn.shape[1] == gu.shape[2] * 2
+        and dn.shape[2] * 2 == gu.shape[1] // 2
+        and all(t.is_contiguous() for t in (gu, gus, dn, dns))
+    )  # fmt: skip
+    ok = shapes and bw_scales_ok(experts)
+    key = (gus.data_ptr(), dns.data_ptr())
+    if ok:
+        _REFUSED.discard(key)
+    else:
+        _REFUSED.add(key)
+    return ok
+
+
 def _validate(x, experts, routing, top_k):
     a_expert, a_weight = routing
     tokens = x.shape[0]
@@ -82,6 +132,9 @@ def _validate(x, experts, routing, top_k):
             raise ValueError(f"experts[{name!r}] must be contiguous")
     if top_k > _mtpk.MAX_TOP_K:
         raise ValueError(f"top_k {top_k} exceeds {_mtpk.MAX_TOP_K}")
+    if _REFUSED and (experts["gate_up_scale"].data_ptr(), experts["down_scale"].data_ptr()) in _REFUSED:
+        raise ValueError("these experts failed supports(): a block with e8m0 scale 255 holds a "
+                         "nonzero code, which the in-register decode cannot reproduce")
 
 
 def _workspace(device: torch.device, nbytes: int, scratch: torch.Tensor | None) -> torch.Tensor:
@@ -339,32 +392,34 @@ def grouped_block_count(assignments: int, experts: int, block_m: int) -> int:
 
 def align_blocks(a_expert: torch.Tensor, a_weight: torch.Tensor, expert_range: tuple[int, int],
                  block_m: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-expert `block_m` blocks with a fixed-shape result (`mxfp4_gemv.py:745-800`):
-    `slot_assign[b*block_m + i]` = assignment id or -1, `block_expert[b]` = local expert or the
-    sentinel `experts` for dropped assignments. Torch ops, no host sync."""
+    """Per-expert `block_m` blocks with a fixed-shape result (interface of
+    `mxfp4_gemv.py:745-800`): `slot_assign[b*block_m + i]` = assignment id or -1,
+    `block_expert[b]` = local expert, or the sentinel `experts` for the bucket of dropped
+    assignments and for the unused blocks past the last one. Torch ops, no host sync.
+
+    Bucket `experts` collects the dropped assignments. An assignment's row in its bucket is the
+    number of earlier assignments of that bucket (a running count over the one-hot bucket
+    matrix), its slot is that row past the bucket's first block, and block b belongs to the
+    bucket whose block range contains it (a binary search over the buckets' block ends).
+    """
     lo, hi = expert_range
     experts = hi - lo
     n = a_expert.numel()
     device = a_expert.device
-    live = (a_expert >= lo) & (a_expert < hi) & (a_weight != 0)
-    bucket = torch.where(live, a_expert.to(torch.long) - lo, experts)
-    counts = torch.zeros(experts + 1, dtype=torch.long, device=device)
-    counts.scatter_add_(0, bucket, torch.ones_like(bucket))
-    blocks = -(-counts // block_m)
-    block_start = blocks.cumsum(0) - blocks
-    order = torch.argsort(bucket, stable=True)
-    sorted_bucket = bucket[order]
-    first = counts.cumsum(0) - counts
-    rank = torch.arange(n, device=device) - first[sorted_bucket]
-    slot = block_start[sorted_bucket] * block_m + rank
+    e = a_expert.to(torch.long) - lo
+    bucket = torch.where((e >= 0) & (e < experts) & (a_weight != 0), e, experts)
+    onehot = torch.nn.functional.one_hot(bucket, experts + 1).to(torch.int32)
+    seen = onehot.cumsum(0)  # seen[a, b]: assignments 0..a that fall in bucket b
+    row = seen.gather(1, bucket[:, None])[:, 0].to(torch.long) - 1
+    count = seen[-1].to(torch.long) if n else torch.zeros(experts + 1, dtype=torch.long, device=device)
+    block_end = (-(-count // block_m)).cumsum(0)  # one past each bucket's last block
+    slot = (block_end - (-(-count // block_m)))[bucket] * block_m + row
     n_blocks = grouped_block_count(n, experts, block_m)
     slot_assign = torch.full((n_blocks * block_m,), -1, dtype=torch.int32, device=device)
-    slot_assign.scatter_(0, slot, order.to(torch.int32))
-    marks = torch.full((n_blocks + 1,), -1, dtype=torch.long, device=device)
-    marks.scatter_reduce_(0, block_start.clamp(max=n_blocks), torch.arange(experts + 1, device=device),
-                          reduce="amax")
-    block_expert = marks.cummax(0).values[:n_blocks].to(torch.int32)
-    return slot_assign, block_expert
+    slot_assign[slot] = torch.arange(n, dtype=torch.int32, device=device)
+    blocks = torch.arange(n_blocks, dtype=torch.long, device=device)
+    owner = torch.searchsorted(block_end, blocks, right=True).clamp(max=experts)
+    return slot_assign, owner.to(torch.int32)
 
 
 def reference_moe(
@@ -377,20 +432,30 @@ def reference_moe(
     compute_dtype: torch.dtype | None = None,
     chunk: int = 16,
 ) -> torch.Tensor:
-    """Dequantise-then-`bmm`, the slow readable spelling (`mxfp4_gemv.py:1613-1651`): the torch
-    path selected by `SEED_FUSED_MOE=0` and the arithmetic `fused_moe` reformulates."""
+    """Dequantise-then-multiply in `compute_dtype` (interface of `mxfp4_gemv.py:1613-1651`): the
+    torch path selected by `SEED_FUSED_MOE=0` and the arithmetic `fused_moe` reformulates.
+
+    Every distinct live expert is dequantised once, at most `chunk` experts at a time, and its
+    assignments' token rows go through `x @ gate_upᵀ`, `silu(gate) * up`, `@ downᵀ` and the
+    routing weight together; the weighted rows are added into the output per token.
+    """
     a_expert, a_weight = routing
     lo, hi = expert_range
     dt = compute_dtype or x.dtype
-    keep = ((a_expert >= lo) & (a_expert < hi) & (a_weight != 0)).nonzero(as_tuple=True)[0]
+    e = a_expert.to(torch.long) - lo
+    live = (e >= 0) & (e < hi - lo) & (a_weight != 0)
     out = torch.zeros(x.shape[0], experts["down"].shape[1], dtype=dt, device=x.device)
-    for start in range(0, keep.numel(), chunk):
-        part = keep[start : start + chunk]
-        local = (a_expert[part] - lo).to(torch.long)
-        token = (part // top_k).to(torch.long)
-        gate_up_w = dequant(experts["gate_up"][local], experts["gate_up_scale"][local], dt)
-        down_w = dequant(experts["down"][local], experts["down_scale"][local], dt)
-        gate, up = torch.bmm(x.to(dt)[token][:, None], gate_up_w.transpose(1, 2).contiguous()).chunk(2, -1)
-        y = torch.bmm(torch.nn.functional.silu(gate) * up, down_w.transpose(1, 2).contiguous())[:, 0]
-        out.index_add_(0, token, y * a_weight[part, None].to(dt))
+    ids = torch.arange(a_expert.numel(), device=x.device)
+    used = torch.unique(e[live])
+    xs = x.to(dt)
+    for g in range(0, used.numel(), chunk):
+        group = used[g : g + chunk]
+        w1 = dequant(experts["gate_up"][group], experts["gate_up_scale"][group], dt)
+        w2 = dequant(experts["down"][group], experts["down_scale"][group], dt)
+        for i, ex in enumerate(group.tolist()):
+            mine = ids[live & (e == ex)]
+            rows = xs[mine // top_k]
+            gate, up = (rows @ w1[i].t()).chunk(2, -1)
+            y = (torch.nn.functional.silu(gate) * up) @ w2[i].t()
+            out.index_add_(0, mine // top_k, y * a_weight[mine, None].to(dt))
     return out.to(x.dtype)

@@ -19,7 +19,6 @@ from __future__ import annotations
 
 import json
 import os
-import struct
 import threading
 from concurrent.futures import ThreadPoolExecutor
 from dataclasses import dataclass
@@ -67,35 +66,75 @@ class TensorInfo:
     nbytes: int
 
 
+def _parse_shard(path: Path) -> dict[str, TensorInfo]:
+    """The tensor table of one safetensors file, from the format itself: a little-endian u64
+    header size N, N bytes of UTF-8 JSON mapping each tensor name to its `dtype`, `shape` and
+    `data_offsets` [begin, end) within the data section that follows the header (plus an
+    optional `__metadata__` entry), then the data section. Every entry is checked: a known
+    dtype, a byte range inside the data section, and a size equal to shape x item size."""
+    size = path.stat().st_size
+    with open(path, "rb") as fh:
+        prefix = fh.read(8)
+        if len(prefix) < 8:
+            raise OSError(f"{path}: shorter than a safetensors header")
+        header_len = int.from_bytes(prefix, "little")
+        if header_len > size - 8:
+            raise OSError(f"{path}: header of {header_len} bytes overruns the file")
+        table = json.loads(fh.read(header_len).decode("utf-8"))
+    data_start, data_len = 8 + header_len, size - 8 - header_len
+    out: dict[str, TensorInfo] = {}
+    for key, entry in table.items():
+        if key == "__metadata__":
+            continue
+        dtype = _DTYPES.get(entry.get("dtype"))
+        if dtype is None:
+            raise ValueError(f"{path}: tensor {key} has unsupported dtype {entry.get('dtype')!r}")
+        shape = tuple(int(d) for d in entry["shape"])
+        begin, stop = (int(o) for o in entry["data_offsets"])
+        want = dtype.itemsize
+        for d in shape:
+            want *= d
+        if not 0 <= begin <= stop <= data_len or stop - begin != want:
+            raise ValueError(f"{path}: tensor {key} has byte range [{begin}, {stop}) for "
+                             f"{want} bytes in a {data_len}-byte data section")
+        out[key] = TensorInfo(path, dtype, shape, data_start + begin, stop - begin)
+    return out
+
+
 class Checkpoint:
-    """Tensor name -> (shard, dtype, shape, byte range) from the shard headers; bytes on demand."""
+    """Every tensor of a directory of `*.safetensors` shards, indexed by name from the shard
+    headers (`weights.py:30-59` is the interface: `files`, `has`, `load`); the bytes are read on
+    demand with `os.preadv` through one read-only descriptor per shard, opened on first use."""
 
     def __init__(self, path: str | Path) -> None:
-        self.files = sorted(Path(path).glob("*.safetensors"))
+        root = Path(path)
+        self.files = sorted(root.glob("*.safetensors"))
         if not self.files:
-            raise FileNotFoundError(f"no *.safetensors files under {path}")
-        self._fds: dict[Path, int] = {}
-        self._meta: dict[str, TensorInfo] = {}
-        for f in self.files:
-            fd = os.open(f, os.O_RDONLY)
-            self._fds[f] = fd
-            head = os.pread(fd, 8, 0)
-            if len(head) != 8:
-                raise OSError(f"{f}: truncated safetensors header")
-            (hlen,) = struct.unpack("<Q", head)
-            table = json.loads(os.pread(fd, hlen, 8))
-            base = 8 + hlen
-            for name, info in table.items():
-                if name == "__metadata__":
-                    continue
-                lo, hi = info["data_offsets"]
-                self._meta[name] = TensorInfo(f, _DTYPES[info["dtype"]], tuple(info["shape"]),
-                                              base + lo, hi - lo)
+            raise FileNotFoundError(f"{root} holds no *.safetensors shard")
+        self._index: dict[str, TensorInfo] = {}
+        for shard in self.files:
+            for key, meta in _parse_shard(shard).items():
+                if key in self._index:
+                    raise ValueError(f"tensor {key} appears in {self._index[key].path.name} "
+                                     f"and {shard.name}")
+                self._index[key] = meta
+        self._open: dict[Path, int] = {}
+        self._open_lock = threading.Lock()
+
+    def _fd(self, shard: Path) -> int:
+        fd = self._open.get(shard)
+        if fd is None:
+            with self._open_lock:
+                fd = self._open.get(shard)
+                if fd is None:
+                    fd = self._open[shard] = os.open(shard, os.O_RDONLY)
+        return fd
 
     def close(self) -> None:
-        for fd in self._fds.values():
-            os.close(fd)
-        self._fds.clear()
+        with self._open_lock:
+            for fd in self._open.values():
+                os.close(fd)
+            self._open.clear()
 
     def __del__(self) -> None:
         try:
@@ -104,18 +143,18 @@ class Checkpoint:
             pass
 
     def has(self, name: str) -> bool:
-        return name in self._meta
+        return name in self._index
 
     def names(self) -> list[str]:
-        return sorted(self._meta)
+        return sorted(self._index)
 
     def info(self, name: str) -> TensorInfo:
-        return self._meta[name]
+        return self._index[name]
 
     def read_into(self, name: str, buf: torch.Tensor) -> torch.Tensor:
         """Read the raw bytes of `name` into the front of the uint8 CPU tensor `buf` (pinned or
         not); returns the filled `[nbytes]` view. Safe from many threads."""
-        meta = self._meta[name]
+        meta = self._index[name]
         if buf.dtype != torch.uint8 or buf.device.type != "cpu" or not buf.is_contiguous():
             raise ValueError("buf must be a contiguous uint8 CPU tensor")
         if buf.numel() < meta.nbytes:
@@ -123,7 +162,7 @@ class Checkpoint:
         view = memoryview(buf.numpy()).cast("B")
         got = 0
         while got < meta.nbytes:
-            n = os.preadv(self._fds[meta.path], [view[got:meta.nbytes]], meta.offset + got)
+            n = os.preadv(self._fd(meta.path), [view[got:meta.nbytes]], meta.offset + got)
             if n <= 0:
                 raise OSError(f"short read for {name}")
             got += n
@@ -132,7 +171,7 @@ class Checkpoint:
     def load(self, name: str, device: str | torch.device,
              dtype: torch.dtype | None = None) -> torch.Tensor:
         """Read one tensor onto `device`, cast to `dtype` unless None. Safe from many threads."""
-        meta = self._meta[name]
+        meta = self._index[name]
         device = torch.device(device)
         pin = device.type == "cuda"
         raw = torch.empty(meta.nbytes, dtype=torch.uint8, pin_memory=pin)

@@ -107,3 +107,24 @@ def test_rejected_arguments_launch_nothing(lib):
                                None, None, None) == -1
     assert lib.mtpk_delta_rule(fake, 1, None, 2, 2, 4, 2, 16, 16, fake, fake, fake, fake, fake,
                                None, fake, None) == -1  # 2 rows, 1 slot, no slot map
+
+
+def test_short_work_list_is_rejected(lib):
+    """A work list shorter than the unit bound would drop live assignments: prep, gate_up and
+    down refuse it before any launch (fake pointers are never dereferenced)."""
+    f = 0x1000
+    need = lib.mtpk_moe_max_units(1920, 512)
+    assert lib.mtpk_moe_prep(f, 2, f, 0, 1920, 0, 512, f, f, need - 1, f, None) == -1
+    assert lib.mtpk_moe_gate_up(f, 1, 192, 4096, f, f, 512, 1024, f, f, f, need - 1, 10, f, 2,
+                                1920, None) == -1
+    assert lib.mtpk_moe_down(f, 2, 1920, 1024, f, f, 512, 4096, f, f, f, need - 1, f, None) == -1
+
+
+def test_scale_scan_and_slot_arguments_checked(lib):
+    f = 0x1000
+    assert lib.mtpk_scale_scan(None, f, 16, f, None) == -1
+    assert lib.mtpk_scale_scan(f, f, -1, f, None) == -1
+    # DeltaNet prep / conv commit need a positive slot count
+    assert lib.mtpk_conv_commit(f, 1, f, 0, f, 300, f, 5, 300, 3, 4, None) == -1
+    assert lib.mtpk_deltanet_prep(f, 1, 1000, f, f, 0, f, f, f, 2, 4, 2, 16, 4, 16, 4, 1e-6, 0.25,
+                                  f, f, f, f, f, None) == -1

@@ -184,3 +184,47 @@ def test_conv_commit_matches_the_gather(dev, dtype) -> None:
     want[slots] = torch.gather(window, 2, idx[:, None, :].expand(-1, c, -1))
     deltanet.conv_commit(conv, slots, proj, idx, c)
     assert torch.equal(conv, want)  # untouched slots 1 and 4 included
+
+
+def test_out_of_range_slots_touch_no_state(dev) -> None:
+    """Rows whose slot id lies outside the pool: the delta rule gives zero outputs and leaves
+    every slot as it was (verify and commit), the commit's window update skips them, and the
+    prep reads a zero window for them; the in-range rows are unaffected."""
+    pool, slots, q, k, v, g, beta = _case(3, 5, 4, 2, 16, 16, 3, 4)
+    bad = np.array([slots[0], 5, -1], np.int64)  # row 0 valid, rows 1-2 outside [0, 5)
+    want_pool, want = dn.delta_rule_rows(pool, bad[:1], q[:1], k[:1], v[:1], g[:1], beta[:1])
+    tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, bad, q, k, v, g, beta)
+    out = deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb).cpu().numpy()
+    np.testing.assert_allclose(out[:1], want, rtol=RTOL, atol=ATOL)
+    assert not out[1:].any()
+    assert torch.equal(tp.cpu(), torch.from_numpy(pool))
+    lengths = torch.tensor([2, 4, 4], device=dev)
+    deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb, lengths, want_out=False)
+    want_pool, _ = dn.delta_rule_rows(pool, bad[:1], q[:1], k[:1], v[:1], g[:1], beta[:1], np.array([2]))
+    np.testing.assert_allclose(tp.cpu().numpy(), want_pool, rtol=RTOL, atol=ATOL)
+    others = [s for s in range(5) if s != bad[0]]
+    assert torch.equal(tp.cpu()[others], torch.from_numpy(pool)[others])
+
+    b, t, c, k1 = 3, 4, 96, 3
+    gen = torch.Generator(device="cpu").manual_seed(5)
+    proj = torch.randn(b, t, c + 8, generator=gen).to(dev)
+    conv = torch.randn(4, c, k1, generator=gen).to(dev)
+    sl = torch.tensor([2, 4, -3], device=dev)
+    idx = torch.full((b, k1), 1, device=dev) + torch.arange(k1, device=dev)
+    want_conv = conv.clone()
+    want_conv[2] = torch.cat([conv[2], proj[0, :, :c].T], -1)[:, 1 : 1 + k1]
+    deltanet.conv_commit(conv, sl, proj, idx, c)
+    assert torch.equal(conv, want_conv)
+
+    kh, kd, vh, vd = 1, 16, 2, 32
+    cc = 2 * kh * kd + vh * vd
+    proj = torch.randn(b, t, cc + vh * vd + 2 * vh, generator=gen).to(dev)
+    conv = torch.randn(4, cc, k1, generator=gen).to(dev)
+    w = (torch.randn(cc, k1 + 1, generator=gen) * 0.3).to(dev)
+    a_log, dt_bias = torch.rand(vh).to(dev), torch.rand(vh).to(dev)
+    got = deltanet.prep(proj, conv, sl, w, a_log, dt_bias, kh, kd, vh, vd)
+    zeroed = torch.cat([conv, torch.zeros(1, cc, k1, device=dev)])
+    sl_z = torch.tensor([2, 4, 4], device=dev)  # the two bad rows read slot 4: all zeros
+    want = _torch_prep(proj, zeroed, sl_z, w, a_log, dt_bias, kh, kd, vh, vd)
+    for x, y in zip(got, want, strict=True):
+        torch.testing.assert_close(x, y, rtol=1e-5, atol=1e-6)

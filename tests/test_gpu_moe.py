@@ -235,6 +235,47 @@ def test_real_dims_rel_l2(real_layer, tokens, seed):
     assert err64 <= 2e-3
 
 
+@pytest.mark.parametrize("tokens", [1, 192])
+def test_real_dims_edge_scale_blocks(real_layer, tokens):
+    """Live experts whose gate_up and down rows carry scale-0 (pinned +-0.0) and scale-1
+    (subnormal products) blocks, on the direct path (1 token) and the LDS unit path (192),
+    against the fp64 oracle with the kernels' scale convention and the fp32 device reference
+    (exact dequant). The payload is restored afterwards."""
+    dev = torch.device("cuda:0")
+    print(f"edge-scale MoE M={tokens}", flush=True)
+    a_e, a_w = zipf_routing(tokens, E, TOP_K, seed=tokens + 500, zero_frac=0.05)
+    used = torch.from_numpy(np.unique(a_e)).to(dev).long()
+    saved = {k: real_layer[k][used].clone() for k in ("gate_up_scale", "down_scale")}
+    try:
+        for k in saved:
+            s = real_layer[k][used]
+            flat = s.view(-1)
+            flat[0::7] = 0
+            flat[3::11] = 1
+            real_layer[k][used] = s
+        x = torch.randn(tokens, H, device=dev, generator=torch.Generator(dev).manual_seed(tokens)).to(torch.bfloat16)
+        ae, aw = torch.from_numpy(a_e).to(dev), torch.from_numpy(a_w).to(dev)
+        got = mxfp4_gemv.fused_moe(x, real_layer, (ae, aw), TOP_K, (0, E)).float()
+        ref_b = torch_fp32_reference(x, real_layer, ae.long(), aw, TOP_K).to(torch.bfloat16).float()
+        err = (torch.linalg.norm(got - ref_b) / torch.linalg.norm(ref_b)).item()
+        print(f"  rel-L2 vs fp32 reference = {err:.3e}", flush=True)
+        assert err <= 2e-3
+        pick = list(range(min(tokens, 2)))
+        sel = np.concatenate([np.arange(t * TOP_K, (t + 1) * TOP_K) for t in pick])
+        sub_ids = np.unique(a_e[sel])
+        sub = {k: v[torch.from_numpy(sub_ids).to(dev).long()].cpu().numpy() for k, v in real_layer.items()}
+        remap = {int(e): i for i, e in enumerate(sub_ids)}
+        sub_e = np.array([remap[int(e)] for e in a_e[sel]], np.int32)
+        want = bf16_round(moe_ref.reference_moe(x[pick].float().cpu().numpy(), sub, sub_e, a_w[sel],
+                                                TOP_K, (0, len(sub_ids)), kernel_scales=True))
+        err64 = moe_ref.rel_l2(got[pick].cpu().numpy(), want)
+        print(f"  rel-L2 vs fp64 oracle = {err64:.3e}", flush=True)
+        assert err64 <= 2e-3
+    finally:
+        for k, v in saved.items():
+            real_layer[k][used] = v
+
+
 def test_real_dims_repeat_is_bit_identical(real_layer):
     dev = torch.device("cuda:0")
     a_e, a_w = zipf_routing(192, E, TOP_K, seed=9, zero_frac=0.05)

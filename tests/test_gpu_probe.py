@@ -1,6 +1,6 @@
 """gfx950 building blocks against the oracle: the MFMA 16x16x32 bf16 lane layout the MoE
-kernels assume, and the MXFP4 decode (exact fp32 path over every byte and scale; the kernels'
-in-register hardware-convert path over every byte and scales 2..252)."""
+kernels assume, and the MXFP4 decode (exact fp32 path and the kernels' in-register
+hardware-convert path, each over every byte and every scale), and the load-time scale check."""
 
 import numpy as np
 import pytest
@@ -54,14 +54,53 @@ def test_exact_dequant_every_byte_every_scale(dev):
     assert np.array_equal(got[fin].view(np.uint32), want[fin].view(np.uint32))  # bits, incl. -0.0
 
 
-def test_in_kernel_decode_every_byte_scales_2_to_252(dev):
+def test_in_kernel_decode_every_byte_every_scale(dev):
+    """`decode8`, the decode every MoE kernel runs, against the pinned decode: bit for bit
+    (signed zeros included) at scale bytes 0..254, byte 0 giving +-0.0; at 255 (the OCP NaN
+    scale) the hardware convert gives NaN for every code, which `supports` refuses at load."""
     packed, scale = _all_bytes_all_scales()
     got = mxfp4.dequant_in_kernel(torch.from_numpy(packed).to(dev),
                                   torch.from_numpy(scale).to(dev)).cpu().numpy()
     want = mx.dequant_mxfp4_kernel(packed, scale)
-    rows = (scale[:, 0] >= 2) & (scale[:, 0] <= 252)
+    rows = scale[:, 0] <= 254
     g, w = got[rows], want[rows]
-    # bf16 holds every fp4 * 2^(s-127) exactly in this range; zeros compared by value
-    assert np.array_equal(g, w)
-    nz = w != 0
-    assert np.array_equal(np.signbit(g[nz]), np.signbit(w[nz]))
+    assert np.array_equal(np.isnan(g), np.isnan(w))
+    fin = ~np.isnan(w)
+    assert np.array_equal(g[fin].view(np.uint32), w[fin].view(np.uint32))
+    for s_byte in (0, 1, 253, 254):  # the edges named explicitly: +-0.0, subnormal, overflow
+        r = slice(16 * s_byte, 16 * s_byte + 16)
+        assert np.array_equal(got[r].view(np.uint32), want[r].view(np.uint32)), s_byte
+    assert np.isnan(got[16 * 255 :]).all()
+
+
+def _payload_with_scale(dev, byte, codes_zero):
+    rng = np.random.default_rng(byte)
+    E, H, I = 2, 64, 32
+    ex = {
+        "gate_up": rng.integers(0, 256, (E, 2 * I, H // 2), dtype=np.uint8),
+        "gate_up_scale": rng.integers(118, 123, (E, 2 * I, H // 32), dtype=np.uint8),
+        "down": rng.integers(0, 256, (E, H, I // 2), dtype=np.uint8),
+        "down_scale": rng.integers(118, 123, (E, H, I // 32), dtype=np.uint8),
+    }
+    ex["down_scale"][1, 5, 0] = byte
+    if codes_zero:
+        ex["down"][1, 5, :16] &= 0x88  # only signed zeros in that block
+    return {k: torch.from_numpy(v).to(dev) for k, v in ex.items()}
+
+
+def test_supports_refuses_scale_255_over_nonzero_codes(dev):
+    import mxfp4_gemv
+
+    x = torch.randn(3, 64, device=dev).to(torch.bfloat16)
+    routing = (torch.tensor([0, 1, 1, 0, 0, 1], dtype=torch.int32, device=dev),
+               torch.full((6,), 0.5, device=dev))
+    for byte, zero, ok in ((255, False, False), (255, True, True), (0, False, True), (1, False, True)):
+        ex = _payload_with_scale(dev, byte, zero)
+        assert mxfp4_gemv.bw_scales_ok(ex) is ok
+        assert mxfp4_gemv.supports(ex) is ok
+        if ok:
+            mxfp4_gemv.fused_moe(x, ex, routing, 2, (0, 2))
+        else:
+            with pytest.raises(ValueError, match="supports"):
+                mxfp4_gemv.fused_moe(x, ex, routing, 2, (0, 2))
+        del ex

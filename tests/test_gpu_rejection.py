@@ -170,3 +170,36 @@ def test_sample_rows_inverse_cdf(dev) -> None:
     lf = torch.from_numpy((g.standard_normal((rows, 5000)) * 50).astype(np.float32))  # no ties
     sharp = mtp.sample_rows(lf.to(dev), 1e-3, torch.from_numpy(u).to(dev)).cpu()
     assert torch.equal(sharp, lf.argmax(-1))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_masked_chunk_and_masked_draft_logit(dev, dtype) -> None:
+    """A whole 4096-logit chunk of -inf (and a ragged -inf tail), plus a -inf target logit on a
+    drafted token: margins stay finite, no masked token is drawn, and the decisions and draws
+    follow the oracle."""
+    b, k, vocab = 8, 3, 3 * 4096 + 500
+    tt, dd, tl64, dl64, drafts, ua, us = _case(b, k, vocab, dtype, 21)
+    masked = np.r_[4096:8192, vocab - 300 : vocab]
+    for ten in (tt, dd):
+        ten[..., torch.from_numpy(masked)] = -float("inf")
+    tl64, dl64 = tt.double().numpy(), dd.double().numpy()
+    g = np.random.default_rng(22)
+    drafts = rj.sample_drafts(dl64, g.random((b, k)), 0.7)
+    tt[2, 0, int(drafts[2, 0])] = -float("inf")  # lane 2's first draft has p = 0
+    tl64 = tt.double().numpy()
+    acc, tok, emitted = _check(dev, tt, dd, tl64, dl64, drafts, ua, us, 0.7)
+    assert acc[2] == 0
+    assert not np.isin(tok, masked).any()
+
+
+def test_sample_rows_masked_chunk(dev) -> None:
+    rows, vocab = 6, 3 * 4096
+    g = np.random.default_rng(23)
+    logits = (g.standard_normal((rows, vocab)) * 3).astype(np.float32)
+    logits[:, 4096:8192] = -np.inf
+    u = g.random(rows).astype(np.float32)
+    got = mtp.sample_rows(torch.from_numpy(logits).to(dev), 0.7, torch.from_numpy(u).to(dev)).cpu().numpy()
+    for r in range(rows):
+        p = rj.softmax_t(logits[r].astype(np.float64), 0.7)
+        assert _token_consistent(p, float(u[r]), int(got[r]))
+        assert not 4096 <= got[r] < 8192

@@ -76,3 +76,37 @@ def test_inverse_cdf():
     w = np.array([0.0, 1.0, 0.0, 3.0])
     assert [rj.sample_inverse_cdf(w, r) for r in (0.0, 0.24, 0.25, 0.99)] == [1, 1, 3, 3]
     assert list(itertools.islice((rj.sample_inverse_cdf(np.array([0, 0, 2.0]), 0.5),), 1)) == [2]
+
+
+def test_masked_logits_carry_no_mass():
+    """-inf logits (a masked stretch of the vocabulary) have probability 0: the oracle on the
+    full vocabulary equals the oracle on the vocabulary with the stretch cut out, tokens mapped
+    back; a draft token whose target logit is -inf is rejected; one whose draft logit is -inf
+    (q = 0) is accepted."""
+    rng = np.random.default_rng(4)
+    B, k, V, T = 6, 3, 40, 0.7
+    tl = rng.standard_normal((B, k + 1, V)) * 2
+    dl = tl[:, :k] + rng.standard_normal((B, k, V))
+    cut = np.arange(10, 22)
+    tl[:, :, cut] = -np.inf
+    dl[:, :, cut] = -np.inf
+    keep = np.setdiff1d(np.arange(V), cut)
+    drafts = rj.sample_drafts(dl, rng.random((B, k)), T)
+    assert not np.isin(drafts, cut).any()
+    ua, us = rng.random((B, k)), rng.random(B)
+    acc, tok, margin = rj.rejection_accept(tl, dl, drafts, ua, us, T)
+    remap = np.searchsorted(keep, drafts)
+    acc2, tok2, margin2 = rj.rejection_accept(tl[..., keep], dl[..., keep], remap, ua, us, T)
+    assert np.array_equal(acc, acc2) and np.array_equal(tok, keep[tok2])
+    assert np.allclose(margin, margin2)
+    assert not np.isin(tok, cut).any() and np.isfinite(margin).all()
+    # draft token 0 of lane 0: target logit -inf -> p = 0 -> rejected at position 0
+    t2 = tl.copy()
+    t2[0, 0, drafts[0, 0]] = -np.inf
+    acc3, _, m3 = rj.rejection_accept(t2, dl, drafts, ua, us, T)
+    assert acc3[0] == 0 and m3[0, 0] <= 0
+    # draft logit -inf on the drafted token of lane 1, position 0: q = 0 -> accepted there
+    d2 = dl.copy()
+    d2[1, 0, drafts[1, 0]] = -np.inf
+    _, _, m4 = rj.rejection_accept(tl, d2, drafts, ua, us, T)
+    assert m4[1, 0] > 0

@@ -126,13 +126,44 @@ def test_errors(tmp_path) -> None:
         weights.load_experts(ck, PREFIX, weights.Shard(0, E + 1), "cpu", torch.bfloat16)
 
 
-def test_truncated_shard_is_a_short_read(tmp_path) -> None:
-    save_file({"a": torch.arange(1000, dtype=torch.int64)}, str(tmp_path / "model-0.safetensors"))
+def test_truncated_shard(tmp_path) -> None:
+    """A data section shorter than the header's byte ranges is refused when the shard is
+    indexed; a shard cut after indexing gives a short read, not a partial tensor."""
     f = tmp_path / "model-0.safetensors"
-    f.write_bytes(f.read_bytes()[:-100])
+    save_file({"a": torch.arange(1000, dtype=torch.int64)}, str(f))
+    whole = f.read_bytes()
+    f.write_bytes(whole[:-100])
+    with pytest.raises(ValueError, match="byte range"):
+        weights.Checkpoint(tmp_path)
+    f.write_bytes(whole)
     ck = weights.Checkpoint(tmp_path)
+    f.write_bytes(whole[:-100])
     with pytest.raises(OSError, match="short read"):
         ck.load("a", "cpu")
+
+
+def test_header_checks(tmp_path) -> None:
+    """Sizes that disagree with shape x dtype, unknown dtypes and names present in two shards are
+    format errors."""
+    import json as _json
+
+    def shard(name, table, data):
+        head = _json.dumps(table).encode()
+        (tmp_path / name).write_bytes(len(head).to_bytes(8, "little") + head + data)
+
+    shard("a.safetensors", {"x": {"dtype": "F32", "shape": [3], "data_offsets": [0, 8]}}, bytes(12))
+    with pytest.raises(ValueError, match="byte range"):
+        weights.Checkpoint(tmp_path)
+    shard("a.safetensors", {"x": {"dtype": "Q9", "shape": [3], "data_offsets": [0, 12]}}, bytes(12))
+    with pytest.raises(ValueError, match="dtype"):
+        weights.Checkpoint(tmp_path)
+    shard("a.safetensors", {"x": {"dtype": "F32", "shape": [3], "data_offsets": [0, 12]},
+                            "__metadata__": {"format": "pt"}}, bytes(12))
+    ck = weights.Checkpoint(tmp_path)
+    assert ck.names() == ["x"] and ck.info("x").shape == (3,)
+    shard("b.safetensors", {"x": {"dtype": "F32", "shape": [1], "data_offsets": [0, 4]}}, bytes(4))
+    with pytest.raises(ValueError, match="appears in"):
+        weights.Checkpoint(tmp_path)
 
 
 @pytest.mark.gpu
