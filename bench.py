@@ -116,6 +116,8 @@ def main() -> int:
     ap.add_argument("--no-mtp", action="store_true", help="skip the MTP-round leg")
     ap.add_argument("--no-dense", action="store_true",
                     help="skip the bf16-expert leg (the real checkpoint's MTP-layer MoE)")
+    ap.add_argument("--no-stream", action="store_true",
+                    help="skip the streaming-read probe (the HBM read ceiling at the MoE byte counts)")
     ap.add_argument("--workloads", default="M1,M32,M192",
                     help="comma list of M1, M32, M192; `value` is measured on M192 when listed, "
                          "else on the last one listed")
@@ -243,6 +245,7 @@ def main() -> int:
     if not args.no_cpu and head == "M192":
         cpu = cpu_baseline(layers[0], ins[0], dls[0], args.cpu_seconds)
     direct = runner.direct
+    stream = None if args.no_stream else stream_bench(dev)
     del runner, ins, outs, layers
     torch.cuda.empty_cache()
     accept = None if args.no_accept else accept_bench(dev)
@@ -285,6 +288,7 @@ def main() -> int:
             "algorithmic_bytes": round(gu_bytes),
         },
         "cpu_baseline": cpu,
+        "stream": stream,
         "accept": accept,
         "dense_moe": dense_moe,
         "mtp_round": mtp_round,
@@ -328,6 +332,75 @@ def _time_calls(fn, reps):
     b.record()
     torch.cuda.synchronize()
     return a.elapsed_time(b) * 1e3 / reps  # us
+
+
+STREAM_SIZES = {
+    "M1_down": 10 * (2_097_152 + 131_072),
+    "M1_gate_up": 10 * GATE_UP_BYTES,
+    "M1_layer": 10 * EXPERT_BYTES,
+    "M32_layer": 134 * EXPERT_BYTES,
+    "M192_layer": 351 * EXPERT_BYTES,
+}
+
+
+def stream_bench(dev, calls=24, region_gib=6):
+    """The HBM read ceiling at the MoE's byte counts: `mtpk_probe_stream` (16-byte loads, no
+    stores) reads a window of each size per launch, successive launches taking successive
+    windows of a 6 GiB buffer, so no launch is served by the last-level cache; graph replay,
+    best over grids of 256..4096 workgroups and 8 or 16 loads in flight.
+    `M1_pair_us` chains a gate_up-sized and a down-sized read as two dependent launches, the
+    shape of the M = 1 layer."""
+    import torch
+
+    import _mtpk
+
+    lib = _mtpk.lib()
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+    st = lambda: _mtpk.stream_of(dev)  # noqa: E731
+    region = torch.zeros(region_gib << 30, dtype=torch.uint8, device=dev)
+    span = [(region.data_ptr(), region.numel())]
+
+    def windows(size):
+        out = []
+        for base, n in span:
+            off = 0
+            while off + size <= n:
+                out.append(base + off)
+                off += (size + 4095) // 4096 * 4096
+        return out
+
+    def launch(ptr, size, grid, u):
+        _mtpk.check(lib.mtpk_probe_stream(ptr, size, grid, u, sink.data_ptr(), st()), "mtpk_probe_stream")
+
+    res = {}
+    for name, size in STREAM_SIZES.items():
+        wins = windows(size)
+        best = None
+        for grid in (256, 512, 1024, 2048, 4096):
+            for u in (8, 16):
+                n = min(calls, len(wins))
+                us = _time_graph(lambda i, g=grid, u=u: launch(wins[i], size, g, u), n, n)
+                if best is None or us < best[0]:
+                    best = (us, grid, u)
+        us, grid, u = best
+        res[name] = {"bytes": size, "us": round(us, 2), "gbs": round(size / us / 1e3, 1),
+                     "grid": grid, "loads_in_flight": u}
+        log(f"stream {name}: {size / 1e6:.1f} MB in {us:.2f} us = {size / us / 1e3:.0f} GB/s "
+            f"(grid {grid}, {u} loads in flight)")
+    gu, dn = STREAM_SIZES["M1_gate_up"], STREAM_SIZES["M1_down"]
+    wg, wd = windows(gu), windows(dn)
+    cg, cd = res["M1_gate_up"], res["M1_down"]
+
+    def pair(i):
+        launch(wg[i], gu, cg["grid"], cg["loads_in_flight"])
+        launch(wd[-1 - i], dn, cd["grid"], cd["loads_in_flight"])
+
+    res["M1_pair_us"] = round(_time_graph(pair, min(calls, len(wg)), min(calls, len(wg))), 2)
+    log(f"stream: gate_up-sized then down-sized read, two dependent launches: {res['M1_pair_us']:.2f} us")
+    res["probe"] = "mtpk_probe_stream (16-byte buffer loads, grid-stride, no stores)"
+    del region
+    torch.cuda.empty_cache()
+    return res
 
 
 def accept_bench(dev, b=48, k=3, vocab=248320, temperature=0.7):

@@ -416,6 +416,14 @@ int mtpk_kv_write(const uint16_t* k, int64_t k_row_stride, const uint16_t* v, in
                   int64_t table_stride, const int64_t* base_pos, const uint8_t* keep, int64_t batch,
                   int64_t t, int64_t kv_heads, int64_t head_dim, void* stream);
 
+/* Streaming-read probe (no reference counterpart: a measurement of the HBM read ceiling the MoE
+ * weight streams are compared with). Reads bytes [0, bytes) of `base` with 16-byte loads,
+ * `loads_in_flight` (4, 8 or 16) per thread per iteration, over `grid` workgroups of 256
+ * threads; stores nothing (sink u32 [1024] is written only for a constant no input produces).
+ * bytes <= 4 GiB - 32. */
+int mtpk_probe_stream(const void* base, int64_t bytes, int grid, int loads_in_flight,
+                      uint32_t* sink, void* stream);
+
 /* ---------------------------------------------------------------- test probes
  * In-bounds probe of the compiler builtin this library's MoE relies on: one wave computes
  * d = A(16x32) * B(32x16) with v_mfma_f32_16x16x32_bf16 from per-lane operand registers

@@ -150,6 +150,7 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_void_p],
     ),
     "mtpk_probe_mfma_16x16x32": (c_int, [c_void_p, c_void_p, c_void_p, c_void_p]),
+    "mtpk_probe_stream": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]),
     "mtpk_delta_rule": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,

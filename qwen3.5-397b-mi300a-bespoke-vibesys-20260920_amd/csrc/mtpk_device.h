@@ -103,7 +103,7 @@ __device__ inline void ring_fence() { __builtin_amdgcn_sched_barrier(0); }
 // range, so the subnormal products of byte 1 and the overflow to +-inf at 253..254 come out as
 // in fp32; checked bit for bit on the GPU). Byte 255, the OCP NaN scale, gives NaN for every
 // code, where the pinned decode gives +-inf for nonzero codes: experts holding such a block
-// are refused at load (`mtpk_scales_ok`).
+// are refused at load (`mtpk_scale_scan`).
 struct BlockScale {
   float f;
   uint32_t keep;
