@@ -623,10 +623,21 @@ def cpu_baseline(layer, inp, dl_full, budget_s):
             break
     us_layer = total_t / total_d * dl_full * 1e6
     log(f"cpu baseline: {rows} rows, {total_d} expert dequants in {total_t:.1f}s on {threads} threads")
+    model = "unknown"
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
     return {
         "value": round(total_bytes / total_t / 1e9, 3),
         "unit": "GB/s",
         "cores": threads,
+        "threads": threads,
+        "cpu_count": os.cpu_count(),
+        "cpu_model": model,
         "kind": "port",
         "sample": f"first {rows} of 192 rows in groups of 8 ({total_d} expert dequants, "
                   f"{total_t:.1f} s); torch fp32 restatement of Model._routed_grouped",
