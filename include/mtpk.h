@@ -20,6 +20,7 @@ extern "C" {
 #define MTPK_OK 0
 #define MTPK_EINVAL (-1) /* argument outside the contract: shape, dtype, alignment, null */
 #define MTPK_ENODEV (-2) /* no usable HIP device */
+#define MTPK_ETOOBIG (-3) /* the call needs more scratch than the library's static buffer holds */
 
 /* Element type codes used by the dtype arguments. */
 #define MTPK_F32 0
@@ -188,6 +189,25 @@ int mtpk_fused_moe_shared(const void* x, int x_dtype, int64_t tokens, int64_t hi
                           const void* shared, int shared_dtype, const void* shared_gate,
                           int gate_dtype, int64_t gate_stride, void* workspace,
                           int64_t workspace_bytes, void* out, void* stream);
+
+/* `mtpk_fused_moe_shared` without a workspace argument: its scratch (work list, intermediate
+ * planes, y) is the library's own file-scope device buffer of MTPK_MOE_STATIC_SCRATCH bytes, one
+ * per GPU, held until the process ends. Nothing is allocated, so the call suits code that cannot
+ * call hipMalloc (HIP graph capture, serving loops, harnesses that forbid allocation). No
+ * counterpart in the reference: it exists for those callers. A call whose
+ * mtpk_moe_workspace_bytes(...) exceeds the buffer returns MTPK_ETOOBIG and launches nothing
+ * (bf16 activations at H = 4096, I = 1024, top-10 of 512 fit up to 256 tokens). Every call on a
+ * GPU shares that GPU's buffer, which keeps the last call's contents (no call needs it cleared):
+ * calls that overlap on one GPU (different streams or host threads) race. The other arguments
+ * and the result are those of mtpk_fused_moe_shared. */
+#define MTPK_MOE_STATIC_SCRATCH (64LL << 20)
+int mtpk_fused_moe_static(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                          const uint8_t* gate_up, const uint8_t* gate_up_scale, const uint8_t* down,
+                          const uint8_t* down_scale, int64_t local_experts, int64_t inter_dim,
+                          const void* a_expert, int expert_dtype, const void* a_weight,
+                          int weight_dtype, int top_k, int expert_lo, int expert_hi,
+                          const void* shared, int shared_dtype, const void* shared_gate,
+                          int gate_dtype, int64_t gate_stride, void* out, void* stream);
 
 /* ---------------------------------------------------------------- router top-k
  * Replaces `router_fused.route` / `_fused_route_kernel` (router_fused.py:56-151) and the torch

@@ -18,7 +18,8 @@ LIB_PATH = Path(os.environ.get("MTPK_LIB", str(HERE / "libmtpk.so")))
 """The in-tree build; `MTPK_LIB` points the binding at another build of the same sources."""
 
 F32, BF16, I32, I64, U8 = 0, 1, 2, 3, 4
-EINVAL, ENODEV = -1, -2
+EINVAL, ENODEV, ETOOBIG = -1, -2, -3
+MOE_STATIC_SCRATCH = 64 << 20
 ABI_VERSION = 1
 MAX_TOP_K = 32
 MAX_EXPERTS = 4096
@@ -30,6 +31,12 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
     "mtpk_abi_version": (c_int, []),
     "mtpk_dequant_mxfp4": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_int, c_void_p, c_void_p]),
     "mtpk_scale_scan": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "mtpk_fused_moe_static": (
+        c_int,
+        [c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+         c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int, c_void_p, c_int,
+         c_int64, c_void_p, c_void_p],
+    ),
     "mtpk_moe_max_units": (c_int64, [c_int64, c_int64]),
     "mtpk_moe_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int]),
     "mtpk_moe_prep": (
@@ -199,7 +206,7 @@ def check(status: int, what: str) -> None:
     """Raise on a nonzero status; the message names the entry point and the cause."""
     if status != 0:
         text = lib().mtpk_status_string(status).decode()
-        if status == EINVAL:
+        if status in (EINVAL, ETOOBIG):
             raise ValueError(f"{what}: {text}")
         raise RuntimeError(f"{what}: {text} (status {status})")
 

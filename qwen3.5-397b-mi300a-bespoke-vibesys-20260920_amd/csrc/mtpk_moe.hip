@@ -15,6 +15,8 @@
 // The weight stream is the only HBM-sized traffic; nothing dequantised is ever stored.
 // Lane mapping and K coverage of one MFMA tile: see mtpk_common.h ("MoE lane mapping").
 
+#include <mutex>
+
 #include "mtpk_device.h"
 #include "mtpk_host.h"
 
@@ -1821,6 +1823,72 @@ int mtpk_fused_moe_shared(const void* x, int x_dtype, int64_t tokens, int64_t hi
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
                      expert_hi, out, x_dtype, st);
   return status_of(hipGetLastError());
+}
+
+}  // extern "C"
+
+// The static scratch of mtpk_fused_moe_static. In host code `g_moe_scratch` names a host-side
+// stand-in, not device memory: its device address comes from hipGetSymbolAddress, taken once per
+// device (with that device current) on the entry point's first call there, and only that address
+// is ever passed to a kernel.
+static __device__ __align__(256) uint8_t g_moe_scratch[MTPK_MOE_STATIC_SCRATCH];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::once_flag g_scratch_once[kScratchDevices];
+void* g_scratch_ptr[kScratchDevices];
+hipError_t g_scratch_err[kScratchDevices];
+
+// Device address of this device's g_moe_scratch, or null with *err set.
+void* moe_scratch_of_current_device(int* err) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) {
+    *err = status_of(e);
+    return nullptr;
+  }
+  if (dev < 0 || dev >= kScratchDevices) {
+    *err = MTPK_ENODEV;
+    return nullptr;
+  }
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(g_moe_scratch));
+    g_scratch_ptr[dev] = g_scratch_err[dev] == hipSuccess ? p : nullptr;
+  });
+  if (!g_scratch_ptr[dev]) {
+    *err = g_scratch_err[dev] != hipSuccess ? status_of(g_scratch_err[dev]) : MTPK_ENODEV;
+    return nullptr;
+  }
+  return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+extern "C" {
+
+int mtpk_fused_moe_static(const void* x, int x_dtype, int64_t tokens, int64_t hidden,
+                          const uint8_t* gate_up, const uint8_t* gate_up_scale, const uint8_t* down,
+                          const uint8_t* down_scale, int64_t local_experts, int64_t inter_dim,
+                          const void* a_expert, int expert_dtype, const void* a_weight,
+                          int weight_dtype, int top_k, int expert_lo, int expert_hi,
+                          const void* shared, int shared_dtype, const void* shared_gate,
+                          int gate_dtype, int64_t gate_stride, void* out, void* stream) {
+  if (tokens < 0 || top_k <= 0 || top_k > MTPK_MAX_TOP_K || local_experts <= 0 || inter_dim <= 0 ||
+      hidden <= 0 || !dtype_float_ok(x_dtype))
+    return MTPK_EINVAL;
+  const int64_t need =
+      mtpk_moe_workspace_bytes(tokens, top_k, local_experts, inter_dim, hidden, x_dtype);
+  if (need > MTPK_MOE_STATIC_SCRATCH) return MTPK_ETOOBIG;
+  int err = 0;
+  void* scratch = moe_scratch_of_current_device(&err);
+  if (!scratch) return err;
+  return mtpk_fused_moe_shared(x, x_dtype, tokens, hidden, gate_up, gate_up_scale, down, down_scale,
+                               local_experts, inter_dim, a_expert, expert_dtype, a_weight,
+                               weight_dtype, top_k, expert_lo, expert_hi, shared, shared_dtype,
+                               shared_gate, gate_dtype, gate_stride, scratch,
+                               MTPK_MOE_STATIC_SCRATCH, out, stream);
 }
 
 int mtpk_dequant_mxfp4(const uint8_t* packed, const uint8_t* scale, int64_t rows, int64_t k,

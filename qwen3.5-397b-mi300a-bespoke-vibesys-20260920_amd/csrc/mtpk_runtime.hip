@@ -33,6 +33,8 @@ const char* mtpk_status_string(int status) {
   if (status == MTPK_OK) return "success";
   if (status == MTPK_EINVAL) return "mtpk: invalid argument (shape, dtype, alignment or null pointer)";
   if (status == MTPK_ENODEV) return "mtpk: no usable HIP device";
+  if (status == MTPK_ETOOBIG)
+    return "mtpk: the call needs more scratch than the static buffer holds (MTPK_MOE_STATIC_SCRATCH)";
   if (status > 0) return hipGetErrorString((hipError_t)status);
   return "mtpk: unknown status";
 }
