@@ -215,6 +215,18 @@ def ptr(t: torch.Tensor | None) -> int | None:
     return None if t is None else t.data_ptr()
 
 
+def row_stride(x: torch.Tensor) -> int | None:
+    """Element stride between consecutive rows of `x` `[B, t, ...]` read as `B * t` rows, or
+    None when the two leading dims do not collapse to one stride. A size-1 dim's stride is
+    arbitrary (views and reshapes set it freely), so it neither sets nor checks the stride."""
+    b, t = x.shape[0], x.shape[1]
+    if t == 1:
+        return x.stride(0)
+    if b > 1 and x.stride(0) != t * x.stride(1):
+        return None
+    return x.stride(1)
+
+
 def stream_of(device: torch.device) -> int:
     """Handle of torch's current stream on `device` (what the kernels launch on)."""
     return torch.cuda.current_stream(device).cuda_stream

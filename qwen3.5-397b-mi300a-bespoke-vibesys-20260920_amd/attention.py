@@ -159,7 +159,7 @@ def kv_write(k_pool: torch.Tensor, v_pool: torch.Tensor, k: torch.Tensor, v: tor
     b, t, kvh, hd = k.shape
     for name, x in (("k", k), ("v", v)):
         if x.dtype != torch.bfloat16 or x.shape != (b, t, kvh, hd) or x.stride(3) != 1 or x.stride(2) != hd \
-                or x.stride(0) != t * x.stride(1):
+                or _mtpk.row_stride(x) is None:
             raise ValueError(f"{name} must be bf16 [B, t, kv_heads, hd] with contiguous rows")
     if k_pool.shape[1:] != (kvh, hd) or v_pool.shape[1:] != (kvh, hd, BLOCK):
         raise ValueError("pools do not match the rows' kv_heads / head_dim")
@@ -171,6 +171,6 @@ def kv_write(k_pool: torch.Tensor, v_pool: torch.Tensor, k: torch.Tensor, v: tor
         if kp.numel() != b * t:
             raise ValueError("keep must have B * t entries")
     _mtpk.check(_mtpk.lib().mtpk_kv_write(
-        k.data_ptr(), k.stride(1), v.data_ptr(), v.stride(1), k_pool.data_ptr(), v_pool.data_ptr(),
+        k.data_ptr(), _mtpk.row_stride(k), v.data_ptr(), _mtpk.row_stride(v), k_pool.data_ptr(), v_pool.data_ptr(),
         k_pool.shape[0], table.data_ptr(), table.shape[1], pos.data_ptr(), _mtpk.ptr(kp), b, t, kvh,
         hd, _mtpk.stream_of(device)), "mtpk_kv_write")  # fmt: skip

@@ -79,7 +79,8 @@ def prep(proj: torch.Tensor, conv_state: torch.Tensor, slots: torch.Tensor, conv
     `[B, t, v_heads, v_dim]`, `g`, `beta` `[B, t, v_heads]`."""
     device = _mtpk.require_device(proj, conv_state, slots, conv_w, a_log, dt_bias)
     b, t, width = proj.shape
-    if proj.stride(2) != 1 or proj.stride(0) != t * proj.stride(1):
+    rs = _mtpk.row_stride(proj)
+    if proj.stride(2) != 1 or rs is None:
         raise ValueError("proj must be [B, t, P] with contiguous rows")
     dt = proj.dtype
     for name, ten in (("conv_state", conv_state), ("conv_w", conv_w)):
@@ -95,7 +96,7 @@ def prep(proj: torch.Tensor, conv_state: torch.Tensor, slots: torch.Tensor, conv
     beta = torch.empty(b, t, v_heads, **f32)
     sl = slots.to(torch.int64).contiguous()
     _mtpk.check(_mtpk.lib().mtpk_deltanet_prep(
-        proj.data_ptr(), _mtpk.float_code(dt), proj.stride(1), conv_state.data_ptr(), sl.data_ptr(),
+        proj.data_ptr(), _mtpk.float_code(dt), rs, conv_state.data_ptr(), sl.data_ptr(),
         conv_state.shape[0], conv_w.data_ptr(), a_log.data_ptr(), dt_bias.data_ptr(), b, t, k_heads, k_dim, v_heads, v_dim,
         conv_w.shape[1], float(eps), float(k_dim) ** -0.5, q.data_ptr(), k.data_ptr(), v.data_ptr(),
         g.data_ptr(), beta.data_ptr(), _mtpk.stream_of(device)), "mtpk_deltanet_prep")  # fmt: skip
@@ -109,7 +110,8 @@ def conv_commit(conv_state: torch.Tensor, slots: torch.Tensor, proj: torch.Tenso
     (`mtpk_conv_commit`)."""
     device = _mtpk.require_device(conv_state, slots, proj, idx)
     b, t, _ = proj.shape
-    if proj.stride(2) != 1 or proj.stride(0) != t * proj.stride(1):
+    rs = _mtpk.row_stride(proj)
+    if proj.stride(2) != 1 or rs is None:
         raise ValueError("proj must be [B, t, P] with contiguous rows")
     if proj.dtype != conv_state.dtype or not conv_state.is_contiguous():
         raise ValueError("conv_state must be contiguous and of proj's dtype")
@@ -121,5 +123,5 @@ def conv_commit(conv_state: torch.Tensor, slots: torch.Tensor, proj: torch.Tenso
     _mtpk.check(_mtpk.lib().mtpk_conv_commit(
         conv_state.data_ptr(), _mtpk.float_code(conv_state.dtype), sl.data_ptr(), conv_state.shape[0],
         proj.data_ptr(),
-        proj.stride(1), ix.data_ptr(), b, channels, k1, t, _mtpk.stream_of(device)),
+        rs, ix.data_ptr(), b, channels, k1, t, _mtpk.stream_of(device)),
         "mtpk_conv_commit")  # fmt: skip

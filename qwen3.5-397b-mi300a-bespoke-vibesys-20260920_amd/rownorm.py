@@ -31,9 +31,12 @@ def _layout(x: torch.Tensor, heads: bool) -> tuple[int, int, int, int]:
         lead = x.shape[:-2]
         strides = x.stride()[:-2]
         hpt, hs = x.shape[-2], x.stride(-2)
-    ts = strides[-1] if strides else hpt * hs
-    for i in range(len(lead) - 1):
-        if lead[i + 1] != 1 and strides[i] != strides[i + 1] * lead[i + 1]:
+    # A size-1 dim's stride is arbitrary (views and reshapes set it freely), so only the dims
+    # of size > 1 set and check the token stride.
+    kept = [(n, s) for n, s in zip(lead, strides, strict=True) if n != 1]
+    ts = kept[-1][1] if kept else hpt * hs
+    for (_, s_outer), (n_inner, s_inner) in zip(kept, kept[1:]):
+        if s_outer != s_inner * n_inner:
             raise ValueError("leading dims of the input do not collapse to one token stride")
     tokens = 1
     for n in lead:

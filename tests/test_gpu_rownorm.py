@@ -70,9 +70,11 @@ def test_head_slices_with_rope(dev, dtype, heads, hd, rot):
     close(rownorm.rmsnorm(q, w, 1e-6, heads=True), ref_rms(q, w, 1e-6), dtype)
 
 
-def test_gated_norm_and_l2(dev):
-    """DeltaNet's output norm (gate read from a slice of the input projection) and q/k L2."""
-    b, t, vh, vd = 4, 4, 64, 128
+@pytest.mark.parametrize("t", [4, 1])
+def test_gated_norm_and_l2(dev, t):
+    """DeltaNet's output norm (gate read from a slice of the input projection) and q/k L2. At
+    t = 1 the gate view's size-1 dim has a stride other than the row pitch."""
+    b, vh, vd = 4, 64, 128
     g = torch.Generator(dev).manual_seed(9)
     x = torch.randn(b, t, vh, vd, device=dev, generator=g)
     proj = torch.randn(b, t, 3 * vh * vd, device=dev, generator=g).to(torch.bfloat16)
