@@ -11,6 +11,7 @@ small torch ops of `verify_round_step` (`graph_mtp.py:541-580`) and `LaneTables.
 
 from __future__ import annotations
 
+from collections.abc import Callable
 from dataclasses import dataclass
 
 import torch
@@ -48,14 +49,17 @@ def _commit_limit(accept: torch.Tensor, step_argmax: torch.Tensor, budget: torch
 
 
 class MTPVerifyBuffers:
-    """One bucket's static tensors for the verify + accept + rollback step
-    (`graph_mtp.py:141-178`): written before each replay (`token_matrix`, `pos`, `active`,
-    `block_table`, `write_rows`, `slot_rows`, `budget`, `stops`), read after it
-    (`step_argmax`, `accept_len` and the rollback indices below)."""
+    """One bucket's static tensors for the draft + verify + accept + rollback step
+    (`graph_mtp.py:141-178`, same constructor): written before each replay (`token_matrix`,
+    `pos`, `active`, `block_table`, `write_rows`, `slot_rows`, `budget`, `stops`, `forced_n`,
+    `forced_ids`), read after it (`step_argmax`, `accept_len` and the rollback indices below).
+    Row `j` is the round's `j`-th lane, `slot_rows[j]` its slot. The sizes come from `model`:
+    its hidden width, dtype, block-table width and DeltaNet conv window."""
 
-    def __init__(self, capacity: int, t: int, hidden: int, max_blocks_per_lane: int,
-                 device: torch.device, dtype: torch.dtype = torch.bfloat16,
-                 conv_k1: int = 3) -> None:
+    def __init__(self, model, capacity: int, t: int, device: torch.device) -> None:
+        hidden, dtype = model.cfg.hidden, model.dtype
+        max_blocks_per_lane = model.blocks.max_blocks
+        conv_k1 = model.cfg.conv_k - 1
         self.capacity, self.t, self.conv_k1 = capacity, t, conv_k1
         long = dict(dtype=torch.long, device=device)
         self.token_matrix = torch.zeros(capacity, t, **long)
@@ -82,6 +86,10 @@ class MTPVerifyBuffers:
         self.budget_left = torch.zeros(capacity, **long)
         self.live = torch.zeros(capacity, dtype=torch.bool, device=device)
         self.hidden_src = torch.zeros(capacity, **long)
+        # forced feed: row j's first forced_n[j] drafts are forced_ids[j] and are accepted
+        # unconditionally (zero on every other row)
+        self.forced_n = torch.zeros(capacity, **long)
+        self.forced_ids = torch.zeros(capacity, max(t - 1, 1), **long)
 
 
 @dataclass
@@ -181,11 +189,11 @@ def kv_write_rows(pos: torch.Tensor, block_table: torch.Tensor, t: int, block_si
 # ---------------------------------------------------------------- the device round
 
 
-def draft_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int,
-                     forced: torch.Tensor | None = None, forced_n: torch.Tensor | None = None) -> None:
-    """`m.k` MTP draft steps for the first `b` lanes of `buf`, drafts written into
-    `buf.token_matrix[:, 1:]` (`graph_mtp.py:477-504`). Device-only, no host read. A lane with
-    `forced_n[j] > 0` feeds (and keeps) its forced tokens instead of its first drafts."""
+def _draft_rows(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int,
+                forced: torch.Tensor | None = None, forced_n: torch.Tensor | None = None) -> None:
+    """`m.k` MTP draft steps for the first `b` rows of `buf` (lanes `lanes`), drafts written
+    into `buf.token_matrix[:, 1:]`. Device-only, no host read. A row with `forced_n[j] > 0`
+    feeds (and keeps) its forced tokens instead of its first drafts."""
     hid = mtp_mod.draft_seed(model, model.hidden_cache[lanes])
     tok = buf.token_matrix[:b, :1]
     table = model.blocks.table[lanes]
@@ -199,11 +207,12 @@ def draft_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: in
         buf.token_matrix[:b, s + 1] = tok[:, 0]
 
 
-def verify_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int, ctx_len: int,
-                      forced_n: torch.Tensor | None = None) -> None:
+def _verify_rows(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int, ctx_len: int,
+                 forced_n: torch.Tensor | None = None) -> None:
     """Verify forward over `buf.token_matrix[:b]`, argmax, acceptance with every rollback
     index (`mtpk_greedy_accept`), then the commit of DeltaNet state, MTP cache rows and the
-    cached hidden seed to each lane's accepted length (`graph_mtp.py:513-582`). Device-only."""
+    cached hidden seed to each lane's accepted length. Device-only. Rows with
+    `forced_n[j] > 0` accept their forced drafts unconditionally."""
     t = buf.t
     dev = buf.pos.device
     pos = buf.pos[:b]
@@ -222,13 +231,18 @@ def verify_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: i
     if forced_n is not None:
         # A forced lane commits its forced tokens plus one target token; stop ids and the
         # budget do not apply to forced tokens (`graph_verify_wide.py:196-200`).
-        a = torch.where(forced_n > 0, forced_n, out.accept_len)
-        out.accept_len.copy_(a)
-        out.lengths.copy_(torch.where(buf.active[:b], a + 1, torch.ones_like(a)))
-        out.keep.copy_(buf.active[:b, None] & (torch.arange(t, device=dev)[None, :] <= a[:, None]))
-        out.hidden_src.copy_(torch.arange(b, device=dev) * t + a)
+        # Rows without forced feed keep the acceptance launch's outputs as they are.
+        f = (forced_n > 0) & buf.active[:b]
+        a = forced_n
+        length = a + 1
         win = torch.arange(buf.conv_k1, device=dev)
-        out.conv_idx.copy_(torch.clamp(out.lengths[:, None] + win[None, :], max=buf.conv_k1 + t - 1))
+        keep = torch.arange(t, device=dev)[None, :] <= a[:, None]
+        conv = torch.clamp(length[:, None] + win[None, :], max=buf.conv_k1 + t - 1)
+        out.accept_len.copy_(torch.where(f, a, out.accept_len))
+        out.lengths.copy_(torch.where(f, length, out.lengths))
+        out.keep.copy_(torch.where(f[:, None], keep, out.keep))
+        out.hidden_src.copy_(torch.where(f, torch.arange(b, device=dev) * t + a, out.hidden_src))
+        out.conv_idx.copy_(torch.where(f[:, None], conv, out.conv_idx))
     model.commit(res, lanes, out.lengths, conv_idx=out.conv_idx)
     grid = pos[:, None] + torch.arange(t, device=dev)[None, :]
     raw_seed = model.hidden_cache[lanes]
@@ -242,106 +256,160 @@ def verify_round_step(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: i
     model.hidden_cache[lanes] = res.hidden.reshape(b * t, -1)[out.hidden_src]
 
 
+def _ctx_bound(model) -> int:
+    """Context length every captured round is sized for: the block tables' full capacity, so
+    the attention's key splits do not depend on a round's positions."""
+    return model.blocks.max_blocks * model.cfg.block_size
+
+
+def draft_round_step(model, mtp, buf: MTPVerifyBuffers, t: int) -> Callable[[], None]:
+    """The draft step to capture (`graph_mtp.py:477-504`, same arguments): `t - 1` MTP steps
+    over every row of `buf`, seeded from each row's lane (`slot_rows`) and base token
+    (`token_matrix[:, 0]`), each step's greedy token written into `token_matrix[:, 1 + step]`;
+    rows with `forced_n > 0` feed and keep `forced_ids` instead."""
+    if t != buf.t or t != mtp.k + 1:
+        raise ValueError(f"t={t} does not match the buffers ({buf.t}) and the MTP head (k={mtp.k})")
+
+    def step() -> None:
+        _draft_rows(model, mtp, buf, buf.slot_rows, buf.capacity, buf.forced_ids, buf.forced_n)
+
+    return step
+
+
+build_draft_step = draft_round_step
+"""The reference's alias for the draft entry point (`graph_mtp.py:507-510`)."""
+
+
+def verify_round_step(model, mtp, buf: MTPVerifyBuffers, t: int) -> Callable[[], None]:
+    """The verify step to capture (`graph_mtp.py:513-582`, same arguments): one forward over
+    every row of `buf`, the argmax, commit-limited acceptance with every rollback index, and the
+    commit of DeltaNet state, MTP cache rows and the hidden seed to each row's accepted length."""
+    if t != buf.t:
+        raise ValueError(f"t={t} does not match the buffers ({buf.t})")
+    ctx = _ctx_bound(model)
+
+    def step() -> None:
+        _verify_rows(model, mtp, buf, buf.slot_rows, buf.capacity, ctx, buf.forced_n)
+
+    return step
+
+
+def _fill(model, mtp, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stops, forced) -> None:
+    """Write one round's inputs into `buf` (`MTPVerifyRunner.fill`, `graph_mtp.py:790-870`):
+    every row is a real lane (a bucket is sized to its round), so no row is padding."""
+    b, t, k = len(slots), buf.t, buf.t - 1
+    if b != buf.capacity or len(set(slots)) != b:
+        raise ValueError(f"need {buf.capacity} distinct slots, got {slots}")
+    if stops is not None and any(len(s) > mtp_mod.MAX_STOP_IDS for s in stops):
+        raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
+    for s, p in zip(slots, positions, strict=True):
+        model.blocks.grow(s, p + t)
+    big = 1 << 40
+    rows = []
+    for j, (tk, p) in enumerate(zip(tokens, positions, strict=True)):
+        ids = list(forced[j])[:k] if forced else []
+        st = list(stops[j]) if stops else []
+        rows.append([tk, p, big if budgets is None else budgets[j], int(slots[j]), len(ids),
+                     *(ids + [0] * (max(k, 1) - len(ids))), *(st + [-1] * (mtp_mod.MAX_STOP_IDS - len(st)))])
+    host = torch.tensor(rows, dtype=torch.long).to(buf.pos.device)
+    buf.token_matrix[:, 0] = host[:, 0]
+    buf.pos.copy_(host[:, 1])
+    buf.budget.copy_(host[:, 2])
+    buf.slot_rows.copy_(host[:, 3])
+    buf.forced_n.copy_(host[:, 4])
+    buf.forced_ids.copy_(host[:, 5 : 5 + max(k, 1)])
+    buf.stops.copy_(host[:, 5 + max(k, 1) :])
+    buf.active.fill_(True)
+
+
+def _committed(buf: MTPVerifyBuffers) -> list[list[int]]:
+    """The round's committed ids, `step_argmax[j, : accept + 1]`: one host read."""
+    rows = torch.cat([buf.step_argmax, buf.accept_len[:, None]], dim=1).tolist()
+    return [row[: row[-1] + 1] for row in rows]
+
+
 class MTPVerifyRunner:
-    """Device speculative rounds over static buffers (`graph_mtp.MTPVerifyRunner`,
-    `graph_mtp.py:893-918`): fill, draft, verify + accept + commit, one host read."""
+    """Eager speculative rounds over static per-batch-size buffers (`graph_mtp.MTPVerifyRunner`,
+    `graph_mtp.py:893-918`): fill, draft, verify + accept + commit, one host read. `capacity`
+    (default: every lane of the model) bounds the batch size."""
 
-    def __init__(self, model, capacity: int) -> None:
-        if model.mtp is None:
+    def __init__(self, model, mtp=None, capacity: int | None = None) -> None:
+        mtp = model.mtp if mtp is None else mtp
+        if mtp is None:
             raise ValueError("model has no MTP layer")
-        self.model, self.mtp = model, model.mtp
-        self.t = self.mtp.k + 1
-        c = model.cfg
-        self.buf = MTPVerifyBuffers(capacity, self.t, c.hidden, model.blocks.max_blocks, model.device,
-                                    model.dtype, conv_k1=c.conv_k - 1)
-        self.capacity = capacity
+        self.model, self.mtp = model, mtp
+        self.t = mtp.k + 1
+        self.capacity = model.lanes if capacity is None else capacity
+        self.bufs: dict[int, MTPVerifyBuffers] = {}
 
-    def fill(self, slots, tokens, positions, budgets, stops, forced):
-        buf, b, t = self.buf, len(slots), self.t
-        if not 1 <= b <= self.capacity or len(set(slots)) != b:
-            raise ValueError(f"need 1..{self.capacity} distinct slots, got {slots}")
-        if stops is not None and any(len(s) > mtp_mod.MAX_STOP_IDS for s in stops):
-            raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
-        for s, p in zip(slots, positions, strict=True):
-            self.model.blocks.grow(s, p + t)
-        dev = buf.pos.device
-        big = 1 << 40
-        host = torch.tensor([[tk, p, big if budgets is None else budgets[j]]
-                             for j, (tk, p) in enumerate(zip(tokens, positions, strict=True))], dtype=torch.long)
-        host = host.to(dev)
-        buf.token_matrix[:b, 0] = host[:, 0]
-        buf.pos[:b] = host[:, 1]
-        buf.budget[:b] = host[:, 2]
-        buf.active[:b] = True
-        st = torch.full((b, mtp_mod.MAX_STOP_IDS), -1, dtype=torch.long)
-        for j, ids in enumerate(stops or []):
-            st[j, : len(ids)] = torch.tensor(list(ids), dtype=torch.long)
-        buf.stops[:b] = st.to(dev)
-        if not forced or not any(forced):
-            return None, None
-        k = self.mtp.k
-        ft = torch.zeros(b, k, dtype=torch.long)
-        fn = torch.zeros(b, dtype=torch.long)
-        for j, ids in enumerate(forced):
-            ids = list(ids)[:k]
-            fn[j] = len(ids)
-            ft[j, : len(ids)] = torch.tensor(ids, dtype=torch.long)
-        return ft.to(dev), fn.to(dev)
+    def buffers(self, b: int) -> MTPVerifyBuffers:
+        if not 1 <= b <= self.capacity:
+            raise ValueError(f"batch of {b} lanes: this runner takes 1..{self.capacity}")
+        if b not in self.bufs:
+            self.bufs[b] = MTPVerifyBuffers(self.model, b, self.t, self.model.device)
+        return self.bufs[b]
 
     def speculative_decode(self, slots: list[int], tokens: list[int], positions: list[int],
                            budgets=None, stops=None, forced=None) -> list[list[int]]:
-        """Each slot's committed ids for one round (`Model.speculative_decode`'s contract)."""
-        b = len(slots)
-        ft, fn = self.fill(slots, tokens, positions, budgets, stops, forced)
-        lanes = self.model.lane_index(slots)
-        draft_round_step(self.model, self.mtp, self.buf, lanes, b, ft, fn)
-        verify_round_step(self.model, self.mtp, self.buf, lanes, b, max(positions) + self.t, fn)
-        rows = torch.cat([self.buf.step_argmax[:b], self.buf.accept_len[:b, None]], dim=1).tolist()
-        return [row[: row[-1] + 1] for row in rows]
+        """Each slot's committed ids for one round (`Model.speculative_decode`'s contract);
+        `forced` rows commit their forced drafts plus one target token."""
+        buf = self.buffers(len(slots))
+        _fill(self.model, self.mtp, buf, slots, tokens, positions, budgets, stops, forced)
+        draft_round_step(self.model, self.mtp, buf, self.t)()
+        verify_round_step(self.model, self.mtp, buf, self.t)()
+        return _committed(buf)
 
 
 class GraphMTPRunner(MTPVerifyRunner):
     """`MTPVerifyRunner` with each batch size's draft and verify steps captured in one HIP graph
-    (`GraphMTPRunner`, `graph_mtp.py:1062-1120`). A round writes the static buffers (`fill`),
-    replays the graph and reads the committed ids once. The first round of a batch size runs
-    eagerly on the capture stream (its result is that round's) and is then captured; rounds
-    with forced drafts run eagerly. The attention key splits are sized for the block tables'
-    full capacity, so one graph serves every context length."""
+    (`GraphMTPRunner(model, backend=None)`, `graph_mtp.py:1062-1120`). A round writes the
+    bucket's static buffers, replays its graph and reads the committed ids once; forced feed
+    rides in the buffers, so forced rounds replay the same graph. The first round of a batch size
+    runs eagerly on the capture stream (its result is that round's) and is then captured.
 
-    def __init__(self, model, capacity: int) -> None:
-        super().__init__(model, capacity)
-        self.slots = torch.zeros(capacity, dtype=torch.long, device=model.device)
-        self.ctx_bound = model.blocks.max_blocks * model.cfg.block_size
+    `backend` is the reference's capture-backend slot: HIP graphs through `torch.cuda.CUDAGraph`
+    are the only backend here, so it must be None. `capacity` (keyword) bounds the batch size."""
+
+    def __init__(self, model, backend=None, *, capacity: int | None = None) -> None:
+        if backend is not None:
+            raise ValueError("GraphMTPRunner captures HIP graphs only; backend must be None")
+        super().__init__(model, None, capacity)
         self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
-    def _round(self, b: int) -> None:
-        lanes = self.slots[:b]
-        draft_round_step(self.model, self.mtp, self.buf, lanes, b)
-        verify_round_step(self.model, self.mtp, self.buf, lanes, b, self.ctx_bound)
+    def prepare(self) -> bool:
+        """The reference's boot hook (`graph_mtp.py:1077-1081`): graphs are captured on each
+        batch size's first round instead, so there is nothing to do up front."""
+        return True
+
+    def forced_drafts(self) -> bool:
+        """Whether rounds may carry forced feed (`graph_mtp.py:1116-1118`): always."""
+        return True
+
+    def _round(self, buf: MTPVerifyBuffers) -> None:
+        draft_round_step(self.model, self.mtp, buf, self.t)()
+        verify_round_step(self.model, self.mtp, buf, self.t)()
 
     def speculative_decode(self, slots: list[int], tokens: list[int], positions: list[int],
                            budgets=None, stops=None, forced=None) -> list[list[int]]:
-        if forced and any(forced):
-            return super().speculative_decode(slots, tokens, positions, budgets, stops, forced)
         b = len(slots)
-        self.fill(slots, tokens, positions, budgets, stops, None)
-        self.slots[:b] = torch.tensor(list(slots), dtype=torch.long).to(self.slots.device)
+        buf = self.buffers(b)
+        _fill(self.model, self.mtp, buf, slots, tokens, positions, budgets, stops, forced)
         graph = self.graphs.get(b)
         if graph is None:
-            side = torch.cuda.Stream(self.slots.device)
+            dev = buf.pos.device
+            side = torch.cuda.Stream(dev)
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
-                self._round(b)  # this round, run eagerly; also warms the allocator
+                self._round(buf)  # this round, run eagerly; also warms the allocator
             torch.cuda.current_stream().wait_stream(side)
-            torch.cuda.synchronize(self.slots.device)
+            torch.cuda.synchronize(dev)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                self._round(b)
+                self._round(buf)
             self.graphs[b] = graph
         else:
             graph.replay()
-        rows = torch.cat([self.buf.step_argmax[:b], self.buf.accept_len[:b, None]], dim=1).tolist()
-        return [row[: row[-1] + 1] for row in rows]
+        return _committed(buf)
 
 
 # ---------------------------------------------------------------- sampling-mode acceptance

@@ -43,24 +43,76 @@ def forced_drafts(truth: list[int], accept: int, k: int, vocab: int) -> list[int
     return d
 
 
+def slot_state(model: vm.Model, lane: int, length: int) -> list[torch.Tensor]:
+    """Everything a round commits for slot `lane`, as CPU copies: attention K/V rows of
+    positions < `length` per attention layer, DeltaNet conv and recurrent state per DeltaNet
+    layer, the MTP layer's K/V rows of positions < `length`, and the cached hidden state."""
+    lanes = torch.tensor([lane], device=model.device)
+    pos = torch.arange(length, device=model.device)[None, :]
+    rows = model.blocks.physical_rows(lanes, pos).reshape(-1)
+    out = []
+    for ty, pool in zip(model.cfg.layer_types, model.pool, strict=True):
+        if ty == vm.ATTN:  # V is kept transposed per block
+            out += [pool["k"][rows], attention.read_v(pool["v"], rows)]
+        else:
+            out += [pool["conv"][lane], pool["rec"][lane]]
+    out += [model.mtp.pool["k"][rows], attention.read_v(model.mtp.pool["v"], rows)]
+    out.append(model.cached_hidden(lane))
+    return [x.float().cpu() for x in out]
+
+
 def assert_slot_state_close(a: vm.Model, b: vm.Model, lane: int, length: int,
                             rtol: float = 1e-5, atol: float = 1e-6) -> None:
     """DeltaNet conv/recurrent state, attention and MTP K/V of positions < `length`, and the
     cached hidden state of slot `lane` agree between two models."""
-    lanes = torch.tensor([lane], device=a.device)
-    pos = torch.arange(length, device=a.device)[None, :]
-    rows_a = a.blocks.physical_rows(lanes, pos).reshape(-1)
-    rows_b = b.blocks.physical_rows(lanes.to(b.device), pos.to(b.device)).reshape(-1)
-    def kv(pool, rows):  # K rows and V rows (V is kept transposed per block)
-        return pool["k"][rows], attention.read_v(pool["v"], rows)
+    for ta, tb in zip(slot_state(a, lane, length), slot_state(b, lane, length), strict=True):
+        torch.testing.assert_close(ta, tb, rtol=rtol, atol=atol)
 
-    for ty, pa, pb in zip(a.cfg.layer_types, a.pool, b.pool, strict=True):
+
+def snapshot(model: vm.Model) -> list[torch.Tensor]:
+    """Device copies of every tensor a round writes (layer pools, MTP pool, hidden seeds)."""
+    live = [t for pool in model.pool for t in pool.values()]
+    live += list(model.mtp.pool.values()) + [model.hidden_cache]
+    return [t.clone() for t in live]
+
+
+def restore(model: vm.Model, snap: list[torch.Tensor]) -> None:
+    live = [t for pool in model.pool for t in pool.values()]
+    live += list(model.mtp.pool.values()) + [model.hidden_cache]
+    for t, s in zip(live, snap, strict=True):
+        t.copy_(s)
+
+
+def c5_model(dev, b: int = 48, k: int = 3, ctx: int = 8192):
+    """The config-5 round the benchmark times: real layer dimensions (3 DeltaNet + 1 gated GQA +
+    the MTP layer, 512 MXFP4 experts top-10), `b` lanes, each holding `ctx - 32` positions of
+    seeded random context (K/V, DeltaNet state, hidden seeds). Returns (model, tokens, positions)."""
+    model = vm.Model(vm.verify_cfg(), dev, torch.bfloat16, lanes=b, max_seq=ctx + 64, seed=0,
+                     expert_mode="bytes", moe_rows=b * (k + 1))
+    mtp.attach(model, k=k, seed=1, expert_mode="bytes")
+    start = ctx - 32
+    for lane in range(b):
+        model.blocks.grow(lane, start)
+    g = torch.Generator(device=dev).manual_seed(3)
+    for ty, pool in zip(model.cfg.layer_types, model.pool, strict=True):
         if ty == vm.ATTN:
-            for ta, tb in zip(kv(pa, rows_a), kv(pb, rows_b), strict=True):
-                torch.testing.assert_close(ta.cpu(), tb.cpu(), rtol=rtol, atol=atol)
+            pool["k"].normal_(generator=g)
+            pool["v"].normal_(generator=g)
         else:
-            for name in ("conv", "rec"):
-                torch.testing.assert_close(pa[name][lane].cpu(), pb[name][lane].cpu(), rtol=rtol, atol=atol)
-    for ta, tb in zip(kv(a.mtp.pool, rows_a), kv(b.mtp.pool, rows_b), strict=True):
-        torch.testing.assert_close(ta.cpu(), tb.cpu(), rtol=rtol, atol=atol)
-    torch.testing.assert_close(a.cached_hidden(lane).cpu(), b.cached_hidden(lane).cpu(), rtol=rtol, atol=atol)
+            pool["conv"].normal_(generator=g)
+            pool["rec"].normal_(0, 0.05, generator=g)
+    model.mtp.pool["k"].normal_(generator=g)
+    model.mtp.pool["v"].normal_(generator=g)
+    model.hidden_cache.normal_(generator=g)
+    toks = torch.randint(0, model.cfg.vocab, (b,), generator=torch.Generator().manual_seed(4)).tolist()
+    return model, toks, [start] * b
+
+
+def shape_model(hidden: int, max_blocks: int, conv_k: int = 4, dtype=None):
+    """The attributes `graph_mtp.MTPVerifyBuffers(model, ...)` reads from a model (hidden width,
+    dtype, block-table width, DeltaNet conv window), for tests of the acceptance tail alone."""
+    import types
+
+    return types.SimpleNamespace(cfg=types.SimpleNamespace(hidden=hidden, conv_k=conv_k),
+                                 dtype=dtype or torch.bfloat16,
+                                 blocks=types.SimpleNamespace(max_blocks=max_blocks))

@@ -10,6 +10,7 @@ import pytest
 import torch
 
 import graph_mtp
+from tests.model_helpers import shape_model
 import mtp
 from oracle import accept_ref as ar
 
@@ -167,7 +168,7 @@ def test_keys_path_limits(dev):
 
 
 def test_accept_round_writes_buffers(dev):
-    buf = graph_mtp.MTPVerifyBuffers(8, 4, 64, 4, dev)
+    buf = graph_mtp.MTPVerifyBuffers(shape_model(64, 4), 8, 4, dev)
     rng = np.random.default_rng(3)
     sa = rng.integers(0, 3, (8, 4))
     buf.token_matrix[:, 1:] = dev_long(np.where(rng.random((8, 3)) < 0.7, sa[:, :3], 9), dev)

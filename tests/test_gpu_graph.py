@@ -6,6 +6,7 @@ import pytest
 import torch
 
 import graph_mtp
+from tests.model_helpers import shape_model
 import mxfp4_gemv
 import router_fused
 from tests.moe_inputs import random_experts
@@ -21,7 +22,7 @@ def test_graph_replays_match_eager(dev):
     logits = torch.randn(T, E + 1, device=dev, generator=g).to(torch.bfloat16)
     runner = mxfp4_gemv.MoeLayerRunner(T, K, E, I, H, dev)
     out = torch.empty(T, H, dtype=torch.bfloat16, device=dev)
-    buf = graph_mtp.MTPVerifyBuffers(12, 4, H, 4, dev)
+    buf = graph_mtp.MTPVerifyBuffers(shape_model(H, 4), 12, 4, dev)
     buf.active[:10] = True
     buf.budget.fill_(9)
 
