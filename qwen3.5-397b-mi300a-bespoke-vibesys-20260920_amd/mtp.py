@@ -46,6 +46,16 @@ MTP_K = _read_mtp_k()
 """Draft tokens per round, validated at import (`mtp.py:96-111`)."""
 
 
+def _flag(name: str) -> bool:
+    return os.environ.get(name, "0") not in ("0", "", "false", "False")
+
+
+def mtp_enabled() -> bool:
+    """Whether speculative decoding is on: `SEED_MTP_SERVE=1` or its older alias `SEED_MTP=1`
+    (`mtp.py:57-61`). Read when called, so a process (or a test) can set it after import."""
+    return _flag("SEED_MTP_SERVE") or _flag("SEED_MTP")
+
+
 def greedy_accept_length(draft_tokens: list[int], step_argmax: list[int]) -> int:
     """Longest prefix of `draft_tokens` equal to the target's own greedy prediction at that
     step (`step_argmax[i]` predicts `draft_tokens[i]`)."""
@@ -164,6 +174,74 @@ def attach(model, k: int | None = None, seed: int = 1, expert_mode: str = "quant
     )
     model.mtp = m
     return m
+
+
+def load(ck, full_cfg, tp, dev, dtype: torch.dtype, max_batch: int, kv_rows: int) -> MTP | None:
+    """The checkpoint's MTP module (`mtp.py:131-190`, same arguments), or None when the flag is
+    off or the checkpoint has no `mtp.fc.weight`.
+
+    `ck` is a `weights.Checkpoint`, `full_cfg` the model's `Cfg`, `dev` / `dtype` where and as
+    what the dense tensors land (MXFP4 expert payloads stay uint8). The decoder layer's tensors
+    are stored under the keys a target layer uses: the router rows and the shared expert's gate
+    row concatenated into `router_gate`, its gate and up projections into `shared_gate_up`. The
+    K pool is `[kv_rows, kv_heads, head_dim]` and the V pool the same rows transposed per block,
+    `[kv_rows / block_size, kv_heads, head_dim, block_size]`, indexed by the target's block
+    tables. This build runs on one GPU: `tp` is None or a plan of world size 1. `max_batch`
+    sizes no scratch here (the kernels take their workspaces per call); it is checked only."""
+    import weights as wt
+
+    if not mtp_enabled() or not ck.has("mtp.fc.weight"):
+        return None
+    if tp is not None and getattr(tp, "world", 1) != 1:
+        raise ValueError("this build loads the MTP layer for one GPU (tp world size 1)")
+    c = full_cfg
+    if max_batch < 1:
+        raise ValueError(f"max_batch must be positive, got {max_batch}")
+    if kv_rows <= 0 or kv_rows % c.block_size:
+        raise ValueError(f"kv_rows must be a positive multiple of the block size {c.block_size}")
+    dev = torch.device(dev)
+    qd, kd = c.heads * c.head_dim, c.kv_heads * c.head_dim
+
+    def read(name: str, shape: tuple[int, ...]) -> torch.Tensor:
+        t = ck.load(f"mtp.{name}", dev, dtype)
+        if tuple(t.shape) != shape:
+            raise ValueError(f"mtp.{name}: shape {tuple(t.shape)}, the config needs {shape}")
+        return t
+
+    h, si = c.hidden, c.shared_inter
+    at = "layers.0.self_attn"
+    mlp = "layers.0.mlp"
+    w = {
+        "in_norm": read("layers.0.input_layernorm.weight", (h,)),
+        "post_norm": read("layers.0.post_attention_layernorm.weight", (h,)),
+        "q_proj": read(f"{at}.q_proj.weight", (2 * qd, h)),  # per head: q rows, then gate rows
+        "k_proj": read(f"{at}.k_proj.weight", (kd, h)),
+        "v_proj": read(f"{at}.v_proj.weight", (kd, h)),
+        "o_proj": read(f"{at}.o_proj.weight", (h, qd)),
+        "q_norm": read(f"{at}.q_norm.weight", (c.head_dim,)),
+        "k_norm": read(f"{at}.k_norm.weight", (c.head_dim,)),
+        "router_gate": torch.cat([read(f"{mlp}.gate.weight", (c.experts, h)),
+                                  read(f"{mlp}.shared_expert_gate.weight", (1, h))]),
+        "shared_gate_up": torch.cat([read(f"{mlp}.shared_expert.gate_proj.weight", (si, h)),
+                                     read(f"{mlp}.shared_expert.up_proj.weight", (si, h))]),
+        "shared_down": read(f"{mlp}.shared_expert.down_proj.weight", (h, si)),
+        "experts": wt.load_experts(ck, f"mtp.{mlp}", wt.Shard(0, c.experts), dev, dtype),
+    }
+    gu = w["experts"]["gate_up"]
+    if gu.shape[:2] != (c.experts, 2 * c.inter) or w["experts"]["down"].shape[:2] != (c.experts, h):
+        raise ValueError(f"mtp experts: gate_up {tuple(gu.shape)}, down "
+                         f"{tuple(w['experts']['down'].shape)} do not match the config")
+    return MTP(
+        k=MTP_K,
+        weights=w,
+        fc=read("fc.weight", (h, 2 * h)),
+        pre_fc_norm_embedding=read("pre_fc_norm_embedding.weight", (h,)),
+        pre_fc_norm_hidden=read("pre_fc_norm_hidden.weight", (h,)),
+        norm=read("norm.weight", (h,)),
+        pool={"k": torch.zeros(kv_rows, c.kv_heads, c.head_dim, dtype=dtype, device=dev),
+              "v": torch.zeros(kv_rows // c.block_size, c.kv_heads, c.head_dim, c.block_size,
+                               dtype=dtype, device=dev)},
+    )
 
 
 def draft_seed(model, raw_hidden: torch.Tensor) -> torch.Tensor:
