@@ -137,6 +137,13 @@ def _validate(x, experts, routing, top_k):
                          "nonzero code, which the in-register decode cannot reproduce")
 
 
+_SHARED_WS: dict[tuple[torch.device, int], torch.Tensor] = {}
+"""Grow-only workspace per (device, stream) for calls whose `inter` cannot hold the kernels'
+scratch (the reference's `[max_batch * top_k, intermediate]` buffer is smaller than the
+intermediate planes plus the fp32 partials). Calls on one stream run in order, so they share it;
+a call under graph capture allocates its own instead, which the graph keeps."""
+
+
 def _workspace(device: torch.device, nbytes: int, scratch: torch.Tensor | None) -> torch.Tensor:
     if (
         scratch is not None
@@ -146,7 +153,16 @@ def _workspace(device: torch.device, nbytes: int, scratch: torch.Tensor | None) 
         and scratch.data_ptr() % 256 == 0
     ):
         return scratch
-    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    if torch.cuda.is_current_stream_capturing():
+        # a captured call owns its scratch (allocated once, from the graph's pool)
+        return torch.empty(nbytes, dtype=torch.uint8, device=device)
+    key = (device, _mtpk.stream_of(device))
+    ws = _SHARED_WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        # 1 MiB granules, so a slowly growing batch does not reallocate on every call
+        ws = torch.empty(-(-max(nbytes, 1) // (1 << 20)) << 20, dtype=torch.uint8, device=device)
+        _SHARED_WS[key] = ws
+    return ws
 
 
 def fused_moe(
@@ -172,8 +188,10 @@ def fused_moe(
     `bw_combine_glue` `mxfp4_gemv.py:2266-2312`), with the unfused ops' rounding points.
 
     `inter` is optional caller scratch: used as the kernels' workspace when it is at least
-    `workspace_bytes(...)` bytes, contiguous and 256-byte aligned (the reference sizes it
-    `[max_batch * top_k, intermediate]`; pass `moe_scratch(...)` for a reusable one).
+    `workspace_bytes(...)` bytes, contiguous and 256-byte aligned (`moe_scratch(...)` makes one).
+    A smaller one, such as the reference's `[max_batch * top_k, intermediate]`, or none, takes a
+    grow-only workspace kept per (device, stream): no allocation once it has reached the
+    largest size used. Under graph capture the call allocates its own, once, for the graph.
     `order`, `grouped` and `total_experts` are accepted for signature compatibility: the work
     list groups assignments by expert at every width, so there is nothing for them to select.
     """
