@@ -574,6 +574,29 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
     ms = wall * 1e3 / rounds
     log(f"mtp round: {ms:.2f} ms/round, {committed / rounds:.1f} committed/round, "
         f"{committed / wall:.0f} tok/s")
+
+    # Forced full acceptance: every lane feeds k forced drafts and commits k + 1 tokens per
+    # round (the reference's forced-draft leg), through the same captured graph.
+    gen = torch.Generator().manual_seed(6)
+    forced = [torch.randint(0, model.cfg.vocab, (k,), generator=gen).tolist() for _ in range(b)]
+
+    def forced_round():
+        got = runner.speculative_decode(list(range(b)), toks, pos, forced=forced)
+        n = 0
+        for j, c in enumerate(got):
+            pos[j] += len(c)
+            toks[j] = c[-1]
+            n += len(c)
+        return n
+
+    forced_round()
+    torch.cuda.synchronize()
+    f0 = time.perf_counter()
+    f_committed = sum(forced_round() for _ in range(rounds))
+    torch.cuda.synchronize()
+    f_wall = time.perf_counter() - f0
+    log(f"mtp round, forced full acceptance: {f_wall * 1e3 / rounds:.2f} ms/round, "
+        f"{f_committed / rounds:.1f} committed/round, {f_committed / f_wall:.0f} tok/s")
     res = {
         "workload": f"C5 reduced-depth verify: 3 DeltaNet + 1 gated GQA (32q/2kv, hd 256) + MTP layer, "
                     f"MXFP4 MoE 512 x top-10 per layer, B={b}, k={k}, {ctx}-token paged context",
@@ -583,6 +606,11 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
         "rounds": rounds,
         "weights": "random init (draft acceptance near zero)",
         "runner": "GraphMTPRunner (draft + verify + accept + commit replayed as one HIP graph)",
+        "forced_full_accept": {
+            "ms_per_round": round(f_wall * 1e3 / rounds, 3),
+            "committed_per_round": round(f_committed / rounds, 2),
+            "accepted_tok_s": round(f_committed / f_wall, 1),
+        },
     }
     del runner, model
     torch.cuda.empty_cache()
