@@ -1,67 +1,125 @@
 // Fused router for gfx950: softmax over the expert logits, top-k, renormalise. One wave per
-// token row; the row's logits live in registers (PER per lane), the k selection rounds are
-// 64-bit wave max reductions over (logit, index) keys.
+// token row; the row's logits live in registers (PER per lane, expert e at lane e % 64, slot
+// e / 64).
 //
 // Selection ranks by logit: softmax is strictly increasing in it, so this is the probability
 // order of the exact softmax, with equal logits broken by the lower index (first occurrence).
-// Weights follow the reference arithmetic (router_fused.py:85-107): p = exp(l - max) / sum,
-// then each selected p divided by the sum of the selected ones, accumulated in selection order.
+// Each lane keeps the best of its free slots (the lowest slot among equal logits, i.e. its lowest
+// index); a round takes the wave maximum of those keys with DPP (row shifts, then the row
+// broadcasts: no LDS round trips), finds the lanes holding it with one ballot and, on a tie
+// between lanes, the lowest index with a second DPP reduction; only the winning lane rescans its
+// slots. Weights: the reference's p = exp(l - max) / sum, each selected p divided by the sum of
+// the selected ones (router_fused.py:85-107), computed as exp(l - max) over the selected
+// exp(l - max) accumulated in selection order (the softmax denominator cancels; the result
+// differs from the two-division form by rounding only).
 
 #include "mtpk_device.h"
 #include "mtpk_host.h"
 
 namespace mtpk {
 
-template <int PER>
-__global__ __launch_bounds__(256) void k_route_topk(const void* __restrict__ routing, int rdt,
+// Wave-wide reductions to lane 63 by DPP (gfx9 row_shr 1, 2, 4, 8 inside each 16-lane row, then
+// row_bcast 15 into rows 1 and 3 and row_bcast 31 into rows 2 and 3), read back as a uniform
+// value. `id` is the operation's identity, taken by lanes whose DPP source lies outside the row.
+template <typename Op>
+__device__ inline uint32_t dpp_reduce(uint32_t v, uint32_t id, Op op) {
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, 0x111, 0xf, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, 0x112, 0xf, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, 0x114, 0xf, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, 0x118, 0xf, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, 0x142, 0xa, 0xf, false));
+  v = op(v, (uint32_t)__builtin_amdgcn_update_dpp((int)id, (int)v, 0x143, 0xc, 0xf, false));
+  return (uint32_t)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ inline uint32_t dpp_max_u32(uint32_t v) {
+  return dpp_reduce(v, 0u, [](uint32_t a, uint32_t b) { return a > b ? a : b; });
+}
+__device__ inline uint32_t dpp_min_u32(uint32_t v) {
+  return dpp_reduce(v, 0xffffffffu, [](uint32_t a, uint32_t b) { return a < b ? a : b; });
+}
+__device__ inline float dpp_max_f32(float v) {
+  return bits_f32(dpp_reduce(f32_bits(v), f32_bits(-INFINITY),
+                             [](uint32_t a, uint32_t b) { return f32_bits(fmaxf(bits_f32(a), bits_f32(b))); }));
+}
+
+template <int PER, bool BF16>
+__global__ __launch_bounds__(256) void k_route_topk(const void* __restrict__ routing,
                                                     int64_t stride, int tokens, int E, int top_k,
                                                     float* __restrict__ top_w,
                                                     void* __restrict__ top_i, int idt) {
   const int row = blockIdx.x * 4 + (threadIdx.x / kWave);
   const int lane = threadIdx.x & (kWave - 1);
-  if (row >= tokens) return;
-  float lg[PER], p[PER];
-  bool free_[PER];
+  if (row >= tokens) return;  // uniform over the wave: every DPP below runs with all lanes
+  // The row's E logits as one buffer: every lane issues its PER loads at once, and loads past E
+  // return zeros (they are not used) without a branch around them.
+  constexpr int elt = BF16 ? 2 : 4;
+  const rsrc_t r = make_rsrc(static_cast<const uint8_t*>(routing) + (int64_t)row * stride * elt,
+                             (uint32_t)(E * elt));
+  float lg[PER], e_[PER];
+  uint32_t key[PER];  // order key of a free slot (>= 1), 0 once taken or past E
+#pragma unroll
+  for (int j = 0; j < PER; ++j) {
+    const uint32_t off = (uint32_t)((lane + kWave * j) * elt);
+    lg[j] = BF16 ? bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0))
+                 : bits_f32(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+  }
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    const int e = lane + kWave * j;
-    lg[j] = e < E ? load_float(routing, rdt, (int64_t)row * stride + e) : -INFINITY;
-    free_[j] = e < E;
+    const bool in = lane + kWave * j < E;
+    lg[j] = in ? lg[j] : -INFINITY;
     m = fmaxf(m, lg[j]);
   }
-  m = wave_max(m);
-  float s = 0.f;
+  m = dpp_max_f32(m);
+  // The weights are e_i / sum of the selected e (e = exp(l - max)): the softmax's denominator
+  // cancels from p_i / sum p_sel, so it is never formed.
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
-    p[j] = free_[j] ? __expf(lg[j] - m) : 0.f;
-    s += p[j];
+    const bool in = lane + kWave * j < E;
+    e_[j] = in ? __expf(lg[j] - m) : 0.f;
+    // a key of 0 marks "no candidate"; only NaNs with every payload bit set map below 1
+    key[j] = in ? max(f32_order_key(lg[j]), 1u) : 0u;
   }
-  s = wave_sum(s);
-#pragma unroll
-  for (int j = 0; j < PER; ++j) p[j] = p[j] / s;
 
+  // this lane's best free slot: strictly larger keys only, so the lowest slot wins a tie
+  uint32_t bk = 0;
+  int bj = 0;
+  float bp = 0.f;
+  auto rescan = [&]() {
+    bk = 0;
+    bj = 0;
+    bp = 0.f;
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      if (key[j] > bk) {
+        bk = key[j];
+        bj = j;
+        bp = e_[j];
+      }
+  };
+  rescan();
   float my_w = 0.f, total = 0.f;
   int my_i = 0;
   for (int r = 0; r < top_k; ++r) {
-    uint64_t best = 0;
-#pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      const uint64_t key = free_[j] ? argmax_key(lg[j], (uint32_t)(lane + kWave * j)) : 0ull;
-      best = key > best ? key : best;
+    const uint32_t mk = dpp_max_u32(bk);
+    const uint64_t holders = __ballot(bk == mk);
+    int owner, sel;
+    if (__popcll(holders) == 1) {
+      owner = __ffsll((unsigned long long)holders) - 1;
+      sel = owner + kWave * __builtin_amdgcn_readlane(bj, owner);
+    } else {  // equal logits on several lanes: the lowest expert index
+      sel = (int)dpp_min_u32(bk == mk ? (uint32_t)(lane + kWave * bj) : 0xffffffffu);
+      owner = sel & (kWave - 1);
     }
-    best = wave_max_u64(best);
-    const int sel = (int)argmax_key_index(best);
-    const int owner = sel & (kWave - 1), slot = sel / kWave;
-    float ps = 0.f;
+    const float ps = bits_f32((uint32_t)__builtin_amdgcn_readlane((int)f32_bits(bp), owner));
+    if (lane == owner) {
+      const int slot = sel / kWave;
 #pragma unroll
-    for (int j = 0; j < PER; ++j) {
-      if (j == slot) {
-        ps = p[j];
-        if (lane == owner) free_[j] = false;
-      }
+      for (int j = 0; j < PER; ++j)
+        if (j == slot) key[j] = 0u;
+      rescan();
     }
-    ps = __shfl(ps, owner, kWave);
     total += ps;
     if (lane == r) {
       my_w = ps;
@@ -78,8 +136,12 @@ template <int PER>
 int launch_route(const void* routing, int rdt, int64_t tokens, int64_t stride, int E, int top_k,
                  float* top_w, void* top_i, int idt, hipStream_t st) {
   const unsigned grid = (unsigned)((tokens + 3) / 4);
-  hipLaunchKernelGGL(k_route_topk<PER>, dim3(grid), dim3(256), 0, st, routing, rdt, stride,
-                     (int)tokens, E, top_k, top_w, top_i, idt);
+  if (rdt == MTPK_BF16)
+    hipLaunchKernelGGL((k_route_topk<PER, true>), dim3(grid), dim3(256), 0, st, routing, stride,
+                       (int)tokens, E, top_k, top_w, top_i, idt);
+  else
+    hipLaunchKernelGGL((k_route_topk<PER, false>), dim3(grid), dim3(256), 0, st, routing, stride,
+                       (int)tokens, E, top_k, top_w, top_i, idt);
   return status_of(hipGetLastError());
 }
 
