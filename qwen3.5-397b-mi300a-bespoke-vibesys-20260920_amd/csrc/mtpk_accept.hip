@@ -67,15 +67,26 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
         bi = i0 + first;
       }
     };
-    const int64_t step = (int64_t)kArgmaxThreads * 8;
-    for (int64_t i = begin + (int64_t)tid * 8; i < end; i += kArgmaxLoads * step) {
-      u32x4_t v[kArgmaxLoads];
-#pragma unroll
-      for (int u = 0; u < kArgmaxLoads; ++u)
-        if (i + u * step + 8 <= end) v[u] = ld16(base + i + u * step);
+    // The chunk as one buffer, streamed kArgmaxLoads 16-byte slots per thread at a time and
+    // software-pipelined: the next group's loads are issued before the current group is
+    // scanned, so 2 kArgmaxLoads loads stay in flight. Slots past the chunk read zeros and are
+    // skipped by the index test.
+    constexpr int64_t step = (int64_t)kArgmaxThreads * 8;  // elements per slot over the workgroup
+    const int64_t n = end - begin;
+    const rsrc_t rr = make_rsrc(base + begin, (uint32_t)(n * 2));
+    const int64_t iters = (n + kArgmaxLoads * step - 1) / (kArgmaxLoads * step);
+    u32x4_t va[kArgmaxLoads], vb[kArgmaxLoads];
+    auto issue = [&](u32x4_t* v, int64_t it) {
 #pragma unroll
       for (int u = 0; u < kArgmaxLoads; ++u) {
-        const int64_t i0 = i + u * step;
+        const int64_t e = (it * kArgmaxLoads + u) * step + (int64_t)tid * 8;
+        v[u] = buf16(rr, e < n ? (uint32_t)(e * 2) : kOutOfRange);
+      }
+    };
+    auto scan = [&](const u32x4_t* v, int64_t it) {
+#pragma unroll
+      for (int u = 0; u < kArgmaxLoads; ++u) {
+        const int64_t i0 = begin + (it * kArgmaxLoads + u) * step + (int64_t)tid * 8;
         if (i0 + 8 <= end) {
           chunk8(v[u], i0);
         } else {
@@ -85,6 +96,14 @@ __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
           }
         }
       }
+    };
+    issue(va, 0);
+    for (int64_t it = 0; it < iters; it += 2) {
+      issue(vb, it + 1);
+      scan(va, it);
+      if (it + 1 >= iters) break;
+      issue(va, it + 2);
+      scan(vb, it + 1);
     }
     if (bi >= 0) {
       const uint64_t k = argmax_key(bv, (uint32_t)bi);
