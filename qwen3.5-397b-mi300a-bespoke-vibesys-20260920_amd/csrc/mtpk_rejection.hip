@@ -8,11 +8,12 @@
 // smallest index v with cumsum(w)[v] > r * sum(w), or the last positive index if rounding
 // leaves none.
 //
-// Four launches, all streaming the logits at HBM rate with 16-byte loads:
+// Three launches for rejection (four for plain sampling), streaming the logits with 16-byte loads:
 //   stats : (chunk, row) workgroups -> per-chunk (max, sum exp(z - max)) of z = logit / T
-//   decide: one workgroup per lane, a wave per verify row -> row softmax constants and
-//           margins; for rejection, the accept length (one wave per row when plain sampling)
-//   mass  : (chunk, item) workgroups -> per-chunk sums of the item's draw weights
+//   decide + mass: (chunk, lane) workgroups; each first makes its lane's decision (a wave per
+//           verify row -> row softmax constants, margins, the accept length and the draw), then
+//           sums its chunk's draw weights. Plain sampling: a wave per row for the row constants,
+//           then (chunk, row) workgroups for the mass
 //   pick  : one workgroup per item -> the chunk where the cumulative mass crosses r * total
 //           (one wave: scan and ballot over the chunk masses), then a block scan inside it;
 //           writes the token (and the emitted row)
@@ -135,19 +136,18 @@ __device__ inline float2 rs_row_stats(const float2* part, int64_t r, int nchunk)
   return make_float2(m, wave_sum(s));
 }
 
-// Rejection decision for lane b: one workgroup, its waves take the t verify rows in parallel
-// (row softmax constants and the margin p(x) - u q(x)), then the first negative margin is the
-// accept length.
+// Rejection decision for lane b by one workgroup of kDecideWaves waves: its waves take the t
+// verify rows in parallel (row softmax constants and the margin p(x) - u q(x)), then the first
+// negative margin is the accept length, and *s_item (LDS) the draw it leads to. Outputs are
+// written only where the pointers are non-null.
 constexpr int kDecideWaves = 4;
 constexpr int kMaxT = 64;
 
-__global__ __launch_bounds__(kWave * kDecideWaves) void k_rs_decide(
-    RsRows rr, const float2* __restrict__ part, int nchunk, int B, int k, float inv_t,
-    const int64_t* __restrict__ draft_tokens, const float* __restrict__ u_accept,
-    RsItem* __restrict__ items, int64_t* __restrict__ accept_len, float* __restrict__ margin) {
-  __shared__ float s_mg[kMaxT];
-  __shared__ float4 s_st[kMaxT];
-  const int b = blockIdx.x;
+__device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part, int nchunk, int B,
+                               int k, float inv_t, const int64_t* __restrict__ draft_tokens,
+                               const float* __restrict__ u_accept, int b, float* s_mg, float4* s_st,
+                               RsItem* s_item, RsItem* __restrict__ items,
+                               int64_t* __restrict__ accept_len, float* __restrict__ margin) {
   const int t = k + 1;
   const int wv = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int64_t n_target = (int64_t)B * t;
@@ -197,9 +197,11 @@ __global__ __launch_bounds__(kWave * kDecideWaves) void k_rs_decide(
     it.st = sa.y;
     it.mq = sa.z;
     it.sq = sa.w;
-    items[b] = it;
-    accept_len[b] = a;
+    *s_item = it;
+    if (items) items[b] = it;
+    if (accept_len) accept_len[b] = a;
   }
+  __syncthreads();
 }
 
 // Plain sampling: item r draws from target row r.
@@ -270,6 +272,45 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_mass(RsRows rr, const RsItem*
     const float2 a = red[0], b = red[1], d = red[2], e = red[3];
     mass[(int64_t)item * nchunk + c] =
         make_float2((a.x + b.x) + (d.x + e.x), (a.y + b.y) + (d.y + e.y));
+  }
+}
+
+// Rejection: the lane's decision and its draw's per-chunk mass in one launch, one workgroup per
+// (chunk, lane). Every chunk's workgroup makes the lane's decision itself (a few KB of chunk
+// partials and 2k logits, the same deterministic result in each), so no launch separates the
+// decision from the mass; the chunk-0 workgroup writes the decision's outputs.
+__global__ __launch_bounds__(kRsThreads) void k_rs_decide_mass(
+    RsRows rr, const float2* __restrict__ part, int nchunk, int B, int k, float inv_t,
+    const int64_t* __restrict__ draft_tokens, const float* __restrict__ u_accept,
+    RsItem* __restrict__ items, int64_t* __restrict__ accept_len, float* __restrict__ margin,
+    float2* __restrict__ mass) {
+  static_assert(kRsThreads == kWave * kDecideWaves, "one decision per workgroup");
+  __shared__ float s_mg[kMaxT];
+  __shared__ float4 s_st[kMaxT];
+  __shared__ RsItem s_item;
+  __shared__ float2 red[kRsThreads / kWave];
+  const int c = blockIdx.x, b = blockIdx.y;
+  const bool first = c == 0;
+  rs_decide_lane(rr, part, nchunk, B, k, inv_t, draft_tokens, u_accept, b, s_mg, s_st, &s_item,
+                 first ? items : nullptr, first ? accept_len : nullptr, first ? margin : nullptr);
+  const RsItem it = s_item;
+  float wr[kRsPerThread], wp[kRsPerThread];
+  rs_weights(rr, it, c, inv_t, wr, wp);
+  float sr = 0.f, sp = 0.f;
+#pragma unroll
+  for (int e = 0; e < kRsPerThread; ++e) {
+    sr += wr[e];
+    sp += wp[e];
+  }
+  sr = wave_sum(sr);
+  sp = wave_sum(sp);
+  const int tid = threadIdx.x;
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = make_float2(sr, sp);
+  __syncthreads();
+  if (tid == 0) {
+    const float2 a = red[0], b2 = red[1], d = red[2], e = red[3];
+    mass[(int64_t)b * nchunk + c] =
+        make_float2((a.x + b2.x) + (d.x + e.x), (a.y + b2.y) + (d.y + e.y));
   }
 }
 
@@ -432,11 +473,9 @@ int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int6
                      rr, batch * t, inv_t, part);
   int rc = status_of(hipGetLastError());
   if (rc) return rc;
-  hipLaunchKernelGGL(k_rs_decide, dim3((unsigned)batch), dim3(kWave * kDecideWaves), 0, st, rr, part, (int)nchunk,
-                     (int)batch, k, inv_t, draft_tokens, u_accept, items, accept_len, margin);
-  if ((rc = status_of(hipGetLastError()))) return rc;
-  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)batch),
-                     dim3(kRsThreads), 0, st, rr, items, (int)nchunk, inv_t, mass);
+  hipLaunchKernelGGL(k_rs_decide_mass, dim3((unsigned)nchunk, (unsigned)batch), dim3(kRsThreads), 0,
+                     st, rr, part, (int)nchunk, (int)batch, k, inv_t, draft_tokens, u_accept, items,
+                     accept_len, margin, mass);
   if ((rc = status_of(hipGetLastError()))) return rc;
   hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, items, mass,
                      (int)nchunk, inv_t, u_sample, token, draft_tokens, k, emitted);
