@@ -116,6 +116,8 @@ def main() -> int:
     ap.add_argument("--no-mtp", action="store_true", help="skip the MTP-round leg")
     ap.add_argument("--no-dense", action="store_true",
                     help="skip the bf16-expert leg (the real checkpoint's MTP-layer MoE)")
+    ap.add_argument("--no-full", action="store_true",
+                    help="skip the whole-layer leg (router + routed + shared expert, fused against unfused)")
     ap.add_argument("--no-stream", action="store_true",
                     help="skip the streaming-read probe (the HBM read ceiling at the MoE byte counts)")
     ap.add_argument("--workloads", default="M1,M32,M192",
@@ -245,6 +247,7 @@ def main() -> int:
     if not args.no_cpu and head == "M192":
         cpu = cpu_baseline(layers[0], ins[0], dls[0], args.cpu_seconds)
     direct = runner.direct
+    full_layer = None if args.no_full else full_layer_bench(dev, layers)
     stream = None if args.no_stream else stream_bench(dev)
     del runner, ins, outs, layers
     torch.cuda.empty_cache()
@@ -288,6 +291,7 @@ def main() -> int:
             "algorithmic_bytes": round(gu_bytes),
         },
         "cpu_baseline": cpu,
+        "full_layer": full_layer,
         "stream": stream,
         "accept": accept,
         "dense_moe": dense_moe,
@@ -295,6 +299,56 @@ def main() -> int:
     }
     print(json.dumps(line), flush=True)
     return 0
+
+
+def full_layer_bench(dev, layers, rows=(1, 48, 192), shared_inter=1024):
+    """The whole MoE layer of config 2 (router GEMM, softmax top-10, routed MXFP4 experts, shared
+    expert, gated add) at M rows: `fused_moe_layer` (router and shared expert inside the routed
+    layer's launches) against the same pieces launched one by one, graph replay over the layer
+    copies. Router logits come from random bf16 router weights (N(0, 0.02)), so routing is near
+    uniform, not Zipf."""
+    import torch
+
+    import dense
+    import mxfp4_gemv
+    import router_fused
+
+    dense_w = []
+    for li in range(len(layers)):
+        g = torch.Generator(dev).manual_seed(2000 + li)
+        dense_w.append({
+            "router_gate": (torch.randn(E + 1, H, device=dev, generator=g) * 0.02).to(torch.bfloat16),
+            "shared_gate_up": (torch.randn(2 * shared_inter, H, device=dev, generator=g) * 0.02).to(torch.bfloat16),
+            "shared_down": (torch.randn(H, shared_inter, device=dev, generator=g) * 0.02).to(torch.bfloat16),
+        })  # fmt: skip
+
+    def unfused(h, ex, w, out):
+        routing = dense.linear(h, w["router_gate"])
+        top_w, top_i = router_fused.route(routing, E, TOP_K, index_dtype=torch.int32)
+        shared = dense.linear(dense.silu_linear(h, w["shared_gate_up"]), w["shared_down"])
+        mxfp4_gemv.fused_moe(h, ex, (top_i.reshape(-1), top_w.reshape(-1)), TOP_K, (0, E), out=out,
+                             shared=shared, shared_gate=routing[:, E:])
+
+    def fused(h, ex, w, out):
+        mxfp4_gemv.fused_moe_layer(h, w["router_gate"], w["shared_gate_up"], w["shared_down"], ex,
+                                   TOP_K, (0, E), out=out)
+
+    res = {"workload": "whole MoE layer (router 513 x 4096, top-10 of 512 MXFP4 experts, shared "
+                       "expert 1024, gated add), bf16, random router weights",
+           "timing": f"HIP-graph replay over {len(layers)} layer copies"}
+    for m in rows:
+        hs = [torch.randn(m, H, device=dev, generator=torch.Generator(dev).manual_seed(li)).to(torch.bfloat16)
+              for li in range(len(layers))]
+        outs = [torch.empty(m, H, dtype=torch.bfloat16, device=dev) for _ in layers]
+        r = {}
+        for name, fn in (("unfused_us", unfused), ("fused_us", fused)):
+            def call(c, fn=fn):
+                fn(hs[c], layers[c], dense_w[c], outs[c])
+            r[name] = round(_time_graph(call, len(layers), 2 * len(layers)), 2)
+        res[f"M{m}"] = r
+        log(f"full layer M{m}: unfused {r['unfused_us']:.1f} us, fused {r['fused_us']:.1f} us")
+    del dense_w
+    return res
 
 
 def _time_graph(fn, copies, calls, replays=5):

@@ -209,6 +209,30 @@ int mtpk_fused_moe_static(const void* x, int x_dtype, int64_t tokens, int64_t hi
                           const void* shared, int shared_dtype, const void* shared_gate,
                           int gate_dtype, int64_t gate_stride, void* out, void* stream);
 
+/* ---------------------------------------------------------------- whole MoE layer
+ * Replaces the body of `Model.moe` (model.py:2800-2873): router GEMM (`router_gate`, the experts'
+ * rows then the shared gate's row, as `fuse_moe_dense` concatenates them, model.py:913-928),
+ * softmax top-k renormalised, routed MXFP4 experts, shared expert `swiglu_mlp` (model.py:638-649),
+ * out = routed + sigmoid(shared gate) * shared with the rounding points of the torch chain
+ * (`bw_combine_glue`, mxfp4_gemv.py:2266-2312). The router and the shared expert run inside the
+ * routed layer's launches: (1) router + shared gate/up GEMM tiles, (2) top-k + the shared SiLU
+ * product, (3) the shared down GEMM tiles beside the routed gate_up (tokens <= 4) or the work-list
+ * prep, (4) routed down (+ combine). h, router_gate [router_rows, hidden], shared_gate_up
+ * [2 shared_inter, hidden] and shared_down [hidden, shared_inter] are bf16; out bf16
+ * [tokens, hidden]; tokens <= 256; hidden and shared_inter multiples of 256. top_w f32 /
+ * top_i i32 [tokens, top_k] receive the routing when not null (else it stays in the workspace).
+ * workspace: mtpk_moe_layer_workspace_bytes(...) bytes, 256-byte aligned. */
+int64_t mtpk_moe_layer_workspace_bytes(int64_t tokens, int64_t hidden, int64_t router_rows,
+                                       int64_t shared_inter, int top_k, int64_t local_experts,
+                                       int64_t inter_dim);
+int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint16_t* router_gate,
+                   int64_t router_rows, const uint16_t* shared_gate_up,
+                   const uint16_t* shared_down, int64_t shared_inter, const uint8_t* gate_up,
+                   const uint8_t* gate_up_scale, const uint8_t* down, const uint8_t* down_scale,
+                   int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
+                   int expert_hi, float* top_w, int32_t* top_i, void* workspace,
+                   int64_t workspace_bytes, void* out, void* stream);
+
 /* ---------------------------------------------------------------- router top-k
  * Replaces `router_fused.route` / `_fused_route_kernel` (router_fused.py:56-151) and the torch
  * chain in `Model.moe` (model.py:2840-2843). routing [tokens, >= experts_out] f32|bf16 with

@@ -83,6 +83,13 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_int64, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int,
          c_void_p, c_int, c_int64, c_void_p, c_int64, c_void_p, c_void_p],
     ),
+    "mtpk_moe_layer_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int, c_int64, c_int64]),
+    "mtpk_moe_layer": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_void_p, c_void_p,
+         c_void_p, c_int64, c_void_p, c_void_p],
+    ),
     "mtpk_paged_attention_gated": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,

@@ -18,7 +18,9 @@
 #include <mutex>
 
 #include "mtpk_device.h"
+#include "mtpk_gemm_tile.h"
 #include "mtpk_host.h"
+#include "mtpk_layer.h"
 
 namespace mtpk {
 
@@ -29,12 +31,24 @@ constexpr int kPrepThreads = 1024;
 
 // ---------------------------------------------------------------- prep
 
-__global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
-    const void* __restrict__ a_expert, int edt, const void* __restrict__ a_weight, int wdt,
-    int assignments, int lo, int n_experts, int32_t* __restrict__ sorted,
-    int32_t* __restrict__ units, int max_units, int32_t* __restrict__ n_units) {
-  __shared__ int cnt[MTPK_MAX_EXPERTS];
-  __shared__ int wtot_c[kPrepThreads / kWave], wtot_u[kPrepThreads / kWave];
+// The prep's LDS: per-expert counts (then claim cursors) and the per-wave scan totals.
+template <int NT>
+struct PrepSmem {
+  static constexpr int kTot = MTPK_MAX_EXPERTS * 4;
+  static constexpr int kBytes = kTot + 2 * (NT / kWave) * 4;
+};
+
+// The counting sort on one workgroup of NT threads.
+template <int NT>
+__device__ inline void prep_body(const void* __restrict__ a_expert, int edt,
+                                 const void* __restrict__ a_weight, int wdt, int assignments,
+                                 int lo, int n_experts, int32_t* __restrict__ sorted,
+                                 int32_t* __restrict__ units, int max_units,
+                                 int32_t* __restrict__ n_units, uint8_t* smem) {
+  constexpr int kPrepThreads = NT;
+  int* cnt = reinterpret_cast<int*>(smem);
+  int* wtot_c = reinterpret_cast<int*>(smem + PrepSmem<NT>::kTot);
+  int* wtot_u = wtot_c + NT / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
 
   for (int e = tid; e < n_experts; e += kPrepThreads) cnt[e] = 0;
@@ -96,6 +110,15 @@ __global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
     if (ex >= 0 && ex < n_experts && load_float(a_weight, wdt, a) != 0.f)
       sorted[atomicAdd(&cnt[ex], 1)] = a;
   }
+}
+
+__global__ __launch_bounds__(kPrepThreads) void k_moe_prep(
+    const void* __restrict__ a_expert, int edt, const void* __restrict__ a_weight, int wdt,
+    int assignments, int lo, int n_experts, int32_t* __restrict__ sorted,
+    int32_t* __restrict__ units, int max_units, int32_t* __restrict__ n_units) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[PrepSmem<kPrepThreads>::kBytes];
+  prep_body<kPrepThreads>(a_expert, edt, a_weight, wdt, assignments, lo, n_experts, sorted, units,
+                          max_units, n_units, smem);
 }
 
 // ---------------------------------------------------------------- work units
@@ -506,6 +529,49 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_token(
   }
 }
 
+// ---------------------------------------------------------------- shared expert term
+
+// The shared expert's term of a MoE layer, out = routed + sigmoid(gate) * shared, with the
+// torch chain's rounding points (`Model.moe`, model.py:2871-2872): the routed sum, the sigmoid
+// and the product are each rounded to the output dtype before the final add, so the fused
+// layer gives the same values as the three separate elementwise ops.
+struct SharedTerm {
+  const void* shared;  // [T, H] of dtype sdt, or null
+  int sdt;
+  const void* gate;  // pre-sigmoid logit of token t at gate[t * gate_stride]
+  int gdt;
+  int64_t gate_stride;
+  // or, when set, the shared expert's down projection as the split-K GEMM leaves it: ks fp32
+  // planes of [T, H] (`plane` = T * H apart), summed in split order and rounded to the output
+  // dtype, which are the values the GEMM's own reduction would store
+  const float* part;
+  int ks;
+  int64_t plane;
+};
+
+__device__ inline bool shared_active(const SharedTerm& st) { return st.shared || st.part; }
+
+__device__ inline float round_to(int dt, float v) {
+  return dt == MTPK_BF16 ? bf16_to_f32(f32_to_bf16(v)) : v;
+}
+
+__device__ inline float shared_gate(const SharedTerm& st, int t, int odt) {
+  const float g = load_float(st.gate, st.gdt, (int64_t)t * st.gate_stride);
+  return round_to(odt, 1.f / (1.f + expf(-g)));
+}
+
+__device__ inline float shared_value(const SharedTerm& st, int64_t i, int odt) {
+  if (!st.part) return load_float(st.shared, st.sdt, i);
+  float v = 0.f;
+  for (int k = 0; k < st.ks; ++k) v += st.part[k * st.plane + i];
+  return round_to(odt, v);
+}
+
+__device__ inline float add_shared(const SharedTerm& st, float gs, float routed, int64_t i, int odt) {
+  const float prod = round_to(odt, gs * shared_value(st, i, odt));
+  return round_to(odt, routed) + prod;
+}
+
 // ---------------------------------------------------------------- single-token units (direct mode)
 //
 // In direct mode every unit is one assignment, i.e. one token column of the MFMA tile. The
@@ -533,15 +599,27 @@ struct ScaleRow8 {
 // [8w, 8w + 8) (K <= 4096), stages that quarter of the token's XP activation planes in its own
 // LDS region, issues all 8 trips of gate and up weights, then reduces the four partial tiles
 // in LDS in wave order.
+// LDS of the single-token gate_up: each wave's activation quarter (XP planes), a zero row for
+// the A lanes c >= 1, and the partial tiles of waves 1..3 for the reduction.
+template <int XP>
+struct SingleSmem {
+  static constexpr int kPlaneBytes = kSingleQuarter * 2;  // 2 KB
+  static constexpr int kZero = kMoeWaves * XP * kPlaneBytes;
+  static constexpr int kRed = kZero + kPlaneBytes;
+  static constexpr int kBytes = kRed + (kMoeWaves - 1) * 2 * kWave * 16;
+};
+
 template <int XP, int OP, bool SV>
-__global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_single(
+__device__ inline void gate_up_single_body(
     const uint16_t* __restrict__ x, int64_t x_plane, int K, const uint8_t* __restrict__ wq,
-    const uint8_t* __restrict__ ws, int I, UnitSrc src, int top_k, uint16_t* __restrict__ inter,
-    int64_t inter_plane) {
-  constexpr int kPlaneBytes = kSingleQuarter * 2;  // 2 KB
-  __shared__ __attribute__((aligned(16))) uint8_t xs[kMoeWaves][XP][kPlaneBytes];
-  __shared__ __attribute__((aligned(16))) uint8_t zero[kPlaneBytes];  // the A rows of lanes c >= 1
-  __shared__ f32x4_t red[kMoeWaves - 1][2][kWave];
+    const uint8_t* __restrict__ ws, int I, const UnitSrc& src, int top_k,
+    uint16_t* __restrict__ inter, int64_t inter_plane, uint8_t* smem, int bid, int nblk) {
+  constexpr int kPlaneBytes = SingleSmem<XP>::kPlaneBytes;
+  typedef uint8_t Planes[XP][kPlaneBytes];
+  typedef f32x4_t RedPair[2][kWave];
+  Planes* xs = reinterpret_cast<Planes*>(smem);
+  uint8_t* zero = smem + SingleSmem<XP>::kZero;  // the A rows of lanes c >= 1
+  RedPair* red = reinterpret_cast<RedPair*>(smem + SingleSmem<XP>::kRed);
   const int ntile = I >> 4;
   const int n_items = unit_count(src) * ntile;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
@@ -554,7 +632,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_single(
   if (tid < kPlaneBytes / 16) reinterpret_cast<u32x4_t*>(zero)[tid] = zero16();
   __syncthreads();
 
-  for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
+  for (int item = bid; item < n_items; item += nblk) {
     const int u = item / ntile, nt = item - u * ntile;
     int e, first, cnt;
     unit_get(src, u, e, first, cnt);
@@ -649,6 +727,16 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_single(
   }
 }
 
+template <int XP, int OP, bool SV>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_single(
+    const uint16_t* __restrict__ x, int64_t x_plane, int K, const uint8_t* __restrict__ wq,
+    const uint8_t* __restrict__ ws, int I, UnitSrc src, int top_k, uint16_t* __restrict__ inter,
+    int64_t inter_plane) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[SingleSmem<XP>::kBytes];
+  gate_up_single_body<XP, OP, SV>(x, x_plane, K, wq, ws, I, src, top_k, inter, inter_plane, smem,
+                                  blockIdx.x, gridDim.x);
+}
+
 // down + combine, one token per unit: workgroup item = (token t, 16 hidden rows), 16 waves;
 // wave w streams assignment t * top_k + j for j = w, w + 16, ... over its whole K (<= 1024:
 // all 8 trips in flight), its intermediate row staged in its own LDS region. The weighted
@@ -660,7 +748,7 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
     const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
     const uint8_t* __restrict__ ws, int H, const void* __restrict__ a_expert, int edt,
     const void* __restrict__ a_weight, int wdt, int lo, int n_experts, int tokens, int top_k,
-    void* __restrict__ out, int odt) {
+    void* __restrict__ out, int odt, SharedTerm sh) {
   constexpr int kPlaneBytes = kSingleQuarter * 2;  // 2 KB: K <= 1024
   __shared__ __attribute__((aligned(16))) uint8_t as_[kSingleDownWaves][IP][kPlaneBytes];
   __shared__ __attribute__((aligned(16))) uint8_t zero[kPlaneBytes];  // the A rows of lanes c >= 1
@@ -747,7 +835,9 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
       float v = red[0][lane];
 #pragma unroll
       for (int w2 = 1; w2 < kSingleDownWaves; ++w2) v += red[w2][lane];
-      store_float(out, odt, (int64_t)t * H + rt * 16 + lane, v);
+      const int64_t oi = (int64_t)t * H + rt * 16 + lane;
+      if (shared_active(sh)) v = add_shared(sh, shared_gate(sh, t, odt), v, oi, odt);
+      store_float(out, odt, oi, v);
     }
     __syncthreads();
   }
@@ -1186,32 +1276,6 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
 // out[t, n..n+3] = sum_j w_j * y[t*top_k + j, n..n+3] over live assignments, in j order. The
 // routing of a group of four j is loaded before their y rows so the loads overlap.
 
-// The shared expert's term of a MoE layer, out = routed + sigmoid(gate) * shared, with the
-// torch chain's rounding points (`Model.moe`, model.py:2871-2872): the routed sum, the sigmoid
-// and the product are each rounded to the output dtype before the final add, so the fused
-// layer gives the same values as the three separate elementwise ops.
-struct SharedTerm {
-  const void* shared;  // [T, H] of dtype sdt, or null
-  int sdt;
-  const void* gate;  // pre-sigmoid logit of token t at gate[t * gate_stride]
-  int gdt;
-  int64_t gate_stride;
-};
-
-__device__ inline float round_to(int dt, float v) {
-  return dt == MTPK_BF16 ? bf16_to_f32(f32_to_bf16(v)) : v;
-}
-
-__device__ inline float shared_gate(const SharedTerm& st, int t, int odt) {
-  const float g = load_float(st.gate, st.gdt, (int64_t)t * st.gate_stride);
-  return round_to(odt, 1.f / (1.f + expf(-g)));
-}
-
-__device__ inline float add_shared(const SharedTerm& st, float gs, float routed, int64_t i, int odt) {
-  const float prod = round_to(odt, gs * load_float(st.shared, st.sdt, i));
-  return round_to(odt, routed) + prod;
-}
-
 __global__ __launch_bounds__(256) void k_moe_combine(
     const float* __restrict__ y, const void* __restrict__ a_expert, int edt,
     const void* __restrict__ a_weight, int wdt, int top_k, int H, int lo, int hi,
@@ -1243,7 +1307,7 @@ __global__ __launch_bounds__(256) void k_moe_combine(
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] += w[q] * bits_f32(yv[q][c]);
   }
-  if (st.shared) {
+  if (shared_active(st)) {
     const float gs = shared_gate(st, t, odt);
 #pragma unroll
     for (int c = 0; c < 4; ++c) acc[c] = add_shared(st, gs, acc[c], (int64_t)t * H + n + c, odt);
@@ -1261,6 +1325,49 @@ __global__ __launch_bounds__(256) void k_moe_shared_glue(void* __restrict__ out,
   if (n >= H) return;
   const int64_t i = (int64_t)t * H + n;
   store_float(out, odt, i, add_shared(st, shared_gate(st, t, odt), load_float(out, odt, i), i, odt));
+}
+
+// ---------------------------------------------------------------- MoE layer co-launches
+//
+// The shared expert's down projection runs as GEMM tiles inside launches the routed experts
+// need anyway (`mtpk_moe_layer`): beside the single-token gate_up items on the direct path, and
+// beside the prep's counting sort on the unit path. The GEMM tiles take the lowest workgroup ids,
+// so they are dispatched first and stream next to the routed work; each leaves its fp32 split-K
+// partials for the final combine (`SharedTerm::part`).
+
+template <int TT, bool SV>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_single_gemm(
+    GemmArgs g, int g_blocks, int g_gx, const uint16_t* __restrict__ x, int64_t x_plane, int K,
+    const uint8_t* __restrict__ wq, const uint8_t* __restrict__ ws, int I, UnitSrc src, int top_k,
+    uint16_t* __restrict__ inter, int64_t inter_plane) {
+  constexpr int kA = GemmSmem<TT, 4>::kBytes, kB = SingleSmem<1>::kBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kA > kB ? kA : kB];
+  const int b = blockIdx.x;
+  if (b < g_blocks) {
+    gemm_tile<TT, 1, 4, false>(g, smem, b % g_gx, b / g_gx);
+    return;
+  }
+  gate_up_single_body<1, 2, SV>(x, x_plane, K, wq, ws, I, src, top_k, inter, inter_plane, smem,
+                                b - g_blocks, (int)gridDim.x - g_blocks);
+}
+
+constexpr int kPrepCoThreads = kMoeThreads;
+
+template <int TT>
+__global__ __launch_bounds__(kMoeThreads) void k_moe_prep_gemm(
+    GemmArgs g, int g_gx, const void* __restrict__ a_expert, int edt,
+    const void* __restrict__ a_weight, int wdt, int assignments, int lo, int n_experts,
+    int32_t* __restrict__ sorted, int32_t* __restrict__ units, int max_units,
+    int32_t* __restrict__ n_units) {
+  constexpr int kA = GemmSmem<TT, 4>::kBytes, kB = PrepSmem<kPrepCoThreads>::kBytes;
+  __shared__ __attribute__((aligned(16))) uint8_t smem[kA > kB ? kA : kB];
+  if (blockIdx.x == 0) {
+    prep_body<kPrepCoThreads>(a_expert, edt, a_weight, wdt, assignments, lo, n_experts, sorted,
+                              units, max_units, n_units, smem);
+    return;
+  }
+  const int b = blockIdx.x - 1;
+  gemm_tile<TT, 1, 4, false>(g, smem, b % g_gx, b / g_gx);
 }
 
 // ---------------------------------------------------------------- plane split
@@ -1504,7 +1611,7 @@ template <int IP, bool SV>
 int launch_down_single(const uint16_t* inter, int64_t inter_plane, int K, const uint8_t* wq,
                        const uint8_t* ws, int H, const void* a_expert, int edt, const void* a_weight,
                        int wdt, int lo, int n_experts, int tokens, int top_k, void* out, int odt,
-                       hipStream_t st) {
+                       hipStream_t st, const SharedTerm& sh = SharedTerm{}) {
   static int occ = 0;
   auto kern = k_moe_down_single<IP, SV>;
   constexpr int threads = kSingleDownWaves * kWave;
@@ -1513,7 +1620,7 @@ int launch_down_single(const uint16_t* inter, int64_t inter_plane, int K, const 
   const int grid = (int)(need < cap ? need : cap);
   if (grid == 0) return 0;
   hipLaunchKernelGGL(kern, dim3(grid), dim3(threads), 0, st, inter, inter_plane, K, wq, ws, H,
-                     a_expert, edt, a_weight, wdt, lo, n_experts, tokens, top_k, out, odt);
+                     a_expert, edt, a_weight, wdt, lo, n_experts, tokens, top_k, out, odt, sh);
   return status_of(hipGetLastError());
 }
 
@@ -1725,7 +1832,7 @@ int mtpk_moe_combine(const float* y, const void* a_expert, int expert_dtype, con
   const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
   hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
-                     expert_hi, out, out_dtype, SharedTerm{nullptr, 0, nullptr, 0, 0});
+                     expert_hi, out, out_dtype, SharedTerm{});
   return status_of(hipGetLastError());
 }
 
@@ -1822,6 +1929,215 @@ int mtpk_fused_moe_shared(const void* x, int x_dtype, int64_t tokens, int64_t hi
   hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
                      expert_hi, out, x_dtype, st);
+  return status_of(hipGetLastError());
+}
+
+}  // extern "C"
+
+namespace {
+
+// Token tiles of 16 weight rows per wave, 4 waves: the tile count of one fused-layer GEMM.
+int64_t layer_tiles(int64_t cols) { return (cols + 63) / 64; }
+
+struct LayerPlan {
+  int64_t routed, topw, topi, sgate, wr, wsg, act, wd, total;
+  int ksr, kss, ksd;
+};
+
+LayerPlan layer_plan(int64_t tokens, int64_t hidden, int64_t router_rows, int64_t shared_inter,
+                     int64_t top_k, int64_t local_experts, int64_t inter_dim) {
+  LayerPlan p{};
+  p.ksr = gemm_splits(tokens, router_rows, hidden, kEpiStore);
+  p.kss = gemm_splits(tokens, 2 * shared_inter, hidden, kEpiSilu);
+  p.ksd = gemm_splits(tokens, hidden, shared_inter, kEpiStore);
+  int64_t o = align256(mtpk_moe_workspace_bytes(tokens, top_k, local_experts, inter_dim, hidden,
+                                                MTPK_BF16));
+  p.topw = o;
+  o += align256(tokens * top_k * 4);
+  p.topi = o;
+  o += align256(tokens * top_k * 4);
+  p.sgate = o;
+  o += align256(tokens * 2);
+  p.wr = o;
+  o += align256((int64_t)p.ksr * tokens * router_rows * 4);
+  p.wsg = o;
+  o += align256((int64_t)p.kss * tokens * 2 * shared_inter * 4);
+  p.act = o;
+  o += align256(tokens * shared_inter * 2);
+  p.wd = o;
+  o += align256((int64_t)p.ksd * tokens * hidden * 4);
+  p.total = o;
+  return p;
+}
+
+GemmArgs layer_gemm(const uint16_t* x, const uint16_t* w, int64_t m, int64_t n, int64_t k, int ks,
+                    int epi, float* part) {
+  const int64_t cols = epi == kEpiSilu ? n / 2 : n;
+  return GemmArgs{x, w, (int)m, (int)n, (int)k, ks, epi, MTPK_BF16, (int)cols, nullptr, part,
+                  nullptr, (int)layer_tiles(cols), gemm_groups(m)};
+}
+
+template <int TT, bool SV>
+int launch_gate_up_single_gemm(const GemmArgs& g, const uint16_t* x, int64_t x_plane, int K,
+                               const uint8_t* wq, const uint8_t* ws, int I, const UnitSrc& src,
+                               int64_t units, int top_k, uint16_t* inter, int64_t inter_plane,
+                               hipStream_t st) {
+  static int occ = 0;
+  auto kern = k_moe_gate_up_single_gemm<TT, SV>;
+  const int g_gx = (int)gemm_grid_x(g.tiles, g.RG), g_blocks = g_gx * g.KS;
+  const int routed = grid_for(kern, units * (I >> 4), occ);
+  hipLaunchKernelGGL(kern, dim3(g_blocks + routed), dim3(kMoeThreads), 0, st, g, g_blocks, g_gx,
+                     x, x_plane, K, wq, ws, I, src, top_k, inter, inter_plane);
+  return status_of(hipGetLastError());
+}
+
+template <int TT>
+int launch_prep_gemm(const GemmArgs& g, const void* a_expert, int edt, const void* a_weight,
+                     int wdt, int64_t assignments, int lo, int n_experts, int32_t* sorted,
+                     int32_t* units, int64_t max_units, int32_t* n_units, hipStream_t st) {
+  const int g_gx = (int)gemm_grid_x(g.tiles, g.RG);
+  hipLaunchKernelGGL(k_moe_prep_gemm<TT>, dim3(1 + g_gx * g.KS), dim3(kMoeThreads), 0, st, g,
+                     g_gx, a_expert, edt, a_weight, wdt, (int)assignments, lo, n_experts, sorted,
+                     units, (int)max_units, n_units);
+  return status_of(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+int64_t mtpk_moe_layer_workspace_bytes(int64_t tokens, int64_t hidden, int64_t router_rows,
+                                       int64_t shared_inter, int top_k, int64_t local_experts,
+                                       int64_t inter_dim) {
+  if (tokens <= 0 || tokens > 256 || hidden <= 0 || router_rows <= 1 || shared_inter <= 0 ||
+      top_k <= 0 || local_experts <= 0 || inter_dim <= 0)
+    return 0;
+  return layer_plan(tokens, hidden, router_rows, shared_inter, top_k, local_experts, inter_dim)
+      .total;
+}
+
+int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint16_t* router_gate,
+                   int64_t router_rows, const uint16_t* shared_gate_up,
+                   const uint16_t* shared_down, int64_t shared_inter, const uint8_t* gate_up,
+                   const uint8_t* gate_up_scale, const uint8_t* down, const uint8_t* down_scale,
+                   int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
+                   int expert_hi, float* top_w, int32_t* top_i, void* workspace,
+                   int64_t workspace_bytes, void* out, void* stream) {
+  if (!h || !router_gate || !shared_gate_up || !shared_down || !gate_up || !gate_up_scale ||
+      !down || !down_scale || !workspace || !out)
+    return MTPK_EINVAL;
+  if (tokens < 0 || tokens > 256 || tokens > 65535) return MTPK_EINVAL;
+  const int64_t experts = router_rows - 1;  // the router's last row is the shared expert's gate
+  if (experts <= 0 || experts > MTPK_MAX_ROUTER_EXPERTS || top_k <= 0 || top_k > MTPK_MAX_TOP_K ||
+      top_k > experts)
+    return MTPK_EINVAL;
+  if ((int64_t)expert_hi - expert_lo != local_experts || expert_lo < 0 || expert_hi > experts)
+    return MTPK_EINVAL;
+  if (!gemm_shapes_ok(hidden, inter_dim, local_experts) || hidden % kGemmKC ||
+      shared_inter % kGemmKC || shared_inter % 16 || hidden % 4)
+    return MTPK_EINVAL;
+  if (!aligned16(h) || !aligned16(router_gate) || !aligned16(shared_gate_up) ||
+      !aligned16(shared_down) || !aligned16(gate_up) || !aligned16(down) ||
+      (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return MTPK_EINVAL;
+  if (router_rows * hidden * 2 > 0x7fffffffLL || 2 * shared_inter * hidden * 2 > 0x7fffffffLL)
+    return MTPK_EINVAL;
+  if (tokens == 0) return 0;
+  const LayerPlan pl =
+      layer_plan(tokens, hidden, router_rows, shared_inter, top_k, local_experts, inter_dim);
+  if (workspace_bytes < pl.total) return MTPK_EINVAL;
+  if (gemm_waves(tokens, router_rows, kEpiStore) != 4 ||
+      gemm_waves(tokens, 2 * shared_inter, kEpiSilu) != 4 ||
+      gemm_waves(tokens, hidden, kEpiStore) != 4)
+    return MTPK_EINVAL;  // the co-launches run 4-wave GEMM tiles
+  char* w = static_cast<char*>(workspace);
+  float* tw = top_w ? top_w : reinterpret_cast<float*>(w + pl.topw);
+  int32_t* ti = top_i ? top_i : reinterpret_cast<int32_t*>(w + pl.topi);
+  uint16_t* sgate = reinterpret_cast<uint16_t*>(w + pl.sgate);
+  float* wr = reinterpret_cast<float*>(w + pl.wr);
+  float* wsg = reinterpret_cast<float*>(w + pl.wsg);
+  uint16_t* act = reinterpret_cast<uint16_t*>(w + pl.act);
+  float* wd = reinterpret_cast<float*>(w + pl.wd);
+  const hipStream_t st = (hipStream_t)stream;
+
+  // 1. router logits and the shared expert's gate/up, one launch (split-K partials)
+  int rc = launch_gemm_pair(layer_gemm(h, router_gate, tokens, router_rows, hidden, pl.ksr, kEpiStore, wr),
+                            layer_gemm(h, shared_gate_up, tokens, 2 * shared_inter, hidden, pl.kss, kEpiSilu, wsg),
+                            st);
+  if (rc) return rc;
+  // 2. softmax top-k from the router partials, the shared gate logit, act = silu(gate) * up
+  RouteActArgs ra{wr, pl.ksr, (int)tokens, (int)router_rows, (int)experts, top_k, tw, ti,
+                  MTPK_I32, sgate, wsg, pl.kss, (int)shared_inter, act, 0};
+  rc = launch_route_act(ra, st);
+  if (rc) return rc;
+  // 3.. the routed experts, with the shared down projection's tiles in the first routed launch
+  // and its gated term in the last
+  const GemmArgs gd = layer_gemm(act, shared_down, tokens, hidden, shared_inter, pl.ksd, kEpiStore, wd);
+  SharedTerm sh{};
+  sh.gate = sgate;
+  sh.gdt = MTPK_BF16;
+  sh.gate_stride = 1;
+  sh.part = wd;
+  sh.ks = pl.ksd;
+  sh.plane = tokens * hidden;
+  const int64_t a = tokens * top_k;
+  const int64_t mu = mtpk_moe_max_units(a, local_experts);
+  char* p = w;
+  int32_t* sorted = reinterpret_cast<int32_t*>(p);
+  p += align256(a * 4);
+  int32_t* units = reinterpret_cast<int32_t*>(p);
+  p += align256(3 * mu * 4);
+  int32_t* n_units = reinterpret_cast<int32_t*>(p);
+  p += 256;
+  uint16_t* inter = reinterpret_cast<uint16_t*>(p);
+  p += align256(2 * a * inter_dim * 2);
+  float* y = reinterpret_cast<float*>(p);
+  const int tt = gemm_tt(tokens);
+  static_assert(kDirectMaxTokens <= 16, "the direct path's GEMM tiles hold one token tile");
+  if (tokens <= kDirectMaxTokens && single_gate_up_ok((int)hidden) && single_down_ok((int)inter_dim)) {
+    const UnitSrc src = unit_direct(ti, MTPK_I32, tw, MTPK_F32, expert_lo, expert_hi, a);
+    const bool sv = (hidden / 32) % 32 == 0;
+#define MTPK_GSG(TT_)                                                                          \
+  (sv ? launch_gate_up_single_gemm<TT_, true>(gd, h, tokens * hidden, (int)hidden, gate_up,     \
+                                              gate_up_scale, (int)inter_dim, src, a, top_k,     \
+                                              inter, a * inter_dim, st)                         \
+      : launch_gate_up_single_gemm<TT_, false>(gd, h, tokens * hidden, (int)hidden, gate_up,    \
+                                               gate_up_scale, (int)inter_dim, src, a, top_k,    \
+                                               inter, a * inter_dim, st))
+    rc = MTPK_GSG(1);  // at most 4 token rows: one token tile
+#undef MTPK_GSG
+    if (rc) return rc;
+    const int64_t ip = a * inter_dim;
+    return inter_dim == 1024
+               ? launch_down_single<2, true>(inter, ip, (int)inter_dim, down, down_scale,
+                                             (int)hidden, ti, MTPK_I32, tw, MTPK_F32, expert_lo,
+                                             (int)local_experts, (int)tokens, top_k, out,
+                                             MTPK_BF16, st, sh)
+               : launch_down_single<2, false>(inter, ip, (int)inter_dim, down, down_scale,
+                                              (int)hidden, ti, MTPK_I32, tw, MTPK_F32, expert_lo,
+                                              (int)local_experts, (int)tokens, top_k, out,
+                                              MTPK_BF16, st, sh);
+  }
+#define MTPK_PG(TT_)                                                                          \
+  launch_prep_gemm<TT_>(gd, ti, MTPK_I32, tw, MTPK_F32, a, expert_lo, (int)local_experts, sorted, \
+                        units, mu, n_units, st)
+  switch (tt) {
+    case 1: rc = MTPK_PG(1); break;
+    case 2: rc = MTPK_PG(2); break;
+    case 3: rc = MTPK_PG(3); break;
+    default: rc = MTPK_PG(4); break;
+  }
+#undef MTPK_PG
+  if (rc) return rc;
+  rc = mtpk_moe_gate_up(h, 1, tokens, hidden, gate_up, gate_up_scale, local_experts, inter_dim,
+                        sorted, units, n_units, mu, top_k, inter, 2, a, stream);
+  if (rc) return rc;
+  rc = mtpk_moe_down(inter, 2, a, inter_dim, down, down_scale, local_experts, hidden, sorted,
+                     units, n_units, mu, y, stream);
+  if (rc) return rc;
+  const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
+  hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, st, y, ti, MTPK_I32, tw, MTPK_F32, top_k,
+                     (int)hidden, expert_lo, expert_hi, out, MTPK_BF16, sh);
   return status_of(hipGetLastError());
 }
 

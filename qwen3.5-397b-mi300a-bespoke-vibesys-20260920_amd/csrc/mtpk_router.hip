@@ -14,7 +14,9 @@
 // differs from the two-division form by rounding only).
 
 #include "mtpk_device.h"
+#include "mtpk_gemm_tile.h"
 #include "mtpk_host.h"
+#include "mtpk_layer.h"
 
 namespace mtpk {
 
@@ -43,27 +45,50 @@ __device__ inline float dpp_max_f32(float v) {
                              [](uint32_t a, uint32_t b) { return f32_bits(fmaxf(bits_f32(a), bits_f32(b))); }));
 }
 
+// The row's logits in registers: lane l holds logits l + 64 j (j < PER). Every lane issues its
+// loads at once, and loads past E return zeros (unused) without a branch around them.
 template <int PER, bool BF16>
-__global__ __launch_bounds__(256) void k_route_topk(const void* __restrict__ routing,
-                                                    int64_t stride, int tokens, int E, int top_k,
-                                                    float* __restrict__ top_w,
-                                                    void* __restrict__ top_i, int idt) {
-  const int row = blockIdx.x * 4 + (threadIdx.x / kWave);
-  const int lane = threadIdx.x & (kWave - 1);
-  if (row >= tokens) return;  // uniform over the wave: every DPP below runs with all lanes
-  // The row's E logits as one buffer: every lane issues its PER loads at once, and loads past E
-  // return zeros (they are not used) without a branch around them.
+__device__ inline void load_logits_row(const void* __restrict__ routing, int64_t stride, int row,
+                                       int E, int lane, float (&lg)[PER]) {
   constexpr int elt = BF16 ? 2 : 4;
   const rsrc_t r = make_rsrc(static_cast<const uint8_t*>(routing) + (int64_t)row * stride * elt,
                              (uint32_t)(E * elt));
-  float lg[PER], e_[PER];
-  uint32_t key[PER];  // order key of a free slot (>= 1), 0 once taken or past E
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const uint32_t off = (uint32_t)((lane + kWave * j) * elt);
     lg[j] = BF16 ? bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(r, (int)off, 0, 0))
                  : bits_f32(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
   }
+}
+
+// The same row as the split-K GEMM leaves it: KS fp32 partial planes [KS, rows, cols], summed in
+// split order and rounded to bf16, i.e. the bf16 logits the GEMM's reduction would store.
+template <int PER>
+__device__ inline void load_logits_partials(const float* __restrict__ part, int KS, int rows,
+                                            int cols, int row, int E, int lane, float (&lg)[PER]) {
+  float acc[PER];
+#pragma unroll
+  for (int j = 0; j < PER; ++j) acc[j] = 0.f;
+  for (int ks = 0; ks < KS; ++ks) {
+    const rsrc_t r = make_rsrc(part + ((int64_t)ks * rows + row) * cols, (uint32_t)(E * 4));
+    float v[PER];
+#pragma unroll
+    for (int j = 0; j < PER; ++j)
+      v[j] = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(r, (int)((lane + kWave * j) * 4), 0, 0));
+#pragma unroll
+    for (int j = 0; j < PER; ++j) acc[j] += v[j];
+  }
+#pragma unroll
+  for (int j = 0; j < PER; ++j) lg[j] = bf16_to_f32(f32_to_bf16(acc[j]));
+}
+
+// softmax -> top-k -> renormalise of one row whose logits lane l holds at slots j (expert
+// l + 64 j), written to row `row` of top_w / top_i. Runs on a whole wave (the DPP reductions).
+template <int PER>
+__device__ inline void route_row(float (&lg)[PER], int row, int E, int top_k, int lane,
+                                 float* __restrict__ top_w, void* __restrict__ top_i, int idt) {
+  float e_[PER];
+  uint32_t key[PER];  // order key of a free slot (>= 1), 0 once taken or past E
   float m = -INFINITY;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
@@ -130,6 +155,61 @@ __global__ __launch_bounds__(256) void k_route_topk(const void* __restrict__ rou
     top_w[(int64_t)row * top_k + lane] = my_w / total;
     store_index(top_i, idt, (int64_t)row * top_k + lane, my_i);
   }
+}
+
+template <int PER, bool BF16>
+__global__ __launch_bounds__(256) void k_route_topk(const void* __restrict__ routing,
+                                                    int64_t stride, int tokens, int E, int top_k,
+                                                    float* __restrict__ top_w,
+                                                    void* __restrict__ top_i, int idt) {
+  const int row = blockIdx.x * 4 + (threadIdx.x / kWave);
+  const int lane = threadIdx.x & (kWave - 1);
+  if (row >= tokens) return;  // uniform over the wave: every DPP below runs with all lanes
+  float lg[PER];
+  load_logits_row<PER, BF16>(routing, stride, row, E, lane, lg);
+  route_row<PER>(lg, row, E, top_k, lane, top_w, top_i, idt);
+}
+
+// The MoE layer's second launch (after the router and shared gate_up GEMM tiles have left their
+// split-K partials): workgroups [0, route_blocks) route four token rows each from the router's
+// partials and store the shared gate's logit (column E) rounded to bf16; the others finish the
+// shared expert's gate_up, act[m, j] = bf16(silu(gate) * up) from its partials, 256 values each.
+// Both halves reproduce the bits of the GEMM's own reduction launch.
+template <int PER>
+__global__ __launch_bounds__(256) void k_route_act(RouteActArgs a) {
+  if ((int)blockIdx.x < a.route_blocks) {
+    const int row = blockIdx.x * 4 + (threadIdx.x / kWave);
+    const int lane = threadIdx.x & (kWave - 1);
+    if (row >= a.rows) return;  // uniform over the wave
+    float lg[PER];
+    load_logits_partials<PER>(a.rpart, a.rks, a.rows, a.rcols, row, a.E, lane, lg);
+    if (a.sgate && lane == 0) {
+      float g = 0.f;
+      for (int ks = 0; ks < a.rks; ++ks) g += a.rpart[((int64_t)ks * a.rows + row) * a.rcols + a.E];
+      a.sgate[row] = f32_to_bf16(g);
+    }
+    route_row<PER>(lg, row, a.E, a.top_k, lane, a.top_w, a.top_i, a.idt);
+    return;
+  }
+  const int64_t idx = (int64_t)(blockIdx.x - a.route_blocks) * 256 + threadIdx.x;
+  if (idx >= (int64_t)a.rows * a.scols) return;
+  const int64_t m = idx / a.scols, col = idx - m * a.scols;
+  a.act[idx] = f32_to_bf16(gemm_reduce_value(a.spart, a.sks, a.rows, a.scols, kEpiSilu, m, col));
+}
+
+int launch_route_act(const RouteActArgs& a, hipStream_t st) {
+  RouteActArgs b = a;
+  b.route_blocks = (a.rows + 3) / 4;
+  const int64_t act_blocks = ((int64_t)a.rows * a.scols + 255) / 256;
+  const unsigned grid = (unsigned)(b.route_blocks + act_blocks);
+  const int per = (a.E + kWave - 1) / kWave;
+  if (per <= 4)
+    hipLaunchKernelGGL(k_route_act<4>, dim3(grid), dim3(256), 0, st, b);
+  else if (per <= 8)
+    hipLaunchKernelGGL(k_route_act<8>, dim3(grid), dim3(256), 0, st, b);
+  else
+    hipLaunchKernelGGL(k_route_act<16>, dim3(grid), dim3(256), 0, st, b);
+  return status_of(hipGetLastError());
 }
 
 template <int PER>

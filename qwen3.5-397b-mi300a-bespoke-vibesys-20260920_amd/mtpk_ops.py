@@ -1,8 +1,8 @@
 """The hot path's device entry points as PyTorch custom ops, namespace `mtpk`.
 
 Each op is a `torch.library.custom_op` over the same C-ABI call the Python wrapper makes
-(`mxfp4_gemv.fused_moe`, `router_fused.route`, `mtp.argmax_rows`, `graph_mtp.greedy_accept`,
-`graph_mtp.rejection_sample`), registered for HIP devices only, with a fake kernel that gives
+(`mxfp4_gemv.fused_moe`, `mxfp4_gemv.fused_moe_layer`, `router_fused.route`, `mtp.argmax_rows`,
+`graph_mtp.greedy_accept`, `graph_mtp.rejection_sample`), registered for HIP devices only, with a fake kernel that gives
 the output shapes and dtypes without running anything. That puts the ops in the dispatcher:
 `torch.compile` traces through them as single nodes, FakeTensor / meta propagation works, and a
 HIP graph captures them like any other launch. There is no CPU kernel: a call on CPU tensors
@@ -47,6 +47,34 @@ def _(x, gate_up, gate_up_scale, down, down_scale, a_expert, a_weight, top_k, ex
     torch._check(x.dim() == 2, lambda: "x must be [T, hidden]")
     torch._check(a_expert.numel() == x.shape[0] * top_k, lambda: "one expert id per (token, slot)")
     return x.new_empty(x.shape)
+
+
+# ---------------------------------------------------------------- whole MoE layer
+
+
+@custom_op("mtpk::moe_layer", mutates_args=(), device_types="cuda")
+def moe_layer(h: Tensor, router_gate: Tensor, shared_gate_up: Tensor, shared_down: Tensor,
+              gate_up: Tensor, gate_up_scale: Tensor, down: Tensor, down_scale: Tensor, top_k: int,
+              expert_lo: int, expert_hi: int) -> tuple[Tensor, Tensor, Tensor]:
+    """`mxfp4_gemv.fused_moe_layer`: `(out [T, hidden] bf16, top_w f32 [T, top_k], top_i int32
+    [T, top_k])` -- the layer output and the routing it chose."""
+    experts = {"gate_up": gate_up, "gate_up_scale": gate_up_scale, "down": down,
+               "down_scale": down_scale}
+    t = h.shape[0]
+    tw = torch.empty(t, top_k, dtype=torch.float32, device=h.device)
+    ti = torch.empty(t, top_k, dtype=torch.int32, device=h.device)
+    out = mxfp4_gemv.fused_moe_layer(h, router_gate, shared_gate_up, shared_down, experts, top_k,
+                                     (expert_lo, expert_hi), routing_out=(tw, ti))
+    return out, tw, ti
+
+
+@moe_layer.register_fake
+def _(h, router_gate, shared_gate_up, shared_down, gate_up, gate_up_scale, down, down_scale, top_k,
+      expert_lo, expert_hi):
+    torch._check(h.dim() == 2, lambda: "h must be [T, hidden]")
+    t = h.shape[0]
+    return (h.new_empty(h.shape), h.new_empty(t, top_k, dtype=torch.float32),
+            h.new_empty(t, top_k, dtype=torch.int32))
 
 
 # ---------------------------------------------------------------- router top-k

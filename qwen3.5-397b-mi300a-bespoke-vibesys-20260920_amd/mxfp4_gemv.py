@@ -240,6 +240,104 @@ def fused_moe(
     return out
 
 
+def layer_workspace_bytes(tokens: int, hidden: int, router_rows: int, shared_inter: int, top_k: int,
+                          local_experts: int, intermediate: int) -> int:
+    """Bytes of scratch `fused_moe_layer` needs at these sizes (`mtpk_moe_layer_workspace_bytes`)."""
+    return int(_mtpk.lib().mtpk_moe_layer_workspace_bytes(tokens, hidden, router_rows, shared_inter,
+                                                          top_k, local_experts, intermediate))
+
+
+def layer_fits(h: torch.Tensor, router_gate: torch.Tensor, shared_down: torch.Tensor,
+               experts: dict) -> bool:
+    """Whether `fused_moe_layer` takes these operands: bf16 activations and dense weights, MXFP4
+    experts, 1..256 rows, hidden and the shared expert's width multiples of 256."""
+    return (
+        h.dtype == torch.bfloat16 and router_gate.dtype == torch.bfloat16
+        and shared_down.dtype == torch.bfloat16 and h.dim() == 2 and 1 <= h.shape[0] <= 256
+        and h.shape[1] % 256 == 0 and shared_down.shape[1] % 256 == 0 and "gate_up_scale" in experts
+    )  # fmt: skip
+
+
+def fused_moe_layer(
+    h: torch.Tensor,
+    router_gate: torch.Tensor,
+    shared_gate_up: torch.Tensor,
+    shared_down: torch.Tensor,
+    experts: dict,
+    top_k: int,
+    expert_range: tuple[int, int],
+    *,
+    out: torch.Tensor | None = None,
+    workspace: torch.Tensor | None = None,
+    routing_out: tuple[torch.Tensor, torch.Tensor] | None = None,
+) -> torch.Tensor:
+    """The whole MoE layer of `Model.moe` (`model.py:2800-2873`) for bf16 rows `h` `[T, hidden]`:
+    router GEMM (`router_gate` = the experts' router rows, then the shared gate's row, as
+    `fuse_moe_dense` concatenates them, `model.py:913-928`), softmax top-k renormalised
+    (`router_fused.route`), the routed MXFP4 experts, the shared expert's SwiGLU
+    (`shared_gate_up` = [gate; up], `shared_down`), and `routed + sigmoid(gate) * shared`.
+
+    The router and the shared expert run inside the routed layer's launches (`mtpk_moe_layer`):
+    one launch for the router and shared gate/up GEMM tiles, one for the top-k and the shared
+    SiLU product, then the routed launches with the shared down projection's tiles beside the
+    first and its gated term in the last. Each piece computes the same values as its stand-alone
+    launch (`dense.linear`, `dense.silu_linear`, `router_fused.route`, `fused_moe(shared=)`).
+
+    `routing_out` = (top_w f32 [T, top_k], top_i int32 [T, top_k]) receives the routing when
+    given. `workspace` is optional scratch of `layer_workspace_bytes(...)` bytes; without it the
+    call takes the grow-only per-stream workspace `fused_moe` uses.
+    """
+    lo, hi = expert_range
+    if h.dtype != torch.bfloat16 or h.dim() != 2 or not h.is_contiguous():
+        raise ValueError("h must be a contiguous bf16 [T, hidden] tensor")
+    for name, t in (("router_gate", router_gate), ("shared_gate_up", shared_gate_up),
+                    ("shared_down", shared_down)):
+        if t.dtype != torch.bfloat16 or t.dim() != 2 or not t.is_contiguous():
+            raise ValueError(f"{name} must be a contiguous bf16 matrix")
+    _validate(h, experts, (torch.empty(h.shape[0] * top_k, dtype=torch.int32, device=h.device),
+                           torch.empty(h.shape[0] * top_k, dtype=torch.float32, device=h.device)), top_k)
+    device = _mtpk.require_device(h, router_gate, shared_gate_up, shared_down, experts["gate_up"])
+    tokens, hidden = h.shape
+    gate_up, down = experts["gate_up"], experts["down"]
+    local, intermediate = gate_up.shape[0], gate_up.shape[1] // 2
+    router_rows = router_gate.shape[0]
+    shared_inter = shared_down.shape[1]
+    if (router_gate.shape[1] != hidden or shared_gate_up.shape != (2 * shared_inter, hidden)
+            or shared_down.shape[0] != hidden):
+        raise ValueError("router / shared expert shapes do not match h")
+    if hi - lo != local or down.shape[1] != hidden or gate_up.shape[2] * 2 != hidden:
+        raise ValueError("expert payload shapes do not match h and expert_range")
+    if out is None:
+        out = torch.empty(tokens, hidden, dtype=h.dtype, device=device)
+    elif out.shape != (tokens, hidden) or out.dtype != h.dtype or not out.is_contiguous():
+        raise ValueError("out must be a contiguous bf16 [T, hidden] tensor")
+    tw_ptr = ti_ptr = None
+    if routing_out is not None:
+        tw, ti = routing_out
+        if (tw.dtype != torch.float32 or ti.dtype != torch.int32 or tw.shape != (tokens, top_k)
+                or ti.shape != (tokens, top_k) or not (tw.is_contiguous() and ti.is_contiguous())):
+            raise ValueError("routing_out must be contiguous (f32, int32) [T, top_k] tensors")
+        tw_ptr, ti_ptr = tw.data_ptr(), ti.data_ptr()
+    lib = _mtpk.lib()
+    nbytes = lib.mtpk_moe_layer_workspace_bytes(tokens, hidden, router_rows, shared_inter, top_k,
+                                                local, intermediate)
+    if nbytes <= 0:
+        raise ValueError("unsupported fused_moe_layer sizes (tokens 1..256)")
+    ws = _workspace(device, nbytes, workspace)
+    _mtpk.check(
+        lib.mtpk_moe_layer(
+            h.data_ptr(), tokens, hidden, router_gate.data_ptr(), router_rows,
+            shared_gate_up.data_ptr(), shared_down.data_ptr(), shared_inter,
+            gate_up.data_ptr(), experts["gate_up_scale"].data_ptr(),
+            down.data_ptr(), experts["down_scale"].data_ptr(), local, intermediate,
+            top_k, lo, hi, tw_ptr, ti_ptr, ws.data_ptr(), ws.numel() * ws.element_size(),
+            out.data_ptr(), _mtpk.stream_of(device),
+        ),
+        "mtpk_moe_layer",
+    )  # fmt: skip
+    return out
+
+
 def workspace_bytes(tokens: int, top_k: int, local_experts: int, intermediate: int, hidden: int,
                     dtype: torch.dtype = torch.bfloat16) -> int:
     """Bytes of scratch `fused_moe` needs at these sizes (`mtpk_moe_workspace_bytes`)."""

@@ -533,6 +533,11 @@ class Model:
         """Routed MXFP4 experts + gated shared expert over rows `h` `[N, hidden]`
         (`model.py:2811-2873`)."""
         c = self.cfg
+        if (h.device.type == "cuda" and mxfp4_gemv.available(h.device)
+                and mxfp4_gemv.layer_fits(h, w["router_gate"], w["shared_down"], w["experts"])):
+            # router, shared expert and routed experts in the routed layer's launches
+            return mxfp4_gemv.fused_moe_layer(h.contiguous(), w["router_gate"], w["shared_gate_up"],
+                                              w["shared_down"], w["experts"], c.top_k, (0, c.experts))
         routing = linear(h, w["router_gate"])
         if h.device.type == "cuda":
             top_w, top_i = router_fused.route(routing, c.experts, c.top_k, index_dtype=torch.int32)

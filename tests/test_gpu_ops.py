@@ -34,6 +34,16 @@ def moe_args(dev, tokens=T):
             torch.from_numpy(a_e).to(dev), torch.from_numpy(a_w).to(dev), K, 0, E, shared, gate)
 
 
+def layer_args(dev, tokens=T):
+    """A small whole layer: hidden 256, 16 experts (I = 128), shared expert 256."""
+    x, gu, gus, dn, dns = moe_args(dev, tokens)[:5]
+    g = torch.Generator(dev).manual_seed(11)
+    rg = (torch.randn(E + 1, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    sgu = (torch.randn(2 * 256, H, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    sdn = (torch.randn(H, 256, device=dev, generator=g) * 0.05).to(torch.bfloat16)
+    return x, rg, sgu, sdn, gu, gus, dn, dns, K, 0, E
+
+
 def accept_args(dev):
     g = torch.Generator(dev).manual_seed(7)
     step = torch.randint(0, 9, (B, KD + 1), device=dev, generator=g)
@@ -69,6 +79,7 @@ def argmax_args(dev):
 
 CASES = {
     "fused_moe": (torch.ops.mtpk.fused_moe.default, moe_args),
+    "moe_layer": (torch.ops.mtpk.moe_layer.default, layer_args),
     "route": (torch.ops.mtpk.route.default, route_args),
     "argmax_rows": (torch.ops.mtpk.argmax_rows.default, argmax_args),
     "greedy_accept": (torch.ops.mtpk.greedy_accept.default, accept_args),
@@ -79,9 +90,9 @@ CASES = {
 @pytest.mark.parametrize("name", sorted(CASES))
 def test_opcheck(dev, name):
     op, make = CASES[name]
-    if name == "fused_moe":
+    if name in ("fused_moe", "moe_layer"):
         mxfp4_gemv.supports({k: v for k, v in zip(("gate_up", "gate_up_scale", "down", "down_scale"),
-                                                   make(dev)[1:5], strict=True)})
+                                                   moe_args(dev)[1:5], strict=True)})
     torch.library.opcheck(op, make(dev))
 
 
@@ -91,6 +102,13 @@ def test_ops_equal_the_wrappers(dev):
     ex = {"gate_up": gu, "gate_up_scale": gus, "down": dn, "down_scale": dns}
     want = mxfp4_gemv.fused_moe(x, ex, (ae, aw), k, (lo, hi), shared=shared, shared_gate=gate)
     assert torch.equal(torch.ops.mtpk.fused_moe(*args), want)
+    la = layer_args(dev)
+    h, rg, sgu, sdn = la[:4]
+    tw = torch.empty(T, K, device=dev)
+    ti = torch.empty(T, K, dtype=torch.int32, device=dev)
+    want = mxfp4_gemv.fused_moe_layer(h, rg, sgu, sdn, ex, K, (lo, hi), routing_out=(tw, ti))
+    for a, b in zip(torch.ops.mtpk.moe_layer(*la), (want, tw, ti), strict=True):
+        assert torch.equal(a, b)
     r, e, kk, dt = route_args(dev)
     for a, b in zip(torch.ops.mtpk.route(r, e, kk, dt), router_fused.route(r, e, kk, index_dtype=dt),
                     strict=True):

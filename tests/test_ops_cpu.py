@@ -12,7 +12,7 @@ from torch.fx.experimental.proxy_tensor import make_fx
 import mtp
 import mtpk_ops  # noqa: F401  (registers the ops)
 
-OPS = ("fused_moe", "route", "argmax_rows", "greedy_accept", "rejection_sample")
+OPS = ("fused_moe", "moe_layer", "route", "argmax_rows", "greedy_accept", "rejection_sample")
 
 
 def test_schemas():
@@ -21,6 +21,7 @@ def test_schemas():
                                      "Tensor down, Tensor down_scale, Tensor a_expert, Tensor a_weight")
     assert "Tensor? shared=None, Tensor? shared_gate=None) -> Tensor" in s["fused_moe"]
     assert s["route"].endswith("-> (Tensor, Tensor)")
+    assert s["moe_layer"].endswith("SymInt expert_hi) -> (Tensor, Tensor, Tensor)")
     assert s["greedy_accept"].count("Tensor,") == 10
     assert s["rejection_sample"].endswith("float temperature) -> (Tensor, Tensor, Tensor, Tensor)")
 
@@ -34,6 +35,12 @@ def test_fake_kernels():
             torch.empty(e, h, 4, dtype=torch.uint8), torch.empty(6 * k, dtype=torch.int32),
             torch.empty(6 * k), k, 0, e)
         assert out.shape == (6, h) and out.dtype == torch.bfloat16
+        lo, lw, li = torch.ops.mtpk.moe_layer(
+            torch.empty(6, h, dtype=torch.bfloat16), torch.empty(e + 1, h, dtype=torch.bfloat16),
+            torch.empty(512, h, dtype=torch.bfloat16), torch.empty(h, 256, dtype=torch.bfloat16),
+            torch.empty(e, 256, h // 2, dtype=torch.uint8), torch.empty(e, 256, h // 32, dtype=torch.uint8),
+            torch.empty(e, h, 64, dtype=torch.uint8), torch.empty(e, h, 4, dtype=torch.uint8), k, 0, e)
+        assert (lo.shape, lo.dtype, lw.shape, li.dtype) == ((6, h), torch.bfloat16, (6, k), torch.int32)
         w, i = torch.ops.mtpk.route(torch.empty(6, e + 1, dtype=torch.bfloat16), e, k, torch.int32)
         assert (w.shape, w.dtype, i.shape, i.dtype) == ((6, k), torch.float32, (6, k), torch.int32)
         am = torch.ops.mtpk.argmax_rows(torch.empty(2, 3, v))
