@@ -61,6 +61,14 @@ int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
   return status_of(hipGetLastError());
 }
 
+// The wide form (`gemm_wide`): TT token tiles in one row group, 8 waves x 2 weight streams,
+// 128-K chunks (2 x TT x 16 padded 256-byte rows of LDS: 104 KiB at TT = 12, one workgroup per CU).
+template <int TT>
+__global__ __launch_bounds__(8 * kWave, 2) void k_gemm_wide(GemmArgs a) {
+  __shared__ __attribute__((aligned(16))) uint8_t smem[GemmSmem<TT, 8, 128>::kBytes];
+  gemm_tile<TT, 2, 8, false, 128>(a, smem, blockIdx.x, blockIdx.y);
+}
+
 // Split-K reduction: out[m, col] = epilogue(sum over ks of part[ks, m, .]) in split order.
 __global__ __launch_bounds__(256) void k_gemm_reduce(const float* __restrict__ part, int KS, int M,
                                                      int cols, int epi, void* __restrict__ out,
@@ -156,7 +164,14 @@ int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, i
   if ((int64_t)(tiles + 7) / 8 * 8 * a.RG > INT32_MAX) return MTPK_EINVAL;
   const hipStream_t st = (hipStream_t)stream;
   const int tt = gemm_tt(m);
-  if (epilogue == kEpiSilu)
+  if (gemm_wide(m, n, epilogue)) {
+    a.RG = 1;
+    const int wtt = (int)((m + 15) / 16);
+    if (wtt <= 8)
+      hipLaunchKernelGGL(k_gemm_wide<8>, dim3((unsigned)tiles), dim3(8 * kWave), 0, st, a);
+    else
+      hipLaunchKernelGGL(k_gemm_wide<12>, dim3((unsigned)tiles), dim3(8 * kWave), 0, st, a);
+  } else if (epilogue == kEpiSilu)
     launch_gemm_tt<2, true>(a, tt, tiles, st);
   else
     launch_gemm_tt<1, false>(a, tt, tiles, st);

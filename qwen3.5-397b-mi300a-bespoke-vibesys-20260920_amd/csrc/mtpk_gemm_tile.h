@@ -8,13 +8,7 @@
 
 namespace mtpk {
 
-constexpr int kGemmKC = 256;                 // K per staged chunk
-constexpr int kGemmSteps = kGemmKC / 32;     // MFMA steps per chunk
-// Ring depth in steps. The chunk-end wait for the staged token rows also waits for every ring
-// load issued before them (vmcnt retires in order), so a deeper ring than one chunk's steps + 1
-// would be drained at each chunk boundary.
-constexpr int kGemmRing = 8;
-constexpr int kGemmRow = kGemmKC * 2 + 16;   // LDS bytes of one token row (padded)
+constexpr int kGemmKC = 256;  // K per staged chunk (the default; the wide form stages 128)
 enum { kEpiStore = 0, kEpiSilu = 1, kEpiArgmax = 2 };
 
 struct GemmArgs {
@@ -29,9 +23,9 @@ struct GemmArgs {
 };
 
 // LDS of one tile: two staging buffers of TT token tiles, then the argmax epilogue's keys.
-template <int TT, int NW>
+template <int TT, int NW, int KC = kGemmKC>
 struct GemmSmem {
-  static constexpr int kStage = TT * 16 * kGemmRow;
+  static constexpr int kStage = TT * 16 * (KC * 2 + 16);
   static constexpr int kKeys = 2 * kStage;
   static constexpr int kBytes = kKeys + NW * TT * 16 * 8;
 };
@@ -41,15 +35,21 @@ struct GemmSmem {
 // 16 NW S weight rows, and every staged activation read feeds S MFMAs. Only S = 1 is launched
 // outside the SiLU pairing: two streams at 48 rows on the LM head measured 471 us against 437
 // (half the waves resident, for half the LDS reads per weight byte).
-template <int TT, int S, int NW, bool SILU>
+template <int TT, int S, int NW, bool SILU, int KC = kGemmKC>
 __device__ inline void gemm_tile(const GemmArgs& a, uint8_t* smem, int bx, int by) {
   static_assert(!SILU || S == 2, "the SiLU epilogue pairs two streams");
   constexpr int NT = NW * kWave;
-  constexpr int kRing = kGemmRing;
-  typedef uint8_t StageBuf[TT * 16 * kGemmRow];
+  constexpr int kSteps = KC / 32;          // MFMA steps per chunk
+  // Ring depth: one chunk of steps. The chunk-end wait for the staged token rows also waits for
+  // every ring load issued before them (vmcnt retires in order), so a deeper ring would be
+  // drained at each chunk boundary.
+  constexpr int kRing = kSteps;
+  constexpr int kRow = KC * 2 + 16;        // LDS bytes of one token row (padded)
+  constexpr int kPieces = KC / 8;          // 16-byte pieces of a token row per chunk
+  typedef uint8_t StageBuf[TT * 16 * kRow];
   typedef uint64_t KeyRow[TT * 16];
   StageBuf* xs = reinterpret_cast<StageBuf*>(smem);
-  KeyRow* kred = reinterpret_cast<KeyRow*>(smem + GemmSmem<TT, NW>::kKeys);
+  KeyRow* kred = reinterpret_cast<KeyRow*>(smem + GemmSmem<TT, NW, KC>::kKeys);
   const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
   // Workgroup -> (weight tile, row group). With several row groups, the groups of one tile
@@ -68,8 +68,8 @@ __device__ inline void gemm_tile(const GemmArgs& a, uint8_t* smem, int bx, int b
   const int ks = by;
   const int m0 = rg * 16 * TT;                             // first token row of this group
   const int Mg = a.M - m0 < 16 * TT ? a.M - m0 : 16 * TT;  // its rows
-  const int kc_per = a.K / kGemmKC / a.KS;  // chunks of this split
-  const int k0 = ks * kc_per * kGemmKC;
+  const int kc_per = a.K / KC / a.KS;  // chunks of this split
+  const int k0 = ks * kc_per * KC;
   const int nchunk = kc_per;
   // weight rows of this wave: stream s at r0 + s N/2 (SILU) or r0 + 16 NW s
   const int r0 = tile * 16 * NW * (SILU ? 1 : S) + 16 * wave + ln.c;
@@ -85,32 +85,32 @@ __device__ inline void gemm_tile(const GemmArgs& a, uint8_t* smem, int bx, int b
   const rsrc_t rx = make_rsrc(a.x, (uint32_t)((int64_t)a.M * a.K * 2));
   // ring step st of this split: K = k0 + 32 st + 8 g .. + 7 of each stream's row
   auto issue = [&](u32x4_t* v, int st) {
-    const bool in = st < nchunk * kGemmSteps;
+    const bool in = st < nchunk * kSteps;
 #pragma unroll
     for (int s = 0; s < S; ++s) {
       const uint32_t off = (uint32_t)(((int64_t)wrow[s] * a.K + k0 + 32 * st + 8 * ln.g) * 2);
       v[s] = buf16(rw, (wok[s] && in) ? off : kOutOfRange);
     }
   };
-  // staging: load j moves 16 bytes of token row (NT j + tid) / 32, column (tid % 32) * 16
-  constexpr int kSL = TT * 16 * 32 / NT;  // 16-byte loads per thread per chunk
-  static_assert(kSL * NT == TT * 16 * 32, "staging split");
-  static_assert(kRing == kGemmSteps, "one ring slot per step of a chunk");
+  // staging: load j moves 16 bytes of token row (NT j + tid) / kPieces, column
+  // ((NT j + tid) % kPieces) * 16
+  constexpr int kSL = TT * 16 * kPieces / NT;  // 16-byte loads per thread per chunk
+  static_assert(kSL * NT == TT * 16 * kPieces, "staging split");
   u32x4_t sreg[kSL];
   auto stage_load = [&](int c) {
 #pragma unroll
     for (int j = 0; j < kSL; ++j) {
-      const int p = j * NT + tid, row = p >> 5, col = p & 31;
+      const int p = j * NT + tid, row = p / kPieces, col = p % kPieces;
       const bool ok = c < nchunk && row < Mg;
-      sreg[j] = buf16(rx, ok ? (uint32_t)(((int64_t)(m0 + row) * a.K + k0 + c * kGemmKC + col * 8) * 2)
+      sreg[j] = buf16(rx, ok ? (uint32_t)(((int64_t)(m0 + row) * a.K + k0 + c * KC + col * 8) * 2)
                              : kOutOfRange);
     }
   };
   auto stage_store = [&](int b) {
 #pragma unroll
     for (int j = 0; j < kSL; ++j) {
-      const int p = j * NT + tid, row = p >> 5, col = p & 31;
-      lds16_store(&xs[b][row * kGemmRow + col * 16], sreg[j]);
+      const int p = j * NT + tid, row = p / kPieces, col = p % kPieces;
+      lds16_store(&xs[b][row * kRow + col * 16], sreg[j]);
     }
   };
 
@@ -135,19 +135,19 @@ __device__ inline void gemm_tile(const GemmArgs& a, uint8_t* smem, int bx, int b
   do {
     const uint8_t* buf = xs[c & 1];
 #pragma unroll
-    for (int st = 0; st < kGemmSteps; ++st) {
+    for (int st = 0; st < kSteps; ++st) {
       u32x4_t* slot = ring[st];
-      const uint8_t* arow = buf + ln.c * kGemmRow + (32 * st + 8 * ln.g) * 2;
+      const uint8_t* arow = buf + ln.c * kRow + (32 * st + 8 * ln.g) * 2;
       u32x4_t av[TT];
 #pragma unroll
-      for (int t = 0; t < TT; ++t) av[t] = lds16(arow + t * 16 * kGemmRow);
+      for (int t = 0; t < TT; ++t) av[t] = lds16(arow + t * 16 * kRow);
 #pragma unroll
       for (int s = 0; s < S; ++s)
 #pragma unroll
         for (int t = 0; t < TT; ++t)
           acc[s][t] = mfma16x16x32(as_bf16x8(av[t]), as_bf16x8(slot[s]), acc[s][t]);
       ring_fence();
-      issue(slot, c * kGemmSteps + st + kRing);
+      issue(slot, c * kSteps + st + kRing);
       ring_fence();
     }
     if (c + 1 < nchunk) stage_store((c + 1) & 1);
@@ -254,15 +254,25 @@ inline int gemm_waves(int64_t m, int64_t n, int epi) {
   return (m + 15) / 16 >= 3 && cols / 128 >= 2 * (int64_t)device_cu_count() ? 8 : 4;
 }
 
+// The wide form for 65..192 token rows on wide N (the verify LM head): one row group of TT =
+// ceil(M / 16) token tiles, 8 waves with two weight streams each (256 weight rows per tile), token
+// rows staged in 128-K chunks. Every weight is read once for all rows; the 64-row groups would
+// stream the tile's weights once per group.
+constexpr int kWideMaxRows = 192;
+inline bool gemm_wide(int64_t m, int64_t n, int epi) {
+  return m > 64 && m <= kWideMaxRows && epi != kEpiSilu &&
+         gemm_cols(n, epi) >= 256 * 2 * (int64_t)device_cu_count();
+}
+
 inline int64_t gemm_tiles(int64_t m, int64_t n, int epi) {
-  const int64_t rows = 16 * gemm_waves(m, n, epi);
+  const int64_t rows = gemm_wide(m, n, epi) ? 256 : 16 * gemm_waves(m, n, epi);
   return (gemm_cols(n, epi) + rows - 1) / rows;
 }
 
 // Split count: a power of two dividing K / 256, enough workgroups for ~3 per CU, at least 4
 // chunks per split; argmax takes no split.
 inline int gemm_splits(int64_t m, int64_t n, int64_t k, int epi) {
-  if (epi == kEpiArgmax) return 1;
+  if (epi == kEpiArgmax || gemm_wide(m, n, epi)) return 1;
   const int64_t tiles = gemm_tiles(m, n, epi);
   const int64_t chunks = k / kGemmKC;
   const int64_t wgs = tiles * gemm_groups(m);
