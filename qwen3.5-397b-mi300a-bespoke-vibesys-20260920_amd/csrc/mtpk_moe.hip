@@ -896,8 +896,8 @@ struct StageGeom {
 
 // gate_up, LDS variant (bf16 x, hi/lo intermediate, chunked scales). Item = (unit, 4 tiles of
 // 16 intermediate rows), wave w takes tile 4q + w. Chunks of 512 K = 4 trips = one ring turn.
-template <int D>
-__global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
+template <int D, int NW>
+__global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
     const uint16_t* __restrict__ x, int64_t x_elems, int K, const uint8_t* __restrict__ wq,
     const uint8_t* __restrict__ ws, int I, UnitSrc src, int top_k, uint16_t* __restrict__ inter,
     int64_t inter_plane) {
@@ -905,7 +905,11 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
   static_assert(D == TPC, "one ring turn per staged chunk");
   using G = StageGeom<KC, 1>;
   __shared__ __attribute__((aligned(16))) uint8_t xs[2][G::kBuf];
-  const int ntile = I >> 4, ngroup = (ntile + kMoeWaves - 1) / kMoeWaves;
+  // with 8 waves the 32 scale rows of each wave no longer fit in the idle chunk buffer
+  constexpr int kScaleScratch = NW * 32 * 128 + NW * 16;
+  __shared__ __attribute__((aligned(16))) uint8_t sscr[NW == 4 ? 16 : kScaleScratch];
+  constexpr int RPW = 16 / NW;  // staged token rows per wave
+  const int ntile = I >> 4, ngroup = (ntile + NW - 1) / NW;
   const int n_items = min(sload(src.n_units, 0), src.max_units) * ngroup;
   const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
   const MoeLane ln = moe_lane(lane);
@@ -925,7 +929,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
     int32_t om[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) om[i] = src.sorted[first + min(moe_out_slot(ln.g, i), cnt - 1)];
-    const int nt_raw = q * kMoeWaves + wave;
+    const int nt_raw = q * NW + wave;
     const bool wave_ok = nt_raw < ntile;
     const int nt = wave_ok ? nt_raw : ntile - 1;
     const int eu = e;
@@ -934,22 +938,22 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
     const uint32_t row = (uint32_t)(nt * 16 + ln.c);
     const uint32_t og = row * (uint32_t)row_bytes, ou = og + (uint32_t)I * (uint32_t)row_bytes;
     const uint32_t osg = row * (uint32_t)nb, osu = osg + (uint32_t)(I * nb);
-    uint32_t sx[4];
+    uint32_t sx[RPW];
 #pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int r = 4 * k + wave;
+    for (int k = 0; k < RPW; ++k) {
+      const int r = NW * k + wave;
       const int tok = sload(src.sorted, first + min(r, cnt - 1)) / top_k;
       sx[k] = r < cnt ? (uint32_t)tok * (uint32_t)K * 2u + (uint32_t)lane * 16u : kOutOfRange;
     }
-    u32x4_t sreg[4];
+    u32x4_t sreg[RPW];
     auto stage_load = [&](int c) {
       const uint32_t bad = (uint32_t)!(c < nchunk) << 31;
 #pragma unroll
-      for (int k = 0; k < 4; ++k) sreg[k] = buf16(rx, (sx[k] + (uint32_t)c * (KC * 2)) | bad);
+      for (int k = 0; k < RPW; ++k) sreg[k] = buf16(rx, (sx[k] + (uint32_t)c * (KC * 2)) | bad);
     };
     auto stage_store = [&](int b) {
 #pragma unroll
-      for (int k = 0; k < 4; ++k) lds16_store(&xs[b][(4 * k + wave) * G::kRow + lane * 16], sreg[k]);
+      for (int k = 0; k < RPW; ++k) lds16_store(&xs[b][(NW * k + wave) * G::kRow + lane * 16], sreg[k]);
     };
 
     auto issue = [&](u32x4_t& wg, u32x4_t& wu, int tr) {
@@ -1001,11 +1005,14 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_gate_up_lds(
     for (int s = 0; s < D; ++s) issue(rg[s], ru[s], s);
     ring_fence();
     {
-      uint8_t* scr = xs[1] + wave * (32 * nb);
+      uint8_t* scr = (NW == 4 ? xs[1] : sscr) + wave * (32 * nb);
+      uint8_t* spare = (NW == 4 ? xs[1] : sscr) + NW * 32 * nb + wave * 16;
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
+        // lanes past the wave's scale rows store their (zero) load to a spare 16 bytes past the
+        // slices instead of branching around the store
         const int idx = k * kWave + lane;
-        if (idx < units) lds16_store(scr + idx * 16, sload4[k]);
+        lds16_store(idx < units ? scr + idx * 16 : spare, sload4[k]);
       }
       __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave reads back only its own slice
       const uint32_t sel01 = lane_byte_sel01(ln.g);
@@ -1515,11 +1522,29 @@ bool chunked_scales(int K, int split, int D) {
 }
 
 // Unit-mode gate_up with the activation rows staged in LDS (bf16 x, K a multiple of 512).
+// Batches of at least this many tokens run gate_up with 8-wave workgroups (one staged copy of
+// the unit's activation rows for 128 intermediate rows, two workgroups per CU): measured 4-5%
+// faster at 192 rows (Zipf routing, 393 units), slower at 32 rows, where the 8 items per unit
+// leave the grid a short tail of a few items per workgroup.
+constexpr int64_t kGateUpWideTokens = 96;
+
 int launch_gate_up_lds(const uint16_t* x, int64_t x_elems, int K, const uint8_t* wq,
                        const uint8_t* ws, int I, const UnitSrc& src, int64_t max_units, int top_k,
-                       uint16_t* inter, int64_t inter_plane, hipStream_t st) {
+                       uint16_t* inter, int64_t inter_plane, int64_t tokens, hipStream_t st) {
+  if (tokens >= kGateUpWideTokens) {
+    static int occ8 = 0;
+    auto kern = k_moe_gate_up_lds<4, 8>;
+    const int64_t items = max_units * (((I >> 4) + 7) / 8);
+    if (occ8 == 0) occ8 = occupancy_per_cu(kern, 8 * kWave);
+    const int64_t cap = (int64_t)device_cu_count() * occ8;
+    const int grid = (int)(items < cap ? items : cap);
+    if (grid == 0) return 0;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(8 * kWave), 0, st, x, x_elems, K, wq, ws, I, src,
+                       top_k, inter, inter_plane);
+    return status_of(hipGetLastError());
+  }
   static int occ = 0;
-  auto kern = k_moe_gate_up_lds<4>;
+  auto kern = k_moe_gate_up_lds<4, 4>;
   const int64_t items = max_units * (((I >> 4) + kMoeWaves - 1) / kMoeWaves);
   const int grid = grid_for(kern, items, occ);
   if (grid == 0) return 0;
@@ -1535,7 +1560,7 @@ int launch_gate_up(int xp, const uint16_t* x, int64_t x_plane, int K, const uint
   const bool split = max_units * (I >> 4) < (int64_t)device_cu_count() * 16;
   if (xp == 1 && !split && K % 512 == 0 && K <= 4096)
     return launch_gate_up_lds(x, x_plane, K, wq, ws, I, src, max_units, top_k, inter, inter_plane,
-                              st);
+                              x_plane / K, st);
 #define MTPK_GU(XP_, OP_, SP_, D_)                                                           \
   (chunked_scales(K, SP_, D_)                                                                \
        ? launch_gate_up_t<XP_, OP_, SP_, D_, true>(x, x_plane, K, wq, ws, I, src, max_units, \
