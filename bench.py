@@ -85,6 +85,11 @@ def layer_bytes(m, dl):
     return dl * EXPERT_BYTES + 2 * m * H * 2
 
 
+def gate_up_kernel(m: int) -> str:
+    """The gate_up kernel the unit path launches at m rows (8-wave workgroups from 96 rows)."""
+    return "k_moe_gate_up_lds<4, 8>" if m >= 96 else "k_moe_gate_up_lds<4, 4>"
+
+
 def profiled_traffic(kernel: str) -> float | None:
     """HBM bytes per launch of `kernel` (fetched + written, calibrated) from the committed
     rocprofv3 PMC summary profiles/moe_kernels_mi355x.md, or None if it has no row for it."""
@@ -278,13 +283,13 @@ def main() -> int:
         "gbs_graph": {k: round(v["gbs"], 1) for k, v in results.items()},
         "d_live": {k: round(v["d_live_mean"], 1) for k, v in results.items()},
         "roofline": {
-            "kernel": "k_moe_gate_up_single<1,2,true> (direct)" if direct else "k_moe_gate_up_lds<4>",
+            "kernel": "k_moe_gate_up_single<1,2,true> (direct)" if direct else gate_up_kernel(head_m),
             "bound": "hbm",
             "achieved": round(gu_gbs, 1),
             "peak": PEAK_GBS,
             "unit": "GB/s",
             "frac": round(gu_gbs / PEAK_GBS, 4),
-            "traffic": None if direct else profiled_traffic("mtpk::k_moe_gate_up_lds<4>"),
+            "traffic": None if direct else profiled_traffic("mtpk::" + gate_up_kernel(head_m)),
             "traffic_source": "profiles/moe_kernels_mi355x.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
                               "copy-calibrated)",
             "avg_us": round(gu_ms * 1e3, 2),
