@@ -141,6 +141,21 @@ int mtpk_moe_combine(const float* y, const void* a_expert, int expert_dtype, con
                      int weight_dtype, int64_t tokens, int top_k, int64_t hidden, int expert_lo,
                      int expert_hi, void* out, int out_dtype, void* stream);
 
+/* Combine of rows that already carry their routing weight: replaces `bw_combine` and
+ * `bw_combine_glue` (mxfp4_gemv.py:2440-2488, kernels :2240-2312), whose y comes from a down
+ * projection that applies the weight in its epilogue (moe_hip.hip:401, mxfp4_gemv.py:2232-2236).
+ * out[t, n] = sum over t's live assignments (expert in [expert_lo, expert_hi) and a_weight != 0;
+ * dead rows of y are never read, so y needs no zero fill) of y[t*top_k + j, n], in j order, in
+ * f32; tokens with none get zeros. y f32 (16-byte aligned) or bf16 (8-byte aligned)
+ * [tokens*top_k, hidden], hidden % 4 == 0. With shared != NULL the shared expert's term is
+ * added as in mtpk_fused_moe_shared (routed sum, sigmoid(shared_gate[t * gate_stride]) and the
+ * product each rounded to out_dtype, then the add); shared = NULL is `bw_combine`. */
+int mtpk_moe_combine_rows(const void* y, int y_dtype, const void* a_expert, int expert_dtype,
+                          const void* a_weight, int weight_dtype, int64_t tokens, int top_k,
+                          int64_t hidden, int expert_lo, int expert_hi, const void* shared,
+                          int shared_dtype, const void* shared_gate, int gate_dtype,
+                          int64_t gate_stride, void* out, int out_dtype, void* stream);
+
 /* f32 [n] -> `nplanes` bf16 planes [nplanes, n] whose sum is the input (2 planes: 16
  * significant bits; 3 planes: all 24). */
 int mtpk_split_planes(const float* src, int64_t n, int nplanes, uint16_t* planes, void* stream);

@@ -70,6 +70,11 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         [c_void_p, c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int64, c_int, c_int,
          c_void_p, c_int, c_void_p],
     ),
+    "mtpk_moe_combine_rows": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int64, c_int, c_int,
+         c_void_p, c_int, c_void_p, c_int, c_int64, c_void_p, c_int, c_void_p],
+    ),
     "mtpk_split_planes": (c_int, [c_void_p, c_int64, c_int, c_void_p, c_void_p]),
     "mtpk_fused_moe": (
         c_int,

@@ -1323,6 +1323,63 @@ __global__ __launch_bounds__(256) void k_moe_combine(
   for (int c = 0; c < 4; ++c) store_float(out, odt, (int64_t)t * H + n + c, acc[c]);
 }
 
+// The combine of rows that already carry their routing weight (the staging of a down
+// projection that applies the weight in its epilogue): out[t, n..n+3] = sum_j y[t*top_k + j]
+// over live assignments (expert in [lo, hi) and weight != 0; dead rows are never read), in j
+// order, in fp32, then the shared term when there is one. y is f32 or bf16 (YB).
+template <bool YB>
+__global__ __launch_bounds__(256) void k_moe_combine_rows(
+    const void* __restrict__ y, const void* __restrict__ a_expert, int edt,
+    const void* __restrict__ a_weight, int wdt, int top_k, int H, int lo, int hi,
+    void* __restrict__ out, int odt, SharedTerm st) {
+  const int t = blockIdx.y;
+  const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (n >= H) return;
+  float acc[4] = {0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < top_k; j0 += 4) {
+    bool live[4];
+    int64_t a[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int j = j0 + q;
+      a[q] = (int64_t)t * top_k + j;
+      live[q] = false;
+      if (j < top_k) {
+        const int64_t e = load_index(a_expert, edt, a[q]);
+        live[q] = e >= lo && e < hi && load_float(a_weight, wdt, a[q]) != 0.f;
+      }
+    }
+    float v[4][4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      if (YB) {
+        uint2 b = make_uint2(0u, 0u);
+        if (live[q]) b = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(y) + a[q] * H + n);
+        v[q][0] = bits_f32(b.x << 16);
+        v[q][1] = bits_f32(b.x & 0xffff0000u);
+        v[q][2] = bits_f32(b.y << 16);
+        v[q][3] = bits_f32(b.y & 0xffff0000u);
+      } else {
+        const u32x4_t b = live[q] ? ld16(static_cast<const float*>(y) + a[q] * H + n) : zero16();
+#pragma unroll
+        for (int c = 0; c < 4; ++c) v[q][c] = bits_f32(b[c]);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+      if (live[q])
+#pragma unroll
+        for (int c = 0; c < 4; ++c) acc[c] += v[q][c];
+  }
+  if (shared_active(st)) {
+    const float gs = shared_gate(st, t, odt);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) acc[c] = add_shared(st, gs, acc[c], (int64_t)t * H + n + c, odt);
+  }
+#pragma unroll
+  for (int c = 0; c < 4; ++c) store_float(out, odt, (int64_t)t * H + n + c, acc[c]);
+}
+
 // The shared term over a routed output already in `out` (the direct path, whose down kernel
 // writes the routed sum itself).
 __global__ __launch_bounds__(256) void k_moe_shared_glue(void* __restrict__ out, int odt, int H,
@@ -1858,6 +1915,30 @@ int mtpk_moe_combine(const float* y, const void* a_expert, int expert_dtype, con
   hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
                      expert_hi, out, out_dtype, SharedTerm{});
+  return status_of(hipGetLastError());
+}
+
+int mtpk_moe_combine_rows(const void* y, int y_dtype, const void* a_expert, int expert_dtype,
+                          const void* a_weight, int weight_dtype, int64_t tokens, int top_k,
+                          int64_t hidden, int expert_lo, int expert_hi, const void* shared,
+                          int shared_dtype, const void* shared_gate, int gate_dtype,
+                          int64_t gate_stride, void* out, int out_dtype, void* stream) {
+  if (!y || !a_expert || !a_weight || !out) return MTPK_EINVAL;
+  if (!dtype_float_ok(y_dtype) || !dtype_index_ok(expert_dtype) || !dtype_float_ok(weight_dtype) ||
+      !dtype_float_ok(out_dtype))
+    return MTPK_EINVAL;
+  if (tokens < 0 || tokens > 65535 || hidden <= 0 || hidden % 4 || top_k <= 0) return MTPK_EINVAL;
+  if (reinterpret_cast<uintptr_t>(y) & (y_dtype == MTPK_F32 ? 15u : 7u)) return MTPK_EINVAL;
+  if (shared && (!shared_gate || !dtype_float_ok(shared_dtype) || !dtype_float_ok(gate_dtype) ||
+                 gate_stride < 0))
+    return MTPK_EINVAL;
+  if (tokens == 0) return 0;
+  const SharedTerm st{shared, shared_dtype, shared_gate, gate_dtype, gate_stride};
+  const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
+  auto kern = y_dtype == MTPK_F32 ? k_moe_combine_rows<false> : k_moe_combine_rows<true>;
+  hipLaunchKernelGGL(kern, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert, expert_dtype,
+                     a_weight, weight_dtype, top_k, (int)hidden, expert_lo, expert_hi, out,
+                     out_dtype, st);
   return status_of(hipGetLastError());
 }
 

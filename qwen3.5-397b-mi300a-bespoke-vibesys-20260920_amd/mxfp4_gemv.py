@@ -22,7 +22,6 @@ from __future__ import annotations
 
 import os
 from collections.abc import Callable
-from dataclasses import dataclass
 
 import torch
 
@@ -438,55 +437,116 @@ class MoeLayerRunner:
 # ---------------------------------------------------------------- staged pieces
 
 
-@dataclass
 class BwPlan:
-    """Work list of one MoE call (`mxfp4_gemv.BwPlan`'s role): expert-grouped assignment ids,
-    units `(local expert, first position, count <= 16)` and their device-side count."""
+    """Device work list of one staged MoE call (`mxfp4_gemv.BwPlan`, mxfp4_gemv.py:2320-2346):
+    `sorted` i32 [tokens * top_k] (live assignment ids grouped by local expert), `unit` i32
+    [3 * u_max] of (local expert, first position in `sorted`, count <= block_t) and the
+    device-side `n_units` i32 [1]. Every shape is a Python int, so a captured graph replays with
+    the same buffers; `bw_prep` rewrites all of them, and none needs zeroing.
 
-    sorted: torch.Tensor
-    unit: torch.Tensor
-    n_units: torch.Tensor
-    u_max: int
+    `block_t` must be 16 (`UNIT_TOKENS`: one MFMA N tile per unit). `u_max` is the library's
+    own bound (`mtpk_moe_max_units`). `cursor` and `xp` are None: the counting sort keeps its
+    counters in LDS, and these kernels read x in its own K order, so there is no permuted
+    activation copy to make (`permute_x` is accepted for the caller's sake and changes nothing).
+    `reduction` and `dtype` are x's width and dtype, checked by `bw_prep`."""
+
+    def __init__(self, tokens: int, top_k: int, reduction: int, local_experts: int,
+                 device: torch.device, dtype: torch.dtype, *, block_t: int = UNIT_TOKENS,
+                 permute_x: bool = True) -> None:
+        if block_t != UNIT_TOKENS:
+            raise ValueError(f"BwPlan: block_t must be {UNIT_TOKENS} (tokens per work unit), got {block_t}")
+        if tokens < 0 or top_k <= 0 or local_experts <= 0:
+            raise ValueError(f"BwPlan: bad sizes tokens={tokens} top_k={top_k} local_experts={local_experts}")
+        assignments = tokens * top_k
+        self.tokens, self.top_k, self.reduction, self.dtype = tokens, top_k, reduction, dtype
+        self.local_experts, self.block_t = local_experts, block_t
+        self.u_max = int(_mtpk.lib().mtpk_moe_max_units(assignments, local_experts))
+        self.cursor = None
+        self.sorted = torch.empty(max(assignments, 1), dtype=torch.int32, device=device)
+        self.unit = torch.empty(max(3 * self.u_max, 3), dtype=torch.int32, device=device)
+        self.n_units = torch.empty(1, dtype=torch.int32, device=device)
+        self.xp = None
 
 
-def bw_prep(a_expert: torch.Tensor, a_weight: torch.Tensor, expert_range: tuple[int, int]) -> BwPlan:
-    """Counting sort of live assignments by local expert (`mtpk_moe_prep`); no host sync."""
-    device = _mtpk.require_device(a_expert, a_weight)
+def bw_prep(x: torch.Tensor, a_expert: torch.Tensor, a_weight: torch.Tensor,
+            expert_range: tuple[int, int], plan: BwPlan) -> None:
+    """Routing work list into `plan` (`mxfp4_gemv.bw_prep`, mxfp4_gemv.py:2349-2376): one
+    counting-sort launch (`mtpk_moe_prep`) over the live assignments (expert in `expert_range`
+    and weight != 0); no host sync."""
+    device = _mtpk.require_device(x, a_expert, a_weight, plan.sorted)
     lo, hi = expert_range
     a = a_expert.numel()
-    lib = _mtpk.lib()
-    u_max = int(lib.mtpk_moe_max_units(a, hi - lo))
-    sorted_ = torch.full((max(a, 1),), -1, dtype=torch.int32, device=device)
-    unit = torch.zeros(max(3 * u_max, 3), dtype=torch.int32, device=device)
-    n_units = torch.zeros(1, dtype=torch.int32, device=device)
+    if x.dim() != 2 or x.shape != (plan.tokens, plan.reduction) or x.dtype != plan.dtype:
+        raise ValueError(f"bw_prep: x {tuple(x.shape)} {x.dtype} does not match the plan "
+                         f"({plan.tokens}, {plan.reduction}) {plan.dtype}")
+    if a != plan.tokens * plan.top_k or a_weight.numel() != a:
+        raise ValueError(f"bw_prep: routing has {a} / {a_weight.numel()} entries, the plan "
+                         f"{plan.tokens * plan.top_k}")
+    if not 0 <= hi - lo <= plan.local_experts:
+        raise ValueError(f"bw_prep: expert_range {expert_range} spans more than the plan's "
+                         f"{plan.local_experts} local experts")
     _mtpk.check(
-        lib.mtpk_moe_prep(
+        _mtpk.lib().mtpk_moe_prep(
             a_expert.data_ptr(), _mtpk.index_code(a_expert.dtype),
             a_weight.data_ptr(), _mtpk.float_code(a_weight.dtype),
-            a, lo, hi, sorted_.data_ptr(), unit.data_ptr(), u_max, n_units.data_ptr(),
-            _mtpk.stream_of(device),
+            a, lo, hi, plan.sorted.data_ptr(), plan.unit.data_ptr(), plan.u_max,
+            plan.n_units.data_ptr(), _mtpk.stream_of(device),
         ),
         "mtpk_moe_prep",
     )  # fmt: skip
-    return BwPlan(sorted_, unit, n_units, u_max)
 
 
-def bw_combine(y: torch.Tensor, routing: tuple[torch.Tensor, torch.Tensor], top_k: int,
-               expert_range: tuple[int, int], out: torch.Tensor) -> torch.Tensor:
-    """`out[t] = sum_j w[t, j] * y[t*top_k + j]` over live assignments, fixed j order."""
-    a_expert, a_weight = routing
-    device = _mtpk.require_device(y, a_expert, a_weight, out)
+def _combine_rows(y, a_expert, a_weight, expert_range, top_k, out, shared, gate, what) -> None:
     lo, hi = expert_range
     tokens, hidden = out.shape
+    device = _mtpk.require_device(y, a_expert, a_weight, out)
+    if y.shape != (tokens * top_k, hidden) or not y.is_contiguous() or not out.is_contiguous():
+        raise ValueError(f"{what}: y must be a contiguous [{tokens * top_k}, {hidden}] tensor and "
+                         f"out contiguous, got y {tuple(y.shape)}")
+    if a_expert.numel() != tokens * top_k or a_weight.numel() != tokens * top_k:
+        raise ValueError(f"{what}: routing must have {tokens * top_k} entries")
+    sp, sd, gp, gd, gs = None, _mtpk.F32, None, _mtpk.F32, 0
+    if shared is not None:
+        _mtpk.require_device(shared, gate)
+        sp, sd = shared.data_ptr(), _mtpk.float_code(shared.dtype)
+        gp, gd, gs = gate.data_ptr(), _mtpk.float_code(gate.dtype), gate.stride(0)
     _mtpk.check(
-        _mtpk.lib().mtpk_moe_combine(
-            y.data_ptr(), a_expert.data_ptr(), _mtpk.index_code(a_expert.dtype),
-            a_weight.data_ptr(), _mtpk.float_code(a_weight.dtype), tokens, top_k, hidden,
-            lo, hi, out.data_ptr(), _mtpk.float_code(out.dtype), _mtpk.stream_of(device),
+        _mtpk.lib().mtpk_moe_combine_rows(
+            y.data_ptr(), _mtpk.float_code(y.dtype), a_expert.data_ptr(),
+            _mtpk.index_code(a_expert.dtype), a_weight.data_ptr(), _mtpk.float_code(a_weight.dtype),
+            tokens, top_k, hidden, lo, hi, sp, sd, gp, gd, gs, out.data_ptr(),
+            _mtpk.float_code(out.dtype), _mtpk.stream_of(device),
         ),
-        "mtpk_moe_combine",
+        "mtpk_moe_combine_rows",
     )  # fmt: skip
-    return out
+
+
+def bw_combine(y: torch.Tensor, a_expert: torch.Tensor, a_weight: torch.Tensor,
+               expert_range: tuple[int, int], top_k: int, out: torch.Tensor) -> None:
+    """`out[t] = sum_j y[t*top_k + j]` over t's live assignments, in j order, in fp32
+    (`mxfp4_gemv.bw_combine`, mxfp4_gemv.py:2440-2446): y's rows already carry the routing
+    weight, and dead rows are never read (no zero fill needed). One launch
+    (`mtpk_moe_combine_rows`); y f32 or bf16, out f32 or bf16."""
+    _combine_rows(y, a_expert, a_weight, expert_range, top_k, out, None, None, "bw_combine")
+
+
+def bw_combine_glue(y: torch.Tensor, a_expert: torch.Tensor, a_weight: torch.Tensor,
+                    expert_range: tuple[int, int], top_k: int, shared: torch.Tensor,
+                    gate: torch.Tensor, out: torch.Tensor) -> None:
+    """`bw_combine` plus the shared expert's term in the same launch
+    (`mxfp4_gemv.bw_combine_glue`, mxfp4_gemv.py:2449-2488): `out[t] = routed_sum +
+    sigmoid(gate[t, 0]) * shared[t]`, with the routed sum, the sigmoid and the product each
+    rounded to `out`'s dtype before the add, as `bw_combine` followed by the three torch ops
+    rounds them. `gate` is `[tokens, >= 1]` with unit column stride; only column 0 is read,
+    through its own row stride (a view into the router GEMM output)."""
+    tokens, hidden = out.shape
+    if shared.shape != (tokens, hidden) or not shared.is_contiguous():
+        raise ValueError(f"bw_combine_glue: shared must be a contiguous [{tokens}, {hidden}] tensor, "
+                         f"got shape {tuple(shared.shape)}")
+    if gate.dim() != 2 or gate.shape[0] != tokens or gate.stride(1) != 1:
+        raise ValueError(f"bw_combine_glue: gate must have {tokens} rows and unit column stride, "
+                         f"got shape {tuple(gate.shape)}, stride {gate.stride()}")
+    _combine_rows(y, a_expert, a_weight, expert_range, top_k, out, shared, gate, "bw_combine_glue")
 
 
 def expert_sorted_order(a_expert: torch.Tensor) -> torch.Tensor:
@@ -497,8 +557,12 @@ def expert_sorted_order(a_expert: torch.Tensor) -> torch.Tensor:
 def fused_expert_order(a_expert: torch.Tensor, num_experts: int, *, cursor=None) -> torch.Tensor:
     """Expert-grouping permutation from the HIP counting sort: set-identical to
     `expert_sorted_order` per expert (`mxfp4_gemv.py:990-1017`)."""
-    ones = torch.ones(a_expert.numel(), dtype=torch.float32, device=a_expert.device)
-    return bw_prep(a_expert, ones, (0, num_experts)).sorted[: a_expert.numel()]
+    a = a_expert.numel()
+    ones = torch.ones(a, dtype=torch.float32, device=a_expert.device)
+    x = torch.empty(a, 1, dtype=torch.bfloat16, device=a_expert.device)
+    plan = BwPlan(a, 1, 1, num_experts, a_expert.device, torch.bfloat16)
+    bw_prep(x, a_expert, ones, (0, num_experts), plan)
+    return plan.sorted[:a]
 
 
 def grouped_block_count(assignments: int, experts: int, block_m: int) -> int:

@@ -58,3 +58,34 @@ def test_reference_moe_matches_the_fp64_oracle(seed):
     want = moe_ref.reference_moe(x, ex, a_e, a_w, 2, (0, 6))
     assert moe_ref.rel_l2(got, want) < 1e-6
     assert not got[3].any()
+
+
+def test_staged_pieces_keep_the_reference_signatures():
+    """`bw_prep`, `BwPlan`, `bw_combine` and `bw_combine_glue` take the reference's parameters
+    (mxfp4_gemv.py:2320-2346, :2349, :2440, :2449)."""
+    import inspect
+
+    names = lambda f: list(inspect.signature(f).parameters)  # noqa: E731
+    assert names(mxfp4_gemv.bw_prep) == ["x", "a_expert", "a_weight", "expert_range", "plan"]
+    assert names(mxfp4_gemv.bw_combine) == ["y", "a_expert", "a_weight", "expert_range", "top_k", "out"]
+    assert names(mxfp4_gemv.bw_combine_glue) == ["y", "a_expert", "a_weight", "expert_range", "top_k",
+                                                 "shared", "gate", "out"]
+    assert names(mxfp4_gemv.BwPlan) == ["tokens", "top_k", "reduction", "local_experts", "device", "dtype",
+                                        "block_t", "permute_x"]
+
+
+def test_bw_plan_sizes_and_rejections():
+    plan = mxfp4_gemv.BwPlan(48, 10, 4096, 512, torch.device("cpu"), torch.bfloat16)
+    assert plan.block_t == 16 and plan.cursor is None and plan.xp is None
+    assert plan.sorted.shape == (480,) and plan.unit.shape == (3 * plan.u_max,)
+    # each live expert adds at most one partial unit beyond the full ones
+    assert plan.u_max >= min(512, 480) and plan.u_max <= min(512, 480) + 480 // 16
+    with pytest.raises(ValueError, match="block_t"):
+        mxfp4_gemv.BwPlan(48, 10, 4096, 512, torch.device("cpu"), torch.bfloat16, block_t=32)
+    x = torch.zeros(48, 4096, dtype=torch.bfloat16)
+    e, w = random_routing(48, 512, 10, seed=0)
+    with pytest.raises(ValueError, match="device tensors"):
+        mxfp4_gemv.bw_prep(x, torch.from_numpy(e), torch.from_numpy(w), (0, 512), plan)
+    out = torch.empty(48, 4096, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="device tensors"):
+        mxfp4_gemv.bw_combine(torch.zeros(480, 4096), torch.from_numpy(e), torch.from_numpy(w), (0, 512), 10, out)
