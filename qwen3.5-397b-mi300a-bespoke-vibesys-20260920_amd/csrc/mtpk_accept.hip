@@ -15,12 +15,14 @@ namespace mtpk {
 
 constexpr int kArgmaxThreads = 256;
 // 16-byte loads in flight per thread, and the workgroup count the chunking aims at. Measured
-// over [192 | 48, 248320] bf16: 4 loads and about 1024 workgroups beat 2/8/16 loads and
-// 512/2048/4096 workgroups (fewer, longer workgroups win at 48 rows; no setting gains at 192);
-// a 1024-thread workgroup per row, which would drop the second launch, streams at only about
-// 40 GB/s per CU and lost at every row count.
+// over [192 | 48, 248320] bf16: 4 loads beat 2/8/16, and about 1536 workgroups (six per CU,
+// all resident at once at this kernel's occupancy, the same number on every CU at 192 and 48
+// rows) beat 512/768/1024/2048/4096 (greedy accept at 192 rows: 24.4 us against 25.9 us at
+// 1024, whose 4.5 per CU leave half the CUs a workgroup longer); a 1024-thread workgroup per
+// row, which would drop the second launch, streams at only about 40 GB/s per CU and lost at
+// every row count.
 constexpr int kArgmaxLoads = 4;
-constexpr int64_t kArgmaxWorkgroups = 1024;
+constexpr int64_t kArgmaxWorkgroups = 1536;
 
 __global__ __launch_bounds__(kArgmaxThreads) void k_argmax_partial(
     const void* __restrict__ logits, int dt, int64_t stride, int64_t vocab, int64_t chunk,
