@@ -38,7 +38,11 @@ struct PrepSmem {
   static constexpr int kBytes = kTot + 2 * (NT / kWave) * 4;
 };
 
-// The counting sort on one workgroup of NT threads.
+// The counting sort on one workgroup of NT threads. The live test of a thread's first
+// kPrepKeep assignments is kept in registers from the counting pass for the placing pass, which
+// then reloads the routing only past them.
+constexpr int kPrepKeep = 4;
+
 template <int NT>
 __device__ inline void prep_body(const void* __restrict__ a_expert, int edt,
                                  const void* __restrict__ a_weight, int wdt, int assignments,
@@ -51,9 +55,22 @@ __device__ inline void prep_body(const void* __restrict__ a_expert, int edt,
   int* wtot_u = wtot_c + NT / kWave;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
 
+  int keep[kPrepKeep];  // local expert of assignment tid + i * NT, or -1 when it is dead
+#pragma unroll
+  for (int i = 0; i < kPrepKeep; ++i) {
+    const int a = tid + i * kPrepThreads;
+    keep[i] = -1;
+    if (a < assignments) {
+      const int64_t ex = load_index(a_expert, edt, a) - lo;
+      if (ex >= 0 && ex < n_experts && load_float(a_weight, wdt, a) != 0.f) keep[i] = (int)ex;
+    }
+  }
   for (int e = tid; e < n_experts; e += kPrepThreads) cnt[e] = 0;
   __syncthreads();
-  for (int a = tid; a < assignments; a += kPrepThreads) {
+#pragma unroll
+  for (int i = 0; i < kPrepKeep; ++i)
+    if (keep[i] >= 0) atomicAdd(&cnt[keep[i]], 1);
+  for (int a = tid + kPrepKeep * kPrepThreads; a < assignments; a += kPrepThreads) {
     const int64_t ex = load_index(a_expert, edt, a) - lo;
     if (ex >= 0 && ex < n_experts && load_float(a_weight, wdt, a) != 0.f) atomicAdd(&cnt[ex], 1);
   }
@@ -105,7 +122,10 @@ __device__ inline void prep_body(const void* __restrict__ a_expert, int edt,
   }
   if (tid == 0) *n_units = min(total_units, max_units);
   __syncthreads();
-  for (int a = tid; a < assignments; a += kPrepThreads) {
+#pragma unroll
+  for (int i = 0; i < kPrepKeep; ++i)
+    if (keep[i] >= 0) sorted[atomicAdd(&cnt[keep[i]], 1)] = tid + i * kPrepThreads;
+  for (int a = tid + kPrepKeep * kPrepThreads; a < assignments; a += kPrepThreads) {
     const int64_t ex = load_index(a_expert, edt, a) - lo;
     if (ex >= 0 && ex < n_experts && load_float(a_weight, wdt, a) != 0.f)
       sorted[atomicAdd(&cnt[ex], 1)] = a;
@@ -1281,7 +1301,10 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
 // ---------------------------------------------------------------- combine (unit mode)
 //
 // out[t, n..n+3] = sum_j w_j * y[t*top_k + j, n..n+3] over live assignments, in j order. The
-// routing of a group of four j is loaded before their y rows so the loads overlap.
+// routing of a group of kCombineGroup j is loaded first, then all of the group's live y rows at
+// once, then they are summed in j order: two memory latencies per group (one group up to
+// top_k = 16) instead of two per four j.
+constexpr int kCombineGroup = 16;
 
 __global__ __launch_bounds__(256) void k_moe_combine(
     const float* __restrict__ y, const void* __restrict__ a_expert, int edt,
@@ -1291,25 +1314,25 @@ __global__ __launch_bounds__(256) void k_moe_combine(
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < top_k; j0 += 4) {
-    float w[4];
-    int64_t a[4];
+  for (int j0 = 0; j0 < top_k; j0 += kCombineGroup) {
+    float w[kCombineGroup];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kCombineGroup; ++q) {
       const int j = j0 + q;
-      a[q] = (int64_t)t * top_k + j;
       w[q] = 0.f;
       if (j < top_k) {
-        const int64_t e = load_index(a_expert, edt, a[q]);
-        const float wv = load_float(a_weight, wdt, a[q]);
+        const int64_t a = (int64_t)t * top_k + j;
+        const int64_t e = load_index(a_expert, edt, a);
+        const float wv = load_float(a_weight, wdt, a);
         if (e >= lo && e < hi) w[q] = wv;
       }
     }
-    u32x4_t yv[4];
+    u32x4_t yv[kCombineGroup];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) yv[q] = w[q] != 0.f ? ld16(y + a[q] * H + n) : zero16();
+    for (int q = 0; q < kCombineGroup; ++q)
+      yv[q] = w[q] != 0.f ? ld16(y + ((int64_t)t * top_k + j0 + q) * H + n) : zero16();
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < kCombineGroup; ++q)
       if (w[q] != 0.f)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] += w[q] * bits_f32(yv[q][c]);
@@ -1336,11 +1359,11 @@ __global__ __launch_bounds__(256) void k_moe_combine_rows(
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < top_k; j0 += 4) {
-    bool live[4];
-    int64_t a[4];
+  for (int j0 = 0; j0 < top_k; j0 += kCombineGroup) {
+    bool live[kCombineGroup];
+    int64_t a[kCombineGroup];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kCombineGroup; ++q) {
       const int j = j0 + q;
       a[q] = (int64_t)t * top_k + j;
       live[q] = false;
@@ -1349,9 +1372,9 @@ __global__ __launch_bounds__(256) void k_moe_combine_rows(
         live[q] = e >= lo && e < hi && load_float(a_weight, wdt, a[q]) != 0.f;
       }
     }
-    float v[4][4];
+    float v[kCombineGroup][4];
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
+    for (int q = 0; q < kCombineGroup; ++q) {
       if (YB) {
         uint2 b = make_uint2(0u, 0u);
         if (live[q]) b = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(y) + a[q] * H + n);
@@ -1366,7 +1389,7 @@ __global__ __launch_bounds__(256) void k_moe_combine_rows(
       }
     }
 #pragma unroll
-    for (int q = 0; q < 4; ++q)
+    for (int q = 0; q < kCombineGroup; ++q)
       if (live[q])
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] += v[q][c];
