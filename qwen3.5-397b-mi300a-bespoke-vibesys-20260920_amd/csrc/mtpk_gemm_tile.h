@@ -224,14 +224,28 @@ __device__ inline void gemm_tile(const GemmArgs& a, uint8_t* smem, int bx, int b
 
 // One element of the split-K reduction: out[m, col] = epilogue(sum over ks of part[ks, m, .]) in
 // split order (the SiLU epilogue reads the gate half, then the up half of each partial row).
+// The planes are loaded kReducePlanes at a time and then summed in split order, so a value waits
+// for one memory latency per group of planes rather than one per plane.
+constexpr int kReducePlanes = 8;
+
 __device__ inline float gemm_reduce_value(const float* __restrict__ part, int KS, int M, int cols,
                                           int epi, int64_t m, int64_t col) {
   const int pc = epi == kEpiSilu ? 2 * cols : cols;
   float g = 0.f, u = 0.f;
-  for (int ks = 0; ks < KS; ++ks) {
-    const float* p = part + ((int64_t)ks * M + m) * pc;
-    g += p[col];
-    if (epi == kEpiSilu) u += p[cols + col];
+  for (int k0 = 0; k0 < KS; k0 += kReducePlanes) {
+    float vg[kReducePlanes], vu[kReducePlanes];
+#pragma unroll
+    for (int i = 0; i < kReducePlanes; ++i) {
+      const float* p = part + ((int64_t)(k0 + i) * M + m) * pc;
+      vg[i] = k0 + i < KS ? p[col] : 0.f;
+      vu[i] = k0 + i < KS && epi == kEpiSilu ? p[cols + col] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < kReducePlanes; ++i)
+      if (k0 + i < KS) {
+        g += vg[i];
+        if (epi == kEpiSilu) u += vu[i];
+      }
   }
   return epi == kEpiSilu ? g / (1.f + __expf(-g)) * u : g;
 }

@@ -582,8 +582,17 @@ __device__ inline float shared_gate(const SharedTerm& st, int t, int odt) {
 
 __device__ inline float shared_value(const SharedTerm& st, int64_t i, int odt) {
   if (!st.part) return load_float(st.shared, st.sdt, i);
+  // the planes loaded together, then summed in split order
+  constexpr int kPlanes = 8;
   float v = 0.f;
-  for (int k = 0; k < st.ks; ++k) v += st.part[k * st.plane + i];
+  for (int k0 = 0; k0 < st.ks; k0 += kPlanes) {
+    float p[kPlanes];
+#pragma unroll
+    for (int k = 0; k < kPlanes; ++k) p[k] = k0 + k < st.ks ? st.part[(k0 + k) * st.plane + i] : 0.f;
+#pragma unroll
+    for (int k = 0; k < kPlanes; ++k)
+      if (k0 + k < st.ks) v += p[k];
+  }
   return round_to(odt, v);
 }
 

@@ -69,14 +69,24 @@ __device__ inline void load_logits_partials(const float* __restrict__ part, int 
   float acc[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) acc[j] = 0.f;
-  for (int ks = 0; ks < KS; ++ks) {
-    const rsrc_t r = make_rsrc(part + ((int64_t)ks * rows + row) * cols, (uint32_t)(E * 4));
-    float v[PER];
+  // four planes' loads in flight at once, then summed in split order
+  constexpr int kPlanes = 4;
+  for (int k0 = 0; k0 < KS; k0 += kPlanes) {
+    float v[kPlanes][PER];
 #pragma unroll
-    for (int j = 0; j < PER; ++j)
-      v[j] = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(r, (int)((lane + kWave * j) * 4), 0, 0));
+    for (int i = 0; i < kPlanes; ++i) {
+      const bool in = k0 + i < KS;
+      const rsrc_t r = make_rsrc(part + ((int64_t)(in ? k0 + i : 0) * rows + row) * cols, (uint32_t)(E * 4));
 #pragma unroll
-    for (int j = 0; j < PER; ++j) acc[j] += v[j];
+      for (int j = 0; j < PER; ++j)
+        v[i][j] = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(
+            r, (int)(in ? (uint32_t)((lane + kWave * j) * 4) : kOutOfRange), 0, 0));
+    }
+#pragma unroll
+    for (int i = 0; i < kPlanes; ++i)
+      if (k0 + i < KS)
+#pragma unroll
+        for (int j = 0; j < PER; ++j) acc[j] += v[i][j];
   }
 #pragma unroll
   for (int j = 0; j < PER; ++j) lg[j] = bf16_to_f32(f32_to_bf16(acc[j]));
