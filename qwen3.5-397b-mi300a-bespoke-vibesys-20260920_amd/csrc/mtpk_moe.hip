@@ -1310,11 +1310,14 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
 // ---------------------------------------------------------------- combine (unit mode)
 //
 // out[t, n..n+3] = sum_j w_j * y[t*top_k + j, n..n+3] over live assignments, in j order. The
-// routing of a group of kCombineGroup j is loaded first, then all of the group's live y rows at
-// once, then they are summed in j order: two memory latencies per group (one group up to
-// top_k = 16) instead of two per four j.
+// routing of a group of G j is loaded first, then all of the group's live y rows at once, then
+// they are summed in j order: two memory latencies per group. Few tokens: G = 16, one group up
+// to top_k = 16 (M = 32: 6.4 against 6.7 us); many tokens, where the launch streams tens of MB of
+// y, G = 4 (M = 192: 8.9 against 9.7 us with G = 16).
 constexpr int kCombineGroup = 16;
+constexpr int64_t kCombineWideTokens = 96;
 
+template <int G>
 __global__ __launch_bounds__(256) void k_moe_combine(
     const float* __restrict__ y, const void* __restrict__ a_expert, int edt,
     const void* __restrict__ a_weight, int wdt, int top_k, int H, int lo, int hi,
@@ -1323,10 +1326,10 @@ __global__ __launch_bounds__(256) void k_moe_combine(
   const int n = (blockIdx.x * blockDim.x + threadIdx.x) * 4;
   if (n >= H) return;
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int j0 = 0; j0 < top_k; j0 += kCombineGroup) {
-    float w[kCombineGroup];
+  for (int j0 = 0; j0 < top_k; j0 += G) {
+    float w[G];
 #pragma unroll
-    for (int q = 0; q < kCombineGroup; ++q) {
+    for (int q = 0; q < G; ++q) {
       const int j = j0 + q;
       w[q] = 0.f;
       if (j < top_k) {
@@ -1336,12 +1339,12 @@ __global__ __launch_bounds__(256) void k_moe_combine(
         if (e >= lo && e < hi) w[q] = wv;
       }
     }
-    u32x4_t yv[kCombineGroup];
+    u32x4_t yv[G];
 #pragma unroll
-    for (int q = 0; q < kCombineGroup; ++q)
+    for (int q = 0; q < G; ++q)
       yv[q] = w[q] != 0.f ? ld16(y + ((int64_t)t * top_k + j0 + q) * H + n) : zero16();
 #pragma unroll
-    for (int q = 0; q < kCombineGroup; ++q)
+    for (int q = 0; q < G; ++q)
       if (w[q] != 0.f)
 #pragma unroll
         for (int c = 0; c < 4; ++c) acc[c] += w[q] * bits_f32(yv[q][c]);
@@ -1944,7 +1947,8 @@ int mtpk_moe_combine(const float* y, const void* a_expert, int expert_dtype, con
   if (!aligned16(y)) return MTPK_EINVAL;
   if (tokens == 0) return 0;
   const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
-  hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
+  hipLaunchKernelGGL(tokens < kCombineWideTokens ? k_moe_combine<kCombineGroup> : k_moe_combine<4>,
+                     grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
                      expert_hi, out, out_dtype, SharedTerm{});
   return status_of(hipGetLastError());
@@ -2064,7 +2068,8 @@ int mtpk_fused_moe_shared(const void* x, int x_dtype, int64_t tokens, int64_t hi
                      units, n_units, mu, y, stream);
   if (rc) return rc;
   const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
-  hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
+  hipLaunchKernelGGL(tokens < kCombineWideTokens ? k_moe_combine<kCombineGroup> : k_moe_combine<4>,
+                     grid, dim3(256), 0, (hipStream_t)stream, y, a_expert,
                      expert_dtype, a_weight, weight_dtype, top_k, (int)hidden, expert_lo,
                      expert_hi, out, x_dtype, st);
   return status_of(hipGetLastError());
@@ -2274,7 +2279,8 @@ int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint
                      units, n_units, mu, y, stream);
   if (rc) return rc;
   const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
-  hipLaunchKernelGGL(k_moe_combine, grid, dim3(256), 0, st, y, ti, MTPK_I32, tw, MTPK_F32, top_k,
+  hipLaunchKernelGGL(tokens < kCombineWideTokens ? k_moe_combine<kCombineGroup> : k_moe_combine<4>,
+                     grid, dim3(256), 0, st, y, ti, MTPK_I32, tw, MTPK_F32, top_k,
                      (int)hidden, expert_lo, expert_hi, out, MTPK_BF16, sh);
   return status_of(hipGetLastError());
 }
