@@ -62,34 +62,44 @@ __device__ inline void load_logits_row(const void* __restrict__ routing, int64_t
 }
 
 // The same row as the split-K GEMM leaves it: KS fp32 partial planes [KS, rows, cols], summed in
-// split order and rounded to bf16, i.e. the bf16 logits the GEMM's reduction would store.
+// split order and rounded to bf16, i.e. the bf16 logits the GEMM's reduction would store. Also
+// returns column E (the shared expert's gate logit, when the row has one) summed the same way
+// and not rounded; its loads travel with the row's.
 template <int PER>
-__device__ inline void load_logits_partials(const float* __restrict__ part, int KS, int rows,
-                                            int cols, int row, int E, int lane, float (&lg)[PER]) {
+__device__ inline float load_logits_partials(const float* __restrict__ part, int KS, int rows,
+                                             int cols, int row, int E, int lane, float (&lg)[PER]) {
   float acc[PER];
 #pragma unroll
   for (int j = 0; j < PER; ++j) acc[j] = 0.f;
   // four planes' loads in flight at once, then summed in split order
   constexpr int kPlanes = 4;
+  const bool extra = E < cols;
+  float ge = 0.f;
   for (int k0 = 0; k0 < KS; k0 += kPlanes) {
-    float v[kPlanes][PER];
+    float v[kPlanes][PER], ve[kPlanes];
 #pragma unroll
     for (int i = 0; i < kPlanes; ++i) {
       const bool in = k0 + i < KS;
-      const rsrc_t r = make_rsrc(part + ((int64_t)(in ? k0 + i : 0) * rows + row) * cols, (uint32_t)(E * 4));
+      const rsrc_t r = make_rsrc(part + ((int64_t)(in ? k0 + i : 0) * rows + row) * cols,
+                                 (uint32_t)((E + (extra ? 1 : 0)) * 4));
 #pragma unroll
       for (int j = 0; j < PER; ++j)
         v[i][j] = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(
-            r, (int)(in ? (uint32_t)((lane + kWave * j) * 4) : kOutOfRange), 0, 0));
+            r, (int)(in && lane + kWave * j < E ? (uint32_t)((lane + kWave * j) * 4) : kOutOfRange), 0, 0));
+      ve[i] = bits_f32(__builtin_amdgcn_raw_buffer_load_b32(
+          r, (int)(in && extra ? (uint32_t)(E * 4) : kOutOfRange), 0, 0));
     }
 #pragma unroll
     for (int i = 0; i < kPlanes; ++i)
-      if (k0 + i < KS)
+      if (k0 + i < KS) {
 #pragma unroll
         for (int j = 0; j < PER; ++j) acc[j] += v[i][j];
+        ge += ve[i];
+      }
   }
 #pragma unroll
   for (int j = 0; j < PER; ++j) lg[j] = bf16_to_f32(f32_to_bf16(acc[j]));
+  return ge;
 }
 
 // softmax -> top-k -> renormalise of one row whose logits lane l holds at slots j (expert
@@ -172,7 +182,7 @@ __global__ __launch_bounds__(256) void k_route_topk(const void* __restrict__ rou
                                                     int64_t stride, int tokens, int E, int top_k,
                                                     float* __restrict__ top_w,
                                                     void* __restrict__ top_i, int idt) {
-  const int row = blockIdx.x * 4 + (threadIdx.x / kWave);
+  const int row = uniform(blockIdx.x * 4 + (threadIdx.x / kWave));  // per wave: resources in SGPRs
   const int lane = threadIdx.x & (kWave - 1);
   if (row >= tokens) return;  // uniform over the wave: every DPP below runs with all lanes
   float lg[PER];
@@ -188,16 +198,12 @@ __global__ __launch_bounds__(256) void k_route_topk(const void* __restrict__ rou
 template <int PER>
 __global__ __launch_bounds__(256) void k_route_act(RouteActArgs a) {
   if ((int)blockIdx.x < a.route_blocks) {
-    const int row = blockIdx.x * 4 + (threadIdx.x / kWave);
+    const int row = uniform(blockIdx.x * 4 + (threadIdx.x / kWave));  // per wave: resources in SGPRs
     const int lane = threadIdx.x & (kWave - 1);
     if (row >= a.rows) return;  // uniform over the wave
     float lg[PER];
-    load_logits_partials<PER>(a.rpart, a.rks, a.rows, a.rcols, row, a.E, lane, lg);
-    if (a.sgate && lane == 0) {
-      float g = 0.f;
-      for (int ks = 0; ks < a.rks; ++ks) g += a.rpart[((int64_t)ks * a.rows + row) * a.rcols + a.E];
-      a.sgate[row] = f32_to_bf16(g);
-    }
+    const float g = load_logits_partials<PER>(a.rpart, a.rks, a.rows, a.rcols, row, a.E, lane, lg);
+    if (a.sgate && lane == 0) a.sgate[row] = f32_to_bf16(g);
     route_row<PER>(lg, row, a.E, a.top_k, lane, a.top_w, a.top_i, a.idt);
     return;
   }
