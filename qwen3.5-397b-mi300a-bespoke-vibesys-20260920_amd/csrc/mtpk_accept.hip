@@ -182,6 +182,23 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
   const int k = t - 1;
   __shared__ unsigned long long s_key[kKeyRows];
   int len = 0;
+  // The lane's loads that do not depend on the step argmax (drafts, stop ids, budget, state) go
+  // out before the key fold, so their latency overlaps it: kPre of each into registers.
+  const int64_t* drow = draft + (int64_t)(j < B ? j : 0) * ds;
+  const int64_t* srow = stops + (int64_t)(j < B ? j : 0) * n_stops;
+  int64_t dv[kPre], sv[kPre];
+  int64_t bud = 0, p0 = 0;
+  bool act = false;
+  if (j < B) {
+#pragma unroll
+    for (int u = 0; u < kPre; ++u) {
+      dv[u] = u < k ? drow[u] : 0;
+      sv[u] = u < n_stops ? srow[u] : 0;
+    }
+    bud = budget[j];
+    act = active[j] != 0;
+    p0 = next_pos ? pos[j] : 0;
+  }
   if (keys) {
     const int rows = B * t;
     for (int r = j; r < rows; r += kAcceptThreads) s_key[r] = 0;
@@ -200,20 +217,11 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
   if (j < B) {
     const int64_t* row = keys ? reinterpret_cast<const int64_t*>(s_key) + (int64_t)j * t
                               : sa + (int64_t)j * ss;
-    const int64_t* drow = draft + (int64_t)j * ds;
-    const int64_t* srow = stops + (int64_t)j * n_stops;
-    // Every load of the row is issued at once, the first kPre verify columns, drafts and stop
-    // ids into registers: compared one after another they cost an HBM round trip each.
-    int64_t rv[kPre], dv[kPre], sv[kPre];
+    // The first kPre verify columns into registers together: compared one after another they
+    // would cost a memory round trip each.
+    int64_t rv[kPre];
 #pragma unroll
-    for (int u = 0; u < kPre; ++u) {
-      rv[u] = u < t ? row[u] : 0;
-      dv[u] = u < k ? drow[u] : 0;
-      sv[u] = u < n_stops ? srow[u] : 0;
-    }
-    const int64_t bud = budget[j];
-    const bool act = active[j] != 0;
-    const int64_t p0 = next_pos ? pos[j] : 0;
+    for (int u = 0; u < kPre; ++u) rv[u] = u < t ? row[u] : 0;
     auto column = [&](int s) {
       int64_t v = 0;
 #pragma unroll

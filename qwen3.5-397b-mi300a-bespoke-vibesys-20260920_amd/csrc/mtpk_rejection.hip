@@ -124,10 +124,17 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_stats(RsRows rr, int64_t n_ta
 // A chunk partial's share of a row sum with row max m; a massless (-inf) chunk adds nothing.
 __device__ inline float rs_share(float2 v, float m) { return v.x > -INFINITY ? v.y * __expf(v.x - m) : 0.f; }
 
-// Combine a row's chunk partials (one wave): max M and sum S of exp(z - M).
-__device__ inline float2 rs_row_stats(const float2* part, int64_t r, int nchunk) {
+// A lane's first chunk partial of row r (chunk = lane), or the empty (-inf, 0).
+__device__ inline float2 rs_first_partial(const float2* part, int64_t r, int nchunk) {
   const int lane = threadIdx.x & (kWave - 1);
-  const float2 v0 = lane < nchunk ? part[r * nchunk + lane] : make_float2(-INFINITY, 0.f);
+  return lane < nchunk ? part[r * nchunk + lane] : make_float2(-INFINITY, 0.f);
+}
+
+// Combine a row's chunk partials (one wave): max M and sum S of exp(z - M). v0 is the lane's
+// first partial (rs_first_partial), loaded ahead by the caller so that its latency overlaps
+// other loads.
+__device__ inline float2 rs_row_stats(float2 v0, const float2* part, int64_t r, int nchunk) {
+  const int lane = threadIdx.x & (kWave - 1);
   float m = v0.x;
   for (int c = lane + kWave; c < nchunk; c += kWave) m = fmaxf(m, part[r * nchunk + c].x);
   m = wave_max(m);
@@ -152,7 +159,11 @@ __device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part
   const int wv = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int64_t n_target = (int64_t)B * t;
   for (int i = wv; i < t; i += kDecideWaves) {
-    // The token and its two logits first (their loads overlap the partials' below).
+    // The rows' chunk partials, then the token and its two logits: the partials do not depend
+    // on the token, so their loads are in flight while the token's chain runs.
+    const float2 pt = rs_first_partial(part, (int64_t)b * t + i, nchunk);
+    const float2 pq = i < k ? rs_first_partial(part, n_target + (int64_t)b * k + i, nchunk)
+                            : make_float2(-INFINITY, 0.f);
     const int64_t x = i < k ? draft_tokens[(int64_t)b * k + i] : -1;
     const float ua = i < k ? u_accept[(int64_t)b * k + i] : 0.f;
     const bool in_vocab = x >= 0 && x < rr.vocab;
@@ -161,11 +172,11 @@ __device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part
       lt = load_float(rr.target, rr.dt, ((int64_t)b * t + i) * rr.vocab + x) * inv_t;
       lq = load_float(rr.draft, rr.dt, ((int64_t)b * k + i) * rr.vocab + x) * inv_t;
     }
-    const float2 st = rs_row_stats(part, (int64_t)b * t + i, nchunk);
+    const float2 st = rs_row_stats(pt, part, (int64_t)b * t + i, nchunk);
     float2 sq = make_float2(0.f, 1.f);
     float mg = 0.f;
     if (i < k) {
-      sq = rs_row_stats(part, n_target + (int64_t)b * k + i, nchunk);
+      sq = rs_row_stats(pq, part, n_target + (int64_t)b * k + i, nchunk);
       if (in_vocab) {
         const float p = __expf(lt - st.x) / st.y, q = __expf(lq - sq.x) / sq.y;
         mg = p - ua * q;
@@ -208,7 +219,7 @@ __device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part
 __global__ __launch_bounds__(kWave) void k_rs_rows(const float2* __restrict__ part, int nchunk,
                                                   RsItem* __restrict__ items) {
   const int r = blockIdx.x;
-  const float2 st = rs_row_stats(part, r, nchunk);
+  const float2 st = rs_row_stats(rs_first_partial(part, r, nchunk), part, r, nchunk);
   if (threadIdx.x == 0) {
     RsItem it;
     it.trow = r;
@@ -333,6 +344,7 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_pick(
   const int item = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
   const RsItem it = items[item];
+  const int64_t dtok = emitted && tid < k ? draft_tokens[(int64_t)item * k + tid] : 0;
   if (wv == 0) {
     // One wave finds the chunk where the cumulative mass crosses r * total: totals by a wave
     // sum, then 64 chunks at a time by an inclusive scan and a ballot.
@@ -412,14 +424,11 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_pick(
     atomicMax(&s_best, lastp);
     __syncthreads();
   }
-  if (tid == 0) {
+  // the emitted row by its first k + 1 threads at once (draft token i was loaded at the start)
+  if (tid <= k) {
     const int64_t v = s_best < 0 ? 0 : s_best;
-    token[item] = v;
-    if (emitted) {
-      const int t = k + 1;
-      for (int i = 0; i < t; ++i)
-        emitted[(int64_t)item * t + i] = i < it.a ? draft_tokens[(int64_t)item * k + i] : v;
-    }
+    if (tid == 0) token[item] = v;
+    if (emitted) emitted[(int64_t)item * (k + 1) + tid] = tid < it.a ? dtok : v;
   }
 }
 
