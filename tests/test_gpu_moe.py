@@ -276,6 +276,32 @@ def test_real_dims_edge_scale_blocks(real_layer, tokens):
             real_layer[k][used] = v
 
 
+@pytest.mark.parametrize("tokens", [1, 7, 48, 192])
+def test_real_dims_pile_up(real_layer, tokens):
+    """Every token routed to the same ten experts (the reference's `pile_up` case,
+    `test_moe_hip.py:198-222`): at 192 tokens each expert carries twelve 16-token units in one
+    launch, all reading the same weights. Against the fp32 device reference, and the direct
+    path (1 token) and unit path must agree with it alike."""
+    dev = torch.device("cuda:0")
+    print(f"pile-up MoE M={tokens}", flush=True)
+    rng = np.random.default_rng(tokens + 900)
+    hot = rng.permutation(E)[:TOP_K].astype(np.int32)
+    a_e = np.tile(hot, tokens)
+    a_w = rng.random((tokens, TOP_K)).astype(np.float32)
+    a_w = (a_w / a_w.sum(-1, keepdims=True)).reshape(-1)
+    x = torch.randn(tokens, H, device=dev, generator=torch.Generator(dev).manual_seed(tokens + 900)).to(torch.bfloat16)
+    ae, aw = torch.from_numpy(a_e).to(dev), torch.from_numpy(a_w).to(dev)
+    got = mxfp4_gemv.fused_moe(x, real_layer, (ae, aw), TOP_K, (0, E)).float()
+    ref_b = torch_fp32_reference(x, real_layer, ae.long(), aw, TOP_K).to(torch.bfloat16).float()
+    err = (torch.linalg.norm(got - ref_b) / torch.linalg.norm(ref_b)).item()
+    print(f"  rel-L2 vs fp32 reference = {err:.3e}", flush=True)
+    assert err <= 2e-3
+    # a token's output does not depend on which other tokens share its units
+    one = mxfp4_gemv.fused_moe(x[-1:], real_layer, (ae[:TOP_K], aw[-TOP_K:]), TOP_K, (0, E)).float()
+    err1 = (torch.linalg.norm(got[-1:] - one) / torch.linalg.norm(one)).item()
+    assert err1 <= 2e-3
+
+
 def test_real_dims_repeat_is_bit_identical(real_layer):
     dev = torch.device("cuda:0")
     a_e, a_w = zipf_routing(192, E, TOP_K, seed=9, zero_frac=0.05)
