@@ -198,55 +198,70 @@ def main() -> int:
             li = w % L
             runner.run(ins[li][0], layers[li], ins[li][1], ins[li][2], (0, E), outs[li])
         torch.cuda.synchronize()
-        # graph replay: one capture holds a step on every layer copy
+        # graph replay: one capture holds GRAPH_ROUNDS steps on every layer copy in turn (24
+        # layer steps, as a round's graph holds all of its layers; a 4-step graph adds the
+        # graph launch gap to every fourth step)
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):
-            for li in range(L):
-                runner.run(ins[li][0], layers[li], ins[li][1], ins[li][2], (0, E), outs[li])
-        for _ in range(2):
+            for _ in range(GRAPH_ROUNDS):
+                for li in range(L):
+                    runner.run(ins[li][0], layers[li], ins[li][1], ins[li][2], (0, E), outs[li])
+        for _ in range(3):
             graph.replay()
         torch.cuda.synchronize()
-        reps = max(1, args.steps // L)
+        reps = max(3, args.steps // (L * GRAPH_ROUNDS))
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
             graph.replay()
         e1.record()
         torch.cuda.synchronize()
-        us = e0.elapsed_time(e1) * 1e3 / (reps * L)
+        us = e0.elapsed_time(e1) * 1e3 / (reps * L * GRAPH_ROUNDS)
         byts = float(np.mean([layer_bytes(m, d) for d in dls]))
         results[name] = {"us_per_layer": us, "gbs": byts / us / 1e3, "d_live_mean": float(np.mean(dls)),
                          "graph": True}
         log(f"{name}: {us:.1f} us/layer (graph replay), {byts / us / 1e3:.0f} GB/s, D_live~{np.mean(dls):.0f}")
         results[name]["_state"] = (runner, ins, outs, dls)
 
-    # timed region for `value`: K eager steps of the headline workload with HIP events around
-    # gate_up and down
+    # timed region for `value`: K eager steps of the headline workload, with nothing between the
+    # two events but the steps (the reference times its layer as a whole, `bench_moe_bw.py`)
     runner, ins, outs, dls = results[head].pop("_state")
     for k in results:
         results[k].pop("_state", None)
-    ev = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-              for _ in range(args.steps)] for k in ("gate_up", "down")}
     torch.cuda.synchronize()
     t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     wall0 = time.perf_counter()
     t0.record()
     for s in range(args.steps):
         li = s % L
-        runner.run(ins[li][0], layers[li], ins[li][1], ins[li][2], (0, E), outs[li],
-                   events={"gate_up": ev["gate_up"][s], "down": ev["down"][s]})
+        runner.run(ins[li][0], layers[li], ins[li][1], ins[li][2], (0, E), outs[li])
     t1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
     ms = t0.elapsed_time(t1) / args.steps
+    # the same K steps again with HIP events around gate_up and down on the launch stream: the
+    # roofline kernel's live duration. The event records add about 13 us to a step, which is
+    # why they stay out of the region `value` is timed on.
+    ev = {k: [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(args.steps)] for k in ("gate_up", "down")}
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for s in range(args.steps):
+        li = s % L
+        runner.run(ins[li][0], layers[li], ins[li][1], ins[li][2], (0, E), outs[li],
+                   events={"gate_up": ev["gate_up"][s], "down": ev["down"][s]})
+    e1.record()
+    torch.cuda.synchronize()
+    ms_events = e0.elapsed_time(e1) / args.steps
     gu_ms = float(np.mean([a.elapsed_time(b) for a, b in ev["gate_up"]]))
     dn_ms = float(np.mean([a.elapsed_time(b) for a, b in ev["down"]]))
     step_bytes = [layer_bytes(head_m, dls[s % L]) for s in range(args.steps)]
     value = float(np.mean(step_bytes)) / (ms * 1e-3) / 1e9
     gu_bytes = float(np.mean([dls[s % L] * GATE_UP_BYTES + head_m * H * 2 for s in range(args.steps)]))
     gu_gbs = gu_bytes / (gu_ms * 1e-3) / 1e9
-    log(f"eager {head}: {ms * 1e3:.1f} us/step, gate_up {gu_ms * 1e3:.1f} us ({gu_gbs:.0f} GB/s), "
-        f"down {dn_ms * 1e3:.1f} us, wall {wall:.2f}s")
+    log(f"eager {head}: {ms * 1e3:.1f} us/step; with per-kernel events {ms_events * 1e3:.1f} us/step, "
+        f"gate_up {gu_ms * 1e3:.1f} us ({gu_gbs:.0f} GB/s), down {dn_ms * 1e3:.1f} us, wall {wall:.2f}s")
 
     cpu = None
     if not args.no_cpu and head == "M192":
@@ -276,7 +291,9 @@ def main() -> int:
         "config": {
             "workload": WORKLOAD_TEXT[head],
             "rows": head_m, "hidden": H, "intermediate": I, "experts": E, "top_k": TOP_K,
-            "layer_copies": L, "timing": "eager stream, HIP events",
+            "layer_copies": L,
+            "timing": "eager stream, HIP events around the K steps; a second pass of the same K steps "
+                      "with events around each kernel gives roofline.avg_us",
         },
         "frac_of_peak": round(value / PEAK_GBS, 4),
         "us_per_layer": {k: round(v["us_per_layer"], 2) for k, v in results.items()},
@@ -293,6 +310,7 @@ def main() -> int:
             "traffic_source": "profiles/moe_kernels_mi355x.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
                               "copy-calibrated)",
             "avg_us": round(gu_ms * 1e3, 2),
+            "step_us_with_kernel_events": round(ms_events * 1e3, 2),
             "algorithmic_bytes": round(gu_bytes),
         },
         "cpu_baseline": cpu,
@@ -392,6 +410,8 @@ def _time_calls(fn, reps):
     torch.cuda.synchronize()
     return a.elapsed_time(b) * 1e3 / reps  # us
 
+
+GRAPH_ROUNDS = 6  # passes over the layer copies per captured graph (per-layer timing)
 
 STREAM_SIZES = {
     "M1_down": 10 * (2_097_152 + 131_072),
