@@ -367,7 +367,7 @@ def full_layer_bench(dev, layers, rows=(1, 48, 192), shared_inter=1024):
         for name, fn in (("unfused_us", unfused), ("fused_us", fused)):
             def call(c, fn=fn):
                 fn(hs[c], layers[c], dense_w[c], outs[c])
-            r[name] = round(_time_graph(call, len(layers), 2 * len(layers)), 2)
+            r[name] = round(_time_graph(call, len(layers), GRAPH_ROUNDS * len(layers)), 2)
         res[f"M{m}"] = r
         log(f"full layer M{m}: unfused {r['unfused_us']:.1f} us, fused {r['fused_us']:.1f} us")
     del dense_w
