@@ -302,6 +302,47 @@ def test_real_dims_pile_up(real_layer, tokens):
     assert err1 <= 2e-3
 
 
+@pytest.mark.parametrize("tokens", [3, 48])
+def test_real_dims_fp32_activations(real_layer, tokens):
+    """fp32 x at real dims (split into three bf16 planes, 3-plane intermediate): the direct path
+    (3 tokens) and the unit path, against the fp32 device reference without bf16 rounding."""
+    dev = torch.device("cuda:0")
+    print(f"real-dims MoE fp32 x M={tokens}", flush=True)
+    a_e, a_w = zipf_routing(tokens, E, TOP_K, seed=tokens + 700, zero_frac=0.05)
+    x = torch.randn(tokens, H, device=dev, generator=torch.Generator(dev).manual_seed(tokens + 700))
+    ae, aw = torch.from_numpy(a_e).to(dev).long(), torch.from_numpy(a_w).to(dev)
+    got = mxfp4_gemv.fused_moe(x, real_layer, (ae, aw), TOP_K, (0, E))
+    assert got.dtype == torch.float32
+    ref = torch_fp32_reference(x, real_layer, ae, aw, TOP_K)
+    err = (torch.linalg.norm(got - ref) / torch.linalg.norm(ref)).item()
+    print(f"  rel-L2 vs fp32 reference = {err:.3e}", flush=True)
+    assert err <= 1e-5
+
+
+def test_real_dims_expert_shards_sum_to_the_whole(real_layer):
+    """Expert-parallel sharding at real dims (192 rows, int64 routing, fp32 x so that the shard
+    outputs carry no bf16 rounding): the outputs of the four 128-expert shards (each dropping the
+    other shards' assignments on the device) sum to the unsharded layer, and each matches its
+    own fp32 reference."""
+    dev = torch.device("cuda:0")
+    a_e, a_w = zipf_routing(192, E, TOP_K, seed=801, zero_frac=0.05)
+    x = torch.randn(192, H, device=dev, generator=torch.Generator(dev).manual_seed(801))
+    ae, aw = torch.from_numpy(a_e).to(dev).long(), torch.from_numpy(a_w).to(dev)
+    whole = mxfp4_gemv.fused_moe(x, real_layer, (ae, aw), TOP_K, (0, E)).double()
+    parts = torch.zeros_like(whole)
+    for lo in range(0, E, 128):
+        local = {k: v[lo:lo + 128] for k, v in real_layer.items()}
+        got = mxfp4_gemv.fused_moe(x, local, (ae, aw), TOP_K, (lo, lo + 128)).double()
+        own = (ae >= lo) & (ae < lo + 128)
+        ref = torch_fp32_reference(x, real_layer, ae, aw * own, TOP_K).double()
+        err = (torch.linalg.norm(got - ref) / torch.linalg.norm(ref)).item()
+        assert err <= 1e-5
+        parts += got
+    err = (torch.linalg.norm(parts - whole) / torch.linalg.norm(whole)).item()
+    print(f"  rel-L2 of the shard sum vs the whole = {err:.3e}", flush=True)
+    assert err <= 1e-5
+
+
 def test_real_dims_repeat_is_bit_identical(real_layer):
     dev = torch.device("cuda:0")
     a_e, a_w = zipf_routing(192, E, TOP_K, seed=9, zero_frac=0.05)
