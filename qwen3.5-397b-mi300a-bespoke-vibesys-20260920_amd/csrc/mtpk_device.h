@@ -47,6 +47,22 @@ __device__ inline u32x4_t buf16(rsrc_t r, uint32_t off, uint32_t soff) {
   return __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, (int)soff, 0));
 }
 
+// Direct-to-LDS form of buf16: lane L's 16 bytes land at lds + 16 L (lds wave-uniform), and no
+// register holds them. The load counts in vmcnt like the others, in issue order; the reader of
+// the LDS bytes waits for it with vmcnt_wait.
+typedef __attribute__((address_space(3))) void lds_void_t;
+__device__ inline void buf16_lds(rsrc_t r, uint32_t off, uint8_t* lds) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (lds_void_t*)lds, 16, (int)off, 0, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) alone (gfx9 encoding, expcnt and lgkmcnt fields at their no-wait values):
+// every vector memory load but the N most recently issued has completed.
+template <int N>
+__device__ inline void vmcnt_wait() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | 0x0F70);
+}
+
 __device__ inline uint32_t buf1(rsrc_t r, uint32_t off) {
   return (uint32_t)__builtin_amdgcn_raw_buffer_load_b8(r, (int)off, 0, 0);
 }

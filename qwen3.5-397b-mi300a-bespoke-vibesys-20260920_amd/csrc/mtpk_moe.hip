@@ -1107,10 +1107,10 @@ __global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
 
 // down, LDS variant (hi/lo intermediate planes, chunked scales). Item = (unit, 4 x R tiles of
 // 16 hidden rows), wave w takes tiles (4q + w) R .. + R. Chunks of 256 K = 2 trips = one turn
-// of the D = 2 ring; each chunk stages both planes. Items are software-pipelined: while an item
-// runs its last two chunks, the workgroup already issues its next grid-stride item's scale
-// rows, first two activation chunks and first D ring trips, so an item starts with its loads
-// in flight instead of waiting a full memory latency with the ring drained.
+// of the D = 2 ring; each chunk stages both planes. Items are software-pipelined: the workgroup
+// issues its next grid-stride item's scale rows when an item starts and, while the item runs its
+// last two chunks, the next one's first two activation chunks and first D ring trips, so an item
+// starts with its loads in flight instead of waiting a full memory latency with the ring drained.
 template <int R>
 __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
     const uint16_t* __restrict__ inter, int64_t inter_plane, int K, const uint8_t* __restrict__ wq,
@@ -1185,29 +1185,25 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
     for (int k = 0; k < 4; ++k)
       lds16_store(&xs[b][(4 * k + wave) * G::kRow + sp * G::kPlaneBytes + scol * 16], sreg[k]);
   };
-  // The wave's R * 16 scale rows (nb bytes each) come in with full-line loads, pass through
-  // the wave's own LDS scratch, and each lane keeps its lane group's bytes packed per four
+  // The wave's R * 16 scale rows (nb bytes each) come in with full-line direct-to-LDS loads into
+  // the wave's own LDS scratch (piece idx at 16 idx; lanes past the pieces load out of range
+  // into the scratch's unread tail), and each lane keeps its lane group's bytes packed per four
   // trips: pd[r][Q] byte s is tile r's trip 4Q + s.
-  u32x4_t sld[2];
   auto scale_load = [&](const Item& m) {
     const rsrc_t rs = make_rsrc(ws + (int64_t)m.e * H * nb, (uint32_t)(H * nb));
+    ring_fence();
 #pragma unroll
     for (int k = 0; k < 2; ++k) {
       const int idx = k * kWave + lane;
       const int rr = idx / segs, sg = idx - rr * segs;
       const uint32_t grow = (uint32_t)(min(m.tile0 + rr / 16, rtiles - 1) * 16 + (rr & 15));
       const bool live = m.cnt > 0 && idx < nscale;
-      sld[k] = buf16(rs, (grow * (uint32_t)nb + (uint32_t)sg * 16u) | ((uint32_t)!live << 31), 0u);
+      buf16_lds(rs, (grow * (uint32_t)nb + (uint32_t)sg * 16u) | ((uint32_t)!live << 31), scr + k * kWave * 16);
     }
+    ring_fence();
   };
   uint32_t pd[R][2];
   auto scale_unpack = [&]() {
-#pragma unroll
-    for (int k = 0; k < 2; ++k) {
-      const int idx = k * kWave + lane;
-      if (idx < nscale) lds16_store(scr + idx * 16, sld[k]);
-    }
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // the wave reads back only its own slice
 #pragma unroll
     for (int r = 0; r < R; ++r)
 #pragma unroll
@@ -1217,7 +1213,7 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
   };
 
   // Prologue of the workgroup's first item; every later item finds the same loads issued by
-  // its predecessor's last chunks. An item with cnt == 0 (none in a prep work list) only ever
+  // its predecessor's K loop. An item with cnt == 0 (none in a prep work list) only ever
   // issues out-of-range loads and stores nothing.
   u32x4_t ring[D][R];
   Item cur = fetch(blockIdx.x);
@@ -1230,13 +1226,18 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
     for (int r = 0; r < R; ++r)
       ring[s][r] = load_w(wq + (int64_t)cur.e * exp_bytes, cur.tile0, r, s, cur.cnt > 0);
   ring_fence();
-  stage_store(0);  // waits for chunk 0, hence for the scale rows issued before it
+  stage_store(0);
+  vmcnt_wait<D * R>();  // the scale rows, issued before chunk 0 and the ring
   scale_unpack();
   stage_load(cur, 1);
   lds_barrier();
 
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const Item nxt = fetch(item + gridDim.x);
+    // The scratch is free once this item's scales are unpacked (their LDS reads completed): the
+    // next item's scale rows go in now, ahead of every load of this item's K loop.
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+    scale_load(nxt);
     const bool pf = nxt.cnt > 0, live = cur.cnt > 0;
     const uint8_t* const wc = wq + (int64_t)cur.e * exp_bytes;
     const uint8_t* const wn = wq + (int64_t)nxt.e * exp_bytes;
@@ -1289,11 +1290,13 @@ __global__ __launch_bounds__(kMoeThreads) void k_moe_down_lds(
       // buffer (c + 1) & 1 was last read in chunk c - 1; past the last chunk it takes the next
       // item's chunk 0 (nchunk is even)
       stage_store((c + 1) & 1);
-      if (c + 2 == nchunk) scale_load(nxt);
       stage_load(c + 2 < nchunk ? cur : nxt, c + 2 < nchunk ? c + 2 : c + 2 - nchunk);
       lds_barrier();
     } while (++c < nchunk);
-    scale_unpack();  // the next item's scale rows, issued two chunks ago
+    // the next item's scale rows, issued before the K loop (the last stage_store waited for
+    // every load but the last chunk's D R refills and the next item's chunk 1)
+    vmcnt_wait<D * R + 4>();
+    scale_unpack();
 
 #pragma unroll
     for (int r = 0; r < R; ++r) {

@@ -69,6 +69,11 @@ MANY = [
     (96, 12, 512, 512, 8, "uniform", "bf16"),
     (160, 40, 512, 512, 4, "zipf", "bf16"),
     (64, 24, 1024, 1024, 10, "zipf", "bf16"),
+    # the LDS kernels at three and four 512-K chunks (K = 1536 and 2048), with 4-wave
+    # (80 tokens) and 8-wave (160, 200) gate_up workgroups
+    (80, 40, 1536, 1024, 10, "zipf", "bf16"),
+    (160, 24, 1536, 1024, 8, "zipf", "bf16"),
+    (200, 32, 2048, 1024, 6, "uniform", "bf16"),
 ]
 
 
