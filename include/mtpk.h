@@ -437,9 +437,11 @@ int mtpk_rownorm(const void* x, int x_dtype, int64_t x_token_stride, int64_t x_h
  * base_pos int64 [batch]: query row s of lane b is at base_pos[b] + s and attends to positions
  * 0 .. base_pos[b] + s (q head h uses kv head h / (heads / kv_heads)). out bf16, q's shape.
  * head_dim 64, 128 or 256. fp32 scores and softmax, bf16 probabilities into the PV product.
- * n_split key splits per (lane, kv head) (mtpk_attention_splits picks one from a host bound on
- * the context); n_split > 1 needs mtpk_attention_workspace_bytes of workspace. */
-int mtpk_attention_splits(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads, int64_t max_ctx);
+ * n_split key splits per (lane, kv head) (mtpk_attention_splits picks one from the shape and a
+ * host bound on the context, so that every workgroup is resident at once; 0 for a shape the
+ * kernel does not take); n_split > 1 needs mtpk_attention_workspace_bytes of workspace. */
+int mtpk_attention_splits(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads,
+                          int64_t head_dim, int64_t max_ctx);
 int64_t mtpk_attention_workspace_bytes(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads,
                                        int64_t head_dim, int n_split);
 int mtpk_paged_attention(const uint16_t* q, int64_t batch, int64_t t, int64_t heads,

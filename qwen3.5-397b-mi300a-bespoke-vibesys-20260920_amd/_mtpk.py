@@ -175,7 +175,7 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
          c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
-    "mtpk_attention_splits": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int64]),
+    "mtpk_attention_splits": (c_int, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int64]),
     "mtpk_attention_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64, c_int]),
     "mtpk_paged_attention": (
         c_int,

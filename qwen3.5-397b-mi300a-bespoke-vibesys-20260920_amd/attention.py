@@ -82,7 +82,7 @@ def paged_attention(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
     table = block_table.to(torch.int32).contiguous()
     pos = base_pos.to(torch.int64).contiguous()
     lib = _mtpk.lib()
-    n_split = int(lib.mtpk_attention_splits(b, t, heads, kvh, max(int(ctx_len), 1)))
+    n_split = int(lib.mtpk_attention_splits(b, t, heads, kvh, hd, max(int(ctx_len), 1)))
     ws_bytes = int(lib.mtpk_attention_workspace_bytes(b, t, heads, kvh, hd, n_split))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     out = torch.empty_like(q)
@@ -132,7 +132,7 @@ def paged_attention_gated(q: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.T
     table = block_table.to(torch.int32).contiguous()
     pos = base_pos.to(torch.int64).contiguous()
     lib = _mtpk.lib()
-    n_split = int(lib.mtpk_attention_splits(b, t, heads, kvh, max(int(ctx_len), 1)))
+    n_split = int(lib.mtpk_attention_splits(b, t, heads, kvh, hd, max(int(ctx_len), 1)))
     ws_bytes = int(lib.mtpk_attention_workspace_bytes(b, t, heads, kvh, hd, n_split))
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     out = torch.empty(b, t, heads, hd, dtype=torch.bfloat16, device=device)

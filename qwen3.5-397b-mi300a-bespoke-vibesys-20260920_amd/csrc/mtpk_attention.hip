@@ -335,12 +335,30 @@ __global__ __launch_bounds__(256) void k_attention_merge(
   for (int e = 0; e < 4; ++e) orow[e] = attn_out_value(io, acc[e] * inv, b, hq, st, d + e);
 }
 
-int attention_splits(int64_t B, int64_t kvh, int row_groups, int64_t max_ctx) {
+// Workgroups of k_paged_attention<HD> resident on the whole device at once.
+int attention_slots(int hd) {
+  static int occ[3] = {0, 0, 0};
+  const int i = hd == 64 ? 0 : hd == 128 ? 1 : 2;
+  if (occ[i] == 0) {
+    occ[i] = hd == 64    ? occupancy_per_cu(k_paged_attention<64>, kAttnThreads)
+             : hd == 128 ? occupancy_per_cu(k_paged_attention<128>, kAttnThreads)
+                         : occupancy_per_cu(k_paged_attention<256>, kAttnThreads);
+    if (occ[i] < 1) occ[i] = 1;
+  }
+  return device_cu_count() * occ[i];
+}
+
+// The largest key-split count whose workgroups all run in one round of resident slots, at
+// least 8 tiles per split and at most 64 splits. A second, partly filled round leaves CUs idle
+// for its whole length, and every extra split adds partials to the merge: at 48 lanes, 2 kv
+// heads of 256 and 8192 keys (96 workgroups per split, 512 slots), 5 splits take 179 us per
+// call against 199 us for 8 and 10 and 220 us for 12 and 16.
+int attention_splits(int hd, int64_t B, int64_t kvh, int row_groups, int64_t max_ctx) {
   const int64_t wgs = B * kvh * row_groups;
-  const int64_t want = (3 * (int64_t)device_cu_count() + wgs - 1) / (wgs > 0 ? wgs : 1);
+  const int64_t fit = attention_slots(hd) / (wgs > 0 ? wgs : 1);
   const int64_t tiles = (max_ctx + kAttnKeys - 1) / kAttnKeys;
   const int64_t cap = tiles / 8 > 1 ? tiles / 8 : 1;  // at least 8 tiles per split
-  int64_t n = want < cap ? want : cap;
+  int64_t n = fit < cap ? fit : cap;
   if (n > 64) n = 64;
   return n < 1 ? 1 : (int)n;
 }
@@ -409,10 +427,12 @@ using namespace mtpk;
 
 extern "C" {
 
-int mtpk_attention_splits(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads, int64_t max_ctx) {
+int mtpk_attention_splits(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads,
+                          int64_t head_dim, int64_t max_ctx) {
   if (batch <= 0 || t <= 0 || kv_heads <= 0 || heads % kv_heads) return 0;
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256) return 0;
   const int row_groups = (int)((heads / kv_heads * t + kAttnRows - 1) / kAttnRows);
-  return attention_splits(batch, kv_heads, row_groups, max_ctx);
+  return attention_splits((int)head_dim, batch, kv_heads, row_groups, max_ctx);
 }
 
 int64_t mtpk_attention_workspace_bytes(int64_t batch, int64_t t, int64_t heads, int64_t kv_heads,
