@@ -96,11 +96,16 @@ def profiled_traffic(kernel: str) -> float | None:
     path = ROOT / "profiles" / "moe_kernels_mi355x.md"
     if not path.exists():
         return None
-    for line in path.read_text().splitlines():
+    text = path.read_text()
+    pmc = text.find("## HBM traffic per dispatch")
+    if pmc < 0:
+        return None
+    # PMC rows: kernel | grid | dispatches | FETCH_SIZE KiB | WRITE_SIZE KiB | fetched GB | written GB
+    for line in text[pmc:].splitlines():
         cells = [c.strip() for c in line.strip().strip("|").split("|")]
-        if len(cells) == 6 and cells[0] == f"`{kernel}`":
+        if len(cells) == 7 and cells[0] == f"`{kernel}`":
             try:
-                return (float(cells[4]) + float(cells[5])) * 1e9
+                return (float(cells[5]) + float(cells[6])) * 1e9
             except ValueError:
                 return None
     return None
