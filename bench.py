@@ -618,6 +618,10 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
     model = vm.Model(vm.verify_cfg(), dev, torch.bfloat16, lanes=b, max_seq=ctx + 64, seed=0,
                      expert_mode="bytes", moe_rows=b * (k + 1))
     mtp.attach(model, k=k, seed=1, expert_mode="bytes")
+    # boot: capture the B-row bucket and validate the replay against the eager round
+    runner = graph_mtp.GraphMTPRunner(model, buckets=[b])
+    validated = runner.prepare()
+    log(f"mtp round: captured bucket {b}, validation {'passed' if validated else 'FAILED (eager rounds)'}")
     start = ctx - 32
     for lane in range(b):
         model.blocks.grow(lane, start)
@@ -632,7 +636,6 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
     model.mtp.pool["k"].normal_(generator=g)
     model.mtp.pool["v"].normal_(generator=g)
     model.hidden_cache.normal_(generator=g)
-    runner = graph_mtp.GraphMTPRunner(model, capacity=b)
     toks = torch.randint(0, model.cfg.vocab, (b,), generator=torch.Generator().manual_seed(4)).tolist()
     pos = [start] * b
     torch.cuda.synchronize()
@@ -690,6 +693,7 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
         "rounds": rounds,
         "weights": "random init (draft acceptance near zero)",
         "runner": "GraphMTPRunner (draft + verify + accept + commit replayed as one HIP graph)",
+        "capture_validated": bool(validated),
         "forced_full_accept": {
             "ms_per_round": round(f_wall * 1e3 / rounds, 3),
             "committed_per_round": round(f_committed / rounds, 2),

@@ -37,7 +37,9 @@ extern "C" {
 /* Human-readable text for a status code (static storage). */
 const char* mtpk_status_string(int status);
 
-/* ABI revision of this header; bumped on any signature change. */
+/* ABI revision of this header; bumped on any signature change. The library returns the value
+ * it was built with, and the Python binding refuses a library whose value differs. */
+#define MTPK_ABI_VERSION 2
 int mtpk_abi_version(void);
 
 /* ---------------------------------------------------------------- MXFP4 dequant
@@ -247,6 +249,16 @@ int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint
                    int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
                    int expert_hi, float* top_w, int32_t* top_i, void* workspace,
                    int64_t workspace_bytes, void* out, void* stream);
+/* 1 when `mtpk_moe_layer` accepts these operands (given a large enough workspace), else 0: the
+ * same checks, run without a launch and without dereferencing a pointer (pointers are tested
+ * for null and 16-byte alignment only). Lets a caller choose the unfused launches up front, as
+ * `Model.moe` chooses between `fuse_moe_dense` and the separate ops (model.py:913-928). */
+int mtpk_moe_layer_supported(const void* h, int64_t tokens, int64_t hidden, const void* router_gate,
+                             int64_t router_rows, const void* shared_gate_up,
+                             const void* shared_down, int64_t shared_inter, const void* gate_up,
+                             const void* gate_up_scale, const void* down, const void* down_scale,
+                             int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
+                             int expert_hi);
 
 /* ---------------------------------------------------------------- router top-k
  * Replaces `router_fused.route` / `_fused_route_kernel` (router_fused.py:56-151) and the torch
@@ -274,6 +286,9 @@ int mtpk_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
  * Inputs: step_argmax i64 [B, t] (row stride sa_stride), draft i64 [B, k] (row stride
  * draft_stride, e.g. token_matrix[:, 1:]), active u8 [B], pos i64 [B], budget i64 [B],
  * stops i64 [B, n_stops] padded with -1, conv_k1 = conv kernel width - 1.
+ * forced_n i64 [B] (may be NULL): a row with forced_n > 0 accepts exactly min(forced_n, k)
+ * drafts, unclamped by stops and budget, and its budget_left is budget - 1 (the forced
+ * override of graph_verify_wide.py:196-200 and LaneTables.update, mtp_overlap.py:53-71).
  * Outputs (any may be NULL except accept_len):
  *   accept_len i64 [B]  commit-limited accept length a
  *   lengths i64 [B]     a + 1 on active rows, 1 on padding rows
@@ -285,8 +300,8 @@ int mtpk_argmax_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
  *   hidden_src i64 [B]  j*t + a, the verify row whose hidden state seeds the next draft */
 int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
                        int64_t draft_stride, const uint8_t* active, const int64_t* pos,
-                       const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
-                       int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                       const int64_t* budget, const int64_t* stops, int n_stops,
+                       const int64_t* forced_n, int batch, int t, int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
                        int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
                        int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                        int64_t* hidden_src, void* stream);
@@ -302,8 +317,8 @@ int mtpk_argmax_keys(const void* logits, int dtype, int64_t rows, int64_t vocab,
 int mtpk_greedy_accept_keys(const uint64_t* keys, int64_t chunks, int64_t* step_argmax,
                             int64_t sa_stride, const int64_t* draft, int64_t draft_stride,
                             const uint8_t* active, const int64_t* pos, const int64_t* budget,
-                            const int64_t* stops, int n_stops, int batch, int t, int conv_k1,
-                            int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                            const int64_t* stops, int n_stops, const int64_t* forced_n, int batch,
+                            int t, int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
                             int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
                             int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                             int64_t* hidden_src, void* stream);

@@ -15,13 +15,19 @@ Reference functions, each restated below with its citation:
   called at `graph_mtp.py:578-580`), the committed tokens / bonus (`graph_mtp.py:887-891`),
   the lane-table update (`mtp_overlap.py:53-71`: next token, next position, budget left,
   live), and the KV physical rows `block * bs + pos % bs` (`graph_mtp.py:857-860`,
-  `block_pool.py:38` for the reserved block 0 of padding rows).
+  `block_pool.py:38` for the reserved block 0 of padding rows). With `forced_n`, the forced
+  override of the wide verify (`graph_verify_wide.py:196-200`: a forced row's accept length
+  is its forced count, unclamped by stops and budget) and the lane table's one-token charge
+  for forced rows (`mtp_overlap.py:62-64`).
 
 Pinning (tests/test_oracle_accept.py): the reference tests' literal vectors —
 `_accept_len` -> [3, 2, 1, 0] (`test_graph_mtp.py:305-318`), `_commit_limit` -> [1, 1, 1, 0, 0]
 (`test_mtp_serve.py:216-231`), `greedy_accept_length` 3/0/2 (`test_mtp.py:272-281`),
 `_fixed_prefix_pack_index` three cases (`test_graph_mtp.py:321-332`) — plus scalar-vs-batched
-agreement on random rows and brute-force argmax on tiny rows with planted ties.
+agreement on random rows and brute-force argmax on tiny rows with planted ties. The forced
+form (no reference vectors exist) is pinned by equivalence: a forced row's outputs equal an
+unforced row's whose drafts agree for exactly its forced count with no stop id and an unbounded
+budget, except `budget_left`, which is charged one token.
 """
 
 from __future__ import annotations
@@ -103,21 +109,26 @@ def round_indices(
     budget: np.ndarray,
     stops: np.ndarray,
     conv_k1: int,
+    forced_n: np.ndarray | None = None,
 ) -> dict[str, np.ndarray]:
     """Every per-round output the captured verify step derives from its argmaxes.
 
     `draft [B, k]`, `step_argmax [B, t]` with `t = k + 1`, `active [B]` bool, `pos`/`budget`
-    `[B]`, `stops [B, S]` padded with -1, `conv_k1` = conv kernel size - 1.
+    `[B]`, `stops [B, S]` padded with -1, `conv_k1` = conv kernel size - 1, `forced_n [B]`
+    (optional) the forced draft count of each row.
     """
     b, t = step_argmax.shape
     a = commit_limit_batched(accept_len(draft, step_argmax), step_argmax, budget, stops)
+    forced = np.zeros(b, dtype=bool) if forced_n is None else np.asarray(forced_n) > 0
+    if forced_n is not None:
+        a = np.where(forced, np.asarray(forced_n), a).astype(np.int64)
     lengths = np.where(active, a + 1, 1).astype(np.int64)
     src, cu = fixed_prefix_pack_index(lengths, t)
     win = np.arange(conv_k1)
     conv_idx = np.minimum(lengths[:, None] + win[None, :], conv_k1 + t - 1).astype(np.int64)
     keep = active[:, None] & (np.arange(t)[None, :] <= a[:, None])
     bonus = step_argmax[np.arange(b), a]
-    left = budget - (a + 1)
+    left = budget - np.where(forced, 1, a + 1)
     stopped = (stops == bonus[:, None]).any(1)
     return {
         "accept_len": a,

@@ -20,7 +20,7 @@ LIB_PATH = Path(os.environ.get("MTPK_LIB", str(HERE / "libmtpk.so")))
 F32, BF16, I32, I64, U8 = 0, 1, 2, 3, 4
 EINVAL, ENODEV, ETOOBIG = -1, -2, -3
 MOE_STATIC_SCRATCH = 64 << 20
-ABI_VERSION = 1
+ABI_VERSION = 2
 MAX_TOP_K = 32
 MAX_EXPERTS = 4096
 MAX_ROUTER_EXPERTS = 1024
@@ -95,6 +95,11 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_void_p, c_void_p,
          c_void_p, c_int64, c_void_p, c_void_p],
     ),
+    "mtpk_moe_layer_supported": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int],
+    ),
     "mtpk_paged_attention_gated": (
         c_int,
         [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64,
@@ -146,14 +151,14 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
     "mtpk_greedy_accept": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int,
-         c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+         c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
     "mtpk_greedy_accept_keys": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p,
-         c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+         c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
     "mtpk_argmax_keys": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "mtpk_rejection_workspace_bytes": (c_int64, [c_int64, c_int, c_int64]),
@@ -209,7 +214,10 @@ def lib() -> ctypes.CDLL:
         fn.restype = restype
         fn.argtypes = argtypes
     if handle.mtpk_abi_version() != ABI_VERSION:
-        raise RuntimeError("libmtpk.so ABI version does not match the Python binding")
+        raise RuntimeError(
+            f"libmtpk.so at {LIB_PATH} has ABI version {handle.mtpk_abi_version()}, the binding "
+            f"expects {ABI_VERSION}: rebuild it (`python __graft_entry__.py build`)"
+        )
     _lib = handle
     return handle
 

@@ -166,12 +166,16 @@ constexpr int kKeyRows = 4096;  // B * t bound of the keys path: one u64 of LDS 
 // then first folds them into one key per verify row (LDS max, so any key order gives the same
 // first-occurrence winner), writes the indices to sa_out and reads the verify columns from
 // LDS: the argmax needs no second launch.
+// forced_n (optional): a row with forced_n[j] > 0 accepts exactly min(forced_n[j], k) drafts,
+// which are not generated output, so the stop ids and the budget do not clamp them and the
+// budget is charged the one target token (graph_verify_wide.py:196-200, mtp_overlap.py:53-71);
+// every other output follows from that accept length.
 __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
     const uint64_t* __restrict__ keys, int chunks, int64_t* sa_out,
     const int64_t* sa, int64_t ss, const int64_t* __restrict__ draft, int64_t ds,
     const uint8_t* __restrict__ active, const int64_t* __restrict__ pos,
-    const int64_t* __restrict__ budget, const int64_t* __restrict__ stops, int n_stops, int B,
-    int t, int conv_k1, int64_t* __restrict__ accept_len, int64_t* __restrict__ lengths,
+    const int64_t* __restrict__ budget, const int64_t* __restrict__ stops, int n_stops,
+    const int64_t* __restrict__ forced_n, int B, int t, int conv_k1, int64_t* __restrict__ accept_len, int64_t* __restrict__ lengths,
     int64_t* __restrict__ packed_src, int32_t* __restrict__ packed_cu,
     int64_t* __restrict__ conv_idx, uint8_t* __restrict__ keep, int64_t* __restrict__ bonus,
     int64_t* __restrict__ next_pos, int64_t* __restrict__ budget_left,
@@ -187,7 +191,7 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
   const int64_t* drow = draft + (int64_t)(j < B ? j : 0) * ds;
   const int64_t* srow = stops + (int64_t)(j < B ? j : 0) * n_stops;
   int64_t dv[kPre], sv[kPre];
-  int64_t bud = 0, p0 = 0;
+  int64_t bud = 0, p0 = 0, fn = 0;
   bool act = false;
   if (j < B) {
 #pragma unroll
@@ -197,6 +201,7 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
     }
     bud = budget[j];
     act = active[j] != 0;
+    fn = forced_n ? forced_n[j] : 0;
     p0 = next_pos ? pos[j] : 0;
   }
   if (keys) {
@@ -253,6 +258,7 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
     int64_t lim = acc < first_stop ? acc : first_stop;
     if (bud - 1 < lim) lim = bud - 1;
     if (lim < 0) lim = 0;
+    if (fn > 0) lim = fn < k ? fn : k;  // forced drafts: accepted as they are
     const int a = (int)lim;
     len = act ? a + 1 : 1;
     accept_len[j] = a;
@@ -260,7 +266,7 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
     const int64_t bn = column(a);
     if (bonus) bonus[j] = bn;
     if (next_pos) next_pos[j] = p0 + a + 1;
-    const int64_t left = bud - (a + 1);
+    const int64_t left = bud - (fn > 0 ? 1 : a + 1);
     if (budget_left) budget_left[j] = left;
     if (live) live[j] = (!is_stop(bn) && left > 0) ? 1 : 0;
     if (hidden_src) hidden_src[j] = (int64_t)j * t + a;
@@ -350,8 +356,8 @@ namespace {
 int greedy_accept_launch(const uint64_t* keys, int chunks, int64_t* sa_out,
                          const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
                          int64_t draft_stride, const uint8_t* active, const int64_t* pos,
-                         const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
-                         int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                         const int64_t* budget, const int64_t* stops, int n_stops,
+                         const int64_t* forced_n, int batch, int t, int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
                          int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
                          int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                          int64_t* hidden_src, void* stream) {
@@ -363,7 +369,7 @@ int greedy_accept_launch(const uint64_t* keys, int chunks, int64_t* sa_out,
   if (sa_stride < t || (t > 1 && draft_stride < t - 1)) return MTPK_EINVAL;
   hipLaunchKernelGGL(k_greedy_accept, dim3(1), dim3(kAcceptThreads), 0, (hipStream_t)stream,
                      keys, chunks, sa_out, step_argmax, sa_stride, draft, draft_stride, active, pos,
-                     budget, stops, n_stops, batch, t, conv_k1, accept_len, lengths, packed_src,
+                     budget, stops, n_stops, forced_n, batch, t, conv_k1, accept_len, lengths, packed_src,
                      packed_cu, conv_idx, keep, bonus, next_pos, budget_left, live, hidden_src);
   return status_of(hipGetLastError());
 }
@@ -372,13 +378,13 @@ int greedy_accept_launch(const uint64_t* keys, int chunks, int64_t* sa_out,
 
 int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int64_t* draft,
                        int64_t draft_stride, const uint8_t* active, const int64_t* pos,
-                       const int64_t* budget, const int64_t* stops, int n_stops, int batch, int t,
-                       int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                       const int64_t* budget, const int64_t* stops, int n_stops,
+                       const int64_t* forced_n, int batch, int t, int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
                        int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
                        int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                        int64_t* hidden_src, void* stream) {
   return greedy_accept_launch(nullptr, 0, nullptr, step_argmax, sa_stride, draft, draft_stride,
-                              active, pos, budget, stops, n_stops, batch, t, conv_k1, accept_len,
+                              active, pos, budget, stops, n_stops, forced_n, batch, t, conv_k1, accept_len,
                               lengths, packed_src, packed_cu, conv_idx, keep, bonus, next_pos,
                               budget_left, live, hidden_src, stream);
 }
@@ -386,15 +392,15 @@ int mtpk_greedy_accept(const int64_t* step_argmax, int64_t sa_stride, const int6
 int mtpk_greedy_accept_keys(const uint64_t* keys, int64_t chunks, int64_t* step_argmax,
                             int64_t sa_stride, const int64_t* draft, int64_t draft_stride,
                             const uint8_t* active, const int64_t* pos, const int64_t* budget,
-                            const int64_t* stops, int n_stops, int batch, int t, int conv_k1,
-                            int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                            const int64_t* stops, int n_stops, const int64_t* forced_n, int batch,
+                            int t, int conv_k1, int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
                             int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
                             int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                             int64_t* hidden_src, void* stream) {
   if (!keys || chunks < 1 || chunks > 65535) return MTPK_EINVAL;
   if ((int64_t)batch * t > kKeyRows) return MTPK_EINVAL;
   return greedy_accept_launch(keys, (int)chunks, step_argmax, step_argmax, sa_stride, draft,
-                              draft_stride, active, pos, budget, stops, n_stops, batch, t, conv_k1,
+                              draft_stride, active, pos, budget, stops, n_stops, forced_n, batch, t, conv_k1,
                               accept_len, lengths, packed_src, packed_cu, conv_idx, keep, bonus,
                               next_pos, budget_left, live, hidden_src, stream);
 }

@@ -2162,6 +2162,38 @@ int64_t mtpk_moe_layer_workspace_bytes(int64_t tokens, int64_t hidden, int64_t r
       .total;
 }
 
+int mtpk_moe_layer_supported(const void* h, int64_t tokens, int64_t hidden, const void* router_gate,
+                             int64_t router_rows, const void* shared_gate_up,
+                             const void* shared_down, int64_t shared_inter, const void* gate_up,
+                             const void* gate_up_scale, const void* down, const void* down_scale,
+                             int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
+                             int expert_hi) {
+  if (!h || !router_gate || !shared_gate_up || !shared_down || !gate_up || !gate_up_scale ||
+      !down || !down_scale)
+    return 0;
+  if (tokens < 0 || tokens > 256 || tokens > 65535) return 0;
+  const int64_t experts = router_rows - 1;  // the router's last row is the shared expert's gate
+  if (experts <= 0 || experts > MTPK_MAX_ROUTER_EXPERTS || top_k <= 0 || top_k > MTPK_MAX_TOP_K ||
+      top_k > experts)
+    return 0;
+  if ((int64_t)expert_hi - expert_lo != local_experts || expert_lo < 0 || expert_hi > experts)
+    return 0;
+  if (!gemm_shapes_ok(hidden, inter_dim, local_experts) || hidden % kGemmKC ||
+      shared_inter <= 0 || shared_inter % kGemmKC || shared_inter % 16 || hidden % 4)
+    return 0;
+  if (!aligned16(h) || !aligned16(router_gate) || !aligned16(shared_gate_up) ||
+      !aligned16(shared_down) || !aligned16(gate_up) || !aligned16(down))
+    return 0;
+  if (router_rows * hidden * 2 > 0x7fffffffLL || 2 * shared_inter * hidden * 2 > 0x7fffffffLL)
+    return 0;
+  // the co-launches run 4-wave GEMM tiles
+  if (tokens > 0 && (gemm_waves(tokens, router_rows, kEpiStore) != 4 ||
+                     gemm_waves(tokens, 2 * shared_inter, kEpiSilu) != 4 ||
+                     gemm_waves(tokens, hidden, kEpiStore) != 4))
+    return 0;
+  return 1;
+}
+
 int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint16_t* router_gate,
                    int64_t router_rows, const uint16_t* shared_gate_up,
                    const uint16_t* shared_down, int64_t shared_inter, const uint8_t* gate_up,
@@ -2169,33 +2201,16 @@ int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint
                    int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
                    int expert_hi, float* top_w, int32_t* top_i, void* workspace,
                    int64_t workspace_bytes, void* out, void* stream) {
-  if (!h || !router_gate || !shared_gate_up || !shared_down || !gate_up || !gate_up_scale ||
-      !down || !down_scale || !workspace || !out)
+  if (!workspace || !out || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MTPK_EINVAL;
+  if (!mtpk_moe_layer_supported(h, tokens, hidden, router_gate, router_rows, shared_gate_up,
+                                shared_down, shared_inter, gate_up, gate_up_scale, down, down_scale,
+                                local_experts, inter_dim, top_k, expert_lo, expert_hi))
     return MTPK_EINVAL;
-  if (tokens < 0 || tokens > 256 || tokens > 65535) return MTPK_EINVAL;
-  const int64_t experts = router_rows - 1;  // the router's last row is the shared expert's gate
-  if (experts <= 0 || experts > MTPK_MAX_ROUTER_EXPERTS || top_k <= 0 || top_k > MTPK_MAX_TOP_K ||
-      top_k > experts)
-    return MTPK_EINVAL;
-  if ((int64_t)expert_hi - expert_lo != local_experts || expert_lo < 0 || expert_hi > experts)
-    return MTPK_EINVAL;
-  if (!gemm_shapes_ok(hidden, inter_dim, local_experts) || hidden % kGemmKC ||
-      shared_inter % kGemmKC || shared_inter % 16 || hidden % 4)
-    return MTPK_EINVAL;
-  if (!aligned16(h) || !aligned16(router_gate) || !aligned16(shared_gate_up) ||
-      !aligned16(shared_down) || !aligned16(gate_up) || !aligned16(down) ||
-      (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
-    return MTPK_EINVAL;
-  if (router_rows * hidden * 2 > 0x7fffffffLL || 2 * shared_inter * hidden * 2 > 0x7fffffffLL)
-    return MTPK_EINVAL;
+  const int64_t experts = router_rows - 1;
   if (tokens == 0) return 0;
   const LayerPlan pl =
       layer_plan(tokens, hidden, router_rows, shared_inter, top_k, local_experts, inter_dim);
   if (workspace_bytes < pl.total) return MTPK_EINVAL;
-  if (gemm_waves(tokens, router_rows, kEpiStore) != 4 ||
-      gemm_waves(tokens, 2 * shared_inter, kEpiSilu) != 4 ||
-      gemm_waves(tokens, hidden, kEpiStore) != 4)
-    return MTPK_EINVAL;  // the co-launches run 4-wave GEMM tiles
   char* w = static_cast<char*>(workspace);
   float* tw = top_w ? top_w : reinterpret_cast<float*>(w + pl.topw);
   int32_t* ti = top_i ? top_i : reinterpret_cast<int32_t*>(w + pl.topi);

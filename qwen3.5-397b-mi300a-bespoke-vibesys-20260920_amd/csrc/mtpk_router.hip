@@ -8,10 +8,9 @@
 // index); a round takes the wave maximum of those keys with DPP (row shifts, then the row
 // broadcasts: no LDS round trips), finds the lanes holding it with one ballot and, on a tie
 // between lanes, the lowest index with a second DPP reduction; only the winning lane rescans its
-// slots. Weights: the reference's p = exp(l - max) / sum, each selected p divided by the sum of
-// the selected ones (router_fused.py:85-107), computed as exp(l - max) over the selected
-// exp(l - max) accumulated in selection order (the softmax denominator cancels; the result
-// differs from the two-division form by rounding only).
+// slots. Weights: the reference's arithmetic (router_fused.py:85-107), p = exp(l - max) / S with
+// S the sum over every expert's exp(l - max), then each selected p divided by the sum of the
+// selected p accumulated in selection order.
 
 #include "mtpk_device.h"
 #include "mtpk_gemm_tile.h"
@@ -43,6 +42,11 @@ __device__ inline uint32_t dpp_min_u32(uint32_t v) {
 __device__ inline float dpp_max_f32(float v) {
   return bits_f32(dpp_reduce(f32_bits(v), f32_bits(-INFINITY),
                              [](uint32_t a, uint32_t b) { return f32_bits(fmaxf(bits_f32(a), bits_f32(b))); }));
+}
+
+__device__ inline float dpp_sum_f32(float v) {
+  return bits_f32(dpp_reduce(f32_bits(v), 0u,
+                             [](uint32_t a, uint32_t b) { return f32_bits(bits_f32(a) + bits_f32(b)); }));
 }
 
 // The row's logits in registers: lane l holds logits l + 64 j (j < PER). Every lane issues its
@@ -117,15 +121,19 @@ __device__ inline void route_row(float (&lg)[PER], int row, int E, int top_k, in
     m = fmaxf(m, lg[j]);
   }
   m = dpp_max_f32(m);
-  // The weights are e_i / sum of the selected e (e = exp(l - max)): the softmax's denominator
-  // cancels from p_i / sum p_sel, so it is never formed.
+  float part = 0.f;
 #pragma unroll
   for (int j = 0; j < PER; ++j) {
     const bool in = lane + kWave * j < E;
     e_[j] = in ? __expf(lg[j] - m) : 0.f;
+    part += e_[j];
     // a key of 0 marks "no candidate"; only NaNs with every payload bit set map below 1
     key[j] = in ? max(f32_order_key(lg[j]), 1u) : 0u;
   }
+  // the softmax probabilities p = e / S; a selected p is then divided by the selected p's sum
+  const float denom = dpp_sum_f32(part);
+#pragma unroll
+  for (int j = 0; j < PER; ++j) e_[j] = e_[j] / denom;
 
   // this lane's best free slot: strictly larger keys only, so the lowest slot wins a tie
   uint32_t bk = 0;

@@ -27,7 +27,7 @@ int device_cu_count() {
 
 extern "C" {
 
-int mtpk_abi_version(void) { return 1; }
+int mtpk_abi_version(void) { return MTPK_ABI_VERSION; }
 
 const char* mtpk_status_string(int status) {
   if (status == MTPK_OK) return "success";

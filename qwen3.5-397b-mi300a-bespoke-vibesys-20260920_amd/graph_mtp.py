@@ -134,11 +134,14 @@ KEY_ROWS = 4096
 def greedy_accept(step_argmax: torch.Tensor, draft: torch.Tensor, active: torch.Tensor,
                   pos: torch.Tensor, budget: torch.Tensor, stops: torch.Tensor, conv_k1: int,
                   *, out: AcceptResult | None = None,
-                  keys: tuple[torch.Tensor, int] | None = None) -> AcceptResult:
+                  keys: tuple[torch.Tensor, int] | None = None,
+                  forced_n: torch.Tensor | None = None) -> AcceptResult:
     """`mtpk_greedy_accept` on device tensors: step_argmax i64 [B, t], draft i64 [B, t-1] (row
     stride free, unit column stride), active bool [B], pos/budget i64 [B], stops i64 [B, S].
     With `keys` (`mtp.argmax_keys` of the [B * t, vocab] verify logits) the same launch first
-    finishes the argmax and writes it into `step_argmax` (`mtpk_greedy_accept_keys`)."""
+    finishes the argmax and writes it into `step_argmax` (`mtpk_greedy_accept_keys`). With
+    `forced_n` i64 [B], rows with `forced_n > 0` accept exactly their forced drafts (no stop or
+    budget clamp, one token charged to the budget), and every output follows from that."""
     device = _mtpk.require_device(step_argmax, draft, active, pos, budget, stops)
     b, t = step_argmax.shape
     if draft.shape != (b, t - 1) or (t > 1 and draft.stride(1) != 1) or step_argmax.stride(1) != 1:
@@ -162,13 +165,16 @@ def greedy_accept(step_argmax: torch.Tensor, draft: torch.Tensor, active: torch.
         key_t, chunks = keys
         if key_t.shape != (b * t, chunks) or not key_t.is_contiguous():
             raise ValueError(f"keys must be contiguous [{b * t}, {chunks}]")
+    if forced_n is not None and (forced_n.shape != (b,) or forced_n.dtype != torch.int64
+                                 or not forced_n.is_contiguous()):
+        raise ValueError(f"forced_n must be a contiguous int64 [{b}] tensor")
     _mtpk.check(
         (_mtpk.lib().mtpk_greedy_accept_keys if keys is not None else _mtpk.lib().mtpk_greedy_accept)(
             *((keys[0].data_ptr(), keys[1]) if keys is not None else ()),
             step_argmax.data_ptr(), step_argmax.stride(0), draft.data_ptr(),
             draft.stride(0) if t > 1 else 0, active.contiguous().data_ptr(),
             pos.contiguous().data_ptr(), budget.contiguous().data_ptr(), stops.data_ptr(),
-            stops.shape[1], b, t, conv_k1, out.accept_len.data_ptr(), out.lengths.data_ptr(),
+            stops.shape[1], _mtpk.ptr(forced_n), b, t, conv_k1, out.accept_len.data_ptr(), out.lengths.data_ptr(),
             out.packed_src.data_ptr(), out.packed_cu.data_ptr(),
             out.conv_idx.data_ptr() if conv_k1 > 0 else None, out.keep.data_ptr(),
             out.bonus.data_ptr(), out.next_pos.data_ptr(), out.budget_left.data_ptr(),
@@ -182,78 +188,98 @@ def greedy_accept(step_argmax: torch.Tensor, draft: torch.Tensor, active: torch.
 def kv_write_rows(pos: torch.Tensor, block_table: torch.Tensor, t: int, block_size: int) -> torch.Tensor:
     """Physical KV rows `block * bs + pos % bs` of a round's t positions (`graph_mtp.py:857-860`)."""
     grid = pos[:, None] + torch.arange(t, device=pos.device)[None, :]
-    block_id = torch.gather(block_table.long(), 1, (grid // block_size).long())
-    return block_id * block_size + grid % block_size
+    return vm.table_rows(block_table, grid, block_size)
+
+
+RESERVED_BLOCK = 0
+"""The block id padding rows' tables hold: never handed to a lane (`block_pool.py:38`)."""
+
+
+def accept_torch(step_argmax: torch.Tensor, draft: torch.Tensor, active: torch.Tensor,
+                 pos: torch.Tensor, budget: torch.Tensor, stops: torch.Tensor, conv_k1: int,
+                 forced_n: torch.Tensor | None, out: AcceptResult) -> None:
+    """What `greedy_accept` computes, in the reference's tensor ops, for CPU tensors (the CPU
+    engine's verify tail, `graph_mtp.py:541-580`, `graph_verify_wide.py:196-200`,
+    `mtp_overlap.py:53-71`); device tensors take the HIP kernel."""
+    b, t = step_argmax.shape
+    a = _commit_limit(_accept_len(draft, step_argmax), step_argmax, budget, stops)
+    forced = torch.zeros_like(active) if forced_n is None else forced_n > 0
+    if forced_n is not None:
+        a = torch.where(forced, forced_n.clamp(max=t - 1), a)
+    lengths = torch.where(active, a + 1, torch.ones_like(a))
+    src, cu = _fixed_prefix_pack_index(lengths, t)
+    win = torch.arange(conv_k1, device=a.device)
+    rows = torch.arange(b, device=a.device)
+    bonus = step_argmax[rows, a]
+    left = budget - torch.where(forced, torch.ones_like(a), a + 1)
+    stopped = (stops == bonus[:, None]).any(-1)
+    for dst, val in ((out.accept_len, a), (out.lengths, lengths), (out.packed_src, src),
+                     (out.packed_cu, cu), (out.conv_idx, (lengths[:, None] + win).clamp(max=conv_k1 + t - 1)),
+                     (out.keep, active[:, None] & (torch.arange(t, device=a.device)[None, :] <= a[:, None])),
+                     (out.bonus, bonus), (out.next_pos, pos + a + 1), (out.budget_left, left),
+                     (out.live, ~stopped & (left > 0)), (out.hidden_src, rows * t + a)):
+        dst.copy_(val)
 
 
 # ---------------------------------------------------------------- the device round
 
 
-def _draft_rows(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int,
-                forced: torch.Tensor | None = None, forced_n: torch.Tensor | None = None) -> None:
-    """`m.k` MTP draft steps for the first `b` rows of `buf` (lanes `lanes`), drafts written
-    into `buf.token_matrix[:, 1:]`. Device-only, no host read. A row with `forced_n[j] > 0`
-    feeds (and keeps) its forced tokens instead of its first drafts."""
-    hid = mtp_mod.draft_seed(model, model.hidden_cache[lanes])
-    tok = buf.token_matrix[:b, :1]
-    table = model.blocks.table[lanes]
+def _draft_rows(model, m, buf: MTPVerifyBuffers) -> None:
+    """`m.k` MTP draft steps over every row of `buf`, drafts written into
+    `buf.token_matrix[:, 1:]` (`draft_round_step`, `graph_mtp.py:477-504`): seeded from the
+    fill-time copy `buf.draft_hidden`, reading the MTP cache through `buf.block_table`. A row
+    with `forced_n[j] > 0` feeds (and keeps) its forced tokens instead of its first drafts.
+    Padding rows (`active` False) write no MTP cache row. No host read."""
+    hid = mtp_mod.draft_seed(model, buf.draft_hidden)
+    tok = buf.token_matrix[:, :1]
     on_device = vm.kv_write_in_kernel(model)
     for s in range(m.k):
-        pos = buf.pos[:b] + s
-        rows = None if on_device else model.blocks.physical_rows(lanes, pos[:, None])[:, 0]
-        hid, tok = mtp_mod.draft_step(model, m, hid, tok, pos, rows, table)
-        if forced is not None:
-            tok = torch.where((forced_n > s)[:, None], forced[:, s : s + 1], tok)
-        buf.token_matrix[:b, s + 1] = tok[:, 0]
+        rows = None if on_device else buf.write_rows[:, s]
+        hid, tok = mtp_mod.draft_step(model, m, hid, tok, buf.pos + s, rows, buf.block_table,
+                                      buf.block_valid, buf.active)
+        tok = torch.where((buf.forced_n > s)[:, None], buf.forced_ids[:, s : s + 1], tok)
+        buf.token_matrix[:, s + 1] = tok[:, 0]
 
 
-def _verify_rows(model, m, buf: MTPVerifyBuffers, lanes: torch.Tensor, b: int, ctx_len: int,
-                 forced_n: torch.Tensor | None = None) -> None:
-    """Verify forward over `buf.token_matrix[:b]`, argmax, acceptance with every rollback
-    index (`mtpk_greedy_accept`), then the commit of DeltaNet state, MTP cache rows and the
-    cached hidden seed to each lane's accepted length. Device-only. Rows with
-    `forced_n[j] > 0` accept their forced drafts unconditionally."""
-    t = buf.t
+def _verify_rows(model, m, buf: MTPVerifyBuffers, ctx_len: int) -> None:
+    """Verify forward over every row of `buf.token_matrix`, argmax, acceptance with every
+    rollback index (`mtpk_greedy_accept`, forced rows accepting their forced drafts), then the
+    commit of DeltaNet state, MTP cache rows and the hidden seed to each row's accepted length
+    (`verify_round_step`, `graph_mtp.py:513-582`). Reads `buf.block_table` and
+    `buf.draft_hidden`; padding rows (`active` False) touch no lane state: no K/V row, no
+    DeltaNet commit, no MTP cache row, no hidden seed. No host read."""
+    t, b = buf.t, buf.capacity
     dev = buf.pos.device
-    pos = buf.pos[:b]
-    res = model.forward_rows(buf.token_matrix[:b], lanes, pos, ctx_len)
+    pos, slots, active = buf.pos, buf.slot_rows, buf.active
+    res = model.forward_rows(buf.token_matrix, slots, pos, ctx_len, block_table=buf.block_table,
+                             active=active)
     logits = model.logits(res.hidden)
-    keys = None
-    if dev.type == "cuda" and b * t <= KEY_ROWS:  # the accept launch finishes the argmax
-        keys = mtp_mod.argmax_keys(logits.reshape(b * t, -1))
+    out = AcceptResult(buf.accept_len, buf.lengths, buf.packed_src, buf.packed_cu, buf.conv_idx,
+                       buf.keep, buf.bonus, buf.next_pos, buf.budget_left, buf.live, buf.hidden_src)
+    draft = buf.token_matrix[:, 1:]
+    if dev.type == "cuda":
+        keys = None
+        if b * t <= KEY_ROWS:  # the accept launch finishes the argmax
+            keys = mtp_mod.argmax_keys(logits.reshape(b * t, -1))
+        else:
+            buf.step_argmax.copy_(model.argmax(logits).view(b, t))
+        greedy_accept(buf.step_argmax, draft, active, pos, buf.budget, buf.stops, buf.conv_k1,
+                      out=out, keys=keys, forced_n=buf.forced_n)
     else:
-        buf.step_argmax[:b] = model.argmax(logits).view(b, t)
-    out = AcceptResult(buf.accept_len[:b], buf.lengths[:b], buf.packed_src[: b * t],
-                       buf.packed_cu[: b + 1], buf.conv_idx[:b], buf.keep[:b], buf.bonus[:b],
-                       buf.next_pos[:b], buf.budget_left[:b], buf.live[:b], buf.hidden_src[:b])
-    greedy_accept(buf.step_argmax[:b], buf.token_matrix[:b, 1:], buf.active[:b], pos,
-                  buf.budget[:b], buf.stops[:b], buf.conv_k1, out=out, keys=keys)
-    if forced_n is not None:
-        # A forced lane commits its forced tokens plus one target token; stop ids and the
-        # budget do not apply to forced tokens (`graph_verify_wide.py:196-200`).
-        # Rows without forced feed keep the acceptance launch's outputs as they are.
-        f = (forced_n > 0) & buf.active[:b]
-        a = forced_n
-        length = a + 1
-        win = torch.arange(buf.conv_k1, device=dev)
-        keep = torch.arange(t, device=dev)[None, :] <= a[:, None]
-        conv = torch.clamp(length[:, None] + win[None, :], max=buf.conv_k1 + t - 1)
-        out.accept_len.copy_(torch.where(f, a, out.accept_len))
-        out.lengths.copy_(torch.where(f, length, out.lengths))
-        out.keep.copy_(torch.where(f[:, None], keep, out.keep))
-        out.hidden_src.copy_(torch.where(f, torch.arange(b, device=dev) * t + a, out.hidden_src))
-        out.conv_idx.copy_(torch.where(f[:, None], conv, out.conv_idx))
-    model.commit(res, lanes, out.lengths, conv_idx=out.conv_idx)
+        buf.step_argmax.copy_(model.argmax(logits).view(b, t))
+        accept_torch(buf.step_argmax, draft, active, pos, buf.budget, buf.stops, buf.conv_k1,
+                     buf.forced_n, out)
+    model.commit(res, slots, out.lengths, conv_idx=out.conv_idx, active=active)
     grid = pos[:, None] + torch.arange(t, device=dev)[None, :]
-    raw_seed = model.hidden_cache[lanes]
-    previous = torch.cat([raw_seed[:, None], res.hidden[:, :-1]], dim=1)
+    previous = torch.cat([buf.draft_hidden[:, None], res.hidden[:, :-1]], dim=1)
     if vm.kv_write_in_kernel(model):
-        mtp_mod.cache_target_rows(model, m, buf.token_matrix[:b], previous, grid, None, out.keep,
-                                  block_table=model.blocks.table[lanes], base_pos=pos)
+        mtp_mod.cache_target_rows(model, m, buf.token_matrix, previous, grid, None, out.keep,
+                                  block_table=buf.block_table, base_pos=pos)
     else:
-        mtp_mod.cache_target_rows(model, m, buf.token_matrix[:b], previous, grid,
-                                  model.blocks.physical_rows(lanes, grid), out.keep)
-    model.hidden_cache[lanes] = res.hidden.reshape(b * t, -1)[out.hidden_src]
+        mtp_mod.cache_target_rows(model, m, buf.token_matrix, previous, grid, buf.write_rows, out.keep)
+    seed = res.hidden.reshape(b * t, -1)[out.hidden_src]
+    # padding rows name an idle lane and write back its own seed: no row of the round writes it
+    model.hidden_cache[slots] = torch.where(active[:, None], seed, model.hidden_cache[slots])
 
 
 def _ctx_bound(model) -> int:
@@ -264,14 +290,14 @@ def _ctx_bound(model) -> int:
 
 def draft_round_step(model, mtp, buf: MTPVerifyBuffers, t: int) -> Callable[[], None]:
     """The draft step to capture (`graph_mtp.py:477-504`, same arguments): `t - 1` MTP steps
-    over every row of `buf`, seeded from each row's lane (`slot_rows`) and base token
+    over every row of `buf`, seeded from `draft_hidden` and the base token
     (`token_matrix[:, 0]`), each step's greedy token written into `token_matrix[:, 1 + step]`;
     rows with `forced_n > 0` feed and keep `forced_ids` instead."""
     if t != buf.t or t != mtp.k + 1:
         raise ValueError(f"t={t} does not match the buffers ({buf.t}) and the MTP head (k={mtp.k})")
 
     def step() -> None:
-        _draft_rows(model, mtp, buf, buf.slot_rows, buf.capacity, buf.forced_ids, buf.forced_n)
+        _draft_rows(model, mtp, buf)
 
     return step
 
@@ -283,107 +309,138 @@ build_draft_step = draft_round_step
 def verify_round_step(model, mtp, buf: MTPVerifyBuffers, t: int) -> Callable[[], None]:
     """The verify step to capture (`graph_mtp.py:513-582`, same arguments): one forward over
     every row of `buf`, the argmax, commit-limited acceptance with every rollback index, and the
-    commit of DeltaNet state, MTP cache rows and the hidden seed to each row's accepted length."""
+    commit of DeltaNet state, MTP cache rows and the hidden seed to each active row's accepted
+    length."""
     if t != buf.t:
         raise ValueError(f"t={t} does not match the buffers ({buf.t})")
     ctx = _ctx_bound(model)
 
     def step() -> None:
-        _verify_rows(model, mtp, buf, buf.slot_rows, buf.capacity, ctx, buf.forced_n)
+        _verify_rows(model, mtp, buf, ctx)
 
     return step
 
 
+def pad_slot_for(slots, lanes: int) -> int:
+    """The lane padding rows name (`graph_decode.pad_slot_for`'s role): the lowest lane not in
+    this round, so no real row of the round writes it and padding reads only idle state."""
+    taken = set(int(s) for s in slots)
+    for lane in range(lanes):
+        if lane not in taken:
+            return lane
+    raise ValueError("a padded round needs a lane outside the round")
+
+
 def _fill(model, mtp, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stops, forced) -> None:
-    """Write one round's inputs into `buf` (`MTPVerifyRunner.fill`, `graph_mtp.py:790-870`):
-    every row is a real lane (a bucket is sized to its round), so no row is padding."""
-    b, t, k = len(slots), buf.t, buf.t - 1
-    if b != buf.capacity or len(set(slots)) != b:
-        raise ValueError(f"need {buf.capacity} distinct slots, got {slots}")
+    """Write one round's inputs into `buf`, padding to `buf.capacity` rows
+    (`MTPVerifyRunner.fill`, `graph_mtp.py:795-874`; `MTP_INTERFACE.md:17-33`). Row `j < n` is the
+    round's `j`-th lane; rows `>= n` are padding: `active` False, position 0, an idle lane as
+    slot, no stop ids, budget `t`, and the reserved block in every block-table entry. Also
+    writes the fill-owned `block_table`, `block_valid`, `write_rows` and `draft_hidden`."""
+    n, t, k = len(slots), buf.t, buf.t - 1
+    lanes = model.lanes
+    if not 1 <= n <= buf.capacity or len(set(slots)) != n:
+        raise ValueError(f"need 1..{buf.capacity} distinct slots, got {slots}")
+    if any(not 0 <= int(s) < lanes for s in slots):
+        raise ValueError(f"slots must lie in [0, {lanes}), got {slots}")
+    for name, seq in (("tokens", tokens), ("positions", positions), ("budgets", budgets),
+                      ("stops", stops), ("forced", forced)):
+        if seq is not None and len(seq) != n:
+            raise ValueError(f"{name} has {len(seq)} entries for {n} slots")
     if stops is not None and any(len(s) > mtp_mod.MAX_STOP_IDS for s in stops):
         raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
     for s, p in zip(slots, positions, strict=True):
         model.blocks.grow(s, p + t)
+    pad = pad_slot_for(slots, lanes) if n < buf.capacity else 0
     big = 1 << 40
+    width = max(k, 1)
     rows = []
-    for j, (tk, p) in enumerate(zip(tokens, positions, strict=True)):
-        ids = list(forced[j])[:k] if forced else []
-        st = list(stops[j]) if stops else []
-        rows.append([tk, p, big if budgets is None else budgets[j], int(slots[j]), len(ids),
-                     *(ids + [0] * (max(k, 1) - len(ids))), *(st + [-1] * (mtp_mod.MAX_STOP_IDS - len(st)))])
+    for j in range(buf.capacity):
+        if j < n:
+            ids = list(forced[j])[:k] if forced else []
+            st = list(stops[j]) if stops else []
+            rows.append([tokens[j], positions[j], big if budgets is None else budgets[j], int(slots[j]),
+                         len(ids), 1, *(ids + [0] * (width - len(ids))),
+                         *(st + [-1] * (mtp_mod.MAX_STOP_IDS - len(st)))])
+        else:
+            rows.append([0, 0, t, pad, 0, 0, *([0] * width), *([-1] * mtp_mod.MAX_STOP_IDS)])
     host = torch.tensor(rows, dtype=torch.long).to(buf.pos.device)
+    buf.token_matrix.zero_()
     buf.token_matrix[:, 0] = host[:, 0]
     buf.pos.copy_(host[:, 1])
     buf.budget.copy_(host[:, 2])
     buf.slot_rows.copy_(host[:, 3])
     buf.forced_n.copy_(host[:, 4])
-    buf.forced_ids.copy_(host[:, 5 : 5 + max(k, 1)])
-    buf.stops.copy_(host[:, 5 + max(k, 1) :])
-    buf.active.fill_(True)
+    buf.active.copy_(host[:, 5] != 0)
+    buf.forced_ids.copy_(host[:, 6 : 6 + width])
+    buf.stops.copy_(host[:, 6 + width :])
+    bs = model.cfg.block_size
+    buf.block_table.copy_(torch.where(buf.active[:, None], model.blocks.table[buf.slot_rows],
+                                      torch.full_like(buf.block_table, RESERVED_BLOCK)))
+    buf.block_valid.copy_(((buf.pos + t + bs - 1) // bs).to(torch.int32))
+    buf.write_rows.copy_(kv_write_rows(buf.pos, buf.block_table, t, bs))
+    buf.draft_hidden.copy_(model.hidden_cache[buf.slot_rows])
 
 
-def _committed(buf: MTPVerifyBuffers) -> list[list[int]]:
-    """The round's committed ids, `step_argmax[j, : accept + 1]`: one host read."""
-    rows = torch.cat([buf.step_argmax, buf.accept_len[:, None]], dim=1).tolist()
+def _committed(buf: MTPVerifyBuffers, n: int | None = None) -> list[list[int]]:
+    """The first `n` rows' committed ids, `step_argmax[j, : accept + 1]`: one host read."""
+    n = buf.capacity if n is None else n
+    rows = torch.cat([buf.step_argmax[:n], buf.accept_len[:n, None]], dim=1).tolist()
     return [row[: row[-1] + 1] for row in rows]
 
 
-class MTPVerifyRunner:
-    """Eager speculative rounds over static per-batch-size buffers (`graph_mtp.MTPVerifyRunner`,
-    `graph_mtp.py:893-918`): fill, draft, verify + accept + commit, one host read. `capacity`
-    (default: every lane of the model) bounds the batch size."""
+def build_buckets(capacity: int) -> list[int]:
+    """Round capacities a runner keeps buffers (and graphs) for: powers of two below
+    `capacity`, then `capacity` (the role of `graph_decode.build_buckets`)."""
+    out, b = [], 1
+    while b < capacity:
+        out.append(b)
+        b *= 2
+    return out + [capacity]
 
-    def __init__(self, model, mtp=None, capacity: int | None = None) -> None:
+
+class MTPVerifyRunner:
+    """Eager speculative rounds over static per-bucket buffers (`graph_mtp.MTPVerifyRunner`,
+    `graph_mtp.py:622-976`): fill (padding the round to the smallest bucket that holds it),
+    draft, verify + accept + commit, one host read. `capacity` (default: every lane of the model)
+    bounds the batch size; `buckets` (default `build_buckets(capacity)`) are the round sizes
+    buffers are kept for."""
+
+    def __init__(self, model, mtp=None, capacity: int | None = None,
+                 buckets: list[int] | None = None) -> None:
         mtp = model.mtp if mtp is None else mtp
         if mtp is None:
             raise ValueError("model has no MTP layer")
         self.model, self.mtp = model, mtp
         self.t = mtp.k + 1
         self.capacity = model.lanes if capacity is None else capacity
+        if not 1 <= self.capacity <= model.lanes:
+            raise ValueError(f"capacity {self.capacity} outside 1..{model.lanes} lanes")
+        self.buckets = sorted(set(buckets)) if buckets else build_buckets(self.capacity)
+        if self.buckets[0] < 1 or self.buckets[-1] > model.lanes:
+            raise ValueError(f"buckets {self.buckets} must lie in 1..{model.lanes}")
+        self.capacity = self.buckets[-1]
         self.bufs: dict[int, MTPVerifyBuffers] = {}
 
-    def buffers(self, b: int) -> MTPVerifyBuffers:
-        if not 1 <= b <= self.capacity:
-            raise ValueError(f"batch of {b} lanes: this runner takes 1..{self.capacity}")
+    def bucket_for(self, n: int) -> int:
+        """The smallest bucket holding `n` rows (`graph_decode.bucket_for`)."""
+        for b in self.buckets:
+            if b >= n:
+                return b
+        raise ValueError(f"batch of {n} lanes: this runner takes 1..{self.capacity}")
+
+    def buffers(self, n: int) -> MTPVerifyBuffers:
+        """The buffers of the bucket serving an `n`-lane round."""
+        if n < 1:
+            raise ValueError("a round needs at least one lane")
+        b = self.bucket_for(n)
         if b not in self.bufs:
             self.bufs[b] = MTPVerifyBuffers(self.model, b, self.t, self.model.device)
         return self.bufs[b]
 
-    def speculative_decode(self, slots: list[int], tokens: list[int], positions: list[int],
-                           budgets=None, stops=None, forced=None) -> list[list[int]]:
-        """Each slot's committed ids for one round (`Model.speculative_decode`'s contract);
-        `forced` rows commit their forced drafts plus one target token."""
-        buf = self.buffers(len(slots))
+    def fill(self, buf: MTPVerifyBuffers, slots, tokens, positions, budgets=None, stops=None,
+             forced=None) -> None:
         _fill(self.model, self.mtp, buf, slots, tokens, positions, budgets, stops, forced)
-        draft_round_step(self.model, self.mtp, buf, self.t)()
-        verify_round_step(self.model, self.mtp, buf, self.t)()
-        return _committed(buf)
-
-
-class GraphMTPRunner(MTPVerifyRunner):
-    """`MTPVerifyRunner` with each batch size's draft and verify steps captured in one HIP graph
-    (`GraphMTPRunner(model, backend=None)`, `graph_mtp.py:1062-1120`). A round writes the
-    bucket's static buffers, replays its graph and reads the committed ids once; forced feed
-    rides in the buffers, so forced rounds replay the same graph. The first round of a batch size
-    runs eagerly on the capture stream (its result is that round's) and is then captured.
-
-    `backend` is the reference's capture-backend slot: HIP graphs through `torch.cuda.CUDAGraph`
-    are the only backend here, so it must be None. `capacity` (keyword) bounds the batch size."""
-
-    def __init__(self, model, backend=None, *, capacity: int | None = None) -> None:
-        if backend is not None:
-            raise ValueError("GraphMTPRunner captures HIP graphs only; backend must be None")
-        super().__init__(model, None, capacity)
-        self.graphs: dict[int, torch.cuda.CUDAGraph] = {}
-
-    def prepare(self) -> bool:
-        """The reference's boot hook (`graph_mtp.py:1077-1081`): graphs are captured on each
-        batch size's first round instead, so there is nothing to do up front."""
-        return True
-
-    def forced_drafts(self) -> bool:
-        """Whether rounds may carry forced feed (`graph_mtp.py:1116-1118`): always."""
-        return True
 
     def _round(self, buf: MTPVerifyBuffers) -> None:
         draft_round_step(self.model, self.mtp, buf, self.t)()
@@ -391,25 +448,168 @@ class GraphMTPRunner(MTPVerifyRunner):
 
     def speculative_decode(self, slots: list[int], tokens: list[int], positions: list[int],
                            budgets=None, stops=None, forced=None) -> list[list[int]]:
-        b = len(slots)
-        buf = self.buffers(b)
-        _fill(self.model, self.mtp, buf, slots, tokens, positions, budgets, stops, forced)
-        graph = self.graphs.get(b)
-        if graph is None:
-            dev = buf.pos.device
-            side = torch.cuda.Stream(dev)
-            side.wait_stream(torch.cuda.current_stream())
-            with torch.cuda.stream(side):
-                self._round(buf)  # this round, run eagerly; also warms the allocator
-            torch.cuda.current_stream().wait_stream(side)
-            torch.cuda.synchronize(dev)
-            graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(graph):
-                self._round(buf)
-            self.graphs[b] = graph
+        """Each slot's committed ids for one round (`Model.speculative_decode`'s contract);
+        `forced` rows commit their forced drafts plus one target token."""
+        buf = self.buffers(len(slots))
+        self.fill(buf, slots, tokens, positions, budgets, stops, forced)
+        self._round(buf)
+        return _committed(buf, len(slots))
+
+
+class CudaGraphBackend:
+    """Captures a step as one HIP graph (`torch.cuda.CUDAGraph`) and returns its replay."""
+
+    def capture(self, fn: Callable[[], None], device: torch.device) -> Callable[[], None]:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+        return graph.replay
+
+
+class EagerBackend:
+    """Runs the step itself at every replay: the capture-free backend the reference's tests
+    use (`EagerBackend`), which lets the runner's bucketing and validation run on the CPU."""
+
+    def capture(self, fn: Callable[[], None], device: torch.device) -> Callable[[], None]:
+        return fn
+
+
+REQUIRE_GRAPH_ENV = "SEED_MTP_REQUIRE_GRAPH"
+"""`=1`: a bucket that fails capture or validation raises instead of serving eager rounds
+(`graph_mtp.py:112-116`)."""
+
+
+class GraphMTPRunner(MTPVerifyRunner):
+    """`MTPVerifyRunner` with each bucket's draft and verify steps captured as one graph
+    (`GraphMTPRunner(model, backend=None)`, `graph_mtp.py:1062-1120`). A round pads to its
+    bucket, writes the bucket's static buffers, replays its graph and reads the committed ids
+    once; forced feed rides in the buffers, so forced rounds replay the same graph.
+
+    `prepare()` (boot) captures every bucket and validates each capture against the eager step
+    on a synthetic round (`graph_mtp.py:712-769`, `:978-1059`); a bucket that fails disables
+    the captured round, and rounds then run eagerly, or, under `SEED_MTP_REQUIRE_GRAPH=1`,
+    `prepare()` raises. Without `prepare()`, a bucket is captured on its first round (which
+    runs eagerly) and is not validated. `backend` is the capture backend: None for HIP graphs,
+    or `EagerBackend()`."""
+
+    def __init__(self, model, backend=None, *, capacity: int | None = None,
+                 buckets: list[int] | None = None) -> None:
+        super().__init__(model, None, capacity, buckets)
+        self.backend = CudaGraphBackend() if backend is None else backend
+        self.graphs: dict[int, Callable[[], None]] = {}
+        self.enabled = True
+        self.validated: dict[int, bool] = {}
+        self.eager_rounds = 0
+
+    def forced_drafts(self) -> bool:
+        """Whether rounds may carry forced feed (`graph_mtp.py:1116-1118`): always."""
+        return True
+
+    def _capture(self, buf: MTPVerifyBuffers) -> Callable[[], None]:
+        return self.backend.capture(lambda: self._round(buf), buf.pos.device)
+
+    def _eager_round(self, buf: MTPVerifyBuffers) -> None:
+        """The bucket's round run eagerly before its capture, on a side stream on a device (so
+        every lazy allocation and library handle exists before capture begins)."""
+        dev = buf.pos.device
+        if dev.type != "cuda":
+            self._round(buf)
+            return
+        side = torch.cuda.Stream(dev)
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            self._round(buf)
+        torch.cuda.current_stream().wait_stream(side)
+        torch.cuda.synchronize(dev)
+
+    def _reset_lanes(self) -> None:
+        for lane in range(self.model.lanes):
+            self.model.reset(lane)
+
+    def _validate(self, bucket: int, buf: MTPVerifyBuffers, replay: Callable[[], None]) -> bool:
+        """One synthetic round on `bucket` fresh lanes, eager and replayed from the same state:
+        committed ids and every lane's resulting state must agree bit for bit. Positions past
+        the first KV block, budgets and a stop id that clamp some rows mid-accept."""
+        model, t = self.model, self.t
+        vocab, bs = model.cfg.vocab, model.cfg.block_size
+        slots = list(range(bucket))
+        tokens = [(7 * i + 3) % vocab for i in range(bucket)]
+        positions = [bs + 1 + i % 3 for i in range(bucket)]
+        budgets = [1 + i % t for i in range(bucket)]
+        stops = [[(5 * i) % vocab] for i in range(bucket)]
+        self._reset_lanes()
+        grid = torch.arange(model.hidden_cache.numel(), device=model.device)
+        model.hidden_cache.copy_((grid.reshape(model.hidden_cache.shape) * 0.37).sin().to(model.hidden_cache.dtype))
+        before = [{k: v.clone() for k, v in p.items() if k in ("conv", "rec")} for p in model.pool]
+        seed = model.hidden_cache.clone()
+        self.fill(buf, slots, tokens, positions, budgets, stops)
+        self._round(buf)
+        want = _committed(buf, bucket)
+        want_state = ([{k: v.clone() for k, v in p.items() if k in ("conv", "rec")} for p in model.pool],
+                      model.hidden_cache.clone())
+        for p, snap in zip(model.pool, before, strict=True):
+            for k, v in snap.items():
+                p[k].copy_(v)
+        model.hidden_cache.copy_(seed)
+        self.fill(buf, slots, tokens, positions, budgets, stops)
+        replay()
+        got = _committed(buf, bucket)
+        ok = got == want and torch.equal(model.hidden_cache, want_state[1])
+        for p, snap in zip(model.pool, want_state[0], strict=True):
+            for k, v in snap.items():
+                ok = ok and torch.equal(p[k], v)
+        return bool(ok)
+
+    def prepare(self) -> bool:
+        """Capture and validate every bucket (the reference's boot hook, `graph_mtp.py:712-769`).
+        Boot-only: every lane must be idle; all lanes are reset afterwards. Returns whether the
+        captured round is enabled."""
+        import os
+
+        model = self.model
+        if any(model.blocks.host[lane] for lane in range(model.lanes)):
+            raise RuntimeError("prepare() is boot-only: some lanes hold KV blocks")
+        self.graphs, self.validated = {}, {}
+        ok = True
+        try:
+            for bucket in self.buckets:
+                buf = self.buffers(bucket)
+                # warm every lazy allocation on real rows, then capture from a clean state
+                self._reset_lanes()
+                self.fill(buf, list(range(bucket)), [0] * bucket, [0] * bucket)
+                self._eager_round(buf)
+                self._reset_lanes()
+                replay = self._capture(buf)
+                good = self._validate(bucket, buf, replay)
+                self.validated[bucket] = good
+                self.graphs[bucket] = replay
+                ok = ok and good
+        except Exception as exc:  # a failed capture disables the captured round, as a mismatch does
+            if os.environ.get(REQUIRE_GRAPH_ENV, "0") == "1":
+                raise RuntimeError(f"{REQUIRE_GRAPH_ENV}: captured MTP round failed: {exc!r}") from exc
+            ok = False
+        finally:
+            self._reset_lanes()
+        self.enabled = ok
+        if not ok and os.environ.get(REQUIRE_GRAPH_ENV, "0") == "1":
+            raise RuntimeError(f"{REQUIRE_GRAPH_ENV}: captured MTP round failed validation "
+                               f"({self.validated})")
+        return ok
+
+    def speculative_decode(self, slots: list[int], tokens: list[int], positions: list[int],
+                           budgets=None, stops=None, forced=None) -> list[list[int]]:
+        if not self.enabled:
+            self.eager_rounds += 1
+            return super().speculative_decode(slots, tokens, positions, budgets, stops, forced)
+        buf = self.buffers(len(slots))
+        self.fill(buf, slots, tokens, positions, budgets, stops, forced)
+        replay = self.graphs.get(buf.capacity)
+        if replay is None:
+            self._eager_round(buf)  # this round, run eagerly; then the bucket is captured
+            self.graphs[buf.capacity] = self._capture(buf)
         else:
-            graph.replay()
-        return _committed(buf)
+            replay()
+        return _committed(buf, len(slots))
 
 
 # ---------------------------------------------------------------- sampling-mode acceptance

@@ -271,9 +271,9 @@ def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: 
     `(hid [B, hidden], tok [B, 1])` -> the next pair. `rope_pos` `[B]` is the fed token's
     position, `write_rows` `[B]` its MTP pool row (None when `verify_model.kv_write_in_kernel`:
     the K/V write maps the position through the table), `block_table` `[B, blocks]` the lanes'
-    tables.
-    `block_valid` and `active` are accepted for signature compatibility: the attention reads
-    the table up to its width and masks by position, and inactive lanes write their own rows."""
+    tables. `active` `[B]` bool (optional) masks the step's persistent write, its MTP K/V row:
+    padding rows write nothing. `block_valid` is accepted for signature compatibility (the
+    attention reads the table up to its width and masks by position)."""
     import verify_model as vm
 
     c, w = model.cfg, mtp.weights
@@ -281,7 +281,8 @@ def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: 
     h = vm.rmsnorm(x, w["in_norm"], c.eps)
     attn = vm.gated_attention(model, w, mtp.pool, h, rope_pos,
                               None if write_rows is None else write_rows.reshape(-1, 1),
-                              block_table, block_table.shape[1])
+                              block_table, block_table.shape[1],
+                              None if active is None else active[:, None])
     x, hm = vm.add_rmsnorm(x, attn, w["post_norm"], c.eps)
     _, normed = vm.add_rmsnorm(x, model.moe(w, hm[:, 0])[:, None], mtp.norm, c.eps)
     normed = normed[:, 0]

@@ -32,7 +32,16 @@ def dequant_mxfp4(packed: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype)
         raise ValueError(f"packed {tuple(packed.shape)} and scale {tuple(scale.shape)} disagree")
     if packed.device.type == "cuda":
         return _dequant_device(packed, scale).to(dtype)
-    lut = torch.tensor(_FP4_VALUES, dtype=torch.float32)
+    return dequant_torch(packed, scale, dtype)
+
+
+def dequant_torch(packed: torch.Tensor, scale: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """The reference's torch table lookup (`mxfp4.py:32-51`) on `packed`'s own device: the
+    CPU engine's dequant, and on a device the decode of the `SEED_FUSED_MOE=0` torch path
+    (scale byte 0 gives 2**-127, 255 gives +-inf / NaN, as torch's exp2 does)."""
+    if packed.shape[:-1] != scale.shape[:-1] or packed.shape[-1] * 2 != scale.shape[-1] * BLOCK:
+        raise ValueError(f"packed {tuple(packed.shape)} and scale {tuple(scale.shape)} disagree")
+    lut = torch.tensor(_FP4_VALUES, dtype=torch.float32, device=packed.device)
     lo = lut[(packed & 0xF).int()]
     hi = lut[(packed >> 4).int()]
     values = torch.stack([lo, hi], dim=-1).flatten(-2)
@@ -58,7 +67,8 @@ def _dequant_device(packed: torch.Tensor, scale: torch.Tensor, mode: int = 0) ->
 
 def dequant_in_kernel(packed: torch.Tensor, scale: torch.Tensor) -> torch.Tensor:
     """fp32 view of the MoE kernels' own in-register decode (hardware fp4 -> bf16 convert with
-    the block scale folded in). Exact for scale bytes 2..252; a test probe, not a serving op."""
+    the block scale folded in). Equal to the exact dequant bit for bit for scale bytes 0..254
+    (byte 0 as +-0.0); byte 255 gives NaN for every code. A test probe, not a serving op."""
     return _dequant_device(packed, scale, mode=1)
 
 

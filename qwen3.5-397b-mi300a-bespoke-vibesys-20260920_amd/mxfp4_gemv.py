@@ -62,8 +62,10 @@ def use_grouped(assignments: int, experts: int) -> bool:
     return assignments >= GROUPED_MIN_PER_EXPERT * max(experts, 1)
 
 
-_REFUSED: set[tuple[int, int]] = set()
-"""(gate_up_scale, down_scale) data pointers of expert payloads `supports` refused."""
+_VERDICT_ATTR = "_mtpk_decode_exact"
+"""Attribute `supports` sets on the two scale tensors it checked: True when the in-register
+decode reproduces them, False when it refused them. It lives and dies with those tensor objects,
+so a freed address that a later tensor reuses inherits nothing, and a copy is checked anew."""
 
 
 def bw_scales_ok(experts: dict) -> bool:
@@ -92,8 +94,11 @@ def bw_scales_ok(experts: dict) -> bool:
 def supports(experts: dict) -> bool:
     """Load-time check that `fused_moe` computes these experts exactly (the role of
     `moe_hip.supports`, `moe_hip.py:204-215`): contiguous MXFP4 payloads of matching shapes
-    and `bw_scales_ok`. A refusal is remembered, and `fused_moe` then raises `ValueError` for
-    these tensors instead of decoding them. One host sync."""
+    and `bw_scales_ok`. The verdict is kept on the two scale tensors, and `fused_moe` /
+    `fused_moe_layer` then raise `ValueError` for refused ones instead of decoding them.
+    `weights.load_experts` runs it for every MXFP4 shard it loads onto a device, and the first
+    `fused_moe` call that meets scale tensors with no verdict runs it then (outside graph
+    capture; a captured call on unchecked tensors cannot sync and is not checked). One host sync."""
     gu, gus, dn, dns = (experts[k] for k in ("gate_up", "gate_up_scale", "down", "down_scale"))
     shapes = (
         gu.dim() == 3 and dn.dim() == 3 and gu.shape[1] % 2 == 0
@@ -103,13 +108,23 @@ def supports(experts: dict) -> bool:
         and dn.shape[2] * 2 == gu.shape[1] // 2
         and all(t.is_contiguous() for t in (gu, gus, dn, dns))
     )  # fmt: skip
-    ok = shapes and bw_scales_ok(experts)
-    key = (gus.data_ptr(), dns.data_ptr())
-    if ok:
-        _REFUSED.discard(key)
-    else:
-        _REFUSED.add(key)
+    ok = bool(shapes and bw_scales_ok(experts))
+    setattr(gus, _VERDICT_ATTR, ok)
+    setattr(dns, _VERDICT_ATTR, ok)
     return ok
+
+
+def require_supported(experts: dict, what: str) -> None:
+    """`supports(experts)`, raising `ValueError` (naming `what`) on a refusal: the boot-time
+    form for loaders, so a checkpoint the kernels cannot decode exactly fails at load rather
+    than at its first MoE call."""
+    if not supports(experts):
+        raise ValueError(
+            f"{what}: the MXFP4 experts fail supports(): a 32-element block with e8m0 scale 255 "
+            "holds a nonzero code (or the payloads are not contiguous MXFP4 pairs of matching "
+            "shapes), which the fused kernels cannot decode exactly; SEED_FUSED_MOE=0 selects "
+            "the torch dequant path"
+        )
 
 
 def _validate(x, experts, routing, top_k):
@@ -131,7 +146,13 @@ def _validate(x, experts, routing, top_k):
             raise ValueError(f"experts[{name!r}] must be contiguous")
     if top_k > _mtpk.MAX_TOP_K:
         raise ValueError(f"top_k {top_k} exceeds {_mtpk.MAX_TOP_K}")
-    if _REFUSED and (experts["gate_up_scale"].data_ptr(), experts["down_scale"].data_ptr()) in _REFUSED:
+    gus, dns = experts["gate_up_scale"], experts["down_scale"]
+    verdict = (getattr(gus, _VERDICT_ATTR, None), getattr(dns, _VERDICT_ATTR, None))
+    if None in verdict and x.device.type == "cuda" and not torch.cuda.is_current_stream_capturing():
+        # scale tensors no loader checked (a copy, a hand-built dict): scanned once, here
+        supports(experts)
+        verdict = (getattr(gus, _VERDICT_ATTR), getattr(dns, _VERDICT_ATTR))
+    if False in verdict:
         raise ValueError("these experts failed supports(): a block with e8m0 scale 255 holds a "
                          "nonzero code, which the in-register decode cannot reproduce")
 
@@ -246,15 +267,35 @@ def layer_workspace_bytes(tokens: int, hidden: int, router_rows: int, shared_int
                                                           top_k, local_experts, intermediate))
 
 
-def layer_fits(h: torch.Tensor, router_gate: torch.Tensor, shared_down: torch.Tensor,
-               experts: dict) -> bool:
-    """Whether `fused_moe_layer` takes these operands: bf16 activations and dense weights, MXFP4
-    experts, 1..256 rows, hidden and the shared expert's width multiples of 256."""
-    return (
-        h.dtype == torch.bfloat16 and router_gate.dtype == torch.bfloat16
-        and shared_down.dtype == torch.bfloat16 and h.dim() == 2 and 1 <= h.shape[0] <= 256
-        and h.shape[1] % 256 == 0 and shared_down.shape[1] % 256 == 0 and "gate_up_scale" in experts
-    )  # fmt: skip
+def layer_fits(h: torch.Tensor, router_gate: torch.Tensor, shared_gate_up: torch.Tensor,
+               shared_down: torch.Tensor, experts: dict, top_k: int,
+               expert_range: tuple[int, int]) -> bool:
+    """Whether `fused_moe_layer` takes these operands (else the caller runs the separate ops):
+    contiguous bf16 activations and dense weights, contiguous MXFP4 experts, and every check of
+    `mtpk_moe_layer` itself (`mtpk_moe_layer_supported`: 1..256 rows, hidden and the shared
+    expert's width multiples of 256, top_k <= experts <= 1024, 16-byte aligned operands, 32-bit
+    weight offsets, the 4-wave GEMM tiles of its co-launches). No launch, no host sync."""
+    if not (h.dim() == 2 and 1 <= h.shape[0] <= 256 and "gate_up_scale" in experts
+            and "down_scale" in experts):
+        return False
+    dense = (h, router_gate, shared_gate_up, shared_down)
+    if any(t.dtype != torch.bfloat16 or t.dim() != 2 or not t.is_contiguous() for t in dense):
+        return False
+    names = ("gate_up", "gate_up_scale", "down", "down_scale")
+    if any(experts[k].dim() != 3 or not experts[k].is_contiguous() for k in names):
+        return False
+    gate_up, down = experts["gate_up"], experts["down"]
+    hidden, shared_inter = h.shape[1], shared_down.shape[1]
+    if (router_gate.shape[1] != hidden or shared_gate_up.shape != (2 * shared_inter, hidden)
+            or shared_down.shape[0] != hidden or down.shape[1] != hidden
+            or gate_up.shape[2] * 2 != hidden):
+        return False
+    lo, hi = expert_range
+    return bool(_mtpk.lib().mtpk_moe_layer_supported(
+        h.data_ptr(), h.shape[0], hidden, router_gate.data_ptr(), router_gate.shape[0],
+        shared_gate_up.data_ptr(), shared_down.data_ptr(), shared_inter, gate_up.data_ptr(),
+        experts["gate_up_scale"].data_ptr(), down.data_ptr(), experts["down_scale"].data_ptr(),
+        gate_up.shape[0], gate_up.shape[1] // 2, top_k, lo, hi))
 
 
 def fused_moe_layer(

@@ -278,14 +278,24 @@ def kv_write_in_kernel(model: "Model") -> bool:
     return model.device.type == "cuda" and model.dtype == torch.bfloat16
 
 
+def table_rows(block_table: torch.Tensor, pos: torch.Tensor, block_size: int) -> torch.Tensor:
+    """Physical pool rows `block * block_size + pos % block_size` of positions `pos` `[B, t]`
+    through per-row block tables `block_table` `[B, blocks]` (`graph_mtp.py:857-860`)."""
+    blk = torch.gather(block_table.long(), 1, pos.long() // block_size)
+    return blk * block_size + pos.long() % block_size
+
+
 def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_pos: torch.Tensor,
-                    write_rows: torch.Tensor, block_table: torch.Tensor, ctx_blocks: int) -> torch.Tensor:
+                    write_rows: torch.Tensor, block_table: torch.Tensor, ctx_blocks: int,
+                    keep: torch.Tensor | None = None) -> torch.Tensor:
     """Gated GQA attention of `t` rows per lane (`h` `[B, t, hidden]`, normed): q/gate
     projection, q/k RMSNorm, partial RoPE at `base_pos + s`, this round's K/V written at
     `write_rows` `[B, t]` of `pool`, causal paged attention, `o_proj(out * sigmoid(gate))`
     (`model.py:2158-2290`, `model.py:3519-3577`; the MTP layer's `_attn_rows`, `mtp.py:233-279`,
     is the same call on its own pool). When `kv_write_in_kernel(model)`, `write_rows` may be
-    None: the K/V write maps positions to pool rows through `block_table` itself."""
+    None: the K/V write maps positions to pool rows through `block_table` itself. `keep`
+    `[B, t]` bool (optional) masks the K/V writes: rows with False write nothing (on the torch
+    path they write into row 0, which lies in the reserved block 0 that no lane owns)."""
     c = model.cfg
     b, t, _ = h.shape
     qg = F.linear(h, w["q_proj"]).view(b, t, c.heads, 2 * c.head_dim)
@@ -302,9 +312,11 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
         cos, sin = model.cos[pos][:, :, None], model.sin[pos][:, :, None]  # [B, t, 1, rot]
         q, k = apply_rope(q, cos, sin), apply_rope(k, cos, sin)
     if kv_write_in_kernel(model):  # positions -> pool rows through the table, inside the kernel
-        attention.kv_write(pool["k"], pool["v"], k, v, block_table, base_pos)
+        attention.kv_write(pool["k"], pool["v"], k, v, block_table, base_pos, keep)
     else:
         rows = write_rows.reshape(-1).long()
+        if keep is not None:
+            rows = torch.where(keep.reshape(-1), rows, torch.zeros_like(rows))
         pool["k"][rows] = k.reshape(-1, c.kv_heads, c.head_dim)
         attention.write_v(pool["v"], rows, v.reshape(-1, c.kv_heads, c.head_dim))
     if attention.supported(q, c.block_size):
@@ -363,8 +375,7 @@ class BlockTables:
 
     def physical_rows(self, lanes: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """Physical pool rows of positions `pos` `[B, t]` of lanes `lanes` `[B]` (device)."""
-        blk = torch.gather(self.table[lanes.long()].long(), 1, pos.long() // self.block_size)
-        return blk * self.block_size + pos.long() % self.block_size
+        return table_rows(self.table[lanes.long()], pos, self.block_size)
 
 
 # ---------------------------------------------------------------- weights
@@ -540,11 +551,13 @@ class Model:
         """Routed MXFP4 experts + gated shared expert over rows `h` `[N, hidden]`
         (`model.py:2811-2873`)."""
         c = self.cfg
-        if (h.device.type == "cuda" and mxfp4_gemv.available(h.device)
-                and mxfp4_gemv.layer_fits(h, w["router_gate"], w["shared_down"], w["experts"])):
-            # router, shared expert and routed experts in the routed layer's launches
-            return mxfp4_gemv.fused_moe_layer(h.contiguous(), w["router_gate"], w["shared_gate_up"],
-                                              w["shared_down"], w["experts"], c.top_k, (0, c.experts))
+        if h.device.type == "cuda" and mxfp4_gemv.available(h.device):
+            hc = h.contiguous()
+            if mxfp4_gemv.layer_fits(hc, w["router_gate"], w["shared_gate_up"], w["shared_down"],
+                                     w["experts"], c.top_k, (0, c.experts)):
+                # router, shared expert and routed experts in the routed layer's launches
+                return mxfp4_gemv.fused_moe_layer(hc, w["router_gate"], w["shared_gate_up"],
+                                                  w["shared_down"], w["experts"], c.top_k, (0, c.experts))
         routing = linear(h, w["router_gate"])
         if h.device.type == "cuda":
             top_w, top_i = router_fused.route(routing, c.experts, c.top_k, index_dtype=torch.int32)
@@ -561,11 +574,11 @@ class Model:
             return mxfp4_gemv.fused_moe(h.contiguous(), w["experts"], assign, c.top_k, (0, c.experts),
                                         inter=self.moe_ws, shared=shared.contiguous(),
                                         shared_gate=routing[:, c.experts :])
-        elif h.device.type == "cuda":
-            raise RuntimeError("SEED_FUSED_MOE=0 has no device path in this build")
         else:
+            # SEED_FUSED_MOE=0 (or the CPU): the torch dequant-then-multiply path of
+            # `_routed_grouped` (`model.py:3170-3236`), dequantised by the torch table lookup
             routed = mxfp4_gemv.reference_moe(h, w["experts"], assign, c.top_k, (0, c.experts),
-                                              mxfp4.dequant_mxfp4)
+                                              mxfp4.dequant_torch)
         return routed + torch.sigmoid(routing[:, c.experts :]) * shared
 
     def _dense_moe(self, ex: dict, h: torch.Tensor, top_i: torch.Tensor,
@@ -587,18 +600,20 @@ class Model:
         return out.to(h.dtype)
 
     def attention_rows(self, w: dict, pool: dict, h: torch.Tensor, lanes: torch.Tensor,
-                       base_pos: torch.Tensor, ctx_len: int) -> torch.Tensor:
-        """Gated GQA attention for `t` rows per lane at positions `base_pos + s` over the
-        lanes' own block tables (`attn_verify`, `model.py:3519-3577`). `ctx_len` is a host
-        bound on `base_pos + t`."""
+                       base_pos: torch.Tensor, ctx_len: int, block_table: torch.Tensor | None = None,
+                       keep: torch.Tensor | None = None) -> torch.Tensor:
+        """Gated GQA attention for `t` rows per lane at positions `base_pos + s` (`attn_verify`,
+        `model.py:3519-3577`) over `block_table` `[B, blocks]` (default: the lanes' own tables),
+        K/V writes masked by `keep` `[B, t]`. `ctx_len` is a host bound on `base_pos + t`."""
         c = self.cfg
         t = h.shape[1]
+        table = self.blocks.table[lanes] if block_table is None else block_table
         rows = None
         if not kv_write_in_kernel(self):
             pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
-            rows = self.blocks.physical_rows(lanes, pos)
+            rows = table_rows(table, pos, c.block_size)
         ctx_blocks = (ctx_len + c.block_size - 1) // c.block_size
-        return gated_attention(self, w, pool, h, base_pos, rows, self.blocks.table[lanes], ctx_blocks)
+        return gated_attention(self, w, pool, h, base_pos, rows, table, ctx_blocks, keep)
 
     def deltanet_verify(self, w: dict, pool: dict, h: torch.Tensor,
                         lanes: torch.Tensor) -> tuple[torch.Tensor, DeltaNetRows]:
@@ -640,11 +655,13 @@ class Model:
         return mixer, DeltaNetRows(raw.contiguous(), q, k, v, g, beta)
 
     def deltanet_commit(self, pool: dict, rows: DeltaNetRows, lanes: torch.Tensor,
-                        lengths: torch.Tensor, conv_idx: torch.Tensor | None = None) -> None:
+                        lengths: torch.Tensor, conv_idx: torch.Tensor | None = None,
+                        active: torch.Tensor | None = None) -> None:
         """Advance slot `lanes[j]`'s conv window and recurrent state by `lengths[j]` of the
         verified rows (1..t) (`deltanet_verify_rollback`, `model.py:3907-3972`). `conv_idx`
         `[B, conv_k - 1]`, when given, is the acceptance kernel's window index
-        `min(lengths + w, conv_k - 2 + t)`; it is computed here otherwise."""
+        `min(lengths + w, conv_k - 2 + t)`; it is computed here otherwise. Rows with `active`
+        False (padding) leave every slot as it is."""
         c = self.cfg
         k1 = c.conv_k - 1
         t = rows.q.shape[1]
@@ -653,34 +670,48 @@ class Model:
             idx = conv_idx.long()
         else:
             idx = (n[:, None] + torch.arange(k1, device=self.device)[None, :]).clamp(max=k1 + t - 1)
-        if self.device.type == "cuda" and rows.proj is not None:
-            deltanet.conv_commit(pool["conv"], lanes, rows.proj, idx, c.conv_dim)
-            deltanet.delta_rule(pool["rec"], lanes, rows.q, rows.k, rows.v, rows.g, rows.beta, n,
+        if self.device.type == "cuda":
+            # the kernels skip a row whose slot lies outside the pool: padding commits nothing
+            slots = lanes if active is None else torch.where(active, lanes, torch.full_like(lanes, -1))
+            if rows.proj is not None:
+                deltanet.conv_commit(pool["conv"], slots, rows.proj, idx, c.conv_dim)
+            else:
+                window = torch.cat([pool["conv"][lanes], rows.raw_qkv], dim=-1)  # [B, C, k1 + t]
+                new = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
+                if active is not None:
+                    new = torch.where(active[:, None, None], new, pool["conv"][lanes])
+                pool["conv"][lanes] = new
+            deltanet.delta_rule(pool["rec"], slots, rows.q, rows.k, rows.v, rows.g, rows.beta, n,
                                 want_out=False)
             return
         window = torch.cat([pool["conv"][lanes], rows.raw_qkv], dim=-1)  # [B, C, k1 + t]
-        pool["conv"][lanes] = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
-        if self.device.type == "cuda":
-            deltanet.delta_rule(pool["rec"], lanes, rows.q, rows.k, rows.v, rows.g, rows.beta, n,
-                                want_out=False)
-            return
+        conv = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
         rep = c.v_heads // c.k_heads
         qe, ke = rows.q.repeat_interleave(rep, dim=2), rows.k.repeat_interleave(rep, dim=2)
         state = pool["rec"][lanes]
         for s in range(t):
             nxt, _ = delta_rule_step(state, qe[:, s], ke[:, s], rows.v[:, s], rows.g[:, s], rows.beta[:, s])
             state = torch.where((s < n)[:, None, None, None], nxt, state)
-        pool["rec"][lanes] = state
+        sel = torch.arange(lanes.shape[0]) if active is None else active.nonzero()[:, 0]
+        pool["conv"][lanes[sel]] = conv[sel]
+        pool["rec"][lanes[sel]] = state[sel]
 
     # ------------------------------------------------------------ forward
 
-    def forward_rows(self, ids: torch.Tensor, lanes, base_pos: torch.Tensor, ctx_len: int) -> VerifyOut:
+    def forward_rows(self, ids: torch.Tensor, lanes, base_pos: torch.Tensor, ctx_len: int, *,
+                     block_table: torch.Tensor | None = None,
+                     active: torch.Tensor | None = None) -> VerifyOut:
         """The wide forward over fed tokens `ids` `[B, t]` at positions `base_pos[b] + s`
         (`verify_and_commit`'s layer loop, `mtp.py:767-772`). Writes the rows' K/V; DeltaNet
-        state is left for `commit`. `ctx_len` is a host bound on `max(base_pos) + t`."""
+        state is left for `commit`. `ctx_len` is a host bound on `max(base_pos) + t`.
+
+        `block_table` `[B, blocks]` (a round buffer's, `graph_mtp.py:141-178`) replaces the
+        lanes' own tables for the attention reads and the K/V writes; rows with `active` False
+        (padding) read their slot's state but write no K/V."""
         c = self.cfg
         lanes = self.lane_index(lanes)
         base_pos = base_pos.to(self.device, torch.long)
+        keep = None if active is None else active[:, None].expand(ids.shape[0], ids.shape[1])
         x = self.embed[ids.to(self.device)]
         res = VerifyOut(x)
         pending = None  # the previous layer's MoE output, added in front of the next norm
@@ -691,7 +722,7 @@ class Model:
             else:
                 x, h = add_rmsnorm(x, pending, w["in_norm"], c.eps)
             if ty == ATTN:
-                mixer = self.attention_rows(w, pool, h, lanes, base_pos, ctx_len)
+                mixer = self.attention_rows(w, pool, h, lanes, base_pos, ctx_len, block_table, keep)
             else:
                 mixer, rows = self.deltanet_verify(w, pool, h, lanes)
                 res.dn_rows[i] = rows
@@ -702,11 +733,12 @@ class Model:
         return res
 
     def commit(self, res: VerifyOut, lanes, lengths: torch.Tensor,
-               conv_idx: torch.Tensor | None = None) -> None:
-        """Advance every DeltaNet layer's state of `lanes` by `lengths` verified rows."""
+               conv_idx: torch.Tensor | None = None, active: torch.Tensor | None = None) -> None:
+        """Advance every DeltaNet layer's state of `lanes` by `lengths` verified rows; rows with
+        `active` False (padding) leave their slots untouched."""
         lanes = self.lane_index(lanes)
         for i, rows in res.dn_rows.items():
-            self.deltanet_commit(self.pool[i], rows, lanes, lengths, conv_idx)
+            self.deltanet_commit(self.pool[i], rows, lanes, lengths, conv_idx, active)
 
     def unembed(self, normed: torch.Tensor) -> torch.Tensor:
         return F.linear(normed, self.lm_head)

@@ -199,7 +199,11 @@ def load_experts(ck: Checkpoint, p: str, sh: Shard, dev: torch.device | str,
     `gate_up` `[count, 2I, ...]` (gate rows, then up rows), `down` `[count, H, ...]` and, for an
     MXFP4 checkpoint, `gate_up_scale` / `down_scale` (`model.py:758-804`). MXFP4 payloads stay
     uint8; dense checkpoints are cast to `dtype`. Local expert i is global expert
-    `sh.start + i`."""
+    `sh.start + i`.
+
+    An MXFP4 shard loaded onto a device that runs the fused kernels (`mxfp4_gemv.available`)
+    is checked there and then (`mxfp4_gemv.require_supported`, the reference's boot check
+    `model.py:1568-1575`): a block the kernels cannot decode exactly raises `ValueError` here."""
     dev = torch.device(dev)
     quant = ck.has(f"{p}.experts.{sh.start}.gate_proj.weight_scale")
     if sh.count <= 0:
@@ -246,4 +250,9 @@ def load_experts(ck: Checkpoint, p: str, sh: Shard, dev: torch.device | str,
     if quant:
         ex["gate_up_scale"] = stacked(("gate_proj", "up_proj"), "weight_scale", None)
         ex["down_scale"] = stacked(("down_proj",), "weight_scale", None)
+        if dev.type == "cuda":
+            import mxfp4_gemv
+
+            if mxfp4_gemv.available(dev):
+                mxfp4_gemv.require_supported(ex, f"{p} experts [{sh.start}, {sh.start + sh.count})")
     return ex

@@ -23,10 +23,11 @@ def dev_long(a, dev):
     return torch.from_numpy(np.ascontiguousarray(np.asarray(a, dtype=np.int64))).to(dev)
 
 
-def accept(dev, sa, draft, active, pos, budget, stops, conv_k1=3):
+def accept(dev, sa, draft, active, pos, budget, stops, conv_k1=3, forced_n=None):
     return graph_mtp.greedy_accept(
         dev_long(sa, dev), dev_long(draft, dev), torch.from_numpy(np.asarray(active, bool)).to(dev),
         dev_long(pos, dev), dev_long(budget, dev), dev_long(stops, dev), conv_k1,
+        forced_n=None if forced_n is None else dev_long(forced_n, dev),
     )
 
 
@@ -84,6 +85,33 @@ def test_random_batches_every_output(dev, seed, b, k):
     for name, w in want.items():
         got = getattr(r, name).cpu().numpy()
         assert np.array_equal(got.astype(w.dtype), w), name
+
+
+@pytest.mark.parametrize("seed", range(3))
+@pytest.mark.parametrize("b,k", [(1, 1), (9, 2), (48, 3), (1024, 3)])
+def test_forced_rows_every_output(dev, seed, b, k):
+    """Forced feed (`forced_n > 0`): the row accepts exactly its forced drafts, stop ids and
+    budget notwithstanding, and every lane-table and rollback output follows from that
+    (`accept_ref.round_indices(..., forced_n)`), bit for bit; unforced rows of the same batch
+    are as without forcing."""
+    rng = np.random.default_rng(seed * 10 + b)
+    t = k + 1
+    sa = rng.integers(0, 5, (b, t))
+    draft = np.where(rng.random((b, k)) < 0.6, sa[:, :k], rng.integers(0, 5, (b, k)))
+    active = rng.random(b) < 0.85
+    pos = rng.integers(0, 8000, b)
+    budget = rng.integers(1, 6, b)
+    stops = np.where(rng.random((b, 8)) < 0.2, rng.integers(0, 5, (b, 8)), -1)
+    forced_n = np.where(rng.random(b) < 0.5, rng.integers(1, k + 1, b), 0)
+    want = ar.round_indices(draft, sa, active, pos, budget, stops, 3, forced_n)
+    r = accept(dev, sa, draft, active, pos, budget, stops, 3, forced_n)
+    for name, w in want.items():
+        got = getattr(r, name).cpu().numpy()
+        assert np.array_equal(got.astype(w.dtype), w), name
+    plain = accept(dev, sa, draft, active, pos, budget, stops, 3, np.zeros(b, np.int64))
+    free = ar.round_indices(draft, sa, active, pos, budget, stops, 3)
+    for name, w in free.items():
+        assert np.array_equal(getattr(plain, name).cpu().numpy().astype(w.dtype), w), name
 
 
 def test_argmax_first_occurrence_and_zero_signs(dev):
@@ -146,6 +174,15 @@ def test_keys_path_finishes_the_argmax(dev, dt, b, t, v):
         dev_long(budget, dev), dev_long(stops, dev), 3, keys=mtp.argmax_keys(logits))
     assert np.array_equal(step_argmax.cpu().numpy(), want_sa)
     want = ar.round_indices(draft, want_sa, active, pos, budget, stops, 3)
+    for name, w in want.items():
+        assert np.array_equal(getattr(r, name).cpu().numpy().astype(w.dtype), w), name
+    # the same launch with forced feed on some rows
+    forced_n = np.where(rng.random(b) < 0.5, rng.integers(0, t, b), 0)
+    r = graph_mtp.greedy_accept(
+        step_argmax, dev_long(draft, dev), torch.from_numpy(active).to(dev), dev_long(pos, dev),
+        dev_long(budget, dev), dev_long(stops, dev), 3, keys=mtp.argmax_keys(logits),
+        forced_n=dev_long(forced_n, dev))
+    want = ar.round_indices(draft, want_sa, active, pos, budget, stops, 3, forced_n)
     for name, w in want.items():
         assert np.array_equal(getattr(r, name).cpu().numpy().astype(w.dtype), w), name
 

@@ -29,6 +29,20 @@ def test_config1_prefill_logits_match_cpu(dev) -> None:
         assert int(got.argmax()) == int(want.argmax())
 
 
+def test_config1_torch_moe_path_on_device(dev, monkeypatch) -> None:
+    """`SEED_FUSED_MOE=0`, the reference's A/B switch: the device model takes the torch
+    dequant-then-multiply MoE (`_routed_grouped`, `model.py:3170-3236`) instead of the fused
+    kernels, and its logits still match the CPU model's."""
+    import mxfp4_gemv
+
+    monkeypatch.setenv("SEED_FUSED_MOE", "0")
+    assert not mxfp4_gemv.available(dev)
+    ids = mh.prompts(1)
+    want = mh.build("cpu").prefill(0, ids[0])
+    got = mh.build(dev).prefill(0, ids[0]).cpu()
+    torch.testing.assert_close(got, want, rtol=1e-4, atol=2e-5)
+
+
 @pytest.mark.parametrize("k", [1, 3])
 def test_config1_speculative_rounds_match_greedy(dev, k: int) -> None:
     """2 prompts of 16 ids, 32 tokens: the device rounds commit the CPU greedy sequence."""
@@ -261,3 +275,117 @@ def test_config5_full_size_graph_rounds(dev) -> None:
     assert same >= 0.9 * total
     assert float(worst_t.median()) < 1e-2
     assert int((worst_t > 2e-2).sum()) <= b // 4
+
+
+# ---------------------------------------------------------------- buckets and padding rows
+
+
+def _idle(model, lanes) -> list[torch.Tensor]:
+    out = []
+    for lane in lanes:
+        out += [p[n][lane].clone() for p in model.pool for n in ("conv", "rec") if n in p]
+        out += [model.hidden_cache[lane].clone(), model.blocks.table[lane].clone()]
+    return out
+
+
+def test_config1_padded_graph_bucket_matches_unpadded(dev) -> None:
+    """A 3-lane round replayed on a captured 4-row bucket (one padding row naming idle lane 3)
+    commits what the unpadded 3-row eager round of an identical model commits, round after
+    round, the lanes' state agrees, and lane 3 comes out untouched
+    (`seed_tests/test_graph_mtp.py:260-299`)."""
+    k = 3
+    ids = mh.prompts(3)
+    a, b = mh.build(dev, k=k, lanes=4), mh.build(dev, k=k, lanes=4)
+    toks, pos = [], []
+    for lane, p in enumerate(ids):
+        toks.append(int(a.argmax(a.prefill(lane, p)[None])[0]))
+        b.prefill(lane, p)
+        pos.append(len(p))
+    idle = _idle(a, [3])
+    padded = graph_mtp.GraphMTPRunner(a, buckets=[4])
+    exact = graph_mtp.MTPVerifyRunner(b, buckets=[3, 4])
+    lanes = [0, 1, 2]
+    for r in range(4):
+        got = padded.speculative_decode(lanes, toks, pos, budgets=[40, 40, 3 + r], stops=[[], [7], []])
+        want = exact.speculative_decode(lanes, toks, pos, budgets=[40, 40, 3 + r], stops=[[], [7], []])
+        assert got == want, f"round {r}"
+        for j, c in enumerate(got):
+            pos[j] += len(c)
+            toks[j] = c[-1]
+    assert list(padded.graphs) == [4]
+    for lane in lanes:
+        mh.assert_slot_state_close(a, b, lane, pos[lane], rtol=1e-5, atol=1e-6)
+    for before, now in zip(idle, _idle(a, [3]), strict=True):
+        assert torch.equal(before, now)
+
+
+def test_graph_prepare_validates_and_refuses_a_divergent_capture(dev, monkeypatch) -> None:
+    """`prepare()` captures every bucket as a HIP graph and replays a synthetic round against
+    the eager step (`graph_mtp.py:712-769`); a capture whose replay diverges (here a host-side
+    perturbation of the argmax after the replay) is refused: rounds then run eagerly, and under
+    SEED_MTP_REQUIRE_GRAPH=1 prepare() raises."""
+
+    class Diverging(graph_mtp.GraphMTPRunner):
+        def _capture(self, buf):
+            inner = super()._capture(buf)
+
+            def replay():
+                inner()
+                buf.step_argmax.add_(1)
+
+            return replay
+
+    good = graph_mtp.GraphMTPRunner(mh.build(dev, k=3, lanes=4), capacity=4)
+    assert good.prepare() is True and good.validated == {1: True, 2: True, 4: True}
+    bad = Diverging(mh.build(dev, k=3, lanes=4), capacity=4)
+    assert bad.prepare() is False and not bad.enabled
+    ids = mh.prompts(2)
+    twin = mh.build(dev, k=3, lanes=4)
+    toks, pos = [], []
+    for lane, p in enumerate(ids):
+        toks.append(int(twin.argmax(twin.prefill(lane, p)[None])[0]))
+        bad.model.prefill(lane, p)
+        good.model.prefill(lane, p)
+        pos.append(len(p))
+    want = graph_mtp.MTPVerifyRunner(twin, capacity=4).speculative_decode([0, 1], toks, pos)
+    assert bad.speculative_decode([0, 1], toks, pos) == want
+    assert good.speculative_decode([0, 1], toks, pos) == want  # a validated graph replay
+    monkeypatch.setenv(graph_mtp.REQUIRE_GRAPH_ENV, "1")
+    with pytest.raises(RuntimeError, match="SEED_MTP_REQUIRE_GRAPH"):
+        Diverging(mh.build(dev, k=3, lanes=4), capacity=4).prepare()
+
+
+def test_config5_bucket48_serves_45_lanes(dev) -> None:
+    """Config 5's dimensions (bf16, 512 MXFP4 experts, vocab 248320): a 48-row captured bucket
+    serving 45 lanes. The three idle lanes (45..47) come out bit-identical (no K/V row, DeltaNet
+    commit or hidden seed from the padding rows), and the 45 real rows' results do not depend on
+    what the padding rows read: re-running the round from the same state after scrambling the
+    idle lanes' state gives bit-identical ids and lane state."""
+    b, k, ctx, n = 48, 3, 256, 45
+    model, toks, pos = mh.c5_model(dev, b, k, ctx)
+    lanes = list(range(n))
+    runner = graph_mtp.GraphMTPRunner(model, buckets=[b])
+    start = mh.snapshot(model)
+    runner.speculative_decode(lanes, toks[:n], pos[:n])  # eager, then captured
+    assert list(runner.graphs) == [b]
+    mh.restore(model, start)
+    idle = _idle(model, range(n, b))
+    got = runner.speculative_decode(lanes, toks[:n], pos[:n])  # graph replay
+    for j, c in enumerate(got):
+        assert 1 <= len(c) <= k + 1 and all(0 <= x < model.cfg.vocab for x in c)
+    for before, now in zip(idle, _idle(model, range(n, b)), strict=True):
+        assert torch.equal(before, now)
+    after = [mh.slot_state(model, j, pos[j] + len(got[j])) for j in lanes]
+
+    mh.restore(model, start)
+    g = torch.Generator(device=dev).manual_seed(77)
+    for p in model.pool:
+        for name in ("conv", "rec"):
+            if name in p:
+                p[name][n:].normal_(generator=g)
+    model.hidden_cache[n:].normal_(generator=g)
+    again = runner.speculative_decode(lanes, toks[:n], pos[:n])  # graph replay
+    assert again == got
+    for j in lanes:
+        for x, y in zip(after[j], mh.slot_state(model, j, pos[j] + len(got[j])), strict=True):
+            assert torch.equal(x, y), j

@@ -103,4 +103,10 @@ def test_supports_refuses_scale_255_over_nonzero_codes(dev):
         else:
             with pytest.raises(ValueError, match="supports"):
                 mxfp4_gemv.fused_moe(x, ex, routing, 2, (0, 2))
+            # the verdict belongs to the refused tensors, not their addresses: a copy that no
+            # one checked is scanned by its first call and refused the same way
+            fresh = {k: v.clone() for k, v in ex.items()}
+            with pytest.raises(ValueError, match="supports"):
+                mxfp4_gemv.fused_moe(x, fresh, routing, 2, (0, 2))
+            del fresh
         del ex

@@ -100,3 +100,48 @@ def test_argmax_first_and_kv_rows():
     table = np.array([[5, 9, 0], [2, 3, 0]])
     rows = ar.kv_rows(np.array([14, 0]), table, 4, 16)
     assert rows.tolist() == [[94, 95, 144, 145], [32, 33, 34, 35]]
+
+
+def test_forced_rows_equal_an_unforced_row_accepting_the_same_count():
+    """A forced row (`graph_verify_wide.py:196-200`) accepts exactly its forced count whatever
+    its drafts, stop ids and budget say: its outputs equal those of an unforced row whose
+    drafts agree with the target for exactly that many steps, with no stop id and an unbounded
+    budget — except `budget_left`, charged one token (`mtp_overlap.py:62-64`). Unforced rows
+    in the same batch are unchanged by the forced ones."""
+    rng = np.random.default_rng(31)
+    for _ in range(50):
+        b, k = int(rng.integers(1, 9)), int(rng.integers(1, 5))
+        t = k + 1
+        sa = rng.integers(0, 6, (b, t))
+        draft = rng.integers(0, 6, (b, k))
+        active = rng.random(b) < 0.8
+        pos = rng.integers(0, 100, b)
+        budget = rng.integers(1, 8, b)
+        stops = np.where(rng.random((b, 2)) < 0.5, rng.integers(0, 6, (b, 2)), -1)
+        forced_n = np.where(rng.random(b) < 0.5, rng.integers(1, k + 1, b), 0)
+        got = ar.round_indices(draft, sa, active, pos, budget, stops, 3, forced_n)
+        plain = ar.round_indices(draft, sa, active, pos, budget, stops, 3)
+        # the equivalent unforced rows: drafts = target for f steps then a mismatch
+        eq_draft = draft.copy()
+        for j in range(b):
+            f = int(forced_n[j])
+            if f:
+                eq_draft[j, :f] = sa[j, :f]
+                if f < k:
+                    eq_draft[j, f] = sa[j, f] + 1
+        big = np.full(b, 1 << 40)
+        eq = ar.round_indices(eq_draft, sa, active, pos, np.where(forced_n > 0, big, budget),
+                              np.where((forced_n > 0)[:, None], -1, stops), 3)
+        for j in range(b):
+            ref = eq if forced_n[j] else plain
+            for key in ("accept_len", "lengths", "conv_idx", "keep", "bonus", "next_pos",
+                        "hidden_src"):
+                assert np.array_equal(got[key][j], ref[key][j]), (key, j)
+            assert got["accept_len"][j] == (forced_n[j] if forced_n[j] else plain["accept_len"][j])
+            charge = 1 if forced_n[j] else plain["accept_len"][j] + 1
+            assert got["budget_left"][j] == budget[j] - charge
+            stopped = bool((stops[j] == got["bonus"][j]).any())
+            assert got["live"][j] == ((not stopped) and got["budget_left"][j] > 0)
+        # the pack map is a function of the lengths alone
+        src, cu = ar.fixed_prefix_pack_index(got["lengths"], t)
+        assert np.array_equal(got["packed_src"], src) and np.array_equal(got["packed_cu"], cu)

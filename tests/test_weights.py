@@ -187,3 +187,38 @@ def test_loaded_experts_run_on_the_device(tmp_path) -> None:
                                (torch.from_numpy(a_e).to(dev), torch.from_numpy(a_w).to(dev)),
                                2, (0, E))
     assert moe_ref.relative_error(got.cpu().numpy(), want) < 1e-5
+
+
+@pytest.mark.gpu
+def test_scale_255_block_fails_at_load(tmp_path, monkeypatch) -> None:
+    """A shard holding a 32-element block with e8m0 scale 255 over nonzero codes (which the
+    in-register decode gives as NaN, the pinned decode as +-inf) is refused by `load_experts`
+    itself, not at its first MoE call. The same block over zero codes loads and runs, and with
+    `SEED_FUSED_MOE=0` (the torch path, which decodes 255 as pinned) the shard loads."""
+    import mxfp4_gemv
+
+    dev = torch.device("cuda:0")
+    tensors, _ = _mxfp4_tensors(seed=12)
+    name = f"{PREFIX}.experts.3.down_proj.weight_scale"
+    packed = f"{PREFIX}.experts.3.down_proj.weight"
+    tensors[name][7, 0] = 255
+    tensors[packed][7, :16] |= 0x11  # nonzero magnitudes in that block
+    _write_shards(tmp_path, tensors)
+    with pytest.raises(ValueError, match="supports"):
+        weights.load_experts(weights.Checkpoint(tmp_path), PREFIX, weights.Shard(0, E), dev,
+                             torch.bfloat16)
+    monkeypatch.setenv("SEED_FUSED_MOE", "0")
+    ex = weights.load_experts(weights.Checkpoint(tmp_path), PREFIX, weights.Shard(0, E), dev,
+                              torch.bfloat16)
+    assert int(ex["down_scale"][3, 7, 0]) == 255
+    monkeypatch.delenv("SEED_FUSED_MOE")
+
+    tensors[packed][7, :16] &= 0x88  # only signed zeros under the 255 scale
+    for f in tmp_path.glob("*.safetensors"):
+        f.unlink()
+    _write_shards(tmp_path, tensors)
+    ex = weights.load_experts(weights.Checkpoint(tmp_path), PREFIX, weights.Shard(0, E), dev,
+                              torch.bfloat16)
+    x = torch.randn(2, H, device=dev).to(torch.bfloat16)
+    routing = (torch.tensor([3, 1, 2, 3], dtype=torch.int32, device=dev), torch.full((4,), 0.5, device=dev))
+    assert torch.isfinite(mxfp4_gemv.fused_moe(x, ex, routing, 2, (0, E)).float()).all()
