@@ -705,14 +705,128 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
     return res
 
 
+def cpu_threads() -> int:
+    """Host threads for the CPU legs: the process's own OpenMP allotment (`OMP_NUM_THREADS`, 16
+    per GPU on the GPU boxes, whose `os.cpu_count()` counts every core of the node), else every
+    core the OS reports."""
+    cores = os.cpu_count() or 1
+    try:
+        return max(1, min(int(os.environ.get("OMP_NUM_THREADS", cores)), cores))
+    except ValueError:
+        return cores
+
+
+def _per_call(fn, budget_s: float, min_reps: int = 3) -> tuple[float, int]:
+    """Mean seconds per call of `fn` over at least `min_reps` calls and about `budget_s`."""
+    fn()
+    reps, t0 = 0, time.perf_counter()
+    while reps < min_reps or time.perf_counter() - t0 < budget_s:
+        fn()
+        reps += 1
+    return (time.perf_counter() - t0) / reps, reps
+
+
+def cpu_legs(threads: int) -> dict:
+    """The rest of the reference's CPU path, timed on the host beside the GPU legs: the torch
+    router chain at M = 192 (`model.py:2840-2843`), config 4's greedy acceptance (the argmax of
+    the bf16 [48, 4, 248320] logits, then the host `greedy_accept_length` / `commit_limit` per
+    lane, `mtp.py:691-726`, and the batched tensor forms, `graph_mtp.py:440-474`), config 4's
+    rejection sampling (the float64 restatement of the method), and config 1's CPU plumbing
+    (the tiny model's greedy MTP decode on the CPU engine, accepted tokens per second)."""
+    import torch
+
+    import graph_mtp
+    import mtp
+    import verify_model as vm
+    from oracle import cpu_path, rejection_ref
+
+    torch.set_num_threads(threads)
+    out = {}
+    g = torch.Generator().manual_seed(11)
+    routing = torch.randn(192, E + 1, generator=g)
+    sec, reps = _per_call(lambda: cpu_path.route(routing, E, TOP_K), 1.0)
+    out["router_chain"] = {"rows": 192, "us_per_call": round(sec * 1e6, 1), "reps": reps}
+
+    b, k, vocab = 48, 3, 248320
+    t = k + 1
+    target = (torch.randn(b, t, vocab, generator=g) * 3).to(torch.bfloat16)
+    draft_logits = (target.float() + torch.randn(b, t, vocab, generator=g)).to(torch.bfloat16)
+    drafts = draft_logits[:, :k].float().argmax(-1)
+    rng = np.random.default_rng(44)
+    budget = torch.from_numpy(rng.integers(1, 8, b))
+    stops = torch.full((b, mtp.MAX_STOP_IDS), -1, dtype=torch.long)
+    stops[:, 0] = torch.from_numpy(rng.integers(0, vocab, b))
+
+    def greedy_host():
+        sa = target.float().argmax(-1)
+        rows, dr = sa.tolist(), drafts.tolist()
+        for j in range(b):
+            a = mtp.greedy_accept_length(dr[j], rows[j][:k])
+            mtp.commit_limit(a, rows[j], int(budget[j]), [int(x) for x in stops[j] if x >= 0])
+
+    def greedy_tensor():
+        sa = target.float().argmax(-1)
+        graph_mtp._commit_limit(graph_mtp._accept_len(drafts, sa), sa, budget, stops)
+
+    sec_h, reps_h = _per_call(greedy_host, 2.0)
+    sec_t, reps_t = _per_call(greedy_tensor, 2.0)
+    sa0 = target.float().argmax(-1)
+    sec_a, _ = _per_call(lambda: graph_mtp._commit_limit(graph_mtp._accept_len(drafts, sa0), sa0,
+                                                         budget, stops), 0.5)
+    out["c4_greedy"] = {"shape": [b, t, vocab], "us_host_forms": round(sec_h * 1e6, 1),
+                        "us_tensor_forms": round(sec_t * 1e6, 1),
+                        "us_accept_tail_only": round(sec_a * 1e6, 1), "reps": [reps_h, reps_t]}
+
+    tnp, dnp = target.float().numpy(), draft_logits[:, :k].float().numpy()
+    ua = rng.random((b, k)).astype(np.float32)
+    us = rng.random(b).astype(np.float32)
+    dtok = dnp.argmax(-1)
+
+    def rejection():
+        rejection_ref.rejection_accept(tnp, dnp, dtok, ua, us, 0.7)
+
+    t0 = time.perf_counter()
+    rejection()
+    out["c4_rejection"] = {"us_per_call": round((time.perf_counter() - t0) * 1e6, 1), "reps": 1,
+                           "form": "float64 restatement of Leviathan et al. Alg. 1"}
+
+    cfg = vm.tiny_cfg()
+    model = vm.Model(cfg, "cpu", torch.float32, lanes=2, max_seq=96, seed=0)
+    mtp.attach(model, k=1, seed=1)
+    gp = torch.Generator().manual_seed(5)
+    prompts = [torch.randint(0, cfg.vocab, (16,), generator=gp).tolist() for _ in range(2)]
+    toks, pos = [], []
+    for lane, p in enumerate(prompts):
+        toks.append(int(model.argmax(model.prefill(lane, p)[None])[0]))
+        pos.append(len(p))
+    made, rounds = [1, 1], 0
+    t0 = time.perf_counter()
+    while min(made) < 32 + 1:
+        got = mtp.speculative_decode(model, [0, 1], toks, pos)
+        rounds += 1
+        for j, c in enumerate(got):
+            made[j] += len(c)
+            pos[j] += len(c)
+            toks[j] = c[-1]
+    wall = time.perf_counter() - t0
+    committed = sum(made) - 2
+    out["c1_plumbing"] = {"accepted_tok_s": round(committed / wall, 1), "rounds": rounds,
+                          "committed": committed, "tokens_per_lane_round": round(committed / rounds / 2, 3),
+                          "wall_s": round(wall, 3),
+                          "workload": "tiny Qwen3.5-MoE (hidden 64, 4 layers, 8 experts top-2, MXFP4), "
+                                      "2 prompts of 16 ids, greedy MTP decode k=1 for 32 tokens"}
+    return out
+
+
 def cpu_baseline(layer, inp, dl_full, budget_s):
     """The reference's CPU path (oracle.cpu_path, torch fp32) on a bounded sample of the M=192
-    workload: consecutive groups of 8 rows until ~budget_s of CPU work; scaled per expert."""
+    workload: consecutive groups of 8 rows until ~budget_s of CPU work; scaled per expert. The
+    other CPU legs (router chain, acceptance, config 1) ride in `legs`."""
     import torch
 
     from oracle import cpu_path
 
-    threads = min(os.cpu_count() or 1, 16)
+    threads = cpu_threads()
     torch.set_num_threads(threads)
     x, a_e, a_w, _ = inp
     ne, nw = a_e.cpu().numpy(), a_w.cpu().numpy()
@@ -758,6 +872,9 @@ def cpu_baseline(layer, inp, dl_full, budget_s):
         "sample": f"first {rows} of 192 rows in groups of 8 ({total_d} expert dequants, "
                   f"{total_t:.1f} s); torch fp32 restatement of Model._routed_grouped",
         "us_per_layer_est": round(us_layer, 1),
+        "threads_rule": "OMP_NUM_THREADS (the process's CPU share; 16 per GPU on the GPU box), "
+                        "capped by os.cpu_count()",
+        "legs": cpu_legs(threads),
     }
 
 

@@ -402,9 +402,9 @@ def build_buckets(capacity: int) -> list[int]:
 class MTPVerifyRunner:
     """Eager speculative rounds over static per-bucket buffers (`graph_mtp.MTPVerifyRunner`,
     `graph_mtp.py:622-976`): fill (padding the round to the smallest bucket that holds it),
-    draft, verify + accept + commit, one host read. `capacity` (default: every lane of the model)
-    bounds the batch size; `buckets` (default `build_buckets(capacity)`) are the round sizes
-    buffers are kept for."""
+    draft, verify + accept + commit, one host read. `capacity` (default, and at most: every lane
+    of the model) bounds the batch size; `buckets` (default `build_buckets(capacity)`) are the
+    round sizes buffers are kept for."""
 
     def __init__(self, model, mtp=None, capacity: int | None = None,
                  buckets: list[int] | None = None) -> None:
@@ -413,9 +413,9 @@ class MTPVerifyRunner:
             raise ValueError("model has no MTP layer")
         self.model, self.mtp = model, mtp
         self.t = mtp.k + 1
-        self.capacity = model.lanes if capacity is None else capacity
-        if not 1 <= self.capacity <= model.lanes:
-            raise ValueError(f"capacity {self.capacity} outside 1..{model.lanes} lanes")
+        self.capacity = model.lanes if capacity is None else min(capacity, model.lanes)
+        if self.capacity < 1:
+            raise ValueError(f"capacity {capacity} leaves no lane")
         self.buckets = sorted(set(buckets)) if buckets else build_buckets(self.capacity)
         if self.buckets[0] < 1 or self.buckets[-1] > model.lanes:
             raise ValueError(f"buckets {self.buckets} must lie in 1..{model.lanes}")

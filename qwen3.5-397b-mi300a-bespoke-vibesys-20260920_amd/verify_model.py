@@ -523,6 +523,9 @@ class Model:
         self.hidden_cache = torch.zeros(lanes, cfg.hidden, dtype=dtype, device=dev)
         self.cos, self.sin = rope_table(cfg, max_seq, dev)
         self.mtp = None
+        self.route_log: list | None = None
+        """When a list, every MoE call appends `(layer, h, top_i)`: the layer index (or "mtp"), a
+        copy of its input rows and its selected experts. A test hook; None in serving."""
         self.moe_ws = None
         if dev.type == "cuda":
             rows = moe_rows or lanes * 4
@@ -551,13 +554,20 @@ class Model:
         """Routed MXFP4 experts + gated shared expert over rows `h` `[N, hidden]`
         (`model.py:2811-2873`)."""
         c = self.cfg
+        log = self.route_log
         if h.device.type == "cuda" and mxfp4_gemv.available(h.device):
             hc = h.contiguous()
             if mxfp4_gemv.layer_fits(hc, w["router_gate"], w["shared_gate_up"], w["shared_down"],
                                      w["experts"], c.top_k, (0, c.experts)):
                 # router, shared expert and routed experts in the routed layer's launches
+                routing_out = None
+                if log is not None:
+                    routing_out = (torch.empty(hc.shape[0], c.top_k, dtype=torch.float32, device=h.device),
+                                   torch.empty(hc.shape[0], c.top_k, dtype=torch.int32, device=h.device))
+                    log.append((self._layer_of(w), hc.clone(), routing_out[1]))
                 return mxfp4_gemv.fused_moe_layer(hc, w["router_gate"], w["shared_gate_up"],
-                                                  w["shared_down"], w["experts"], c.top_k, (0, c.experts))
+                                                  w["shared_down"], w["experts"], c.top_k, (0, c.experts),
+                                                  routing_out=routing_out)
         routing = linear(h, w["router_gate"])
         if h.device.type == "cuda":
             top_w, top_i = router_fused.route(routing, c.experts, c.top_k, index_dtype=torch.int32)
@@ -565,6 +575,8 @@ class Model:
             probs = routing[:, : c.experts].float().softmax(-1)
             top_w, top_i = probs.topk(c.top_k, dim=-1)
             top_w = top_w / top_w.sum(-1, keepdim=True)
+        if log is not None:
+            log.append((self._layer_of(w), h.clone(), top_i.clone()))
         assign = (top_i.reshape(-1), top_w.reshape(-1))
         shared = swiglu(h, w["shared_gate_up"], w["shared_down"])
         if "gate_up_scale" not in w["experts"]:
@@ -580,6 +592,12 @@ class Model:
             routed = mxfp4_gemv.reference_moe(h, w["experts"], assign, c.top_k, (0, c.experts),
                                               mxfp4.dequant_torch)
         return routed + torch.sigmoid(routing[:, c.experts :]) * shared
+
+    def _layer_of(self, w: dict):
+        for i, lw in enumerate(self.layers):
+            if lw is w:
+                return i
+        return "mtp"
 
     def _dense_moe(self, ex: dict, h: torch.Tensor, top_i: torch.Tensor,
                    top_w: torch.Tensor) -> torch.Tensor:

@@ -87,9 +87,22 @@ def c5_model(dev, b: int = 48, k: int = 3, ctx: int = 8192):
     """The config-5 round the benchmark times: real layer dimensions (3 DeltaNet + 1 gated GQA +
     the MTP layer, 512 MXFP4 experts top-10), `b` lanes, each holding `ctx - 32` positions of
     seeded random context (K/V, DeltaNet state, hidden seeds). Returns (model, tokens, positions)."""
+    model, _, toks, pos = c5_model_and_runner(dev, b, k, ctx, prepare=False)
+    return model, toks, pos
+
+
+def c5_model_and_runner(dev, b: int = 48, k: int = 3, ctx: int = 8192, prepare: bool = True):
+    """`c5_model` plus a `GraphMTPRunner` with one `b`-row bucket, captured and validated by
+    `prepare()` at boot (before the context is filled) when `prepare`. Returns (model, runner,
+    tokens, positions)."""
+    import graph_mtp
+
     model = vm.Model(vm.verify_cfg(), dev, torch.bfloat16, lanes=b, max_seq=ctx + 64, seed=0,
                      expert_mode="bytes", moe_rows=b * (k + 1))
     mtp.attach(model, k=k, seed=1, expert_mode="bytes")
+    runner = graph_mtp.GraphMTPRunner(model, buckets=[b])
+    if prepare:
+        runner.prepare()
     start = ctx - 32
     for lane in range(b):
         model.blocks.grow(lane, start)
@@ -105,7 +118,7 @@ def c5_model(dev, b: int = 48, k: int = 3, ctx: int = 8192):
     model.mtp.pool["v"].normal_(generator=g)
     model.hidden_cache.normal_(generator=g)
     toks = torch.randint(0, model.cfg.vocab, (b,), generator=torch.Generator().manual_seed(4)).tolist()
-    return model, toks, [start] * b
+    return model, runner, toks, [start] * b
 
 
 def shape_model(hidden: int, max_blocks: int, conv_k: int = 4, dtype=None):

@@ -25,3 +25,16 @@ def test_zipf_routing_shape_and_live_experts():
     assert all(np.unique(r).size == bench.TOP_K for r in a_e.reshape(192, bench.TOP_K))
     d = bench.d_live(a_e, a_w)
     assert 250 < d <= bench.E
+
+
+def test_cpu_threads_follow_the_process_allotment(monkeypatch):
+    import os
+
+    import bench
+
+    monkeypatch.setenv("OMP_NUM_THREADS", "3")
+    assert bench.cpu_threads() == min(3, os.cpu_count())
+    monkeypatch.setenv("OMP_NUM_THREADS", "100000")
+    assert bench.cpu_threads() == os.cpu_count()
+    monkeypatch.delenv("OMP_NUM_THREADS")
+    assert bench.cpu_threads() == os.cpu_count()

@@ -218,16 +218,43 @@ def _rel_l2(a: torch.Tensor, b: torch.Tensor) -> float:
     return float((a - b).norm() / b.norm().clamp_min(1e-30))
 
 
+def _first_divergence(dec: dict, ver: dict, accept: int):
+    """The first committed (step, layer) of one lane, in dependency order, where the two paths
+    selected different expert sets; None when every committed row agrees."""
+    for s in range(accept + 1):
+        for layer in range(len(dec[s])):
+            if set(dec[s][layer][1]) != set(ver[s][layer][1]):
+                return s, layer
+    return None
+
+
+def _boundary_swap(h: torch.Tensor, gate: torch.Tensor, mine: set, other: set, k: int) -> bool:
+    """Whether the experts `other` selected and `mine` did not sit just past the top-k cut of
+    this path's own fp32 router logits (ranks k..k+2): a near-tie flip of the selection, where
+    an indexing bug would select experts far from the cut."""
+    z = h.float() @ gate.float().t()
+    rank = {int(e): r for r, e in enumerate(z.argsort(descending=True).tolist())}
+    return all(rank[e] < k + 3 for e in other - mine) and len(other - mine) <= 2
+
+
 def test_config5_full_size_graph_rounds(dev) -> None:
-    """The benchmark's round at its real size (B=48, k=3, 8192-token context, GraphMTPRunner):
-    normal rounds commit 1..k+1 valid ids per lane and keep every state finite; a forced round
-    (lane j accepts 1 + j % 3 drafts, replayed through the same graph) commits what accept + 1
-    plain decode steps produce and leaves the same slot state, to bf16 rounding (router ties
-    aside)."""
+    """The benchmark's round at its real size (B=48, k=3, 8192-token context): the bucket's HIP
+    graph passes `prepare()` validation, normal rounds commit 1..k+1 valid ids per lane and
+    keep every state finite, and a forced round (lane j accepts 1 + j % 3 drafts, replayed
+    through the same graph) is checked against accept + 1 plain decode steps lane by lane.
+
+    Both paths record each MoE call's selected experts. On every lane whose routing agrees with
+    plain decode in every layer at every committed row, the ids must be exact (an LM-head tie
+    within 2 bf16 ulps aside) and every piece of slot state within 2e-2 rel-L2: the paths round
+    differently in bf16 (48 against 192 rows per GEMM), which on this seed leaves the
+    routing-identical lanes' cached hidden seed at up to 1.7e-2 and every other state component
+    at or below 9.2e-3, where a lane whose routing truly diverged sits near 1e-1 and an indexing
+    error at O(1). A lane may differ only where its first routing difference, in dependency
+    order, is a near-tie swap at the top-10 cut (10 of 48 lanes on this seed)."""
     b, k, ctx = 48, 3, 8192
-    model, toks, pos = mh.c5_model(dev, b, k, ctx)
+    model, runner, toks, pos = mh.c5_model_and_runner(dev, b, k, ctx)
+    assert runner.validated == {b: True}
     lanes = list(range(b))
-    runner = graph_mtp.GraphMTPRunner(model, capacity=b)
     for _ in range(2):
         got = runner.speculative_decode(lanes, toks, pos)
         for j, c in enumerate(got):
@@ -240,41 +267,67 @@ def test_config5_full_size_graph_rounds(dev) -> None:
         for name, ten in p.items():
             assert torch.isfinite(ten.float()).all(), (ty, name)
     before = mh.snapshot(model)
+    t = k + 1
 
-    # plain decode: lane j runs accept_j + 1 greedy steps
+    # plain decode: lane j runs accept_j + 1 greedy steps, routing recorded per step and layer
     accept = [1 + j % 3 for j in range(b)]
     truth = [[toks[j]] for j in range(b)]
-    rows = [[] for _ in range(b)]  # plain decode's logits per lane and step
+    logits_at = [[] for _ in range(b)]
+    dec = [[None] * (k + 1) for _ in range(b)]  # dec[j][s] = [(h, top_i) per layer]
     for s in range(k + 1):
         live = [j for j in lanes if accept[j] >= s]
+        model.route_log = []
         logits = model.decode(live, [truth[j][-1] for j in live], [pos[j] + s for j in live]).float()
+        calls = [c for c in model.route_log if c[0] != "mtp"]
+        model.route_log = None
         for i, j in enumerate(live):
             truth[j].append(int(logits[i].argmax()))
-            rows[j].append(logits[i])
+            logits_at[j].append(logits[i])
+            dec[j][s] = [(c[1][i], c[2][i].tolist()) for c in calls]
     plain = [mh.slot_state(model, j, pos[j] + accept[j] + 1) for j in lanes]
 
-    mh.restore(model, before)
     forced = [truth[j][1 : accept[j] + 1] for j in lanes]
-    got = runner.speculative_decode(lanes, toks, pos, forced=forced)
-    assert len(runner.graphs) == 1
-    # bf16 rounding differs between the 48-row decode and the 192-row verify forward; where it
-    # reorders an exact tie among the router's top-10 logits a lane takes another expert and
-    # its rows differ for real (rel-L2 ~0.1). With 4 routed layers and up to 4 rows per lane a
-    # few lanes in 48 meet such a tie (7 on the seeds here); everything else agrees.
+    mh.restore(model, before)
+    got = runner.speculative_decode(lanes, toks, pos, forced=forced)  # graph replay
+    assert list(runner.graphs) == [b]
+    graph_state = [mh.slot_state(model, j, pos[j] + accept[j] + 1) for j in lanes]
+    # the same forced round eagerly, recording its routing (the capture validated bit-equal)
+    mh.restore(model, before)
+    model.route_log = []
+    eager = graph_mtp.MTPVerifyRunner(model, buckets=[b]).speculative_decode(lanes, toks, pos, forced=forced)
+    calls = [c for c in model.route_log if c[0] != "mtp"]
+    model.route_log = None
+    assert eager == got
+    ver = [[[(calls[layer][1][j * t + s], calls[layer][2][j * t + s].tolist()) for layer in range(len(calls))]
+            for s in range(t)] for j in lanes]
+
+    diverged, exact_lanes, over = [], 0, []
+    comp_max = [0.0] * len(plain[0])
     for j in lanes:
         assert len(got[j]) == accept[j] + 1
-    same = sum(x == y for j in lanes for x, y in zip(got[j], truth[j][1:], strict=False))
-    total = sum(len(got[j]) for j in lanes)
-    worst = []
-    for j in lanes:
-        spec = mh.slot_state(model, j, pos[j] + accept[j] + 1)
-        worst.append(max(_rel_l2(x, y) for x, y in zip(spec, plain[j], strict=True)))
-    worst_t = torch.tensor(worst)
-    print(f"C5 forced round: {same}/{total} ids as plain decode; slot-state rel-L2 median "
-          f"{float(worst_t.median()):.2e}, lanes above 2e-2: {int((worst_t > 2e-2).sum())}")
-    assert same >= 0.9 * total
-    assert float(worst_t.median()) < 1e-2
-    assert int((worst_t > 2e-2).sum()) <= b // 4
+        first = _first_divergence(dec[j], ver[j], accept[j])
+        if first is not None:
+            s, layer = first
+            g = model.layers[layer]["router_gate"][: model.cfg.experts]
+            dset, vset = set(dec[j][s][layer][1]), set(ver[j][s][layer][1])
+            assert _boundary_swap(ver[j][s][layer][0], g, vset, dset, model.cfg.top_k), (j, s, layer)
+            assert _boundary_swap(dec[j][s][layer][0], g, dset, vset, model.cfg.top_k), (j, s, layer)
+            diverged.append(j)
+            continue
+        for s, (x, y) in enumerate(zip(got[j], truth[j][1:], strict=False)):
+            if x != y:  # only an LM-head tie: the verify's pick is within 2 bf16 ulps of the max
+                row = logits_at[j][s]
+                assert float(row.max() - row[x]) <= 2 ** -7 * abs(float(row.max())), (j, s)
+        errs = [_rel_l2(x, y) for x, y in zip(graph_state[j], plain[j], strict=True)]
+        comp_max = [max(a, e) for a, e in zip(comp_max, errs, strict=True)]
+        if max(errs) > 2e-2:
+            over.append((j, int(torch.tensor(errs).argmax()), round(max(errs), 4)))
+        exact_lanes += 1
+    print(f"C5 forced round: {exact_lanes}/{b} lanes route identically and match plain decode; "
+          f"{len(diverged)} lanes take a near-tie router swap first: {diverged}; "
+          f"per-component max state rel-L2 on the identical lanes: {[f'{e:.1e}' for e in comp_max]}")
+    assert not over, f"routing-identical lanes over 2e-2 (lane, component, rel-L2): {over}"
+    assert len(diverged) <= b // 4
 
 
 # ---------------------------------------------------------------- buckets and padding rows

@@ -193,8 +193,9 @@ def test_loaded_experts_run_on_the_device(tmp_path) -> None:
 def test_scale_255_block_fails_at_load(tmp_path, monkeypatch) -> None:
     """A shard holding a 32-element block with e8m0 scale 255 over nonzero codes (which the
     in-register decode gives as NaN, the pinned decode as +-inf) is refused by `load_experts`
-    itself, not at its first MoE call. The same block over zero codes loads and runs, and with
-    `SEED_FUSED_MOE=0` (the torch path, which decodes 255 as pinned) the shard loads."""
+    itself, not at its first MoE call. The same block over zero codes loads and runs (its
+    pinned decode, 0 * 2^128, is NaN in both decodes), and with `SEED_FUSED_MOE=0` (the torch
+    path, which decodes 255 as pinned) the shard loads."""
     import mxfp4_gemv
 
     dev = torch.device("cuda:0")
@@ -221,4 +222,8 @@ def test_scale_255_block_fails_at_load(tmp_path, monkeypatch) -> None:
                               torch.bfloat16)
     x = torch.randn(2, H, device=dev).to(torch.bfloat16)
     routing = (torch.tensor([3, 1, 2, 3], dtype=torch.int32, device=dev), torch.full((4,), 0.5, device=dev))
-    assert torch.isfinite(mxfp4_gemv.fused_moe(x, ex, routing, 2, (0, E)).float()).all()
+    out = mxfp4_gemv.fused_moe(x, ex, routing, 2, (0, E)).float()
+    # the pinned decode of a zero code under scale 255 is 0 * 2^128 = NaN, and both tokens route
+    # to expert 3, whose down row 7 holds that block: NaN in hidden column 7 only
+    assert torch.isnan(out[:, 7]).all()
+    assert torch.isfinite(torch.cat([out[:, :7], out[:, 8:]], dim=1)).all()
