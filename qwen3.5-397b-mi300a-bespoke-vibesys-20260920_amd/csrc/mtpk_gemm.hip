@@ -61,12 +61,204 @@ int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
   return status_of(hipGetLastError());
 }
 
-// The wide form (`gemm_wide`): TT token tiles in one row group, 8 waves x 2 weight streams,
-// 128-K chunks (2 x TT x 16 padded 256-byte rows of LDS: 104 KiB at TT = 12, one workgroup per CU).
+// The wide form (`gemm_wide`, 65..192 token rows on wide N: the verify LM head).
+// One workgroup of NW waves per 16 NW RT weight rows, one workgroup per CU. Wave w owns weight
+// rows 16 RT w .. + 16 RT - 1 (RT row tiles) against all TT token tiles, so one staged A
+// fragment feeds RT MFMAs and one weight fragment TT.
+//  - Weights: a register ring of D steps of 32 K (RT 16-byte loads per lane per step), as the
+//    other weight streams here.
+//  - Token rows: direct-to-LDS buffer loads (no registers held), KC-K chunks of TT x 16 rows x
+//    2 KC bytes, NB chunks in flight. The 16-byte piece p of row r sits at slot p ^ (r & 7) of
+//    the row, so the A reads of 8 consecutive rows hit distinct banks; every load instruction
+//    still covers whole 128-byte lines.
+//  - One barrier per chunk: each wave waits (vmcnt) for its own loads of the chunk, the barrier
+//    makes all waves' loads visible and also frees the buffer read in the previous chunk, which
+//    the chunk NB - 1 ahead is loaded into. The ring's register loads are waited for by the
+//    compiler; the chunk wait is exact and keeps the ring and the later chunks in flight.
+//  - Tile t walks the K chunks from chunk 7 t mod (K / KC) on: with every tile starting at K = 0
+//    all workgroups read the same column range of rows 8 KB apart at the same moment, which
+//    measured 583 against 552 us on [192, 4096] x [248320, 4096] (the weight stream alone 524
+//    against 449 us). A column's sum order is then its tile's; nothing else depends on it.
+// Measured there (graph replay over two weight copies, MI355X): 552 us with the argmax epilogue
+// against 496 us for the library GEMM alone and 521 us with its argmax pass; the token rows'
+// staging (75% of the weight bytes: 192 rows against 256 per tile, the most the register file
+// holds accumulators for) costs about 100 us of it. The model keeps the library GEMM at 192 rows.
+// Epilogues: store (fp32 or bf16) or the first-occurrence argmax keys of bf16(y) per tile.
+template <int TT, int NW, int RT, int KC, int NB, int D>
+struct Wide {
+  static constexpr int kRows = 16 * RT * NW;  // weight rows per tile
+  static constexpr int kChunk = TT * 16 * KC * 2;
+  static constexpr int kLoads = kChunk / 1024 / NW;  // direct loads per wave per chunk
+  static constexpr int kSteps = KC / 32;            // ring steps per chunk
+  static constexpr int kTurn = D / kSteps;          // chunks per loop turn
+  static constexpr int kKeys = NB * kChunk;
+  static constexpr int kBytes = kKeys + NW * TT * 16 * 8;
+};
+// 8 waves x 2 row tiles (two waves per SIMD, 195 VGPRs) measured 566-575 us against 637 us for
+// 4 waves x 4 row tiles (accumulators shuffled between AGPRs and VGPRs in the loop); NB = 3
+// against 4, D = 8 against 4 and 128-K chunks were equal or slower.
+constexpr int kWideNW = 8, kWideRT = 2, kWideKC = 64, kWideNB = 3, kWideD = 4;
 template <int TT>
-__global__ __launch_bounds__(8 * kWave, 2) void k_gemm_wide(GemmArgs a) {
-  __shared__ __attribute__((aligned(16))) uint8_t smem[GemmSmem<TT, 8, 128>::kBytes];
-  gemm_tile<TT, 2, 8, false, 128>(a, smem, blockIdx.x, blockIdx.y);
+using WideCfg = Wide<TT, kWideNW, kWideRT, kWideKC, kWideNB, kWideD>;
+constexpr int kWideRows = 16 * kWideRT * kWideNW;
+constexpr int kWideKStep = kWideKC * (kWideD / (kWideKC / 32));  // K per loop turn
+
+template <int TT, int NW, int RT, int KC, int NB, int D>
+__global__ __launch_bounds__(NW * kWave, 1) void k_gemm_wide(GemmArgs a) {
+  using C = Wide<TT, NW, RT, KC, NB, D>;
+  constexpr int kChunk = C::kChunk, kLoads = C::kLoads, kSteps = C::kSteps, kTurn = C::kTurn;
+  static_assert(kLoads * 1024 * NW == kChunk, "chunk split over the waves");
+  static_assert(D % kSteps == 0 && NB >= 2, "ring depth in whole chunks");
+  // Loads this wave issued after its loads of chunk c, at the chunk's wait: (NB - 2) chunks
+  // and D RT ring loads plus kSteps RT per chunk already looped, for the prologue's chunks, and
+  // (NB - 2) chunks plus (NB - 1) kSteps RT ring loads in the steady state. The smallest is exact
+  // where it applies and waits only for consumed ring steps elsewhere.
+  constexpr int kChunkWait = (NB - 2) * kLoads + RT * (D < kSteps * (NB - 1) ? D : kSteps * (NB - 1));
+  static_assert(kChunkWait < 64, "vmcnt is a 6-bit counter");
+  __shared__ __attribute__((aligned(16))) uint8_t smem[C::kBytes];
+  uint64_t(*kred)[TT * 16] = reinterpret_cast<uint64_t(*)[TT * 16]>(smem + C::kKeys);
+  const int tid = threadIdx.x, wave = uniform(tid / kWave), lane = tid & (kWave - 1);
+  const MoeLane ln = moe_lane(lane);
+  const int tile = blockIdx.x;
+  const int K = a.K, nchunk = K / KC, nstep = K / 32;
+  const int rot = (int)(((int64_t)tile * 7) % nchunk);  // this tile's first chunk
+  int wrow[RT];
+  bool wok[RT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r) {
+    const int row = tile * C::kRows + 16 * RT * wave + 16 * r + ln.c;
+    wok[r] = row < a.N;
+    wrow[r] = wok[r] ? row : 0;
+  }
+  const rsrc_t rw = make_rsrc(a.w, 0x7fffffff);
+  const rsrc_t rx = make_rsrc(a.x, (uint32_t)((int64_t)a.M * K * 2));
+  // weight step st (the st-th of this tile's rotated order): K = 32 st' + 8 g .. + 7 of row wrow[r]
+  auto issue = [&](u32x4_t* v, int st) {
+    const bool in = st < nstep;
+    const int sr = (st + rot * kSteps) % nstep;
+#pragma unroll
+    for (int r = 0; r < RT; ++r) {
+      const uint32_t off = (uint32_t)(((int64_t)wrow[r] * K + 32 * sr + 8 * ln.g) * 2);
+      v[r] = buf16(rw, (wok[r] && in) ? off : kOutOfRange);
+    }
+  };
+  // chunk c into buffer c % NB: load j of this wave fills LDS bytes [1024 q, 1024 q + 1024) of
+  // the chunk, q = kLoads wave + j: row (1024 q + 16 L) / (2 KC), slot s of that row <- piece
+  // s ^ (row & 7)
+  constexpr int kPieces = KC / 8;  // 16-byte pieces per row
+  auto stage = [&](int c) {
+    uint8_t* buf = smem + (c % NB) * kChunk;
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const int q = kLoads * wave + j, slot16 = 64 * q + lane;
+      const int row = slot16 / kPieces, slot = slot16 % kPieces;
+      const int piece = slot ^ (row & 7);
+      const bool ok = c < nchunk && row < a.M;
+      const int cr = (c + rot) % nchunk;
+      buf16_lds(rx, ok ? (uint32_t)(((int64_t)row * K + cr * KC + piece * 8) * 2) : kOutOfRange,
+                buf + 1024 * q);
+    }
+  };
+
+  f32x4_t acc[RT][TT];
+#pragma unroll
+  for (int r = 0; r < RT; ++r)
+#pragma unroll
+    for (int t = 0; t < TT; ++t) acc[r][t] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+
+  // prologue: chunks 0 .. NB - 2, then D ring steps
+#pragma unroll
+  for (int c = 0; c < NB - 1; ++c) stage(c);
+  ring_fence();
+  u32x4_t ring[D][RT];
+#pragma unroll
+  for (int st = 0; st < D; ++st) issue(ring[st], st);
+  ring_fence();
+
+  // kTurn chunks per loop turn, so every ring slot index is a constant (a register array
+  // indexed at run time would live in scratch); K is a multiple of kTurn KC (checked on launch)
+  int c0 = 0;
+#pragma clang loop unroll(disable)
+  do {
+#pragma unroll
+    for (int h = 0; h < kTurn; ++h) {
+      const int c = c0 + h;
+      vmcnt_wait<kChunkWait>();  // this wave's loads of chunk c have landed
+      __builtin_amdgcn_s_barrier();  // ... and every wave's; buffer (c - 1) % NB is free
+      __asm__ volatile("" ::: "memory");  // no LDS read moves above the barrier
+      ring_fence();
+      stage(c + NB - 1);
+      ring_fence();
+      const uint8_t* buf = smem + (c % NB) * kChunk;
+#pragma unroll
+      for (int u = 0; u < kSteps; ++u) {
+        u32x4_t* slot = ring[h * kSteps + u];
+        u32x4_t av[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          const int row = 16 * t + ln.c;
+          av[t] = lds16(buf + row * (KC * 2) + (((4 * u + ln.g) ^ (row & 7)) * 16));
+        }
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+          for (int t = 0; t < TT; ++t)
+            acc[r][t] = mfma16x16x32(as_bf16x8(av[t]), as_bf16x8(slot[r]), acc[r][t]);
+        ring_fence();
+        issue(slot, c * kSteps + u + D);
+        ring_fence();
+      }
+    }
+    c0 += kTurn;
+  } while (c0 < nchunk);
+
+  // lane (g, c): acc[r][t][i] is token m = 16 t + 4 g + i, weight row wrow[r]
+  if (a.epi == kEpiArgmax) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        uint64_t key = 0;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+          const float v = bf16_to_f32(f32_to_bf16(acc[r][t][i]));
+          const uint64_t kr = wok[r] ? argmax_key(v, (uint32_t)wrow[r]) : 0;
+          key = kr > key ? kr : key;
+        }
+#pragma unroll
+        for (int o = 1; o < 16; o <<= 1) {
+          const uint32_t lo = __shfl_xor((uint32_t)key, o, kWave);
+          const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), o, kWave);
+          const uint64_t k2 = ((uint64_t)hi << 32) | lo;
+          key = k2 > key ? k2 : key;
+        }
+        if (ln.c == 0) kred[wave][16 * t + 4 * ln.g + i] = key;
+      }
+    __syncthreads();
+    for (int m = tid; m < a.M; m += NW * kWave) {
+      uint64_t b = kred[0][m];
+#pragma unroll
+      for (int w2 = 1; w2 < NW; ++w2) b = kred[w2][m] > b ? kred[w2][m] : b;
+      a.keys[(int64_t)m * a.tiles + tile] = b;
+    }
+    return;
+  }
+#pragma unroll
+  for (int t = 0; t < TT; ++t)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = 16 * t + 4 * ln.g + i;
+      if (m >= a.M) continue;
+#pragma unroll
+      for (int r = 0; r < RT; ++r)
+        if (wok[r]) store_float(a.out, a.odt, (int64_t)m * a.cols + wrow[r], acc[r][t][i]);
+    }
+}
+
+template <int TT>
+void launch_wide(const GemmArgs& a, int tiles, hipStream_t st) {
+  hipLaunchKernelGGL((k_gemm_wide<TT, kWideNW, kWideRT, kWideKC, kWideNB, kWideD>),
+                     dim3((unsigned)tiles), dim3(kWideNW * kWave), 0, st, a);
 }
 
 // Split-K reduction: out[m, col] = epilogue(sum over ks of part[ks, m, .]) in split order.
@@ -167,10 +359,11 @@ int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, i
   if (gemm_wide(m, n, epilogue)) {
     a.RG = 1;
     const int wtt = (int)((m + 15) / 16);
+    static_assert(kGemmKC % kWideKStep == 0, "K (a multiple of kGemmKC) fills whole loop turns");
     if (wtt <= 8)
-      hipLaunchKernelGGL(k_gemm_wide<8>, dim3((unsigned)tiles), dim3(8 * kWave), 0, st, a);
+      launch_wide<8>(a, tiles, st);
     else
-      hipLaunchKernelGGL(k_gemm_wide<12>, dim3((unsigned)tiles), dim3(8 * kWave), 0, st, a);
+      launch_wide<12>(a, tiles, st);
   } else if (epilogue == kEpiSilu)
     launch_gemm_tt<2, true>(a, tt, tiles, st);
   else

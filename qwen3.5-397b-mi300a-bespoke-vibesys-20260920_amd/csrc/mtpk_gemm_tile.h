@@ -8,7 +8,7 @@
 
 namespace mtpk {
 
-constexpr int kGemmKC = 256;  // K per staged chunk (the default; the wide form stages 128)
+constexpr int kGemmKC = 256;  // K per staged chunk
 enum { kEpiStore = 0, kEpiSilu = 1, kEpiArgmax = 2 };
 
 struct GemmArgs {
@@ -268,10 +268,10 @@ inline int gemm_waves(int64_t m, int64_t n, int epi) {
   return (m + 15) / 16 >= 3 && cols / 128 >= 2 * (int64_t)device_cu_count() ? 8 : 4;
 }
 
-// The wide form for 65..192 token rows on wide N (the verify LM head): one row group of TT =
-// ceil(M / 16) token tiles, 8 waves with two weight streams each (256 weight rows per tile), token
-// rows staged in 128-K chunks. Every weight is read once for all rows; the 64-row groups would
-// stream the tile's weights once per group.
+// The wide form for 65..192 token rows on wide N (the verify LM head, mtpk_gemm.hip
+// k_gemm_wide): one row group of TT = ceil(M / 16) token tiles against 256-row weight tiles, the
+// token rows staged by direct-to-LDS loads. Every weight is read once for all rows; the 64-row
+// groups would stream the tile's weights once per group.
 constexpr int kWideMaxRows = 192;
 inline bool gemm_wide(int64_t m, int64_t n, int epi) {
   return m > 64 && m <= kWideMaxRows && epi != kEpiSilu &&

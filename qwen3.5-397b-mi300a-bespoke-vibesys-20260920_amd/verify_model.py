@@ -125,7 +125,8 @@ FUSED_ARGMAX_ROWS = 64
 """Greedy LM-head rows up to which `next_tokens` runs the GEMM with the argmax in its epilogue.
 Measured on [M, 4096] x [248320, 4096] bf16 against hipBLASLt + the argmax kernel: 390 against
 401 us at 16 rows, 421 against 416 us at 48, 427 against 433 us at 64; at 192 rows the library
-path stays (507 us against 559 us for the one-group wide form)."""
+path stays (521 us with its argmax pass against 552 us for the wide form with the argmax in its
+epilogue, `dense.argmax_linear`)."""
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
