@@ -163,9 +163,8 @@ constexpr int kPre = 8;
 constexpr int kKeyRows = 4096;  // B * t bound of the keys path: one u64 of LDS per verify row
 
 // keys (optional): the argmax chunk keys [B * t, chunks] of k_argmax_partial. The workgroup
-// then first folds them into one key per verify row (LDS max, so any key order gives the same
-// first-occurrence winner), writes the indices to sa_out and reads the verify columns from
-// LDS: the argmax needs no second launch.
+// then first folds them into one key per verify row (a thread per row), writes the indices to
+// sa_out and reads the verify columns from LDS: the argmax needs no second launch.
 // forced_n (optional): a row with forced_n[j] > 0 accepts exactly min(forced_n[j], k) drafts,
 // which are not generated output, so the stop ids and the budget do not clamp them and the
 // budget is charged the one target token (graph_verify_wide.py:196-200, mtp_overlap.py:53-71);
@@ -205,15 +204,22 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
     p0 = next_pos ? pos[j] : 0;
   }
   if (keys) {
+    // One thread per verify row folds the row's chunk keys in registers, eight loads in flight
+    // at a time; the maximum key is the first-occurrence argmax whatever the order.
     const int rows = B * t;
-    for (int r = j; r < rows; r += kAcceptThreads) s_key[r] = 0;
-    __syncthreads();
-    const int64_t n = (int64_t)rows * chunks;
-    for (int64_t i = j; i < n; i += kAcceptThreads)
-      atomicMax(&s_key[i / chunks], (unsigned long long)keys[i]);
-    __syncthreads();
     for (int r = j; r < rows; r += kAcceptThreads) {
-      const int64_t tok = (int64_t)argmax_key_index(s_key[r]);
+      const uint64_t* kr = keys + (int64_t)r * chunks;
+      uint64_t bk = 0;
+      int c = 0;
+      for (; c + 8 <= chunks; c += 8) {
+        uint64_t x[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) x[u] = kr[c + u];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) bk = x[u] > bk ? x[u] : bk;
+      }
+      for (; c < chunks; ++c) bk = kr[c] > bk ? kr[c] : bk;
+      const int64_t tok = (int64_t)argmax_key_index(bk);
       s_key[r] = (unsigned long long)tok;
       sa_out[(int64_t)(r / t) * ss + r % t] = tok;
     }

@@ -8,15 +8,18 @@
 // smallest index v with cumsum(w)[v] > r * sum(w), or the last positive index if rounding
 // leaves none.
 //
-// Three launches for rejection (four for plain sampling), streaming the logits with 16-byte loads:
+// Four launches, streaming the logits with 16-byte loads:
 //   stats : (chunk, row) workgroups -> per-chunk (max, sum exp(z - max)) of z = logit / T
-//   decide + mass: (chunk, lane) workgroups; each first makes its lane's decision (a wave per
-//           verify row -> row softmax constants, margins, the accept length and the draw), then
-//           sums its chunk's draw weights. Plain sampling: a wave per row for the row constants,
-//           then (chunk, row) workgroups for the mass
+//   decide: one workgroup per lane (a wave per verify row -> row softmax constants, margins, the
+//           accept length and the draw it leads to); plain sampling: a wave per row for the row
+//           constants
+//   mass  : (chunk, item) workgroups -> the chunk's sums of the draw weights
 //   pick  : one workgroup per item -> the chunk where the cumulative mass crosses r * total
 //           (one wave: scan and ballot over the chunk masses), then a block scan inside it;
 //           writes the token (and the emitted row)
+// The exponentials are base-2 with the temperature folded into one FMA (exp(l / T - m) =
+// exp2(l log2(e) / T - m log2(e))), and no division touches a logit: at the quotient form the
+// mass launch was bound by the VALU (20 us against 9.2 us now for config 4).
 // Every sum runs in a fixed order, so results are deterministic for fixed shapes.
 
 #include "mtpk_device.h"
@@ -76,49 +79,53 @@ __device__ inline void rs_load(const void* base, int dt, int vec, int64_t row, i
   }
 }
 
-// Block-wide reductions over 256 threads (4 waves), result broadcast to every thread.
-__device__ inline float block_max(float v, float* red) {
-  v = wave_max(v);
-  const int tid = threadIdx.x;
-  __syncthreads();
-  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = v;
-  __syncthreads();
-  return fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-}
-
-__device__ inline float block_sum(float v, float* red) {
-  v = wave_sum(v);
-  const int tid = threadIdx.x;
-  __syncthreads();
-  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = v;
-  __syncthreads();
-  return (red[0] + red[1]) + (red[2] + red[3]);
-}
-
 // rows [0, n_target) are target rows, [n_target, n_target + n_draft) draft rows.
+constexpr float kLog2e = 1.4426950408889634f;
+
+// Chunk partials in one block reduction: each thread's (max, sum of exp relative to that max)
+// over its 16 raw logits, rescaled to the wave max and summed per wave, then the four waves
+// combined by thread 0 in a fixed order. With a = log2(e) / T, exp(l / T - m / T) = exp2(l a -
+// m a): one FMA and one exp2 per logit. The partial is (M / T, S) for the chunk's raw max M;
+// M / T equals the max of the scaled logits (scaling by 1 / T > 0 keeps the order, rounding
+// included).
 __global__ __launch_bounds__(kRsThreads) void k_rs_stats(RsRows rr, int64_t n_target, float inv_t,
                                                         float2* __restrict__ part) {
-  __shared__ float red[kRsThreads / kWave];
+  __shared__ float2 red[kRsThreads / kWave];
   const int c = blockIdx.x, nchunk = gridDim.x;
   const int64_t r = blockIdx.y;
   const bool is_t = r < n_target;
   const void* base = is_t ? rr.target : rr.draft;
   const int64_t row = is_t ? r : r - n_target;
-  float z[kRsPerThread];
-  rs_load(base, rr.dt, rr.vec, row, rr.vocab, c, threadIdx.x, inv_t, z);
-  float m = -INFINITY;
+  float l[kRsPerThread];
+  rs_load(base, rr.dt, rr.vec, row, rr.vocab, c, threadIdx.x, 1.f, l);
+  const float a = inv_t * kLog2e;
+  float ml = -INFINITY;
 #pragma unroll
-  for (int e = 0; e < kRsPerThread; ++e) m = fmaxf(m, z[e]);
-  m = block_max(m, red);
-  // A chunk of -inf logits (a masked stretch of the vocabulary) has no mass: (-inf, 0), not the
-  // NaN of exp(-inf - -inf). m is uniform over the workgroup, so is the branch.
+  for (int e = 0; e < kRsPerThread; ++e) ml = fmaxf(ml, l[e]);
+  // A stretch of -inf logits (a masked part of the vocabulary) has no mass: (-inf, 0), not the
+  // NaN of exp(-inf - -inf).
   float s = 0.f;
-  if (m > -INFINITY) {
+  if (ml > -INFINITY) {
+    const float b = ml * a;
 #pragma unroll
-    for (int e = 0; e < kRsPerThread; ++e) s += __expf(z[e] - m);
+    for (int e = 0; e < kRsPerThread; ++e) s += __builtin_amdgcn_exp2f(fmaf(l[e], a, -b));
   }
-  s = block_sum(s, red);
-  if (threadIdx.x == 0) part[r * nchunk + c] = make_float2(m, s);
+  const float mw = wave_max(ml);
+  s = ml > -INFINITY ? s * __builtin_amdgcn_exp2f((ml - mw) * a) : 0.f;
+  s = wave_sum(s);
+  const int tid = threadIdx.x;
+  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = make_float2(mw, s);
+  __syncthreads();
+  if (tid == 0) {
+    float m = red[0].x;
+#pragma unroll
+    for (int w = 1; w < kRsThreads / kWave; ++w) m = fmaxf(m, red[w].x);
+    float sum = 0.f;
+#pragma unroll
+    for (int w = 0; w < kRsThreads / kWave; ++w)
+      sum += red[w].x > -INFINITY ? red[w].y * __builtin_amdgcn_exp2f((red[w].x - m) * a) : 0.f;
+    part[r * nchunk + c] = make_float2(m * inv_t, sum);
+  }
 }
 
 // A chunk partial's share of a row sum with row max m; a massless (-inf) chunk adds nothing.
@@ -234,16 +241,52 @@ __global__ __launch_bounds__(kWave) void k_rs_rows(const float2* __restrict__ pa
   }
 }
 
-// Draw weights of this thread's 16 slots from the logits z (target) and zq (draft): target p,
-// and the residual max(0, p - q) when the item has a draft row.
-__device__ inline void rs_weights_of(const RsItem& it, const float (&z)[kRsPerThread],
-                                     const float (&zq)[kRsPerThread], float (&wr)[kRsPerThread],
+// Rejection: the lane's decision, one workgroup per lane (its own launch: made inside every mass
+// workgroup instead, its dependent loads delay each workgroup's stream, 14.6 us for the mass
+// launch against 9.2 + 4.8 us for the two).
+__global__ __launch_bounds__(kRsThreads) void k_rs_decide(
+    RsRows rr, const float2* __restrict__ part, int nchunk, int B, int k, float inv_t,
+    const int64_t* __restrict__ draft_tokens, const float* __restrict__ u_accept,
+    RsItem* __restrict__ items, int64_t* __restrict__ accept_len, float* __restrict__ margin) {
+  static_assert(kRsThreads == kWave * kDecideWaves, "one decision per workgroup");
+  __shared__ float s_mg[kMaxT];
+  __shared__ float4 s_st[kMaxT];
+  __shared__ RsItem s_item;
+  const int b = blockIdx.x;
+  rs_decide_lane(rr, part, nchunk, B, k, inv_t, draft_tokens, u_accept, b, s_mg, s_st, &s_item,
+                 items, accept_len, margin);
+}
+
+// The draw weights in base-2 form: p = exp(l / T - mt) / st = exp2(l * a - bt) with a = log2(e) /
+// T and bt = log2(e) mt + log2(st) (bq likewise for the draft row), one FMA and one exp2 per slot
+// where the quotient form costs two exps and two IEEE divisions per slot pair: the mass pass
+// streams 2 x vocab logits per item, and at the division form it was bound by the VALU rather
+// than by HBM.
+struct RsExp {
+  float a, bt, bq;
+  bool has_q;
+};
+
+__device__ inline RsExp rs_exp(const RsItem& it, float inv_t) {
+  RsExp x;
+  x.a = inv_t * kLog2e;
+  x.bt = it.mt * kLog2e + __log2f(it.st);
+  x.bq = it.mq * kLog2e + __log2f(it.sq);
+  x.has_q = it.drow >= 0;
+  return x;
+}
+
+// Draw weights of this thread's 16 slots from the raw logits l (target) and lq (draft): target
+// p, and the residual max(0, p - q) when the item has a draft row. A -inf logit weighs 0.
+__device__ inline void rs_weights_of(const RsExp& x, const float (&l)[kRsPerThread],
+                                     const float (&lq)[kRsPerThread], float (&wr)[kRsPerThread],
                                      float (&wp)[kRsPerThread]) {
 #pragma unroll
-  for (int e = 0; e < kRsPerThread; ++e) wp[e] = __expf(z[e] - it.mt) / it.st;
-  if (it.drow >= 0) {
+  for (int e = 0; e < kRsPerThread; ++e) wp[e] = __builtin_amdgcn_exp2f(fmaf(l[e], x.a, -x.bt));
+  if (x.has_q) {
 #pragma unroll
-    for (int e = 0; e < kRsPerThread; ++e) wr[e] = fmaxf(wp[e] - __expf(zq[e] - it.mq) / it.sq, 0.f);
+    for (int e = 0; e < kRsPerThread; ++e)
+      wr[e] = fmaxf(wp[e] - __builtin_amdgcn_exp2f(fmaf(lq[e], x.a, -x.bq)), 0.f);
   } else {
 #pragma unroll
     for (int e = 0; e < kRsPerThread; ++e) wr[e] = 0.f;
@@ -252,77 +295,10 @@ __device__ inline void rs_weights_of(const RsItem& it, const float (&z)[kRsPerTh
 
 __device__ inline void rs_weights(const RsRows& rr, const RsItem& it, int c, float inv_t,
                                   float (&wr)[kRsPerThread], float (&wp)[kRsPerThread]) {
-  float z[kRsPerThread], zq[kRsPerThread];
-  rs_load(rr.target, rr.dt, rr.vec, it.trow, rr.vocab, c, threadIdx.x, inv_t, z);
-  if (it.drow >= 0) rs_load(rr.draft, rr.dt, rr.vec, it.drow, rr.vocab, c, threadIdx.x, inv_t, zq);
-  rs_weights_of(it, z, zq, wr, wp);
-}
-
-// Per-chunk sums of an item's draw weights, one workgroup per (chunk, item).
-__global__ __launch_bounds__(kRsThreads) void k_rs_mass(RsRows rr, const RsItem* __restrict__ items,
-                                                       int nchunk, float inv_t,
-                                                       float2* __restrict__ mass) {
-  __shared__ float2 red[kRsThreads / kWave];
-  const int c = blockIdx.x;
-  const int item = blockIdx.y;
-  const RsItem it = items[item];
-  float wr[kRsPerThread], wp[kRsPerThread];
-  rs_weights(rr, it, c, inv_t, wr, wp);
-  float sr = 0.f, sp = 0.f;
-#pragma unroll
-  for (int e = 0; e < kRsPerThread; ++e) {
-    sr += wr[e];
-    sp += wp[e];
-  }
-  sr = wave_sum(sr);
-  sp = wave_sum(sp);
-  const int tid = threadIdx.x;
-  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = make_float2(sr, sp);
-  __syncthreads();
-  if (tid == 0) {
-    const float2 a = red[0], b = red[1], d = red[2], e = red[3];
-    mass[(int64_t)item * nchunk + c] =
-        make_float2((a.x + b.x) + (d.x + e.x), (a.y + b.y) + (d.y + e.y));
-  }
-}
-
-// Rejection: the lane's decision and its draw's per-chunk mass in one launch, one workgroup per
-// (chunk, lane). Every chunk's workgroup makes the lane's decision itself (a few KB of chunk
-// partials and 2k logits, the same deterministic result in each), so no launch separates the
-// decision from the mass; the chunk-0 workgroup writes the decision's outputs.
-__global__ __launch_bounds__(kRsThreads) void k_rs_decide_mass(
-    RsRows rr, const float2* __restrict__ part, int nchunk, int B, int k, float inv_t,
-    const int64_t* __restrict__ draft_tokens, const float* __restrict__ u_accept,
-    RsItem* __restrict__ items, int64_t* __restrict__ accept_len, float* __restrict__ margin,
-    float2* __restrict__ mass) {
-  static_assert(kRsThreads == kWave * kDecideWaves, "one decision per workgroup");
-  __shared__ float s_mg[kMaxT];
-  __shared__ float4 s_st[kMaxT];
-  __shared__ RsItem s_item;
-  __shared__ float2 red[kRsThreads / kWave];
-  const int c = blockIdx.x, b = blockIdx.y;
-  const bool first = c == 0;
-  rs_decide_lane(rr, part, nchunk, B, k, inv_t, draft_tokens, u_accept, b, s_mg, s_st, &s_item,
-                 first ? items : nullptr, first ? accept_len : nullptr, first ? margin : nullptr);
-  const RsItem it = s_item;
-  float wr[kRsPerThread], wp[kRsPerThread];
-  rs_weights(rr, it, c, inv_t, wr, wp);
-  float sr = 0.f, sp = 0.f;
-#pragma unroll
-  for (int e = 0; e < kRsPerThread; ++e) {
-    sr += wr[e];
-    sp += wp[e];
-  }
-  sr = wave_sum(sr);
-  sp = wave_sum(sp);
-  const int tid = threadIdx.x;
-  if ((tid & (kWave - 1)) == 0) red[tid / kWave] = make_float2(sr, sp);
-  __syncthreads();
-  if (tid == 0) {
-    const float2 a = red[0], b2 = red[1], d = red[2], e = red[3];
-    mass[(int64_t)b * nchunk + c] =
-        make_float2((a.x + b2.x) + (d.x + e.x), (a.y + b2.y) + (d.y + e.y));
-  }
+  float l[kRsPerThread], lq[kRsPerThread];
+  rs_load(rr.target, rr.dt, rr.vec, it.trow, rr.vocab, c, threadIdx.x, 1.f, l);
+  if (it.drow >= 0) rs_load(rr.draft, rr.dt, rr.vec, it.drow, rr.vocab, c, threadIdx.x, 1.f, lq);
+  rs_weights_of(rs_exp(it, inv_t), l, lq, wr, wp);
 }
 
 __device__ inline float wave_incl_scan_f(float v, int lane) {
@@ -334,22 +310,23 @@ __device__ inline float wave_incl_scan_f(float v, int lane) {
   return v;
 }
 
-__global__ __launch_bounds__(kRsThreads) void k_rs_pick(
-    RsRows rr, const RsItem* __restrict__ items, const float2* __restrict__ mass, int nchunk,
-    float inv_t, const float* __restrict__ u_sample, int64_t* __restrict__ token,
-    const int64_t* __restrict__ draft_tokens, int k, int64_t* __restrict__ emitted) {
-  __shared__ float wtot[kRsThreads / kWave];
-  __shared__ int s_chunk, s_use_r, s_fallback, s_best;
-  __shared__ float s_before, s_target;
-  const int item = blockIdx.x;
+struct RsPickLds {
+  float wtot[kRsThreads / kWave];
+  int chunk, use_r, fallback, best;
+  float before, target;
+};
+
+// The draw of `item` by the whole workgroup from its per-chunk masses `row_mass` (residual,
+// target): one wave finds the chunk where the cumulative mass crosses u * total (a wave sum for
+// the totals, then 64 chunks at a time by an inclusive scan and a ballot), then a block scan
+// inside that chunk. Writes token[item] and, when `emitted` is set, the emitted row.
+__device__ void rs_pick(const RsRows& rr, const RsItem& it, const float2* row_mass, int nchunk,
+                        float inv_t, float u, int64_t item, int64_t* __restrict__ token,
+                        const int64_t* __restrict__ draft_tokens, int k,
+                        int64_t* __restrict__ emitted, RsPickLds& sh) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
-  const RsItem it = items[item];
-  const int64_t dtok = emitted && tid < k ? draft_tokens[(int64_t)item * k + tid] : 0;
+  const int64_t dtok = emitted && tid < k ? draft_tokens[item * k + tid] : 0;
   if (wv == 0) {
-    // One wave finds the chunk where the cumulative mass crosses r * total: totals by a wave
-    // sum, then 64 chunks at a time by an inclusive scan and a ballot.
-    const float u = u_sample[item];
-    const float2* row_mass = mass + (int64_t)item * nchunk;
     const float2 m0 = lane < nchunk ? row_mass[lane] : make_float2(0.f, 0.f);
     float tr = m0.x, tp = m0.y;
     for (int c = lane + kWave; c < nchunk; c += kWave) {
@@ -381,29 +358,29 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_pick(
       cum += __shfl(inc, kWave - 1, kWave);
     }
     if (lane == 0) {
-      s_fallback = chunk < 0;
-      s_chunk = chunk < 0 ? last_pos : chunk;
-      s_use_r = use_r;
-      s_before = cum;
-      s_target = target;
-      s_best = INT32_MAX;
+      sh.fallback = chunk < 0;
+      sh.chunk = chunk < 0 ? last_pos : chunk;
+      sh.use_r = use_r;
+      sh.before = cum;
+      sh.target = target;
+      sh.best = INT32_MAX;
     }
   }
   __syncthreads();
-  const int c = s_chunk;
+  const int c = sh.chunk;
   float wr[kRsPerThread], wp[kRsPerThread];
   rs_weights(rr, it, c, inv_t, wr, wp);
   float w[kRsPerThread];
 #pragma unroll
-  for (int e = 0; e < kRsPerThread; ++e) w[e] = s_use_r ? wr[e] : wp[e];
+  for (int e = 0; e < kRsPerThread; ++e) w[e] = sh.use_r ? wr[e] : wp[e];
   float mine = 0.f;
 #pragma unroll
   for (int e = 0; e < kRsPerThread; ++e) mine += w[e];
   const float inc = wave_incl_scan_f(mine, lane);
-  if (lane == kWave - 1) wtot[wv] = inc;
+  if (lane == kWave - 1) sh.wtot[wv] = inc;
   __syncthreads();
-  float off = s_before;
-  for (int q = 0; q < wv; ++q) off += wtot[q];
+  float off = sh.before;
+  for (int q = 0; q < wv; ++q) off += sh.wtot[q];
   float run = off + inc - mine;
   const int64_t i0 = (int64_t)c * kRsChunk + (int64_t)tid * kRsPerThread;
   int hit = INT32_MAX, lastp = -1;
@@ -411,28 +388,141 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_pick(
   for (int e = 0; e < kRsPerThread; ++e) {
     run += w[e];
     if (w[e] > 0.f) lastp = (int)(i0 + e);
-    if (hit == INT32_MAX && !s_fallback && run > s_target && w[e] > 0.f) hit = (int)(i0 + e);
+    if (hit == INT32_MAX && !sh.fallback && run > sh.target && w[e] > 0.f) hit = (int)(i0 + e);
   }
-  atomicMin(&s_best, hit);
+  atomicMin(&sh.best, hit);
   __syncthreads();
   // Rounding can leave no crossing inside the chunk: take the chunk's last positive slot.
-  const int need_last = s_best == INT32_MAX;
+  const int need_last = sh.best == INT32_MAX;
   __syncthreads();
   if (need_last) {
-    if (tid == 0) s_best = -1;
+    if (tid == 0) sh.best = -1;
     __syncthreads();
-    atomicMax(&s_best, lastp);
+    atomicMax(&sh.best, lastp);
     __syncthreads();
   }
   // the emitted row by its first k + 1 threads at once (draft token i was loaded at the start)
   if (tid <= k) {
-    const int64_t v = s_best < 0 ? 0 : s_best;
+    const int64_t v = sh.best < 0 ? 0 : sh.best;
     if (tid == 0) token[item] = v;
-    if (emitted) emitted[(int64_t)item * (k + 1) + tid] = tid < it.a ? dtok : v;
+    if (emitted) emitted[item * (k + 1) + tid] = tid < it.a ? dtok : v;
+  }
+}
+
+// The draw in a launch of its own (one workgroup per item), after the mass launch.
+__global__ __launch_bounds__(kRsThreads) void k_rs_pick(
+    RsRows rr, const RsItem* __restrict__ items, const float2* __restrict__ mass, int nchunk,
+    float inv_t, const float* __restrict__ u_sample, int64_t* __restrict__ token,
+    const int64_t* __restrict__ draft_tokens, int k, int64_t* __restrict__ emitted) {
+  __shared__ RsPickLds sh;
+  const int item = blockIdx.x;
+  rs_pick(rr, items[item], mass + (int64_t)item * nchunk, nchunk, inv_t, u_sample[item], item,
+          token, draft_tokens, k, emitted, sh);
+}
+
+// Chunks per mass workgroup. Measured at config 4 (48 items of two 248320-logit rows): 1 chunk
+// (2928 workgroups) 9.2 us, 2 and 4 chunks 1-3 us slower in the whole acceptance: more
+// workgroups in flight hide the item load each one starts with better than longer streams do.
+// (A variant whose last workgroup per item also made the draw, found by an agent-scope arrival
+// counter, lost 2-20 us to the counter's same-address atomics.)
+constexpr int kRsMassChunks = 1;
+
+// Per-chunk sums of an item's draw weights (residual, target), one workgroup per (G chunks,
+// item), every load of its chunks in flight before the first is used.
+template <int G>
+__global__ __launch_bounds__(kRsThreads) void k_rs_mass(RsRows rr, const RsItem* __restrict__ items,
+                                                       int nchunk, float inv_t,
+                                                       float2* __restrict__ mass) {
+  __shared__ float2 red[G][kRsThreads / kWave];
+  const int c0 = blockIdx.x * G;
+  const int item = blockIdx.y;
+  const int tid = threadIdx.x;
+  const RsItem it = items[item];
+  auto reduce = [&](int g, const float (&wr)[kRsPerThread], const float (&wp)[kRsPerThread]) {
+    float sr = 0.f, sp = 0.f;
+#pragma unroll
+    for (int e = 0; e < kRsPerThread; ++e) {
+      sr += wr[e];
+      sp += wp[e];
+    }
+    sr = wave_sum(sr);
+    sp = wave_sum(sp);
+    if ((tid & (kWave - 1)) == 0) red[g][tid / kWave] = make_float2(sr, sp);
+  };
+  if (rr.vec && rr.dt == MTPK_BF16) {
+    // Every load of the G chunks (two rows) goes out before the first is used: 16-byte buffer
+    // loads, slots past the row reading zeros, which the index test below turns into -inf as
+    // rs_load does. The logits stay raw: the temperature is in RsExp.
+    const uint32_t bytes = (uint32_t)(rr.vocab * 2);
+    const bool has_q = it.drow >= 0;
+    const RsExp ex = rs_exp(it, inv_t);
+    const rsrc_t rt = make_rsrc(reinterpret_cast<const uint16_t*>(rr.target) + it.trow * rr.vocab, bytes);
+    const rsrc_t rq = make_rsrc(reinterpret_cast<const uint16_t*>(rr.draft) +
+                                    (has_q ? it.drow : 0) * rr.vocab, has_q ? bytes : 0u);
+    u32x4_t vt[G][2], vq[G][2];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t i = (int64_t)(c0 + g) * kRsChunk + (int64_t)tid * kRsPerThread + 8 * h;
+        const uint32_t off = i < rr.vocab ? (uint32_t)(i * 2) : kOutOfRange;
+        vt[g][h] = buf16(rt, off);
+        vq[g][h] = buf16(rq, has_q ? off : kOutOfRange);
+      }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {  // a chunk past the row is all -inf: zero mass, not stored
+      float z[kRsPerThread], zq[kRsPerThread];
+      const int64_t i0 = (int64_t)(c0 + g) * kRsChunk + (int64_t)tid * kRsPerThread;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          const int e = 8 * h + 2 * q;
+          const bool in0 = i0 + e < rr.vocab, in1 = i0 + e + 1 < rr.vocab;
+          z[e] = in0 ? bf16_to_f32((uint16_t)(vt[g][h][q] & 0xffffu)) : -INFINITY;
+          z[e + 1] = in1 ? bf16_to_f32((uint16_t)(vt[g][h][q] >> 16)) : -INFINITY;
+          zq[e] = in0 ? bf16_to_f32((uint16_t)(vq[g][h][q] & 0xffffu)) : -INFINITY;
+          zq[e + 1] = in1 ? bf16_to_f32((uint16_t)(vq[g][h][q] >> 16)) : -INFINITY;
+        }
+      float wr[kRsPerThread], wp[kRsPerThread];
+      rs_weights_of(ex, z, zq, wr, wp);
+      reduce(g, wr, wp);
+    }
+  } else {
+    for (int g = 0; g < G && c0 + g < nchunk; ++g) {
+      float wr[kRsPerThread], wp[kRsPerThread];
+      rs_weights(rr, it, c0 + g, inv_t, wr, wp);
+      reduce(g, wr, wp);
+    }
+  }
+  __syncthreads();
+  if (tid < G && c0 + tid < nchunk) {
+    const float2 a = red[tid][0], b = red[tid][1], d = red[tid][2], e = red[tid][3];
+    mass[(int64_t)item * nchunk + c0 + tid] =
+        make_float2((a.x + b.x) + (d.x + e.x), (a.y + b.y) + (d.y + e.y));
   }
 }
 
 int64_t rs_chunks(int64_t vocab) { return (vocab + kRsChunk - 1) / kRsChunk; }
+int64_t rs_groups(int64_t nchunk) { return (nchunk + kRsMassChunks - 1) / kRsMassChunks; }
+
+// Workspace layout shared by both entry points: chunk partials | items | chunk masses.
+struct RsWorkspace {
+  float2* part;
+  RsItem* items;
+  float2* mass;
+};
+
+RsWorkspace rs_workspace(void* workspace, int64_t items, int64_t rows, int64_t nchunk) {
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  RsWorkspace w;
+  w.part = reinterpret_cast<float2*>(ws);
+  ws += align256(rows * nchunk * (int64_t)sizeof(float2));
+  w.items = reinterpret_cast<RsItem*>(ws);
+  ws += align256(items * (int64_t)sizeof(RsItem));
+  w.mass = reinterpret_cast<float2*>(ws);
+  return w;
+}
 
 }  // namespace mtpk
 
@@ -470,23 +560,21 @@ int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int6
   const int per_vec = dtype == MTPK_BF16 ? 8 : 4;
   RsRows rr{target, draft, dtype, vocab,
             (int)(aligned16(target) && (k == 0 || aligned16(draft)) && vocab % per_vec == 0)};
-  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  float2* part = reinterpret_cast<float2*>(ws);
-  ws += align256(batch * (2 * (int64_t)k + 1) * nchunk * (int64_t)sizeof(float2));
-  RsItem* items = reinterpret_cast<RsItem*>(ws);
-  ws += align256(batch * (int64_t)sizeof(RsItem));
-  float2* mass = reinterpret_cast<float2*>(ws);
+  const RsWorkspace w = rs_workspace(workspace, batch, batch * (2 * (int64_t)k + 1), nchunk);
   const float inv_t = 1.f / temperature;
   const hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_rs_stats, dim3((unsigned)nchunk, (unsigned)rows), dim3(kRsThreads), 0, st,
-                     rr, batch * t, inv_t, part);
+                     rr, batch * t, inv_t, w.part);
   int rc = status_of(hipGetLastError());
   if (rc) return rc;
-  hipLaunchKernelGGL(k_rs_decide_mass, dim3((unsigned)nchunk, (unsigned)batch), dim3(kRsThreads), 0,
-                     st, rr, part, (int)nchunk, (int)batch, k, inv_t, draft_tokens, u_accept, items,
-                     accept_len, margin, mass);
+  hipLaunchKernelGGL(k_rs_decide, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, w.part,
+                     (int)nchunk, (int)batch, k, inv_t, draft_tokens, u_accept, w.items, accept_len,
+                     margin);
   if ((rc = status_of(hipGetLastError()))) return rc;
-  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, items, mass,
+  hipLaunchKernelGGL(k_rs_mass<kRsMassChunks>, dim3((unsigned)rs_groups(nchunk), (unsigned)batch),
+                     dim3(kRsThreads), 0, st, rr, w.items, (int)nchunk, inv_t, w.mass);
+  if ((rc = status_of(hipGetLastError()))) return rc;
+  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, w.items, w.mass,
                      (int)nchunk, inv_t, u_sample, token, draft_tokens, k, emitted);
   return status_of(hipGetLastError());
 }
@@ -508,24 +596,20 @@ int mtpk_sample_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
   if (nchunk > 65535) return MTPK_EINVAL;
   const int per_vec = dtype == MTPK_BF16 ? 8 : 4;
   RsRows rr{logits, nullptr, dtype, vocab, (int)(aligned16(logits) && vocab % per_vec == 0)};
-  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  float2* part = reinterpret_cast<float2*>(ws);
-  ws += align256(rows * nchunk * (int64_t)sizeof(float2));
-  RsItem* items = reinterpret_cast<RsItem*>(ws);
-  ws += align256(rows * (int64_t)sizeof(RsItem));
-  float2* mass = reinterpret_cast<float2*>(ws);
+  const RsWorkspace w = rs_workspace(workspace, rows, rows, nchunk);
   const float inv_t = 1.f / temperature;
   const hipStream_t st = (hipStream_t)stream;
   hipLaunchKernelGGL(k_rs_stats, dim3((unsigned)nchunk, (unsigned)rows), dim3(kRsThreads), 0, st,
-                     rr, rows, inv_t, part);
+                     rr, rows, inv_t, w.part);
   int rc = status_of(hipGetLastError());
   if (rc) return rc;
-  hipLaunchKernelGGL(k_rs_rows, dim3((unsigned)rows), dim3(kWave), 0, st, part, (int)nchunk, items);
+  hipLaunchKernelGGL(k_rs_rows, dim3((unsigned)rows), dim3(kWave), 0, st, w.part, (int)nchunk,
+                     w.items);
   if ((rc = status_of(hipGetLastError()))) return rc;
-  hipLaunchKernelGGL(k_rs_mass, dim3((unsigned)nchunk, (unsigned)rows),
-                     dim3(kRsThreads), 0, st, rr, items, (int)nchunk, inv_t, mass);
+  hipLaunchKernelGGL(k_rs_mass<kRsMassChunks>, dim3((unsigned)rs_groups(nchunk), (unsigned)rows),
+                     dim3(kRsThreads), 0, st, rr, w.items, (int)nchunk, inv_t, w.mass);
   if ((rc = status_of(hipGetLastError()))) return rc;
-  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)rows), dim3(kRsThreads), 0, st, rr, items, mass,
+  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)rows), dim3(kRsThreads), 0, st, rr, w.items, w.mass,
                      (int)nchunk, inv_t, u, token, nullptr, 0, nullptr);
   return status_of(hipGetLastError());
 }

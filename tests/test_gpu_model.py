@@ -250,7 +250,10 @@ def test_config5_full_size_graph_rounds(dev) -> None:
     routing-identical lanes' cached hidden seed at up to 1.7e-2 and every other state component
     at or below 9.2e-3, where a lane whose routing truly diverged sits near 1e-1 and an indexing
     error at O(1). A lane may differ only where its first routing difference, in dependency
-    order, is a near-tie swap at the top-10 cut (10 of 48 lanes on this seed)."""
+    order, is a near-tie swap at the top-10 cut. How many lanes take one depends on rounding
+    anywhere upstream (10 of 48 on this seed with the MoE's K chunks summed from K = 0, 13 with
+    them rotated by output tile), so the count is only capped at a third of the lanes; every such
+    lane is checked to be a swap at the cut itself."""
     b, k, ctx = 48, 3, 8192
     model, runner, toks, pos = mh.c5_model_and_runner(dev, b, k, ctx)
     assert runner.validated == {b: True}
@@ -327,7 +330,7 @@ def test_config5_full_size_graph_rounds(dev) -> None:
           f"{len(diverged)} lanes take a near-tie router swap first: {diverged}; "
           f"per-component max state rel-L2 on the identical lanes: {[f'{e:.1e}' for e in comp_max]}")
     assert not over, f"routing-identical lanes over 2e-2 (lane, component, rel-L2): {over}"
-    assert len(diverged) <= b // 4
+    assert len(diverged) <= b // 3
 
 
 # ---------------------------------------------------------------- buckets and padding rows
