@@ -18,9 +18,9 @@ constexpr int kArgmaxThreads = 256;
 // over [192 | 48, 248320] bf16: 4 loads beat 2/8/16, and about 1536 workgroups (six per CU,
 // all resident at once at this kernel's occupancy, the same number on every CU at 192 and 48
 // rows) beat 512/768/1024/2048/4096 (greedy accept at 192 rows: 24.4 us against 25.9 us at
-// 1024, whose 4.5 per CU leave half the CUs a workgroup longer); a 1024-thread workgroup per
-// row, which would drop the second launch, streams at only about 40 GB/s per CU and lost at
-// every row count.
+// 1024, whose 4.5 per CU leave half the CUs a workgroup longer, and 6144/12288/24576 with
+// shorter chunks: greedy accept 30/42/64 us); a 1024-thread workgroup per row, which would drop
+// the second launch, streams at only about 40 GB/s per CU and lost at every row count.
 constexpr int kArgmaxLoads = 4;
 constexpr int64_t kArgmaxWorkgroups = 1536;
 
@@ -161,6 +161,7 @@ __global__ __launch_bounds__(256) void k_argmax_final(const uint64_t* __restrict
 constexpr int kAcceptThreads = 1024;
 constexpr int kPre = 8;
 constexpr int kKeyRows = 4096;  // B * t bound of the keys path: one u64 of LDS per verify row
+constexpr int kKeyLoads = 32;   // key loads in flight per row in the keys fold
 
 // keys (optional): the argmax chunk keys [B * t, chunks] of k_argmax_partial. The workgroup
 // then first folds them into one key per verify row (a thread per row), writes the indices to
@@ -204,21 +205,21 @@ __global__ __launch_bounds__(kAcceptThreads) void k_greedy_accept(
     p0 = next_pos ? pos[j] : 0;
   }
   if (keys) {
-    // One thread per verify row folds the row's chunk keys in registers, eight loads in flight
-    // at a time; the maximum key is the first-occurrence argmax whatever the order.
+    // One thread per verify row folds the row's chunk keys in registers: up to kKeyLoads loads
+    // in flight at once (one memory round trip), then any further keys kKeyLoads at a time. The
+    // maximum key is the first-occurrence argmax whatever the order. (LDS atomics over all keys,
+    // spread across the workgroup, measured 0.5-1 us slower at 8 and 32 chunks per row.)
     const int rows = B * t;
     for (int r = j; r < rows; r += kAcceptThreads) {
       const uint64_t* kr = keys + (int64_t)r * chunks;
       uint64_t bk = 0;
-      int c = 0;
-      for (; c + 8 <= chunks; c += 8) {
-        uint64_t x[8];
+      for (int c0 = 0; c0 < chunks; c0 += kKeyLoads) {
+        uint64_t x[kKeyLoads];
 #pragma unroll
-        for (int u = 0; u < 8; ++u) x[u] = kr[c + u];
+        for (int u = 0; u < kKeyLoads; ++u) x[u] = c0 + u < chunks ? kr[c0 + u] : 0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) bk = x[u] > bk ? x[u] : bk;
+        for (int u = 0; u < kKeyLoads; ++u) bk = x[u] > bk ? x[u] : bk;
       }
-      for (; c < chunks; ++c) bk = kr[c] > bk ? kr[c] : bk;
       const int64_t tok = (int64_t)argmax_key_index(bk);
       s_key[r] = (unsigned long long)tok;
       sa_out[(int64_t)(r / t) * ss + r % t] = tok;
