@@ -782,6 +782,7 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
   __shared__ __attribute__((aligned(16))) uint8_t as_[kSingleDownWaves][IP][kPlaneBytes];
   __shared__ __attribute__((aligned(16))) uint8_t zero[kPlaneBytes];  // the A rows of lanes c >= 1
   __shared__ float red[kSingleDownWaves][16];
+  __shared__ float s_prod[16];  // the shared expert's gated rows, made by an idle wave
   const int rtiles = H >> 4;
   const int n_items = tokens * rtiles;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid & (kWave - 1);
@@ -793,8 +794,15 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
   if (tid < kPlaneBytes / 16) reinterpret_cast<u32x4_t*>(zero)[tid] = zero16();
   __syncthreads();
 
+  // With top_k < kSingleDownWaves the last wave streams no assignment: it fetches the shared
+  // expert's term while the others stream, so the epilogue does not wait a memory round trip
+  // for it.
+  const bool pre_shared = shared_active(sh) && top_k < kSingleDownWaves;
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int t = item / rtiles, rt = item - t * rtiles;
+    if (pre_shared && wave == kSingleDownWaves - 1 && lane < 16)
+      s_prod[lane] = round_to(odt, shared_gate(sh, t, odt) *
+                                       shared_value(sh, (int64_t)t * H + rt * 16 + lane, odt));
     float tot = 0.f;
     for (int j = wave; j < top_k; j += kSingleDownWaves) {
       const int64_t a = (int64_t)t * top_k + j;
@@ -865,7 +873,10 @@ __global__ __launch_bounds__(kSingleDownWaves * kWave) void k_moe_down_single(
 #pragma unroll
       for (int w2 = 1; w2 < kSingleDownWaves; ++w2) v += red[w2][lane];
       const int64_t oi = (int64_t)t * H + rt * 16 + lane;
-      if (shared_active(sh)) v = add_shared(sh, shared_gate(sh, t, odt), v, oi, odt);
+      if (pre_shared)
+        v = round_to(odt, v) + s_prod[lane];  // add_shared's arithmetic, its product made early
+      else if (shared_active(sh))
+        v = add_shared(sh, shared_gate(sh, t, odt), v, oi, odt);
       store_float(out, odt, oi, v);
     }
     __syncthreads();
