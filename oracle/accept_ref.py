@@ -115,13 +115,13 @@ def round_indices(
 
     `draft [B, k]`, `step_argmax [B, t]` with `t = k + 1`, `active [B]` bool, `pos`/`budget`
     `[B]`, `stops [B, S]` padded with -1, `conv_k1` = conv kernel size - 1, `forced_n [B]`
-    (optional) the forced draft count of each row.
+    (optional) the forced draft count of each row: such a row accepts min(forced_n, k) drafts.
     """
     b, t = step_argmax.shape
     a = commit_limit_batched(accept_len(draft, step_argmax), step_argmax, budget, stops)
     forced = np.zeros(b, dtype=bool) if forced_n is None else np.asarray(forced_n) > 0
-    if forced_n is not None:
-        a = np.where(forced, np.asarray(forced_n), a).astype(np.int64)
+    if forced_n is not None:  # a forced row accepts min(forced, k) drafts
+        a = np.where(forced, np.minimum(np.asarray(forced_n), t - 1), a).astype(np.int64)
     lengths = np.where(active, a + 1, 1).astype(np.int64)
     src, cu = fixed_prefix_pack_index(lengths, t)
     win = np.arange(conv_k1)

@@ -20,7 +20,8 @@ constexpr int kArgmaxThreads = 256;
 // rows) beat 512/768/1024/2048/4096 (greedy accept at 192 rows: 24.4 us against 25.9 us at
 // 1024, whose 4.5 per CU leave half the CUs a workgroup longer, and 6144/12288/24576 with
 // shorter chunks: greedy accept 30/42/64 us); a 1024-thread workgroup per row, which would drop
-// the second launch, streams at only about 40 GB/s per CU and lost at every row count.
+// the second launch, streams at only about 40 GB/s per CU and lost at every row count. Numbering
+// the workgroups row-fastest (each row's chunks on one XCD) measured the same.
 constexpr int kArgmaxLoads = 4;
 constexpr int64_t kArgmaxWorkgroups = 1536;
 

@@ -102,7 +102,7 @@ def test_forced_rows_every_output(dev, seed, b, k):
     pos = rng.integers(0, 8000, b)
     budget = rng.integers(1, 6, b)
     stops = np.where(rng.random((b, 8)) < 0.2, rng.integers(0, 5, (b, 8)), -1)
-    forced_n = np.where(rng.random(b) < 0.5, rng.integers(1, k + 1, b), 0)
+    forced_n = np.where(rng.random(b) < 0.5, rng.integers(1, k + 3, b), 0)  # > k clamps to k
     want = ar.round_indices(draft, sa, active, pos, budget, stops, 3, forced_n)
     r = accept(dev, sa, draft, active, pos, budget, stops, 3, forced_n)
     for name, w in want.items():

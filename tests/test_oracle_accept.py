@@ -103,11 +103,11 @@ def test_argmax_first_and_kv_rows():
 
 
 def test_forced_rows_equal_an_unforced_row_accepting_the_same_count():
-    """A forced row (`graph_verify_wide.py:196-200`) accepts exactly its forced count whatever
-    its drafts, stop ids and budget say: its outputs equal those of an unforced row whose
-    drafts agree with the target for exactly that many steps, with no stop id and an unbounded
-    budget — except `budget_left`, charged one token (`mtp_overlap.py:62-64`). Unforced rows
-    in the same batch are unchanged by the forced ones."""
+    """A forced row (`graph_verify_wide.py:196-200`) accepts exactly its forced count (at most
+    k) whatever its drafts, stop ids and budget say: its outputs equal those of an unforced row
+    whose drafts agree with the target for exactly that many steps, with no stop id and an
+    unbounded budget — except `budget_left`, charged one token (`mtp_overlap.py:62-64`).
+    Unforced rows in the same batch are unchanged by the forced ones."""
     rng = np.random.default_rng(31)
     for _ in range(50):
         b, k = int(rng.integers(1, 9)), int(rng.integers(1, 5))
@@ -118,13 +118,13 @@ def test_forced_rows_equal_an_unforced_row_accepting_the_same_count():
         pos = rng.integers(0, 100, b)
         budget = rng.integers(1, 8, b)
         stops = np.where(rng.random((b, 2)) < 0.5, rng.integers(0, 6, (b, 2)), -1)
-        forced_n = np.where(rng.random(b) < 0.5, rng.integers(1, k + 1, b), 0)
+        forced_n = np.where(rng.random(b) < 0.5, rng.integers(1, k + 3, b), 0)  # > k: clamped
         got = ar.round_indices(draft, sa, active, pos, budget, stops, 3, forced_n)
         plain = ar.round_indices(draft, sa, active, pos, budget, stops, 3)
         # the equivalent unforced rows: drafts = target for f steps then a mismatch
         eq_draft = draft.copy()
         for j in range(b):
-            f = int(forced_n[j])
+            f = min(int(forced_n[j]), k)
             if f:
                 eq_draft[j, :f] = sa[j, :f]
                 if f < k:
@@ -137,7 +137,7 @@ def test_forced_rows_equal_an_unforced_row_accepting_the_same_count():
             for key in ("accept_len", "lengths", "conv_idx", "keep", "bonus", "next_pos",
                         "hidden_src"):
                 assert np.array_equal(got[key][j], ref[key][j]), (key, j)
-            assert got["accept_len"][j] == (forced_n[j] if forced_n[j] else plain["accept_len"][j])
+            assert got["accept_len"][j] == (min(forced_n[j], k) if forced_n[j] else plain["accept_len"][j])
             charge = 1 if forced_n[j] else plain["accept_len"][j] + 1
             assert got["budget_left"][j] == budget[j] - charge
             stopped = bool((stops[j] == got["bonus"][j]).any())
