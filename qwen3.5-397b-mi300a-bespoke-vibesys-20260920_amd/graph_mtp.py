@@ -48,6 +48,11 @@ def _commit_limit(accept: torch.Tensor, step_argmax: torch.Tensor, budget: torch
     return limit.clamp(min=0)
 
 
+STAGE_TOKEN, STAGE_POS, STAGE_BUDGET, STAGE_SLOT, STAGE_FORCED, STAGE_ACTIVE, STAGE_IDS = range(7)
+"""Columns of `MTPVerifyBuffers.staging`: token, position, budget, slot, forced count, active,
+then the forced ids (k columns) and the stop ids (`MAX_STOP_IDS` columns, -1 padded)."""
+
+
 class MTPVerifyBuffers:
     """One bucket's static tensors for the draft + verify + accept + rollback step
     (`graph_mtp.py:141-178`, same constructor): written before each replay (`token_matrix`,
@@ -90,6 +95,13 @@ class MTPVerifyBuffers:
         # unconditionally (zero on every other row)
         self.forced_n = torch.zeros(capacity, **long)
         self.forced_ids = torch.zeros(capacity, max(t - 1, 1), **long)
+        # a round's host inputs, one row per buffer row (`STAGE_*` columns): written on the
+        # host (pinned on a device), copied once, unpacked into the fields above on the device
+        cols = STAGE_IDS + max(t - 1, 1) + mtp_mod.MAX_STOP_IDS
+        self.staging = torch.zeros(capacity, cols, **long)
+        pin = torch.device(device).type == "cuda"
+        self.staging_host = torch.zeros(capacity, cols, dtype=torch.long, pin_memory=pin)
+        self.staged = None  # the event after the last staging copy (device buffers)
 
 
 @dataclass
@@ -331,12 +343,9 @@ def pad_slot_for(slots, lanes: int) -> int:
     raise ValueError("a padded round needs a lane outside the round")
 
 
-def _fill(model, mtp, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stops, forced) -> None:
-    """Write one round's inputs into `buf`, padding to `buf.capacity` rows
-    (`MTPVerifyRunner.fill`, `graph_mtp.py:795-874`; `MTP_INTERFACE.md:17-33`). Row `j < n` is the
-    round's `j`-th lane; rows `>= n` are padding: `active` False, position 0, an idle lane as
-    slot, no stop ids, budget `t`, and the reserved block in every block-table entry. Also
-    writes the fill-owned `block_table`, `block_valid`, `write_rows` and `draft_hidden`."""
+def _stage(model, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stops, forced) -> None:
+    """The host half of `_fill`: checks, the lanes' KV blocks grown for t more positions, and
+    the round's rows written into `buf.staging_host` and copied to `buf.staging` (one copy)."""
     n, t, k = len(slots), buf.t, buf.t - 1
     lanes = model.lanes
     if not 1 <= n <= buf.capacity or len(set(slots)) != n:
@@ -351,35 +360,71 @@ def _fill(model, mtp, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, 
         raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
     for s, p in zip(slots, positions, strict=True):
         model.blocks.grow(s, p + t)
-    pad = pad_slot_for(slots, lanes) if n < buf.capacity else 0
-    big = 1 << 40
+    if buf.staged is not None:
+        buf.staged.synchronize()  # the previous round's copy has left the pinned rows
+    h = buf.staging_host.numpy()
     width = max(k, 1)
-    rows = []
-    for j in range(buf.capacity):
-        if j < n:
-            ids = list(forced[j])[:k] if forced else []
-            st = list(stops[j]) if stops else []
-            rows.append([tokens[j], positions[j], big if budgets is None else budgets[j], int(slots[j]),
-                         len(ids), 1, *(ids + [0] * (width - len(ids))),
-                         *(st + [-1] * (mtp_mod.MAX_STOP_IDS - len(st)))])
-        else:
-            rows.append([0, 0, t, pad, 0, 0, *([0] * width), *([-1] * mtp_mod.MAX_STOP_IDS)])
-    host = torch.tensor(rows, dtype=torch.long).to(buf.pos.device)
+    h[:, STAGE_IDS : STAGE_IDS + width] = 0
+    h[:, STAGE_IDS + width :] = -1
+    h[:n, STAGE_TOKEN] = tokens
+    h[:n, STAGE_POS] = positions
+    h[:n, STAGE_BUDGET] = 1 << 40 if budgets is None else budgets
+    h[:n, STAGE_SLOT] = [int(x) for x in slots]
+    h[:n, STAGE_ACTIVE] = 1
+    h[:n, STAGE_FORCED] = 0
+    for j in range(n):
+        if forced:
+            ids = list(forced[j])[:k]
+            h[j, STAGE_FORCED] = len(ids)
+            h[j, STAGE_IDS : STAGE_IDS + len(ids)] = ids
+        if stops and len(stops[j]):
+            h[j, STAGE_IDS + width : STAGE_IDS + width + len(stops[j])] = list(stops[j])
+    # padding rows: inactive, position 0, budget t, an idle lane as slot, no stop ids
+    h[n:, STAGE_TOKEN] = 0
+    h[n:, STAGE_POS] = 0
+    h[n:, STAGE_BUDGET] = t
+    h[n:, STAGE_SLOT] = pad_slot_for(slots, lanes) if n < buf.capacity else 0
+    h[n:, STAGE_FORCED] = 0
+    h[n:, STAGE_ACTIVE] = 0
+    buf.staging.copy_(buf.staging_host, non_blocking=True)
+    if buf.staging.is_cuda:
+        buf.staged = torch.cuda.Event()
+        buf.staged.record()
+
+
+def _unpack(model, buf: MTPVerifyBuffers) -> None:
+    """The device half of `_fill`: `buf.staging` into the round's fields, and the fill-owned
+    `block_table` (the reserved block on padding rows), `block_valid`, `write_rows` and
+    `draft_hidden` from the model's tables. Only tensor ops on static buffers, so a runner can
+    capture it as a graph of its own."""
+    t, k = buf.t, buf.t - 1
+    width = max(k, 1)
+    st = buf.staging
     buf.token_matrix.zero_()
-    buf.token_matrix[:, 0] = host[:, 0]
-    buf.pos.copy_(host[:, 1])
-    buf.budget.copy_(host[:, 2])
-    buf.slot_rows.copy_(host[:, 3])
-    buf.forced_n.copy_(host[:, 4])
-    buf.active.copy_(host[:, 5] != 0)
-    buf.forced_ids.copy_(host[:, 6 : 6 + width])
-    buf.stops.copy_(host[:, 6 + width :])
+    buf.token_matrix[:, 0] = st[:, STAGE_TOKEN]
+    buf.pos.copy_(st[:, STAGE_POS])
+    buf.budget.copy_(st[:, STAGE_BUDGET])
+    buf.slot_rows.copy_(st[:, STAGE_SLOT])
+    buf.forced_n.copy_(st[:, STAGE_FORCED])
+    buf.active.copy_(st[:, STAGE_ACTIVE] != 0)
+    buf.forced_ids.copy_(st[:, STAGE_IDS : STAGE_IDS + width])
+    buf.stops.copy_(st[:, STAGE_IDS + width :])
     bs = model.cfg.block_size
     buf.block_table.copy_(torch.where(buf.active[:, None], model.blocks.table[buf.slot_rows],
                                       torch.full_like(buf.block_table, RESERVED_BLOCK)))
     buf.block_valid.copy_(((buf.pos + t + bs - 1) // bs).to(torch.int32))
     buf.write_rows.copy_(kv_write_rows(buf.pos, buf.block_table, t, bs))
     buf.draft_hidden.copy_(model.hidden_cache[buf.slot_rows])
+
+
+def _fill(model, mtp, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stops, forced) -> None:
+    """Write one round's inputs into `buf`, padding to `buf.capacity` rows
+    (`MTPVerifyRunner.fill`, `graph_mtp.py:795-874`; `MTP_INTERFACE.md:17-33`). Row `j < n` is the
+    round's `j`-th lane; rows `>= n` are padding: `active` False, position 0, an idle lane as
+    slot, no stop ids, budget `t`, and the reserved block in every block-table entry. Also
+    writes the fill-owned `block_table`, `block_valid`, `write_rows` and `draft_hidden`."""
+    _stage(model, buf, slots, tokens, positions, budgets, stops, forced)
+    _unpack(model, buf)
 
 
 def _committed(buf: MTPVerifyBuffers, n: int | None = None) -> list[list[int]]:
@@ -474,6 +519,10 @@ class EagerBackend:
         return fn
 
 
+_FILLED = ("token_matrix", "pos", "budget", "slot_rows", "forced_n", "active", "forced_ids", "stops",
+           "block_table", "block_valid", "write_rows", "draft_hidden")
+"""The fields a fill writes (validation compares the captured fill's with the eager one's)."""
+
 REQUIRE_GRAPH_ENV = "SEED_MTP_REQUIRE_GRAPH"
 """`=1`: a bucket that fails capture or validation raises instead of serving eager rounds
 (`graph_mtp.py:112-116`)."""
@@ -497,6 +546,7 @@ class GraphMTPRunner(MTPVerifyRunner):
         super().__init__(model, None, capacity, buckets)
         self.backend = CudaGraphBackend() if backend is None else backend
         self.graphs: dict[int, Callable[[], None]] = {}
+        self.unpacks: dict[int, Callable[[], None]] = {}  # each bucket's `_unpack`, captured
         self.enabled = True
         self.validated: dict[int, bool] = {}
         self.eager_rounds = 0
@@ -506,7 +556,21 @@ class GraphMTPRunner(MTPVerifyRunner):
         return True
 
     def _capture(self, buf: MTPVerifyBuffers) -> Callable[[], None]:
+        """The bucket's round as one graph; its fill's device half (`_unpack`) is captured
+        beside it, so a round's fill is one copy and one replay instead of about twenty
+        launches from the host."""
+        self.unpacks[buf.capacity] = self.backend.capture(lambda: _unpack(self.model, buf),
+                                                          buf.pos.device)
         return self.backend.capture(lambda: self._round(buf), buf.pos.device)
+
+    def fill(self, buf: MTPVerifyBuffers, slots, tokens, positions, budgets=None, stops=None,
+             forced=None) -> None:
+        unpack = self.unpacks.get(buf.capacity) if self.enabled else None
+        if unpack is None:
+            _fill(self.model, self.mtp, buf, slots, tokens, positions, budgets, stops, forced)
+            return
+        _stage(self.model, buf, slots, tokens, positions, budgets, stops, forced)
+        unpack()
 
     def _eager_round(self, buf: MTPVerifyBuffers) -> None:
         """The bucket's round run eagerly before its capture, on a side stream on a device (so
@@ -542,7 +606,8 @@ class GraphMTPRunner(MTPVerifyRunner):
         model.hidden_cache.copy_((grid.reshape(model.hidden_cache.shape) * 0.37).sin().to(model.hidden_cache.dtype))
         before = [{k: v.clone() for k, v in p.items() if k in ("conv", "rec")} for p in model.pool]
         seed = model.hidden_cache.clone()
-        self.fill(buf, slots, tokens, positions, budgets, stops)
+        _fill(model, self.mtp, buf, slots, tokens, positions, budgets, stops, None)
+        filled = [getattr(buf, name).clone() for name in _FILLED]
         self._round(buf)
         want = _committed(buf, bucket)
         want_state = ([{k: v.clone() for k, v in p.items() if k in ("conv", "rec")} for p in model.pool],
@@ -551,10 +616,11 @@ class GraphMTPRunner(MTPVerifyRunner):
             for k, v in snap.items():
                 p[k].copy_(v)
         model.hidden_cache.copy_(seed)
-        self.fill(buf, slots, tokens, positions, budgets, stops)
+        self.fill(buf, slots, tokens, positions, budgets, stops)  # the captured unpack, if any
+        ok = all(torch.equal(getattr(buf, name), v) for name, v in zip(_FILLED, filled, strict=True))
         replay()
         got = _committed(buf, bucket)
-        ok = got == want and torch.equal(model.hidden_cache, want_state[1])
+        ok = ok and got == want and torch.equal(model.hidden_cache, want_state[1])
         for p, snap in zip(model.pool, want_state[0], strict=True):
             for k, v in snap.items():
                 ok = ok and torch.equal(p[k], v)
@@ -569,7 +635,7 @@ class GraphMTPRunner(MTPVerifyRunner):
         model = self.model
         if any(model.blocks.host[lane] for lane in range(model.lanes)):
             raise RuntimeError("prepare() is boot-only: some lanes hold KV blocks")
-        self.graphs, self.validated = {}, {}
+        self.graphs, self.validated, self.unpacks = {}, {}, {}
         ok = True
         try:
             for bucket in self.buckets:
