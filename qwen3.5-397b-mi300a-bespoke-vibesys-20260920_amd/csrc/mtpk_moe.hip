@@ -934,13 +934,6 @@ struct StageGeom {
   static_assert(kBytesPerThread == 64, "one staging step is 4 x 16 bytes per thread");
 };
 
-// Items walk their K chunks from chunk q mod (K / 512) on (q the item's row group), not all from
-// K = 0: every item streams the same byte count, so workgroups stay in step, and from one start
-// they would all read the same columns of their rows at once; consecutive items (running side by
-// side) have consecutive q. The rotation depends on the output rows only, so an output's sum
-// order does not depend on which work unit or expert shard its assignment fell into.
-constexpr bool kMoeRotateK = true;
-
 // gate_up, LDS variant (bf16 x, hi/lo intermediate, chunked scales). Item = (unit, 4 tiles of
 // 16 intermediate rows), wave w takes tile 4q + w. Chunks of 512 K = 4 trips = one ring turn.
 template <int D, int NW>
@@ -980,7 +973,6 @@ __global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
     const bool wave_ok = nt_raw < ntile;
     const int nt = wave_ok ? nt_raw : ntile - 1;
     const int eu = e;
-    const int rot = kMoeRotateK ? q % nchunk : 0;  // this item's first K chunk
     const rsrc_t rw = make_rsrc(wq + (int64_t)eu * exp_bytes, exp_bytes);
     const rsrc_t rs = make_rsrc(ws + (int64_t)eu * (2 * I) * nb, (uint32_t)(2 * I * nb));
     const uint32_t row = (uint32_t)(nt * 16 + ln.c);
@@ -996,9 +988,8 @@ __global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
     u32x4_t sreg[RPW];
     auto stage_load = [&](int c) {
       const uint32_t bad = (uint32_t)!(c < nchunk) << 31;
-      const int kc = c < nchunk ? (c + rot) % nchunk : 0;
 #pragma unroll
-      for (int k = 0; k < RPW; ++k) sreg[k] = buf16(rx, (sx[k] + (uint32_t)kc * (KC * 2)) | bad);
+      for (int k = 0; k < RPW; ++k) sreg[k] = buf16(rx, (sx[k] + (uint32_t)c * (KC * 2)) | bad);
     };
     auto stage_store = [&](int b) {
 #pragma unroll
@@ -1006,8 +997,7 @@ __global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
     };
 
     auto issue = [&](u32x4_t& wg, u32x4_t& wu, int tr) {
-      const int trr = tr < ntrip ? ((tr / D + rot) % nchunk) * D + tr % D : tr;
-      const int blk = moe_block(trr, ln.g);
+      const int blk = moe_block(tr, ln.g);
       const uint32_t bad = (uint32_t)!(tr < ntrip) << 31;
       const uint32_t kb = (uint32_t)blk * 16u;
       wg = buf16(rw, (og + kb) | bad);
@@ -1087,15 +1077,13 @@ __global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
     do {
       const int t = c * D;
       const uint8_t* buf = xs[c & 1];
-      // turn c's scales (those of K chunk (c + rot) mod nchunk), by selects on a uniform value
-      // (indexing a register array by it would move the array to scratch, and rotating it makes
-      // every entry loop-carried)
-      const int kc = (c + rot) % nchunk;
+      // turn c's scales, by selects on the uniform c (indexing a register array by c would
+      // move it to scratch, and rotating it makes every entry loop-carried)
       cur_g = sdg[0];
       cur_u = sdu[0];
 #pragma unroll
       for (int T = 1; T < 8; ++T)
-        if (kc == T) {
+        if (c == T) {
           cur_g = sdg[T];
           cur_u = sdu[T];
         }

@@ -251,9 +251,9 @@ def test_config5_full_size_graph_rounds(dev) -> None:
     at or below 9.2e-3, where a lane whose routing truly diverged sits near 1e-1 and an indexing
     error at O(1). A lane may differ only where its first routing difference, in dependency
     order, is a near-tie swap at the top-10 cut. How many lanes take one depends on rounding
-    anywhere upstream (10 of 48 on this seed with the MoE's K chunks summed from K = 0, 13 with
-    them rotated by output tile), so the count is only capped at a third of the lanes; every such
-    lane is checked to be a swap at the cut itself."""
+    anywhere upstream (10 of 48 on this seed; a change of the MoE's K summation order moved it to
+    13), so the count is only capped at a third of the lanes; every such lane is checked to be a
+    swap at the cut itself."""
     b, k, ctx = 48, 3, 8192
     model, runner, toks, pos = mh.c5_model_and_runner(dev, b, k, ctx)
     assert runner.validated == {b: True}
