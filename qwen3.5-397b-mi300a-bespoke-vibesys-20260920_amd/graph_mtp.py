@@ -358,8 +358,7 @@ def _stage(model, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stop
             raise ValueError(f"{name} has {len(seq)} entries for {n} slots")
     if stops is not None and any(len(s) > mtp_mod.MAX_STOP_IDS for s in stops):
         raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
-    for s, p in zip(slots, positions, strict=True):
-        model.blocks.grow(s, p + t)
+    model.blocks.grow_many(slots, [p + t for p in positions])
     if buf.staged is not None:
         buf.staged.synchronize()  # the previous round's copy has left the pinned rows
     h = buf.staging_host.numpy()

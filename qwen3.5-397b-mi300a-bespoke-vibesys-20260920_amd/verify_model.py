@@ -369,6 +369,28 @@ class BlockTables:
         self.table[lane, len(have) : need] = torch.tensor(new, dtype=torch.int32).to(self.device)
         have.extend(new)
 
+    def grow_many(self, lanes, lengths) -> None:
+        """`grow` for several lanes with one host-to-device copy and one scatter for every new
+        table entry (per-lane copies from pageable memory each wait for the stream)."""
+        needs = []
+        for lane, length in zip(lanes, lengths, strict=True):
+            need = (int(length) + self.block_size - 1) // self.block_size
+            if need > self.max_blocks:
+                raise ValueError(f"lane {lane}: {length} positions exceed the table's {self.max_blocks} blocks")
+            needs.append((int(lane), need))
+        upd = []
+        for lane, need in needs:
+            have = self.host[lane]
+            for col in range(len(have), need):
+                blk = self._free.pop()
+                have.append(blk)
+                upd.append((lane, col, blk))
+        if not upd:
+            return
+        pin = self.table.is_cuda
+        u = torch.tensor(upd, dtype=torch.long, pin_memory=pin).to(self.device, non_blocking=pin)
+        self.table[u[:, 0], u[:, 1]] = u[:, 2].to(torch.int32)
+
     def release(self, lane: int) -> None:
         self._free.extend(reversed(self.host[lane]))
         self.host[lane] = []

@@ -149,3 +149,21 @@ def test_prepare_refuses_a_divergent_capture(monkeypatch):
     other, _, _ = _prefilled(4, 0)
     with pytest.raises(RuntimeError, match="SEED_MTP_REQUIRE_GRAPH"):
         _Diverging(other, graph_mtp.EagerBackend(), capacity=4).prepare()
+
+
+def test_grow_many_equals_grow_per_lane():
+    """`BlockTables.grow_many` (one copy per round) hands out the same blocks into the same table
+    entries as `grow` lane by lane, and refuses an over-long lane before changing anything."""
+    import verify_model as vm
+
+    a = vm.BlockTables(4, 96, 16, torch.device("cpu"), seed=3)
+    b = vm.BlockTables(4, 96, 16, torch.device("cpu"), seed=3)
+    for lanes, lengths in (([0, 2], [5, 40]), ([1, 2, 3], [17, 41, 0]), ([0, 3], [80, 33])):
+        for lane, n in zip(lanes, lengths):
+            a.grow(lane, n)
+        b.grow_many(lanes, lengths)
+        assert torch.equal(a.table, b.table) and a.host == b.host and a._free == b._free
+    before = (b.table.clone(), [list(h) for h in b.host], list(b._free))
+    with pytest.raises(ValueError, match="exceed"):
+        b.grow_many([1, 2], [20, 97])
+    assert torch.equal(b.table, before[0]) and b.host == before[1] and b._free == before[2]
