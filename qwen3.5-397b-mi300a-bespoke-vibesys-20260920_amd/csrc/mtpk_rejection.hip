@@ -424,7 +424,7 @@ __global__ __launch_bounds__(kRsThreads) void k_rs_pick(
 // (2928 workgroups) 9.2 us, 2 and 4 chunks 1-3 us slower in the whole acceptance: more
 // workgroups in flight hide the item load each one starts with better than longer streams do.
 // (A variant whose last workgroup per item also made the draw, found by an agent-scope arrival
-// counter, lost 2-20 us to the counter's same-address atomics.)
+// counter, lost 3-20 us to the counter's same-address atomics.)
 constexpr int kRsMassChunks = 1;
 
 // Per-chunk sums of an item's draw weights (residual, target), one workgroup per (G chunks,
