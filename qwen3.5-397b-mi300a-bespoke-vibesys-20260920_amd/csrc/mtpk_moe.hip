@@ -960,6 +960,28 @@ __global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
   // staging: load k of a chunk moves 16 bytes of token row 4k + wave at byte 16 * lane, so
   // every wave instruction reads one row's whole 1 KB chunk (eight full 128-byte lines)
 
+  // The intermediate rows are held in registers and stored kHold items at a time (all of a
+  // workgroup's items at M = 192), not at the end of each item: stores spread through the
+  // weight stream cost the HBM read/write turnarounds (gate_up 300 -> 294 us at M = 192 with 12
+  // items held, 256 VGPRs; the 4-wave form holds 4, keeping two workgroups per CU at M = 32).
+  // Offsets are 32-bit, so a launch whose intermediate plane exceeds that stores at once.
+  constexpr int kHold = NW == 8 ? 12 : 4;
+  const bool hold = inter_plane <= INT32_MAX;
+  uint32_t held_v[kHold][4];  // (hi | lo << 16) bf16 planes of the value
+  int32_t held_d[kHold][4];   // its offset in a plane, or -1
+  int held = 0;
+  auto flush = [&]() {
+#pragma unroll
+    for (int h = 0; h < kHold; ++h)
+      if (h < held)
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (held_d[h][i] >= 0) {
+            inter[held_d[h][i]] = (uint16_t)(held_v[h][i] & 0xffffu);
+            inter[inter_plane + held_d[h][i]] = (uint16_t)(held_v[h][i] >> 16);
+          }
+    held = 0;
+  };
   for (int item = blockIdx.x; item < n_items; item += gridDim.x) {
     const int u = item / ngroup, q = item - u * ngroup;
     const int e = sload(src.units, 3 * u), first = sload(src.units, 3 * u + 1);
@@ -1103,17 +1125,42 @@ __global__ __launch_bounds__(NW * kWave) void k_moe_gate_up_lds(
       lds_barrier();
     } while (++c < nchunk);
 
-    if (wave_ok) {
-      const int n = nt * 16 + ln.c;
+    const int n = nt * 16 + ln.c;
+    if (!hold) {
+      if (wave_ok) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        if (moe_out_slot(ln.g, i) < cnt) {
-          const float gt = accg[i];
-          store_planes<2>(inter + (int64_t)om[i] * I + n, inter_plane, gt / (1.f + __expf(-gt)) * accu[i]);
+        for (int i = 0; i < 4; ++i) {
+          if (moe_out_slot(ln.g, i) < cnt) {
+            const float gt = accg[i];
+            store_planes<2>(inter + (int64_t)om[i] * I + n, inter_plane, gt / (1.f + __expf(-gt)) * accu[i]);
+          }
         }
       }
+      continue;
     }
+    uint32_t pv[4];
+    int32_t pd[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float gt = accg[i];
+      uint16_t hi, lo;
+      split_bf16(gt / (1.f + __expf(-gt)) * accu[i], &hi, &lo);  // store_planes<2>'s split
+      pv[i] = (uint32_t)hi | ((uint32_t)lo << 16);
+      pd[i] = (wave_ok && moe_out_slot(ln.g, i) < cnt) ? om[i] * I + n : -1;
+    }
+    // into slot `held` by selects on the uniform count (an indexed register array would go to
+    // scratch)
+#pragma unroll
+    for (int h = 0; h < kHold; ++h)
+      if (h == held)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          held_v[h][i] = pv[i];
+          held_d[h][i] = pd[i];
+        }
+    if (++held == kHold) flush();
   }
+  flush();
 }
 
 // down, LDS variant (hi/lo intermediate planes, chunked scales). Item = (unit, 4 x R tiles of
