@@ -1705,10 +1705,12 @@ bool chunked_scales(int K, int split, int D) {
 
 // Unit-mode gate_up with the activation rows staged in LDS (bf16 x, K a multiple of 512).
 // Batches of at least this many tokens run gate_up with 8-wave workgroups (one staged copy of
-// the unit's activation rows for 128 intermediate rows, two workgroups per CU): measured 4-5%
-// faster at 192 rows (Zipf routing, 393 units), slower at 32 rows, where the 8 items per unit
-// leave the grid a short tail of a few items per workgroup.
-constexpr int64_t kGateUpWideTokens = 96;
+// the unit's activation rows for 128 intermediate rows, one workgroup per CU at 256 VGPRs with
+// its held outputs): measured 4-5% faster at 192 rows (Zipf routing, 393 units), slower at 32
+// rows (M = 32 layer 180.0-180.9 against 178.8-179.2 us), where the 8 items per unit leave the
+// grid a short tail of a few items per workgroup; at 48 rows (the draft steps' MoE) the MTP
+// round took 8.29 against 8.32-8.33 ms.
+constexpr int64_t kGateUpWideTokens = 48;
 
 int launch_gate_up_lds(const uint16_t* x, int64_t x_elems, int K, const uint8_t* wq,
                        const uint8_t* ws, int I, const UnitSrc& src, int64_t max_units, int top_k,
