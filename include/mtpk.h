@@ -323,6 +323,27 @@ int mtpk_greedy_accept_keys(const uint64_t* keys, int64_t chunks, int64_t* step_
                             int64_t* next_pos, int64_t* budget_left, uint8_t* live,
                             int64_t* hidden_src, void* stream);
 
+/* ---------------------------------------------------------------- round fill
+ * The device half of `MTPVerifyRunner.fill` (graph_mtp.py:795-874): one launch unpacks a round's
+ * staged rows into the captured round's static buffers. staging i64 [rows, 6 + w + n_stops],
+ * w = max(t - 1, 1), one row per buffer row: token, position, budget, slot, forced count,
+ * active (0 | 1), w forced ids, n_stops stop ids. lane_tables i32 [lanes, max_blocks] (every
+ * lane's block table), hidden_cache [lanes, row_bytes] (each lane's seed row, any dtype).
+ * Writes, per row j: token_matrix i64 [rows, t] = (token, 0, ...); pos, budget, slot_rows,
+ * forced_n i64 [rows]; active u8 [rows]; forced_ids i64 [rows, w]; stops i64 [rows, n_stops];
+ * block_table i32 [rows, max_blocks] = the slot's table on active rows, reserved_block on the
+ * others; block_valid i32 [rows] = floor((pos + t + block_size - 1) / block_size); write_rows
+ * i64 [rows, t] = block_table[j][q / block_size] * block_size + q mod block_size at
+ * q = pos + s (floor division; -1 where q / block_size falls outside the table);
+ * draft_hidden [rows, row_bytes] = hidden_cache[slot] (zeros for a slot outside [0, lanes)). */
+int mtpk_round_fill(const int64_t* staging, int64_t rows, int64_t t, int64_t n_stops,
+                    const int32_t* lane_tables, int64_t lanes, int64_t max_blocks,
+                    int64_t block_size, int32_t reserved_block, const void* hidden_cache,
+                    int64_t row_bytes, int64_t* token_matrix, int64_t* pos, int64_t* budget,
+                    int64_t* slot_rows, int64_t* forced_n, uint8_t* active, int64_t* forced_ids,
+                    int64_t* stops, int32_t* block_table, int32_t* block_valid,
+                    int64_t* write_rows, void* draft_hidden, void* stream);
+
 /* ---------------------------------------------------------------- rejection sampling
  * Sampling-mode acceptance for an MTP round at temperature T > 0. The reference engine has no
  * counterpart: it runs MTP rounds only for all-greedy batches (scheduler.py:1775-1793,

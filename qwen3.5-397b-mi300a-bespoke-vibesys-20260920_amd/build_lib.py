@@ -20,7 +20,7 @@ OBJ_DIR = HERE / "_build"
 ARCH = os.environ.get("MTPK_ARCH", "gfx950")
 SOURCES = ["mtpk_runtime.hip", "mtpk_moe.hip", "mtpk_router.hip", "mtpk_accept.hip", "mtpk_deltanet.hip",
            "mtpk_rejection.hip", "mtpk_attention.hip", "mtpk_norm.hip", "mtpk_gemm.hip",
-           "mtpk_moe_dense.hip", "mtpk_probe.hip"]
+           "mtpk_moe_dense.hip", "mtpk_probe.hip", "mtpk_round.hip"]
 
 HIPCC_FLAGS = [
     f"--offload-arch={ARCH}",

@@ -394,8 +394,11 @@ def _stage(model, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stop
 def _unpack(model, buf: MTPVerifyBuffers) -> None:
     """The device half of `_fill`: `buf.staging` into the round's fields, and the fill-owned
     `block_table` (the reserved block on padding rows), `block_valid`, `write_rows` and
-    `draft_hidden` from the model's tables. Only tensor ops on static buffers, so a runner can
-    capture it as a graph of its own."""
+    `draft_hidden` from the model's tables. On a device this is one launch of
+    `mtpk_round_fill`; CPU buffers take the same steps as tensor ops."""
+    if buf.staging.is_cuda:
+        round_fill(model, buf)
+        return
     t, k = buf.t, buf.t - 1
     width = max(k, 1)
     st = buf.staging
@@ -414,6 +417,38 @@ def _unpack(model, buf: MTPVerifyBuffers) -> None:
     buf.block_valid.copy_(((buf.pos + t + bs - 1) // bs).to(torch.int32))
     buf.write_rows.copy_(kv_write_rows(buf.pos, buf.block_table, t, bs))
     buf.draft_hidden.copy_(model.hidden_cache[buf.slot_rows])
+
+
+def round_fill(model, buf: MTPVerifyBuffers) -> None:
+    """`mtpk_round_fill` on device buffers: what `_unpack` computes, in one launch."""
+    table, hidden = model.blocks.table, model.hidden_cache
+    fields = (buf.staging, table, hidden, buf.token_matrix, buf.pos, buf.budget, buf.slot_rows,
+              buf.forced_n, buf.active, buf.forced_ids, buf.stops, buf.block_table,
+              buf.block_valid, buf.write_rows, buf.draft_hidden)
+    device = _mtpk.require_device(*fields)
+    if not all(f.is_contiguous() for f in fields):
+        raise ValueError("round fill needs contiguous buffers and model tables")
+    rows, t = buf.token_matrix.shape
+    lanes, max_blocks = table.shape
+    if (table.dtype != torch.int32 or buf.block_table.shape != (rows, max_blocks)
+            or hidden.dtype != buf.draft_hidden.dtype or hidden.shape[1:] != buf.draft_hidden.shape[1:]
+            or hidden.shape[0] != lanes):
+        raise ValueError("model tables do not match the round buffers")
+    n_stops = buf.stops.shape[1]
+    if buf.staging.shape != (rows, STAGE_IDS + max(t - 1, 1) + n_stops):
+        raise ValueError(f"staging must be [{rows}, {STAGE_IDS + max(t - 1, 1) + n_stops}]")
+    _mtpk.check(
+        _mtpk.lib().mtpk_round_fill(
+            buf.staging.data_ptr(), rows, t, n_stops, table.data_ptr(), lanes, max_blocks,
+            model.cfg.block_size, RESERVED_BLOCK, hidden.data_ptr(),
+            hidden[0].numel() * hidden.element_size(), buf.token_matrix.data_ptr(),
+            buf.pos.data_ptr(), buf.budget.data_ptr(), buf.slot_rows.data_ptr(),
+            buf.forced_n.data_ptr(), buf.active.data_ptr(), buf.forced_ids.data_ptr(),
+            buf.stops.data_ptr(), buf.block_table.data_ptr(), buf.block_valid.data_ptr(),
+            buf.write_rows.data_ptr(), buf.draft_hidden.data_ptr(), _mtpk.stream_of(device),
+        ),
+        "mtpk_round_fill",
+    )
 
 
 def _fill(model, mtp, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stops, forced) -> None:
@@ -518,10 +553,6 @@ class EagerBackend:
         return fn
 
 
-_FILLED = ("token_matrix", "pos", "budget", "slot_rows", "forced_n", "active", "forced_ids", "stops",
-           "block_table", "block_valid", "write_rows", "draft_hidden")
-"""The fields a fill writes (validation compares the captured fill's with the eager one's)."""
-
 REQUIRE_GRAPH_ENV = "SEED_MTP_REQUIRE_GRAPH"
 """`=1`: a bucket that fails capture or validation raises instead of serving eager rounds
 (`graph_mtp.py:112-116`)."""
@@ -545,7 +576,6 @@ class GraphMTPRunner(MTPVerifyRunner):
         super().__init__(model, None, capacity, buckets)
         self.backend = CudaGraphBackend() if backend is None else backend
         self.graphs: dict[int, Callable[[], None]] = {}
-        self.unpacks: dict[int, Callable[[], None]] = {}  # each bucket's `_unpack`, captured
         self.enabled = True
         self.validated: dict[int, bool] = {}
         self.eager_rounds = 0
@@ -555,21 +585,9 @@ class GraphMTPRunner(MTPVerifyRunner):
         return True
 
     def _capture(self, buf: MTPVerifyBuffers) -> Callable[[], None]:
-        """The bucket's round as one graph; its fill's device half (`_unpack`) is captured
-        beside it, so a round's fill is one copy and one replay instead of about twenty
-        launches from the host."""
-        self.unpacks[buf.capacity] = self.backend.capture(lambda: _unpack(self.model, buf),
-                                                          buf.pos.device)
+        """The bucket's round (draft + verify + accept + commit) as one graph. The fill stays
+        outside it: one staging copy and one `mtpk_round_fill` launch."""
         return self.backend.capture(lambda: self._round(buf), buf.pos.device)
-
-    def fill(self, buf: MTPVerifyBuffers, slots, tokens, positions, budgets=None, stops=None,
-             forced=None) -> None:
-        unpack = self.unpacks.get(buf.capacity) if self.enabled else None
-        if unpack is None:
-            _fill(self.model, self.mtp, buf, slots, tokens, positions, budgets, stops, forced)
-            return
-        _stage(self.model, buf, slots, tokens, positions, budgets, stops, forced)
-        unpack()
 
     def _eager_round(self, buf: MTPVerifyBuffers) -> None:
         """The bucket's round run eagerly before its capture, on a side stream on a device (so
@@ -605,8 +623,7 @@ class GraphMTPRunner(MTPVerifyRunner):
         model.hidden_cache.copy_((grid.reshape(model.hidden_cache.shape) * 0.37).sin().to(model.hidden_cache.dtype))
         before = [{k: v.clone() for k, v in p.items() if k in ("conv", "rec")} for p in model.pool]
         seed = model.hidden_cache.clone()
-        _fill(model, self.mtp, buf, slots, tokens, positions, budgets, stops, None)
-        filled = [getattr(buf, name).clone() for name in _FILLED]
+        self.fill(buf, slots, tokens, positions, budgets, stops)
         self._round(buf)
         want = _committed(buf, bucket)
         want_state = ([{k: v.clone() for k, v in p.items() if k in ("conv", "rec")} for p in model.pool],
@@ -615,11 +632,10 @@ class GraphMTPRunner(MTPVerifyRunner):
             for k, v in snap.items():
                 p[k].copy_(v)
         model.hidden_cache.copy_(seed)
-        self.fill(buf, slots, tokens, positions, budgets, stops)  # the captured unpack, if any
-        ok = all(torch.equal(getattr(buf, name), v) for name, v in zip(_FILLED, filled, strict=True))
+        self.fill(buf, slots, tokens, positions, budgets, stops)
         replay()
         got = _committed(buf, bucket)
-        ok = ok and got == want and torch.equal(model.hidden_cache, want_state[1])
+        ok = got == want and torch.equal(model.hidden_cache, want_state[1])
         for p, snap in zip(model.pool, want_state[0], strict=True):
             for k, v in snap.items():
                 ok = ok and torch.equal(p[k], v)
@@ -634,7 +650,7 @@ class GraphMTPRunner(MTPVerifyRunner):
         model = self.model
         if any(model.blocks.host[lane] for lane in range(model.lanes)):
             raise RuntimeError("prepare() is boot-only: some lanes hold KV blocks")
-        self.graphs, self.validated, self.unpacks = {}, {}, {}
+        self.graphs, self.validated = {}, {}
         ok = True
         try:
             for bucket in self.buckets:

@@ -445,3 +445,71 @@ def test_config5_bucket48_serves_45_lanes(dev) -> None:
     for j in lanes:
         for x, y in zip(after[j], mh.slot_state(model, j, pos[j] + len(got[j])), strict=True):
             assert torch.equal(x, y), j
+
+
+def _fill_model(dev, lanes, max_blocks, block_size, hidden, dtype, seed):
+    """The model fields a round fill reads: config sizes, every lane's block table, seeds."""
+    from types import SimpleNamespace as NS
+
+    g = torch.Generator().manual_seed(seed)
+    table = torch.randint(1, 1000, (lanes, max_blocks), generator=g, dtype=torch.int32)
+    seeds = torch.randn(lanes, hidden, generator=g).to(dtype)
+    return NS(cfg=NS(hidden=hidden, conv_k=4, block_size=block_size), dtype=dtype,
+              blocks=NS(max_blocks=max_blocks, table=table.to(dev)), hidden_cache=seeds.to(dev))
+
+
+@pytest.mark.parametrize("dtype,hidden", [(torch.bfloat16, 4096), (torch.float32, 36), (torch.float32, 5)])
+def test_round_fill_matches_the_tensor_fill(dev, dtype, hidden) -> None:
+    """`mtpk_round_fill` (the device fill) writes every field the tensor-op fill writes, bit for
+    bit, from the same staging rows: forced rows, stop ids, padding rows (reserved block, idle
+    slot), positions on and across block boundaries; seeds in bf16 (16-byte copies) and f32
+    rows of 144 and 20 bytes (the byte-copy path)."""
+    lanes, max_blocks, bs, t, cap = 11, 7, 16, 4, 9
+    dm = _fill_model(dev, lanes, max_blocks, bs, hidden, dtype, 5)
+    cm = _fill_model("cpu", lanes, max_blocks, bs, hidden, dtype, 5)
+    db = graph_mtp.MTPVerifyBuffers(dm, cap, t, torch.device(dev))
+    cb = graph_mtp.MTPVerifyBuffers(cm, cap, t, torch.device("cpu"))
+    g = torch.Generator().manual_seed(9)
+    for trial in range(3):
+        st = torch.zeros_like(cb.staging)
+        st[:, graph_mtp.STAGE_TOKEN] = torch.randint(0, 248320, (cap,), generator=g)
+        st[:, graph_mtp.STAGE_POS] = torch.tensor([0, 15, 16, 17, 31, 47, 60, max_blocks * bs - t, 3])
+        st[:, graph_mtp.STAGE_BUDGET] = torch.randint(1, 9, (cap,), generator=g)
+        st[:, graph_mtp.STAGE_SLOT] = torch.randperm(lanes, generator=g)[:cap]
+        st[:, graph_mtp.STAGE_FORCED] = torch.randint(0, t, (cap,), generator=g)
+        st[:, graph_mtp.STAGE_ACTIVE] = (torch.arange(cap) + trial) % 4 != 0
+        st[:, graph_mtp.STAGE_IDS:] = torch.randint(-1, 248320, (cap, st.shape[1] - graph_mtp.STAGE_IDS),
+                                                   generator=g)
+        for buf, junk in ((cb, 7), (db, -3)):  # stale values the fill must overwrite
+            for name in ("token_matrix", "pos", "write_rows", "block_table", "draft_hidden"):
+                getattr(buf, name).fill_(junk)
+        cb.staging.copy_(st)
+        db.staging.copy_(st)
+        graph_mtp._unpack(cm, cb)
+        graph_mtp._unpack(dm, db)
+        torch.cuda.synchronize()
+        for name in ("token_matrix", "pos", "budget", "slot_rows", "forced_n", "active", "forced_ids",
+                     "stops", "block_table", "block_valid", "write_rows", "draft_hidden"):
+            want, got = getattr(cb, name), getattr(db, name).cpu()
+            assert got.dtype == want.dtype and torch.equal(got, want), (trial, name)
+
+
+def test_round_fill_marks_positions_outside_the_table(dev) -> None:
+    """A staged position whose block lies past the table's last column (the host grows every
+    lane's table first, so only a direct caller can stage one) gets write row -1 there, the
+    in-table positions their rows, and nothing is read out of bounds."""
+    lanes, max_blocks, bs, t, cap = 3, 2, 16, 4, 2
+    dm = _fill_model(dev, lanes, max_blocks, bs, 8, torch.bfloat16, 1)
+    db = graph_mtp.MTPVerifyBuffers(dm, cap, t, torch.device(dev))
+    st = torch.zeros_like(db.staging)
+    st[:, graph_mtp.STAGE_POS] = torch.tensor([max_blocks * bs - 2, 5])
+    st[:, graph_mtp.STAGE_SLOT] = torch.tensor([2, 0])
+    st[:, graph_mtp.STAGE_ACTIVE] = 1
+    db.staging.copy_(st)
+    graph_mtp._unpack(dm, db)
+    table = dm.blocks.table.cpu().long()
+    want = [[table[2, 1] * bs + 14, table[2, 1] * bs + 15, -1, -1],
+            [table[0, 0] * bs + 5 + s for s in range(t)]]
+    assert db.write_rows.cpu().tolist() == [[int(x) for x in row] for row in want]
+    assert db.block_valid.cpu().tolist() == [3, 1]
+

@@ -167,33 +167,3 @@ def test_grow_many_equals_grow_per_lane():
     with pytest.raises(ValueError, match="exceed"):
         b.grow_many([1, 2], [20, 97])
     assert torch.equal(b.table, before[0]) and b.host == before[1] and b._free == before[2]
-
-
-class _BadFill(graph_mtp.GraphMTPRunner):
-    """A captured fill that writes one field wrong (a stale budget), standing in for a captured
-    unpack that froze a value."""
-
-    def _capture(self, buf):
-        replay = super()._capture(buf)
-        good = self.unpacks[buf.capacity]
-
-        def unpack():
-            good()
-            buf.budget.add_(1)
-
-        self.unpacks[buf.capacity] = unpack
-        return replay
-
-
-def test_prepare_checks_the_captured_fill():
-    """`prepare()` compares the fields the captured fill writes with the eager fill's: a wrong
-    one disables the captured round, and rounds then fill and run eagerly."""
-    model, _, _ = _prefilled(4, 0)
-    runner = _BadFill(model, graph_mtp.EagerBackend(), capacity=4)
-    assert runner.prepare() is False and not runner.enabled
-    ids = mh.prompts(2)
-    twin, toks, pos = _prefilled(4, 2)
-    for lane, p in enumerate(ids):
-        model.prefill(lane, p)
-    eager = graph_mtp.MTPVerifyRunner(twin, capacity=4)
-    assert runner.speculative_decode([0, 1], toks, pos) == eager.speculative_decode([0, 1], toks, pos)
