@@ -39,7 +39,7 @@ const char* mtpk_status_string(int status);
 
 /* ABI revision of this header; bumped on any signature change. The library returns the value
  * it was built with, and the Python binding refuses a library whose value differs. */
-#define MTPK_ABI_VERSION 2
+#define MTPK_ABI_VERSION 3
 int mtpk_abi_version(void);
 
 /* ---------------------------------------------------------------- MXFP4 dequant
@@ -335,14 +335,25 @@ int mtpk_greedy_accept_keys(const uint64_t* keys, int64_t chunks, int64_t* step_
  * others; block_valid i32 [rows] = floor((pos + t + block_size - 1) / block_size); write_rows
  * i64 [rows, t] = block_table[j][q / block_size] * block_size + q mod block_size at
  * q = pos + s (floor division; -1 where q / block_size falls outside the table);
- * draft_hidden [rows, row_bytes] = hidden_cache[slot] (zeros for a slot outside [0, lanes)). */
+ * draft_hidden [rows, row_bytes] = hidden_cache[slot] (zeros for a slot outside [0, lanes));
+ * pos_grid i64 [rows, t] and pos_steps i64 [t, rows] = pos + s; commit_slots i64 [rows] = slot
+ * on active rows, -1 on the others. */
 int mtpk_round_fill(const int64_t* staging, int64_t rows, int64_t t, int64_t n_stops,
                     const int32_t* lane_tables, int64_t lanes, int64_t max_blocks,
                     int64_t block_size, int32_t reserved_block, const void* hidden_cache,
                     int64_t row_bytes, int64_t* token_matrix, int64_t* pos, int64_t* budget,
                     int64_t* slot_rows, int64_t* forced_n, uint8_t* active, int64_t* forced_ids,
                     int64_t* stops, int32_t* block_table, int32_t* block_valid,
-                    int64_t* write_rows, void* draft_hidden, void* stream);
+                    int64_t* write_rows, void* draft_hidden, int64_t* pos_grid,
+                    int64_t* pos_steps, int64_t* commit_slots, void* stream);
+
+/* The token a draft step feeds forward (`draft_round_step`'s forced override and column write,
+ * graph_mtp.py:477-504): out[j * out_stride] = forced[j * forced_stride] when forced_n[j] > step,
+ * else tok[j * tok_stride], for j < rows (out: the token matrix's column step + 1; forced: the
+ * forced ids' column step). */
+int mtpk_draft_feed(const int64_t* tok, int64_t tok_stride, const int64_t* forced_n,
+                    const int64_t* forced, int64_t forced_stride, int64_t step, int64_t* out,
+                    int64_t out_stride, int64_t rows, void* stream);
 
 /* ---------------------------------------------------------------- rejection sampling
  * Sampling-mode acceptance for an MTP round at temperature T > 0. The reference engine has no
@@ -453,14 +464,21 @@ int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, i
  * x contiguous): x is replaced by x + res in x's dtype, which is also written to sum_out.
  * rope_cos/rope_sin (optional, f32 [positions, rot_dim]) with rope_pos (i64 [tokens]):
  * rotate-half RoPE on the first rot_dim channels of y rounded to the output dtype (dim <= 512;
- * rot_dim a multiple of 16, or 2, 4 or 8). out: contiguous [rows, dim]. dim a multiple of 8, <= 8192;
- * bf16 strides multiples of 8 and pointers 16-byte aligned. */
+ * rot_dim a multiple of 16, or 2, 4 or 8). gather (optional, i64): output token r reads input
+ * token gather[r * gather_stride] of the gather_rows tokens x holds (an embedding lookup by
+ * token id, fused; an id outside [0, gather_rows) reads the nearest row). out: token r's
+ * heads_per_token rows of dim at r * out_token_stride (0: packed, heads_per_token * dim), so two
+ * calls can fill the halves of one concatenated row; the residual form takes no gather and a
+ * packed out. dim a multiple of 8, <= 8192; bf16 strides multiples of 8 and pointers 16-byte
+ * aligned. */
 int mtpk_rownorm(const void* x, int x_dtype, int64_t x_token_stride, int64_t x_head_stride,
                  const void* res, int res_dtype, void* sum_out, const void* w, int w_dtype,
                  int kind, float eps, float scale, const void* gate, int gate_dtype,
                  int64_t gate_token_stride, int64_t gate_head_stride, const float* rope_cos,
                  const float* rope_sin, const int64_t* rope_pos, int rot_dim, void* out,
-                 int out_dtype, int64_t rows, int heads_per_token, int dim, void* stream);
+                 int out_dtype, int64_t rows, int heads_per_token, int dim, const int64_t* gather,
+                 int64_t gather_stride, int64_t gather_rows, int64_t out_token_stride,
+                 void* stream);
 
 /* ---------------------------------------------------------------- paged verify attention
  * Causal GQA attention of t query rows per lane over a paged bf16 KV cache, replacing
@@ -507,11 +525,13 @@ int mtpk_paged_attention_gated(const uint16_t* q, const int64_t* q_strides, cons
  * v_row_stride (elements, row = b * t + s), position base_pos[b] + s, pool row
  * block_table[b][pos / 16] * 16 + pos % 16 of k_pool [pool_rows, kv_heads, head_dim] and of
  * v_pool [pool_rows / 16, kv_heads, head_dim, 16] (the layout mtpk_paged_attention reads).
- * keep (optional, u8 [batch * t]): rows with 0 are not written. head_dim a multiple of 8. */
+ * keep (optional, u8 [batch, t] at element strides keep_b, keep_s; a 0 stride broadcasts, as a
+ * per-lane mask does): rows with 0 are not written. head_dim a multiple of 8. */
 int mtpk_kv_write(const uint16_t* k, int64_t k_row_stride, const uint16_t* v, int64_t v_row_stride,
                   uint16_t* k_pool, uint16_t* v_pool, int64_t pool_rows, const int32_t* block_table,
-                  int64_t table_stride, const int64_t* base_pos, const uint8_t* keep, int64_t batch,
-                  int64_t t, int64_t kv_heads, int64_t head_dim, void* stream);
+                  int64_t table_stride, const int64_t* base_pos, const uint8_t* keep, int64_t keep_b,
+                  int64_t keep_s, int64_t batch, int64_t t, int64_t kv_heads, int64_t head_dim,
+                  void* stream);
 
 /* Streaming-read probe (no reference counterpart: a measurement of the HBM read ceiling the MoE
  * weight streams are compared with). Reads bytes [0, bytes) of `base` with 16-byte loads,

@@ -20,7 +20,7 @@ LIB_PATH = Path(os.environ.get("MTPK_LIB", str(HERE / "libmtpk.so")))
 F32, BF16, I32, I64, U8 = 0, 1, 2, 3, 4
 EINVAL, ENODEV, ETOOBIG = -1, -2, -3
 MOE_STATIC_SCRATCH = 64 << 20
-ABI_VERSION = 2
+ABI_VERSION = 3
 MAX_TOP_K = 32
 MAX_EXPERTS = 4096
 MAX_ROUTER_EXPERTS = 1024
@@ -109,7 +109,7 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
     "mtpk_kv_write": (
         c_int,
         [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p, c_int64,
-         c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_void_p],
+         c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p],
     ),
     "mtpk_deltanet_prep": (
         c_int,
@@ -138,7 +138,8 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         c_int,
         [c_void_p, c_int, c_int64, c_int64, c_void_p, c_int, c_void_p, c_void_p, c_int, c_int,
          ctypes.c_float, ctypes.c_float, c_void_p, c_int, c_int64, c_int64, c_void_p, c_void_p,
-         c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int, c_void_p],
+         c_void_p, c_int, c_void_p, c_int, c_int64, c_int, c_int, c_void_p, c_int64, c_int64,
+         c_int64, c_void_p],
     ),
     "mtpk_route_topk": (
         c_int,
@@ -164,7 +165,11 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int, c_void_p,
          c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
-         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "mtpk_draft_feed": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p],
     ),
     "mtpk_argmax_keys": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "mtpk_rejection_workspace_bytes": (c_int64, [c_int64, c_int, c_int64]),

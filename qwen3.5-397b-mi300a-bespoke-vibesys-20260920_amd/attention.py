@@ -165,12 +165,16 @@ def kv_write(k_pool: torch.Tensor, v_pool: torch.Tensor, k: torch.Tensor, v: tor
         raise ValueError("pools do not match the rows' kv_heads / head_dim")
     table = block_table.to(torch.int32).contiguous()
     pos = base_pos.to(torch.int64).contiguous()
-    kp = None
+    kp, kb, ks = None, 0, 0
     if keep is not None:
-        kp = keep.reshape(-1).to(torch.uint8).contiguous()
-        if kp.numel() != b * t:
+        if keep.numel() != b * t:
             raise ValueError("keep must have B * t entries")
+        # read in place through its strides (a per-lane mask broadcast over t has stride 0);
+        # a bool tensor's bytes are its 0 / 1 values
+        kp = keep.to(device).reshape(b, t)
+        kp = kp.view(torch.uint8) if kp.dtype == torch.bool else kp.to(torch.uint8)
+        kb, ks = kp.stride()
     _mtpk.check(_mtpk.lib().mtpk_kv_write(
         k.data_ptr(), _mtpk.row_stride(k), v.data_ptr(), _mtpk.row_stride(v), k_pool.data_ptr(), v_pool.data_ptr(),
-        k_pool.shape[0], table.data_ptr(), table.shape[1], pos.data_ptr(), _mtpk.ptr(kp), b, t, kvh,
-        hd, _mtpk.stream_of(device)), "mtpk_kv_write")  # fmt: skip
+        k_pool.shape[0], table.data_ptr(), table.shape[1], pos.data_ptr(), _mtpk.ptr(kp), kb, ks, b, t,
+        kvh, hd, _mtpk.stream_of(device)), "mtpk_kv_write")  # fmt: skip

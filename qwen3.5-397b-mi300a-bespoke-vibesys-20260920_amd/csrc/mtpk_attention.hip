@@ -384,8 +384,8 @@ int launch_attention(const AttnIO& io, const uint16_t* k_pool, const uint16_t* v
 // This round's K and V rows into the paged caches (the cache writes of `attn_verify`,
 // model.py:3519-3577, and `graph_mtp.py:857-860`): row (b, s) at position base_pos[b] + s goes to
 // pool row table[b][pos / 16] * 16 + pos % 16, K as a [kv_heads, HD] row, V into channel d,
-// slot pos % 16 of its block's transposed [kv_heads, HD, 16] slab. keep (optional, [B * t])
-// leaves rows with keep == 0 untouched. A thread moves 8 channels of one (row, kv head); a
+// slot pos % 16 of its block's transposed [kv_heads, HD, 16] slab. keep (optional, [B, t] at
+// element strides keep_b, keep_s) leaves rows with keep == 0 untouched. A thread moves 8 channels of one (row, kv head); a
 // position outside the table or a block outside the pool is not written.
 __global__ __launch_bounds__(256) void k_kv_write(const uint16_t* __restrict__ k, int64_t k_row,
                                                   const uint16_t* __restrict__ v, int64_t v_row,
@@ -393,8 +393,8 @@ __global__ __launch_bounds__(256) void k_kv_write(const uint16_t* __restrict__ k
                                                   uint16_t* __restrict__ v_pool, int64_t pool_rows,
                                                   const int32_t* __restrict__ table, int table_stride,
                                                   const int64_t* __restrict__ base_pos,
-                                                  const uint8_t* __restrict__ keep, int B, int t,
-                                                  int kvh, int hd) {
+                                                  const uint8_t* __restrict__ keep, int64_t keep_b,
+                                                  int64_t keep_s, int B, int t, int kvh, int hd) {
   const int pieces = hd / 8;
   const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
   if (i >= (int64_t)B * t * kvh * pieces) return;
@@ -402,8 +402,8 @@ __global__ __launch_bounds__(256) void k_kv_write(const uint16_t* __restrict__ k
   const int64_t rh = i / pieces;  // (row, kv head)
   const int h = (int)(rh % kvh);
   const int64_t row = rh / kvh;
-  if (keep && !keep[row]) return;
   const int b = (int)(row / t), s = (int)(row - (int64_t)b * t);
+  if (keep && !keep[b * keep_b + s * keep_s]) return;
   const int64_t pos = base_pos[b] + s;
   if (pos < 0 || pos / kAttnBlock >= table_stride) return;
   const int64_t blk = table[(int64_t)b * table_stride + pos / kAttnBlock];
@@ -514,8 +514,9 @@ int mtpk_paged_attention_gated(const uint16_t* q, const int64_t* q_strides, cons
 
 int mtpk_kv_write(const uint16_t* k, int64_t k_row_stride, const uint16_t* v, int64_t v_row_stride,
                   uint16_t* k_pool, uint16_t* v_pool, int64_t pool_rows, const int32_t* block_table,
-                  int64_t table_stride, const int64_t* base_pos, const uint8_t* keep, int64_t batch,
-                  int64_t t, int64_t kv_heads, int64_t head_dim, void* stream) {
+                  int64_t table_stride, const int64_t* base_pos, const uint8_t* keep, int64_t keep_b,
+                  int64_t keep_s, int64_t batch, int64_t t, int64_t kv_heads, int64_t head_dim,
+                  void* stream) {
   if (!k || !v || !k_pool || !v_pool || !block_table || !base_pos) return MTPK_EINVAL;
   if (batch < 0 || t <= 0 || kv_heads <= 0 || head_dim <= 0 || head_dim % 8) return MTPK_EINVAL;
   if (k_row_stride < kv_heads * head_dim || v_row_stride < kv_heads * head_dim ||
@@ -525,12 +526,13 @@ int mtpk_kv_write(const uint16_t* k, int64_t k_row_stride, const uint16_t* v, in
     return MTPK_EINVAL;
   if (table_stride <= 0 || table_stride > INT32_MAX || batch * t * kv_heads * head_dim > INT32_MAX)
     return MTPK_EINVAL;
+  if (keep && (keep_b < 0 || keep_s < 0)) return MTPK_EINVAL;
   if (batch == 0) return 0;
   const int64_t n = batch * t * kv_heads * (head_dim / 8);
   hipLaunchKernelGGL(k_kv_write, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, (hipStream_t)stream,
                      k, k_row_stride, v, v_row_stride, k_pool, v_pool, pool_rows, block_table,
-                     (int)table_stride, base_pos, keep, (int)batch, (int)t, (int)kv_heads,
-                     (int)head_dim);
+                     (int)table_stride, base_pos, keep, keep_b, keep_s, (int)batch, (int)t,
+                     (int)kv_heads, (int)head_dim);
   return status_of(hipGetLastError());
 }
 

@@ -7,7 +7,10 @@
 // out, as `x = x + mixer` then `rmsnorm(x)`) and rotate-half RoPE behind (on the first rot_dim channels
 // of the bf16-rounded result, model.py:631-635). Row r is head r % heads_per_token of token
 // r / heads_per_token, read at token * token_stride + head * head_stride, so head slices of a
-// projection output are read in place. fp32 arithmetic throughout.
+// projection output are read in place; with a gather table, token r reads input token
+// gather[r * gather_stride] (an embedding row by token id). Output token r is written at
+// r * out_token_stride + head * dim (two norms can fill the halves of one concatenated row).
+// fp32 arithmetic throughout.
 //
 // Layout of the work (rows of a multiple of 2048 elements without RoPE: k_rownorm_row, one row
 // per workgroup): a row of `dim` elements is split over G = min(64, dim / 8) lanes, each
@@ -43,7 +46,18 @@ struct NormArgs {
   int o_dt;
   int64_t rows;
   int hpt, dim;
+  const int64_t* gather;  // input token of output token r: gather[r * gather_stride] (or r)
+  int64_t gather_stride, gather_rows;
+  int64_t o_ts;  // output token stride (elements)
 };
+
+// the input token read for output token `tok` (a gathered id outside the table reads its
+// nearest row: the callers check ids on the host, this keeps every read in bounds)
+__device__ inline int64_t norm_src_token(const NormArgs& a, int64_t tok) {
+  if (!a.gather) return tok;
+  const int64_t g = a.gather[tok * a.gather_stride];
+  return g < 0 ? 0 : (g >= a.gather_rows ? a.gather_rows - 1 : g);
+}
 
 __device__ inline void load8(const void* p, int dt, int64_t i, float* v) {
   if (dt == MTPK_F32) {
@@ -86,8 +100,8 @@ __global__ __launch_bounds__(256) void k_rownorm(NormArgs a) {
   const int64_t r = ok ? row : 0;
   const int64_t tok = r / a.hpt, head = r - tok * a.hpt;
   const int nch = a.dim / 8 / G;  // chunks per lane (a.dim is a multiple of 8 G)
-  const int64_t xo = tok * a.x_ts + head * a.x_hs;
-  const int64_t oo = r * a.dim;
+  const int64_t xo = norm_src_token(a, tok) * a.x_ts + head * a.x_hs;
+  const int64_t oo = tok * a.o_ts + head * a.dim;
   float v[kNormMaxChunks][8];
   float ss = 0.f;
 #pragma unroll
@@ -191,7 +205,8 @@ __global__ __launch_bounds__(256) void k_rownorm_row(NormArgs a) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wave = tid / kWave;
   const int64_t r = blockIdx.x;
   const int64_t tok = r / a.hpt, head = r - tok * a.hpt;
-  const int64_t xo = tok * a.x_ts + head * a.x_hs, oo = r * a.dim, go = tok * a.g_ts + head * a.g_hs;
+  const int64_t xo = norm_src_token(a, tok) * a.x_ts + head * a.x_hs, oo = tok * a.o_ts + head * a.dim;
+  const int64_t go = tok * a.g_ts + head * a.g_hs;
   float v[NCH][8], wv[NCH][8], gv[NCH][8];
 #pragma unroll
   for (int i = 0; i < NCH; ++i) {
@@ -248,13 +263,20 @@ int mtpk_rownorm(const void* x, int x_dtype, int64_t x_token_stride, int64_t x_h
                  int kind, float eps, float scale, const void* gate, int gate_dtype,
                  int64_t gate_token_stride, int64_t gate_head_stride, const float* rope_cos,
                  const float* rope_sin, const int64_t* rope_pos, int rot_dim, void* out,
-                 int out_dtype, int64_t rows, int heads_per_token, int dim, void* stream) {
+                 int out_dtype, int64_t rows, int heads_per_token, int dim, const int64_t* gather,
+                 int64_t gather_stride, int64_t gather_rows, int64_t out_token_stride,
+                 void* stream) {
   auto fdt = [](int d) { return d == MTPK_F32 || d == MTPK_BF16; };
   if (!x || !out || !fdt(x_dtype) || !fdt(out_dtype)) return MTPK_EINVAL;
   if (kind < 0 || kind > 2 || rows < 0 || heads_per_token < 1 || dim < 8 || dim % 8) return MTPK_EINVAL;
   if (kind != 2 && (!w || !fdt(w_dtype))) return MTPK_EINVAL;
   if (gate && (kind != 1 || !fdt(gate_dtype))) return MTPK_EINVAL;
   if (res && (!sum_out || !fdt(res_dtype) || heads_per_token != 1 || x_token_stride != dim))
+    return MTPK_EINVAL;
+  // 0: outputs packed, token stride heads_per_token * dim; the residual form is packed throughout
+  if (out_token_stride == 0) out_token_stride = (int64_t)heads_per_token * dim;
+  if (out_token_stride < (int64_t)heads_per_token * dim || out_token_stride % 8 ||
+      (res && (gather || out_token_stride != dim)) || (gather && gather_rows < 1))
     return MTPK_EINVAL;
   const int g = dim / 8 >= 64 ? 64 : dim / 8;
   if (g & (g - 1)) return MTPK_EINVAL;  // G a power of two
@@ -278,7 +300,8 @@ int mtpk_rownorm(const void* x, int x_dtype, int64_t x_token_stride, int64_t x_h
   NormArgs a{x,        x_dtype,  x_token_stride, x_head_stride, res,   res_dtype,  sum_out,
              w,        w_dtype,  kind,           eps,           scale, gate,       gate_dtype,
              gate_token_stride, gate_head_stride, rope_cos,     rope_sin, rope_pos, rot_dim,
-             out,      out_dtype, rows,          heads_per_token, dim};
+             out,      out_dtype, rows,          heads_per_token, dim,
+             gather,   gather_stride, gather_rows, out_token_stride};
   const hipStream_t st = (hipStream_t)stream;
   if (!rope_cos && dim % 2048 == 0 && dim <= 8192) {  // one row per workgroup
     if (rows > INT32_MAX) return MTPK_EINVAL;

@@ -4,8 +4,16 @@
 // one transfer; this kernel unpacks it into the captured round's static buffers and derives the
 // fields the fill computes on the device (the round's block tables, block counts, KV write rows
 // and the draft seed), which the reference writes with a copy per field and a chain of small
-// tensor ops (`MTPVerifyRunner.fill`, graph_mtp.py:795-874). One workgroup per buffer row; the
-// only sizeable traffic is the seed row (hidden * 2 bytes in bf16), copied with 16-byte loads.
+// tensor ops (`MTPVerifyRunner.fill`, graph_mtp.py:795-874), plus three index tables the
+// round's steps would otherwise build with small launches of their own: every row's t
+// positions (row major, for the verify rows, and step major, one contiguous row per draft step)
+// and the commit's slot per row (-1 on padding rows, which the commit kernels skip). One
+// workgroup per buffer row; the only sizeable traffic is the seed row (hidden * 2 bytes in
+// bf16), copied with 16-byte loads.
+//
+// Draft feed: after each draft step, one launch puts the token the next step feeds into the
+// token matrix (the forced id while the row has forced drafts left, else the step's greedy
+// token), in place of a compare, a select and a column copy.
 
 #include "mtpk_device.h"
 #include "mtpk_host.h"
@@ -35,6 +43,8 @@ struct RoundFillArgs {
   int32_t *block_table, *block_valid;
   int64_t* write_rows;
   uint8_t* draft_hidden;
+  int64_t *pos_grid, *pos_steps, *commit_slots;  // [rows, t], [t, rows], [rows]
+  int64_t rows;
 };
 
 // Python's floor division and remainder (the fill's `//` and `%` on int64 tensors)
@@ -62,6 +72,7 @@ __global__ __launch_bounds__(kFillThreads) void k_round_fill(RoundFillArgs a) {
     a.forced_n[j] = st[kStageForced];
     a.active[j] = act ? 1 : 0;
     a.block_valid[j] = (int32_t)floor_div(p + a.t + a.block_size - 1, a.block_size);
+    a.commit_slots[j] = act ? slot : -1;
   }
   for (int c = tid; c < a.t; c += kFillThreads) {
     a.token_matrix[j * a.t + c] = c == 0 ? st[kStageToken] : 0;
@@ -75,6 +86,8 @@ __global__ __launch_bounds__(kFillThreads) void k_round_fill(RoundFillArgs a) {
       row = blk * a.block_size + (g - col * a.block_size);
     }
     a.write_rows[j * a.t + c] = row;
+    a.pos_grid[j * a.t + c] = g;
+    a.pos_steps[c * a.rows + j] = g;
   }
   for (int c = tid; c < a.width; c += kFillThreads) a.forced_ids[j * a.width + c] = st[kStageIds + c];
   for (int c = tid; c < a.n_stops; c += kFillThreads)
@@ -91,6 +104,17 @@ __global__ __launch_bounds__(kFillThreads) void k_round_fill(RoundFillArgs a) {
   }
 }
 
+__global__ __launch_bounds__(256) void k_draft_feed(const int64_t* __restrict__ tok, int64_t tok_stride,
+                                                   const int64_t* __restrict__ forced_n,
+                                                   const int64_t* __restrict__ forced,
+                                                   int64_t forced_stride, int64_t step,
+                                                   int64_t* __restrict__ out, int64_t out_stride,
+                                                   int64_t rows) {
+  const int64_t j = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (j >= rows) return;
+  out[j * out_stride] = forced_n[j] > step ? forced[j * forced_stride] : tok[j * tok_stride];
+}
+
 }  // namespace mtpk
 
 using namespace mtpk;
@@ -103,14 +127,16 @@ int mtpk_round_fill(const int64_t* staging, int64_t rows, int64_t t, int64_t n_s
                     int64_t row_bytes, int64_t* token_matrix, int64_t* pos, int64_t* budget,
                     int64_t* slot_rows, int64_t* forced_n, uint8_t* active, int64_t* forced_ids,
                     int64_t* stops, int32_t* block_table, int32_t* block_valid,
-                    int64_t* write_rows, void* draft_hidden, void* stream) {
+                    int64_t* write_rows, void* draft_hidden, int64_t* pos_grid,
+                    int64_t* pos_steps, int64_t* commit_slots, void* stream) {
   if (rows < 0 || rows > INT32_MAX || t < 1 || t > 4096 || n_stops < 0 || n_stops > 4096)
     return MTPK_EINVAL;
   if (lanes < 1 || max_blocks < 1 || max_blocks > INT32_MAX || block_size < 1 || row_bytes < 0)
     return MTPK_EINVAL;
   if (!staging || !lane_tables || !token_matrix || !pos || !budget || !slot_rows || !forced_n ||
       !active || !forced_ids || (n_stops > 0 && !stops) || !block_table || !block_valid ||
-      !write_rows || (row_bytes > 0 && (!hidden_cache || !draft_hidden)))
+      !write_rows || (row_bytes > 0 && (!hidden_cache || !draft_hidden)) || !pos_grid ||
+      !pos_steps || !commit_slots)
     return MTPK_EINVAL;
   if (rows == 0) return 0;
   RoundFillArgs a{};
@@ -139,7 +165,23 @@ int mtpk_round_fill(const int64_t* staging, int64_t rows, int64_t t, int64_t n_s
   a.block_valid = block_valid;
   a.write_rows = write_rows;
   a.draft_hidden = static_cast<uint8_t*>(draft_hidden);
+  a.pos_grid = pos_grid;
+  a.pos_steps = pos_steps;
+  a.commit_slots = commit_slots;
+  a.rows = rows;
   hipLaunchKernelGGL(k_round_fill, dim3((unsigned)rows), dim3(kFillThreads), 0, (hipStream_t)stream, a);
+  return status_of(hipGetLastError());
+}
+
+int mtpk_draft_feed(const int64_t* tok, int64_t tok_stride, const int64_t* forced_n,
+                    const int64_t* forced, int64_t forced_stride, int64_t step, int64_t* out,
+                    int64_t out_stride, int64_t rows, void* stream) {
+  if (rows < 0 || !tok || !forced_n || !forced || !out || step < 0) return MTPK_EINVAL;
+  if (rows == 0) return 0;
+  if ((rows + 255) / 256 > INT32_MAX) return MTPK_EINVAL;
+  hipLaunchKernelGGL(k_draft_feed, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
+                     (hipStream_t)stream, tok, tok_stride, forced_n, forced, forced_stride, step,
+                     out, out_stride, rows);
   return status_of(hipGetLastError());
 }
 

@@ -95,6 +95,11 @@ class MTPVerifyBuffers:
         # unconditionally (zero on every other row)
         self.forced_n = torch.zeros(capacity, **long)
         self.forced_ids = torch.zeros(capacity, max(t - 1, 1), **long)
+        # index tables the fill derives for the steps: row j's positions pos + s, row major and
+        # step major (draft step s reads row s), and the commit's slot (-1 on padding rows)
+        self.pos_grid = torch.zeros(capacity, t, **long)
+        self.pos_steps = torch.zeros(t, capacity, **long)
+        self.commit_slots = torch.full((capacity,), -1, **long)
         # a round's host inputs, one row per buffer row (`STAGE_*` columns): written on the
         # host (pinned on a device), copied once, unpacked into the fields above on the device
         cols = STAGE_IDS + max(t - 1, 1) + mtp_mod.MAX_STOP_IDS
@@ -247,10 +252,30 @@ def _draft_rows(model, m, buf: MTPVerifyBuffers) -> None:
     on_device = vm.kv_write_in_kernel(model)
     for s in range(m.k):
         rows = None if on_device else buf.write_rows[:, s]
-        hid, tok = mtp_mod.draft_step(model, m, hid, tok, buf.pos + s, rows, buf.block_table,
+        # the fed token's positions: row s of the fill's step-major table (pos + s)
+        hid, tok = mtp_mod.draft_step(model, m, hid, tok, buf.pos_steps[s], rows, buf.block_table,
                                       buf.block_valid, buf.active)
-        tok = torch.where((buf.forced_n > s)[:, None], buf.forced_ids[:, s : s + 1], tok)
-        buf.token_matrix[:, s + 1] = tok[:, 0]
+        if tok.is_cuda:  # forced override and the column write in one launch
+            draft_feed(tok[:, 0], buf.forced_n, buf.forced_ids[:, s], s, buf.token_matrix[:, s + 1])
+        else:
+            tok = torch.where((buf.forced_n > s)[:, None], buf.forced_ids[:, s : s + 1], tok)
+            buf.token_matrix[:, s + 1] = tok[:, 0]
+        tok = buf.token_matrix[:, s + 1 : s + 2]
+
+
+def draft_feed(tok: torch.Tensor, forced_n: torch.Tensor, forced: torch.Tensor, step: int,
+               out: torch.Tensor) -> None:
+    """`out[j] = forced[j] if forced_n[j] > step else tok[j]` on device int64 `[B]` vectors (any
+    strides): `mtpk_draft_feed`."""
+    device = _mtpk.require_device(tok, forced_n, forced, out)
+    b = out.shape[0]
+    for name, ten in (("tok", tok), ("forced_n", forced_n), ("forced", forced), ("out", out)):
+        if ten.dtype != torch.int64 or ten.shape != (b,):
+            raise ValueError(f"{name} must be int64 [{b}]")
+    _mtpk.check(_mtpk.lib().mtpk_draft_feed(
+        tok.data_ptr(), tok.stride(0), forced_n.contiguous().data_ptr(), forced.data_ptr(),
+        forced.stride(0), step, out.data_ptr(), out.stride(0), b, _mtpk.stream_of(device)),
+        "mtpk_draft_feed")  # fmt: skip
 
 
 def _verify_rows(model, m, buf: MTPVerifyBuffers, ctx_len: int) -> None:
@@ -264,7 +289,7 @@ def _verify_rows(model, m, buf: MTPVerifyBuffers, ctx_len: int) -> None:
     dev = buf.pos.device
     pos, slots, active = buf.pos, buf.slot_rows, buf.active
     res = model.forward_rows(buf.token_matrix, slots, pos, ctx_len, block_table=buf.block_table,
-                             active=active)
+                             active=active, positions=buf.pos_grid)
     logits = model.logits(res.hidden)
     out = AcceptResult(buf.accept_len, buf.lengths, buf.packed_src, buf.packed_cu, buf.conv_idx,
                        buf.keep, buf.bonus, buf.next_pos, buf.budget_left, buf.live, buf.hidden_src)
@@ -281,8 +306,11 @@ def _verify_rows(model, m, buf: MTPVerifyBuffers, ctx_len: int) -> None:
         buf.step_argmax.copy_(model.argmax(logits).view(b, t))
         accept_torch(buf.step_argmax, draft, active, pos, buf.budget, buf.stops, buf.conv_k1,
                      buf.forced_n, out)
-    model.commit(res, slots, out.lengths, conv_idx=out.conv_idx, active=active)
-    grid = pos[:, None] + torch.arange(t, device=dev)[None, :]
+    if dev.type == "cuda":  # the fill's commit slots: -1 on padding rows, which commit nothing
+        model.commit(res, buf.commit_slots, out.lengths, conv_idx=out.conv_idx)
+    else:
+        model.commit(res, slots, out.lengths, conv_idx=out.conv_idx, active=active)
+    grid = buf.pos_grid
     previous = torch.cat([buf.draft_hidden[:, None], res.hidden[:, :-1]], dim=1)
     if vm.kv_write_in_kernel(model):
         mtp_mod.cache_target_rows(model, m, buf.token_matrix, previous, grid, None, out.keep,
@@ -358,6 +386,10 @@ def _stage(model, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stop
             raise ValueError(f"{name} has {len(seq)} entries for {n} slots")
     if stops is not None and any(len(s) > mtp_mod.MAX_STOP_IDS for s in stops):
         raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
+    vocab = model.cfg.vocab
+    if any(not 0 <= int(x) < vocab for x in tokens) or (
+            forced and any(not 0 <= int(x) < vocab for ids in forced for x in list(ids)[:k])):
+        raise ValueError(f"token ids must lie in [0, {vocab})")
     model.blocks.grow_many(slots, [p + t for p in positions])
     if buf.staged is not None:
         buf.staged.synchronize()  # the previous round's copy has left the pinned rows
@@ -417,6 +449,9 @@ def _unpack(model, buf: MTPVerifyBuffers) -> None:
     buf.block_valid.copy_(((buf.pos + t + bs - 1) // bs).to(torch.int32))
     buf.write_rows.copy_(kv_write_rows(buf.pos, buf.block_table, t, bs))
     buf.draft_hidden.copy_(model.hidden_cache[buf.slot_rows])
+    buf.pos_grid.copy_(buf.pos[:, None] + torch.arange(t, device=buf.pos.device)[None, :])
+    buf.pos_steps.copy_(buf.pos_grid.t())
+    buf.commit_slots.copy_(torch.where(buf.active, buf.slot_rows, torch.full_like(buf.slot_rows, -1)))
 
 
 def round_fill(model, buf: MTPVerifyBuffers) -> None:
@@ -424,7 +459,8 @@ def round_fill(model, buf: MTPVerifyBuffers) -> None:
     table, hidden = model.blocks.table, model.hidden_cache
     fields = (buf.staging, table, hidden, buf.token_matrix, buf.pos, buf.budget, buf.slot_rows,
               buf.forced_n, buf.active, buf.forced_ids, buf.stops, buf.block_table,
-              buf.block_valid, buf.write_rows, buf.draft_hidden)
+              buf.block_valid, buf.write_rows, buf.draft_hidden, buf.pos_grid, buf.pos_steps,
+              buf.commit_slots)
     device = _mtpk.require_device(*fields)
     if not all(f.is_contiguous() for f in fields):
         raise ValueError("round fill needs contiguous buffers and model tables")
@@ -434,6 +470,9 @@ def round_fill(model, buf: MTPVerifyBuffers) -> None:
             or hidden.dtype != buf.draft_hidden.dtype or hidden.shape[1:] != buf.draft_hidden.shape[1:]
             or hidden.shape[0] != lanes):
         raise ValueError("model tables do not match the round buffers")
+    if (buf.pos_grid.shape != (rows, t) or buf.pos_steps.shape != (t, rows)
+            or buf.commit_slots.shape != (rows,)):
+        raise ValueError("the round's index tables do not match its token matrix")
     n_stops = buf.stops.shape[1]
     if buf.staging.shape != (rows, STAGE_IDS + max(t - 1, 1) + n_stops):
         raise ValueError(f"staging must be [{rows}, {STAGE_IDS + max(t - 1, 1) + n_stops}]")
@@ -445,7 +484,8 @@ def round_fill(model, buf: MTPVerifyBuffers) -> None:
             buf.pos.data_ptr(), buf.budget.data_ptr(), buf.slot_rows.data_ptr(),
             buf.forced_n.data_ptr(), buf.active.data_ptr(), buf.forced_ids.data_ptr(),
             buf.stops.data_ptr(), buf.block_table.data_ptr(), buf.block_valid.data_ptr(),
-            buf.write_rows.data_ptr(), buf.draft_hidden.data_ptr(), _mtpk.stream_of(device),
+            buf.write_rows.data_ptr(), buf.draft_hidden.data_ptr(), buf.pos_grid.data_ptr(),
+            buf.pos_steps.data_ptr(), buf.commit_slots.data_ptr(), _mtpk.stream_of(device),
         ),
         "mtpk_round_fill",
     )

@@ -187,7 +187,10 @@ def load(ck, full_cfg, tp, dev, dtype: torch.dtype, max_batch: int, kv_rows: int
     K pool is `[kv_rows, kv_heads, head_dim]` and the V pool the same rows transposed per block,
     `[kv_rows / block_size, kv_heads, head_dim, block_size]`, indexed by the target's block
     tables. This build runs on one GPU: `tp` is None or a plan of world size 1. `max_batch`
-    sizes no scratch here (the kernels take their workspaces per call); it is checked only."""
+    sizes no scratch here (the kernels take their workspaces per call); it is checked only. The
+    attention projections are stacked into one `qkv_proj` weight (`verify_model.fuse_qkv`), the
+    three keys left as views of it."""
+    import verify_model as vm
     import weights as wt
 
     if not mtp_enabled() or not ck.has("mtp.fc.weight"):
@@ -231,6 +234,7 @@ def load(ck, full_cfg, tp, dev, dtype: torch.dtype, max_batch: int, kv_rows: int
     if gu.shape[:2] != (c.experts, 2 * c.inter) or w["experts"]["down"].shape[:2] != (c.experts, h):
         raise ValueError(f"mtp experts: gate_up {tuple(gu.shape)}, down "
                          f"{tuple(w['experts']['down'].shape)} do not match the config")
+    vm.fuse_qkv(w)
     return MTP(
         k=MTP_K,
         weights=w,
@@ -258,6 +262,14 @@ def _combine_rows(model, mtp: MTP, hidden: torch.Tensor, tokens: torch.Tensor) -
     import verify_model as vm
 
     eps = model.cfg.eps
+    h = model.cfg.hidden
+    if hidden.is_cuda and model.embed.is_contiguous() and hidden.is_contiguous():
+        # the embedding lookup rides in the first norm, and both norms write their halves of
+        # the concatenated row: two launches for gather, two norms and the cat
+        x = torch.empty(*tokens.shape, 2 * h, dtype=hidden.dtype, device=hidden.device)
+        rownorm.rmsnorm(model.embed, mtp.pre_fc_norm_embedding, eps, gather=tokens, out=x[..., :h])
+        rownorm.rmsnorm(hidden, mtp.pre_fc_norm_hidden, eps, out=x[..., h:])
+        return vm.linear(x, mtp.fc)
     emb = vm.rmsnorm(model.embed[tokens], mtp.pre_fc_norm_embedding, eps)
     hid = vm.rmsnorm(hidden, mtp.pre_fc_norm_hidden, eps)
     return vm.linear(torch.cat([emb, hid], dim=-1), mtp.fc)
@@ -329,9 +341,12 @@ def cache_target_rows(model, mtp: MTP, tokens: torch.Tensor, raw_previous_hidden
     lead = tokens.shape
     if vm.kv_write_in_kernel(model) and block_table is not None and base_pos is not None:
         rope = (model.cos, model.sin, positions.reshape(-1))
-        k = rownorm.rmsnorm(vm.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim),
-                            w["k_norm"], c.eps, heads=True, rope=rope)
-        v = vm.linear(x, w["v_proj"]).view(*lead, c.kv_heads, c.head_dim)
+        if "kv_proj" in w:  # k and v from one GEMM
+            kp, v = vm.split_kv(vm.linear(x, w["kv_proj"]), c.kv_heads, c.head_dim)
+        else:
+            kp = vm.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim)
+            v = vm.linear(x, w["v_proj"]).view(*lead, c.kv_heads, c.head_dim)
+        k = rownorm.rmsnorm(kp, w["k_norm"], c.eps, heads=True, rope=rope)
         attention.kv_write(mtp.pool["k"], mtp.pool["v"], k, v, block_table, base_pos, keep)
         return
     k = vm.rmsnorm(vm.linear(x, w["k_proj"]).view(*lead, c.kv_heads, c.head_dim),

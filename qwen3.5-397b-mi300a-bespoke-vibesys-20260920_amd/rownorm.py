@@ -45,11 +45,27 @@ def _layout(x: torch.Tensor, heads: bool) -> tuple[int, int, int, int]:
 
 
 def _launch(x, *, kind, w=None, eps=0.0, scale=1.0, gate=None, heads=False, res=None,
-            rope=None, out_dtype=None):
+            rope=None, out_dtype=None, gather=None, out=None):
     dev = _mtpk.require_device(x)
     dim = x.shape[-1]
     ts, hs, hpt, rows = _layout(x, heads)
-    out = torch.empty(x.shape, dtype=out_dtype or x.dtype, device=dev)
+    shape, gp, g_stride, g_rows = x.shape, None, 0, 0
+    if gather is not None:
+        if heads or res is not None or gate is not None or x.dim() != 2:
+            raise ValueError("a gather reads whole rows of a [rows, dim] table")
+        if gather.dtype != torch.int64 or gather.device != dev:
+            raise ValueError("gather must be an int64 device tensor")
+        gp = gather.reshape(-1)
+        shape, rows, g_stride, g_rows = (*gather.shape, dim), gp.numel(), gp.stride(0), x.shape[0]
+    o_ts = 0
+    if out is None:
+        out = torch.empty(shape, dtype=out_dtype or x.dtype, device=dev)
+    else:
+        if out.shape != shape or out.dtype != (out_dtype or x.dtype) or out.device != dev:
+            raise ValueError(f"out must be {tuple(shape)} {out_dtype or x.dtype} on {dev}")
+        o_ts, o_hs, _, _ = _layout(out, heads)
+        if heads and o_hs != dim:
+            raise ValueError("out's heads must be packed")
     g_ts = g_hs = 0
     if gate is not None:
         if gate.shape != x.shape:
@@ -73,18 +89,23 @@ def _launch(x, *, kind, w=None, eps=0.0, scale=1.0, gate=None, heads=False, res=
         _mtpk.ptr(w), _mtpk.float_code(w.dtype) if w is not None else 0, kind, float(eps), float(scale),
         _mtpk.ptr(gate), _mtpk.float_code(gate.dtype) if gate is not None else 0, g_ts, g_hs,
         _mtpk.ptr(cos), _mtpk.ptr(sin), _mtpk.ptr(pos), rot,
-        out.data_ptr(), _mtpk.float_code(out.dtype), rows, hpt, dim, _mtpk.stream_of(dev),
+        out.data_ptr(), _mtpk.float_code(out.dtype), rows, hpt, dim, _mtpk.ptr(gp), g_stride, g_rows,
+        o_ts, _mtpk.stream_of(dev),
     ), "mtpk_rownorm")  # fmt: skip
     return out if res is None else (sum_out, out)
 
 
 def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float, *, heads: bool = False,
-            rope: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None) -> torch.Tensor:
+            rope: tuple[torch.Tensor, torch.Tensor, torch.Tensor] | None = None,
+            gather: torch.Tensor | None = None, out: torch.Tensor | None = None) -> torch.Tensor:
     """`x * rsqrt(mean(x^2) + eps) * (1 + w)` in fp32, x's dtype out. `rope = (cos, sin, pos)`
     then rotates the first `cos.shape[-1]` channels at `pos[token]` (fp32 tables
     `[positions, rot]`; `pos` one entry per token, i.e. per `x.shape[:-2]` element with
-    `heads`)."""
-    return _launch(x, kind=RMS, w=w, eps=eps, heads=heads, rope=rope)
+    `heads`). `gather` (int64, any shape and strides): normalise rows `x[gather]` of the table
+    `x` `[rows, dim]` (the embedding lookup fused; ids are clamped into the table, so callers
+    check them). `out`: write into this tensor (last dim contiguous, rows at one stride, e.g.
+    one half of a concatenated row) instead of a new one; returned."""
+    return _launch(x, kind=RMS, w=w, eps=eps, heads=heads, rope=rope, gather=gather, out=out)
 
 
 def add_rmsnorm(x: torch.Tensor, res: torch.Tensor, w: torch.Tensor,

@@ -286,9 +286,28 @@ def table_rows(block_table: torch.Tensor, pos: torch.Tensor, block_size: int) ->
     return blk * block_size + pos.long() % block_size
 
 
+def fuse_qkv(w: dict) -> dict:
+    """Stack an attention layer's q (with its gate rows), k and v projections into one weight
+    `qkv_proj` (one GEMM for all three) and re-point `q_proj`, `k_proj`, `v_proj` and `kv_proj`
+    at row slices of it; returns `w`."""
+    q, k, v = w["q_proj"], w["k_proj"], w["v_proj"]
+    qkv = torch.cat([q, k, v])
+    a, b = q.shape[0], q.shape[0] + k.shape[0]
+    w.update(qkv_proj=qkv, q_proj=qkv[:a], k_proj=qkv[a:b], v_proj=qkv[b:], kv_proj=qkv[a:])
+    return w
+
+
+def split_kv(kv: torch.Tensor, kv_heads: int, head_dim: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """k and v `[..., kv_heads, head_dim]` views of a `kv_proj` output `[..., 2 kv_heads hd]`."""
+    kd = kv_heads * head_dim
+    lead = kv.shape[:-1]
+    return kv[..., :kd].view(*lead, kv_heads, head_dim), kv[..., kd:].view(*lead, kv_heads, head_dim)
+
+
 def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_pos: torch.Tensor,
                     write_rows: torch.Tensor, block_table: torch.Tensor, ctx_blocks: int,
-                    keep: torch.Tensor | None = None) -> torch.Tensor:
+                    keep: torch.Tensor | None = None,
+                    positions: torch.Tensor | None = None) -> torch.Tensor:
     """Gated GQA attention of `t` rows per lane (`h` `[B, t, hidden]`, normed): q/gate
     projection, q/k RMSNorm, partial RoPE at `base_pos + s`, this round's K/V written at
     `write_rows` `[B, t]` of `pool`, causal paged attention, `o_proj(out * sigmoid(gate))`
@@ -296,14 +315,27 @@ def gated_attention(model: "Model", w: dict, pool: dict, h: torch.Tensor, base_p
     is the same call on its own pool). When `kv_write_in_kernel(model)`, `write_rows` may be
     None: the K/V write maps positions to pool rows through `block_table` itself. `keep`
     `[B, t]` bool (optional) masks the K/V writes: rows with False write nothing (on the torch
-    path they write into row 0, which lies in the reserved block 0 that no lane owns)."""
+    path they write into row 0, which lies in the reserved block 0 that no lane owns).
+    `positions` `[B, t]` (optional) is `base_pos[:, None] + arange(t)` precomputed. A layer with
+    `qkv_proj` (`fuse_qkv`) projects q, gate, k and v with one GEMM."""
     c = model.cfg
     b, t, _ = h.shape
-    qg = F.linear(h, w["q_proj"]).view(b, t, c.heads, 2 * c.head_dim)
+    if "qkv_proj" in w:
+        qd = 2 * c.heads * c.head_dim
+        qkv = linear(h, w["qkv_proj"])
+        qg = qkv[..., :qd].view(b, t, c.heads, 2 * c.head_dim)
+        kp, v = split_kv(qkv[..., qd:], c.kv_heads, c.head_dim)
+    else:
+        qg = F.linear(h, w["q_proj"]).view(b, t, c.heads, 2 * c.head_dim)
+        kp = linear(h, w["k_proj"]).view(b, t, c.kv_heads, c.head_dim)
+        v = linear(h, w["v_proj"]).view(b, t, c.kv_heads, c.head_dim)
     q, gate = qg[..., : c.head_dim], qg[..., c.head_dim :]
-    kp = linear(h, w["k_proj"]).view(b, t, c.kv_heads, c.head_dim)
-    v = linear(h, w["v_proj"]).view(b, t, c.kv_heads, c.head_dim)
-    pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
+    if positions is not None:
+        pos = positions
+    elif t == 1:
+        pos = base_pos.long()[:, None]
+    else:
+        pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
     if h.device.type == "cuda":  # q/k norm and RoPE in one row-norm launch each
         rope = (model.cos, model.sin, pos.reshape(-1))
         q = rownorm.rmsnorm(q, w["q_norm"], c.eps, heads=True, rope=rope)
@@ -443,14 +475,14 @@ def random_experts(cfg: Cfg, device: torch.device, gen: torch.Generator, mode: s
 
 def attention_weights(cfg: Cfg, dtype, device, gen) -> dict:
     qd, kd = cfg.heads * cfg.head_dim, cfg.kv_heads * cfg.head_dim
-    return {
+    return fuse_qkv({
         "q_proj": _normal((2 * qd, cfg.hidden), 0.02, dtype, device, gen),  # per head: q then gate
         "k_proj": _normal((kd, cfg.hidden), 0.02, dtype, device, gen),
         "v_proj": _normal((kd, cfg.hidden), 0.02, dtype, device, gen),
         "o_proj": _normal((cfg.hidden, qd), 0.02, dtype, device, gen),
         "q_norm": _normal((cfg.head_dim,), 0.02, dtype, device, gen),
         "k_norm": _normal((cfg.head_dim,), 0.02, dtype, device, gen),
-    }
+    })
 
 
 def deltanet_weights(cfg: Cfg, dtype, device, gen) -> dict:
@@ -642,10 +674,12 @@ class Model:
 
     def attention_rows(self, w: dict, pool: dict, h: torch.Tensor, lanes: torch.Tensor,
                        base_pos: torch.Tensor, ctx_len: int, block_table: torch.Tensor | None = None,
-                       keep: torch.Tensor | None = None) -> torch.Tensor:
+                       keep: torch.Tensor | None = None,
+                       positions: torch.Tensor | None = None) -> torch.Tensor:
         """Gated GQA attention for `t` rows per lane at positions `base_pos + s` (`attn_verify`,
         `model.py:3519-3577`) over `block_table` `[B, blocks]` (default: the lanes' own tables),
-        K/V writes masked by `keep` `[B, t]`. `ctx_len` is a host bound on `base_pos + t`."""
+        K/V writes masked by `keep` `[B, t]`. `ctx_len` is a host bound on `base_pos + t`;
+        `positions` (optional) the `[B, t]` positions precomputed."""
         c = self.cfg
         t = h.shape[1]
         table = self.blocks.table[lanes] if block_table is None else block_table
@@ -654,7 +688,7 @@ class Model:
             pos = base_pos.long()[:, None] + torch.arange(t, device=h.device)[None, :]
             rows = table_rows(table, pos, c.block_size)
         ctx_blocks = (ctx_len + c.block_size - 1) // c.block_size
-        return gated_attention(self, w, pool, h, base_pos, rows, table, ctx_blocks, keep)
+        return gated_attention(self, w, pool, h, base_pos, rows, table, ctx_blocks, keep, positions)
 
     def deltanet_verify(self, w: dict, pool: dict, h: torch.Tensor,
                         lanes: torch.Tensor) -> tuple[torch.Tensor, DeltaNetRows]:
@@ -741,14 +775,16 @@ class Model:
 
     def forward_rows(self, ids: torch.Tensor, lanes, base_pos: torch.Tensor, ctx_len: int, *,
                      block_table: torch.Tensor | None = None,
-                     active: torch.Tensor | None = None) -> VerifyOut:
+                     active: torch.Tensor | None = None,
+                     positions: torch.Tensor | None = None) -> VerifyOut:
         """The wide forward over fed tokens `ids` `[B, t]` at positions `base_pos[b] + s`
         (`verify_and_commit`'s layer loop, `mtp.py:767-772`). Writes the rows' K/V; DeltaNet
         state is left for `commit`. `ctx_len` is a host bound on `max(base_pos) + t`.
 
         `block_table` `[B, blocks]` (a round buffer's, `graph_mtp.py:141-178`) replaces the
         lanes' own tables for the attention reads and the K/V writes; rows with `active` False
-        (padding) read their slot's state but write no K/V."""
+        (padding) read their slot's state but write no K/V. `positions` (optional) is
+        `base_pos[:, None] + arange(t)` precomputed (a round buffer's `pos_grid`)."""
         c = self.cfg
         lanes = self.lane_index(lanes)
         base_pos = base_pos.to(self.device, torch.long)
@@ -763,7 +799,8 @@ class Model:
             else:
                 x, h = add_rmsnorm(x, pending, w["in_norm"], c.eps)
             if ty == ATTN:
-                mixer = self.attention_rows(w, pool, h, lanes, base_pos, ctx_len, block_table, keep)
+                mixer = self.attention_rows(w, pool, h, lanes, base_pos, ctx_len, block_table, keep,
+                                            positions)
             else:
                 mixer, rows = self.deltanet_verify(w, pool, h, lanes)
                 res.dn_rows[i] = rows
@@ -778,6 +815,9 @@ class Model:
         """Advance every DeltaNet layer's state of `lanes` by `lengths` verified rows; rows with
         `active` False (padding) leave their slots untouched."""
         lanes = self.lane_index(lanes)
+        if active is not None and self.device.type == "cuda":
+            # the kernels skip a row whose slot lies outside the pool: padding commits nothing
+            lanes, active = torch.where(active, lanes, torch.full_like(lanes, -1)), None
         for i, rows in res.dn_rows.items():
             self.deltanet_commit(self.pool[i], rows, lanes, lengths, conv_idx, active)
 

@@ -104,13 +104,18 @@ def test_rejected_arguments_launch_nothing(lib):
     assert lib.mtpk_moe_dense(*args(ws=f + 16)) == -1
     # row norm: null input, dim not a multiple of 8, unknown kind
     assert lib.mtpk_rownorm(None, 0, 64, 64, None, 0, None, None, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
-                            None, None, None, 0, None, 0, 1, 1, 64, None) == -1
+                            None, None, None, 0, None, 0, 1, 1, 64, None, 0, 0, 0, None) == -1
     buf = (ctypes.c_float * 256)()
     p = ctypes.addressof(buf)
     assert lib.mtpk_rownorm(p, 0, 60, 60, None, 0, None, p, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
-                            None, None, None, 0, p, 0, 1, 1, 60, None) == -1
+                            None, None, None, 0, p, 0, 1, 1, 60, None, 0, 0, 0, None) == -1
     assert lib.mtpk_rownorm(p, 0, 64, 64, None, 0, None, p, 0, 7, 1e-6, 1.0, None, 0, 0, 0,
-                            None, None, None, 0, p, 0, 1, 1, 64, None) == -1
+                            None, None, None, 0, p, 0, 1, 1, 64, None, 0, 0, 0, None) == -1
+    # an output token stride below one token's rows, and the residual form with a gather
+    assert lib.mtpk_rownorm(p, 0, 64, 64, None, 0, None, p, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
+                            None, None, None, 0, p, 0, 1, 1, 64, None, 0, 0, 56, None) == -1
+    assert lib.mtpk_rownorm(p, 0, 64, 64, p, 0, p, p, 0, 0, 1e-6, 1.0, None, 0, 0, 0,
+                            None, None, None, 0, p, 0, 1, 1, 64, p, 1, 4, 0, None) == -1
     # rejection sampling: null inputs, then a non-positive temperature with valid-looking
     # pointers (nothing is dereferenced before the checks)
     fake = 0x1000

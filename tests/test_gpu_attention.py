@@ -84,10 +84,11 @@ def test_rejects_bad_arguments(dev) -> None:
                                   v.to(dev)[..., :32].contiguous(), **args)
 
 
-@pytest.mark.parametrize("keep_some", [False, True])
+@pytest.mark.parametrize("keep_some", [False, True, "lanes"])
 def test_kv_write_matches_the_indexed_writes(dev, keep_some) -> None:
     """`attention.kv_write` (positions mapped through the block tables in the kernel) stores
-    exactly what the indexed K write and `write_v` store, and nothing else."""
+    exactly what the indexed K write and `write_v` store, and nothing else; `keep` per row, or
+    a per-lane mask broadcast over the round's rows (read in place, stride 0)."""
     import verify_model as vm
 
     b, t, kvh, hd, lanes_total = 3, 4, 2, 256, 5
@@ -102,7 +103,9 @@ def test_kv_write_matches_the_indexed_writes(dev, keep_some) -> None:
     kp = torch.randn(blocks.rows, kvh, hd, generator=g).to(torch.bfloat16).to(dev)
     vp = torch.randn(blocks.rows // 16, kvh, hd, 16, generator=g).to(torch.bfloat16).to(dev)
     keep = None
-    if keep_some:
+    if keep_some == "lanes":
+        keep = torch.tensor([True, False, True], device=dev)[:, None].expand(b, t)
+    elif keep_some:
         keep = torch.arange(t, device=dev)[None, :] <= torch.tensor([0, 3, 1], device=dev)[:, None]
     want_k, want_v = kp.clone(), vp.clone()
     pos = base[:, None] + torch.arange(t, device=dev)[None, :]

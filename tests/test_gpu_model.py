@@ -462,8 +462,8 @@ def _fill_model(dev, lanes, max_blocks, block_size, hidden, dtype, seed):
 def test_round_fill_matches_the_tensor_fill(dev, dtype, hidden) -> None:
     """`mtpk_round_fill` (the device fill) writes every field the tensor-op fill writes, bit for
     bit, from the same staging rows: forced rows, stop ids, padding rows (reserved block, idle
-    slot), positions on and across block boundaries; seeds in bf16 (16-byte copies) and f32
-    rows of 144 and 20 bytes (the byte-copy path)."""
+    slot, commit slot -1), positions on and across block boundaries and both position tables;
+    seeds in bf16 (16-byte copies) and f32 rows of 144 and 20 bytes (the byte-copy path)."""
     lanes, max_blocks, bs, t, cap = 11, 7, 16, 4, 9
     dm = _fill_model(dev, lanes, max_blocks, bs, hidden, dtype, 5)
     cm = _fill_model("cpu", lanes, max_blocks, bs, hidden, dtype, 5)
@@ -481,7 +481,8 @@ def test_round_fill_matches_the_tensor_fill(dev, dtype, hidden) -> None:
         st[:, graph_mtp.STAGE_IDS:] = torch.randint(-1, 248320, (cap, st.shape[1] - graph_mtp.STAGE_IDS),
                                                    generator=g)
         for buf, junk in ((cb, 7), (db, -3)):  # stale values the fill must overwrite
-            for name in ("token_matrix", "pos", "write_rows", "block_table", "draft_hidden"):
+            for name in ("token_matrix", "pos", "write_rows", "block_table", "draft_hidden",
+                         "pos_grid", "pos_steps", "commit_slots"):
                 getattr(buf, name).fill_(junk)
         cb.staging.copy_(st)
         db.staging.copy_(st)
@@ -489,7 +490,8 @@ def test_round_fill_matches_the_tensor_fill(dev, dtype, hidden) -> None:
         graph_mtp._unpack(dm, db)
         torch.cuda.synchronize()
         for name in ("token_matrix", "pos", "budget", "slot_rows", "forced_n", "active", "forced_ids",
-                     "stops", "block_table", "block_valid", "write_rows", "draft_hidden"):
+                     "stops", "block_table", "block_valid", "write_rows", "draft_hidden", "pos_grid",
+                     "pos_steps", "commit_slots"):
             want, got = getattr(cb, name), getattr(db, name).cpu()
             assert got.dtype == want.dtype and torch.equal(got, want), (trial, name)
 
@@ -512,4 +514,22 @@ def test_round_fill_marks_positions_outside_the_table(dev) -> None:
             [table[0, 0] * bs + 5 + s for s in range(t)]]
     assert db.write_rows.cpu().tolist() == [[int(x) for x in row] for row in want]
     assert db.block_valid.cpu().tolist() == [3, 1]
+
+
+def test_draft_feed_takes_forced_ids_while_they_last(dev) -> None:
+    """`graph_mtp.draft_feed` (`mtpk_draft_feed`) writes each row's fed token into a token-matrix
+    column: the forced id at steps below the row's forced count, else the step's greedy token;
+    the other columns are left alone."""
+    b, t = 7, 4
+    g = torch.Generator().manual_seed(2)
+    forced_n = torch.tensor([0, 1, 2, 3, 3, 0, 2])
+    forced = torch.randint(0, 1000, (b, t - 1), generator=g)
+    greedy = torch.randint(0, 1000, (b, t - 1), generator=g)
+    tm = torch.randint(0, 1000, (b, t), generator=g)
+    dtm = tm.to(dev)
+    for s in range(t - 1):
+        graph_mtp.draft_feed(greedy.to(dev)[:, s], forced_n.to(dev), forced.to(dev)[:, s], s,
+                             dtm[:, s + 1])
+        tm[:, s + 1] = torch.where(forced_n > s, forced[:, s], greedy[:, s])
+    assert torch.equal(dtm.cpu(), tm)
 

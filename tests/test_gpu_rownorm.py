@@ -89,6 +89,32 @@ def test_gated_norm_and_l2(dev, t):
     close(rownorm.l2norm(q, 1e-6, 128 ** -0.5), want, torch.float32)
 
 
+@pytest.mark.parametrize("dtype,dim", [(torch.bfloat16, 4096), (torch.float32, 64)])
+def test_gathered_rows_into_halves_of_one_row(dev, dtype, dim):
+    """The MTP head's input row: `rmsnorm(table[ids])` and `rmsnorm(hidden)` written straight
+    into the two halves of one concatenated row (the embedding lookup fused, ids read through
+    their strides) equal `cat([rmsnorm(table[ids]), rmsnorm(hidden)])` bit for bit, and an id
+    outside the table reads its nearest row."""
+    g = torch.Generator(dev).manual_seed(dim)
+    table = torch.randn(50, dim, device=dev, generator=g).to(dtype)
+    hidden = torch.randn(6, 1, dim, device=dev, generator=g).to(dtype)
+    w1 = (torch.randn(dim, device=dev, generator=g) * 0.02).to(dtype)
+    w2 = (torch.randn(dim, device=dev, generator=g) * 0.02).to(dtype)
+    matrix = torch.randint(0, 50, (6, 4), device=dev, generator=g)
+    ids = matrix[:, 2:3]  # a column of a token matrix: row stride 4
+    x = torch.full((6, 1, 2 * dim), float("nan"), device=dev, dtype=dtype)
+    rownorm.rmsnorm(table, w1, 1e-6, gather=ids, out=x[..., :dim])
+    rownorm.rmsnorm(hidden, w2, 1e-6, out=x[..., dim:])
+    want = torch.cat([rownorm.rmsnorm(table[ids.reshape(-1)].reshape(6, 1, dim), w1, 1e-6),
+                      rownorm.rmsnorm(hidden, w2, 1e-6)], dim=-1)
+    assert torch.equal(x, want)
+    close(x[..., :dim], ref_rms(table[ids.reshape(-1)].reshape(6, 1, dim), w1, 1e-6), dtype)
+    bad = torch.tensor([[-3], [7], [50], [10 ** 9]], device=dev)
+    got = rownorm.rmsnorm(table, w1, 1e-6, gather=bad)
+    near = torch.tensor([0, 7, 49, 49], device=dev)
+    assert torch.equal(got, rownorm.rmsnorm(table[near], w1, 1e-6).reshape(4, 1, dim))
+
+
 def test_rejects_unsupported_layouts(dev):
     x = torch.randn(4, 100, device=dev)
     with pytest.raises(ValueError):
