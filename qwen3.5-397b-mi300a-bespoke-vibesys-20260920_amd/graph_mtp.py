@@ -106,7 +106,9 @@ class MTPVerifyBuffers:
         self.staging = torch.zeros(capacity, cols, **long)
         pin = torch.device(device).type == "cuda"
         self.staging_host = torch.zeros(capacity, cols, dtype=torch.long, pin_memory=pin)
-        self.staged = None  # the event after the last staging copy (device buffers)
+        # recorded after each staging copy (device buffers): the next round's host writes wait
+        # for it before reusing the pinned rows
+        self.staged = torch.cuda.Event() if pin else None
 
 
 @dataclass
@@ -373,12 +375,15 @@ def pad_slot_for(slots, lanes: int) -> int:
 
 def _stage(model, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stops, forced) -> None:
     """The host half of `_fill`: checks, the lanes' KV blocks grown for t more positions, and
-    the round's rows written into `buf.staging_host` and copied to `buf.staging` (one copy)."""
+    the round's rows written into `buf.staging_host` and copied to `buf.staging` (one copy).
+    The device waits while this runs, so the common round (no forced drafts, no stop ids, no
+    lane growing a block) takes builtin checks over the lists and one numpy write per column."""
     n, t, k = len(slots), buf.t, buf.t - 1
     lanes = model.lanes
-    if not 1 <= n <= buf.capacity or len(set(slots)) != n:
+    sl = [int(x) for x in slots]
+    if not 1 <= n <= buf.capacity or len(set(sl)) != n:
         raise ValueError(f"need 1..{buf.capacity} distinct slots, got {slots}")
-    if any(not 0 <= int(s) < lanes for s in slots):
+    if min(sl) < 0 or max(sl) >= lanes:
         raise ValueError(f"slots must lie in [0, {lanes}), got {slots}")
     for name, seq in (("tokens", tokens), ("positions", positions), ("budgets", budgets),
                       ("stops", stops), ("forced", forced)):
@@ -387,10 +392,10 @@ def _stage(model, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stop
     if stops is not None and any(len(s) > mtp_mod.MAX_STOP_IDS for s in stops):
         raise ValueError(f"at most {mtp_mod.MAX_STOP_IDS} stop ids per lane")
     vocab = model.cfg.vocab
-    if any(not 0 <= int(x) < vocab for x in tokens) or (
+    if min(tokens) < 0 or max(tokens) >= vocab or (
             forced and any(not 0 <= int(x) < vocab for ids in forced for x in list(ids)[:k])):
         raise ValueError(f"token ids must lie in [0, {vocab})")
-    model.blocks.grow_many(slots, [p + t for p in positions])
+    model.blocks.grow_many(sl, [p + t for p in positions])
     if buf.staged is not None:
         buf.staged.synchronize()  # the previous round's copy has left the pinned rows
     h = buf.staging_host.numpy()
@@ -400,26 +405,27 @@ def _stage(model, buf: MTPVerifyBuffers, slots, tokens, positions, budgets, stop
     h[:n, STAGE_TOKEN] = tokens
     h[:n, STAGE_POS] = positions
     h[:n, STAGE_BUDGET] = 1 << 40 if budgets is None else budgets
-    h[:n, STAGE_SLOT] = [int(x) for x in slots]
+    h[:n, STAGE_SLOT] = sl
     h[:n, STAGE_ACTIVE] = 1
     h[:n, STAGE_FORCED] = 0
-    for j in range(n):
-        if forced:
-            ids = list(forced[j])[:k]
-            h[j, STAGE_FORCED] = len(ids)
-            h[j, STAGE_IDS : STAGE_IDS + len(ids)] = ids
-        if stops and len(stops[j]):
-            h[j, STAGE_IDS + width : STAGE_IDS + width + len(stops[j])] = list(stops[j])
+    if forced or stops:
+        for j in range(n):
+            if forced:
+                ids = list(forced[j])[:k]
+                h[j, STAGE_FORCED] = len(ids)
+                h[j, STAGE_IDS : STAGE_IDS + len(ids)] = ids
+            if stops and len(stops[j]):
+                h[j, STAGE_IDS + width : STAGE_IDS + width + len(stops[j])] = list(stops[j])
     # padding rows: inactive, position 0, budget t, an idle lane as slot, no stop ids
-    h[n:, STAGE_TOKEN] = 0
-    h[n:, STAGE_POS] = 0
-    h[n:, STAGE_BUDGET] = t
-    h[n:, STAGE_SLOT] = pad_slot_for(slots, lanes) if n < buf.capacity else 0
-    h[n:, STAGE_FORCED] = 0
-    h[n:, STAGE_ACTIVE] = 0
+    if n < buf.capacity:
+        h[n:, STAGE_TOKEN] = 0
+        h[n:, STAGE_POS] = 0
+        h[n:, STAGE_BUDGET] = t
+        h[n:, STAGE_SLOT] = pad_slot_for(sl, lanes)
+        h[n:, STAGE_FORCED] = 0
+        h[n:, STAGE_ACTIVE] = 0
     buf.staging.copy_(buf.staging_host, non_blocking=True)
-    if buf.staging.is_cuda:
-        buf.staged = torch.cuda.Event()
+    if buf.staged is not None:
         buf.staged.record()
 
 
@@ -625,9 +631,15 @@ class GraphMTPRunner(MTPVerifyRunner):
         return True
 
     def _capture(self, buf: MTPVerifyBuffers) -> Callable[[], None]:
-        """The bucket's round (draft + verify + accept + commit) as one graph. The fill stays
-        outside it: one staging copy and one `mtpk_round_fill` launch."""
-        return self.backend.capture(lambda: self._round(buf), buf.pos.device)
+        """The bucket's round as one graph: the fill's device half (`_unpack`, reading the
+        staged rows) and then draft + verify + accept + commit, so a round is one staging copy
+        and one replay. Replaying after `fill()` unpacks the same staged rows again."""
+
+        def step() -> None:
+            _unpack(self.model, buf)
+            self._round(buf)
+
+        return self.backend.capture(step, buf.pos.device)
 
     def _eager_round(self, buf: MTPVerifyBuffers) -> None:
         """The bucket's round run eagerly before its capture, on a side stream on a device (so
@@ -723,13 +735,14 @@ class GraphMTPRunner(MTPVerifyRunner):
             self.eager_rounds += 1
             return super().speculative_decode(slots, tokens, positions, budgets, stops, forced)
         buf = self.buffers(len(slots))
-        self.fill(buf, slots, tokens, positions, budgets, stops, forced)
         replay = self.graphs.get(buf.capacity)
         if replay is None:
+            self.fill(buf, slots, tokens, positions, budgets, stops, forced)
             self._eager_round(buf)  # this round, run eagerly; then the bucket is captured
             self.graphs[buf.capacity] = self._capture(buf)
         else:
-            replay()
+            _stage(self.model, buf, slots, tokens, positions, budgets, stops, forced)
+            replay()  # unpacks the staged rows, then the round
         return _committed(buf, len(slots))
 
 

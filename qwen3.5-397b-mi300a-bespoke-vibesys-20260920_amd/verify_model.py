@@ -382,6 +382,7 @@ class BlockTables:
         gen = torch.Generator().manual_seed(seed)
         self._free = (torch.randperm(self.n_blocks - 1, generator=gen) + 1).tolist()
         self.host = [[] for _ in range(lanes)]
+        self.held_positions = [0] * lanes  # len(host[lane]) * block_size
         self.table = torch.zeros(lanes, self.max_blocks, dtype=torch.int32, device=device)
         self.device = device
 
@@ -400,12 +401,18 @@ class BlockTables:
         new = [self._free.pop() for _ in range(need - len(have))]
         self.table[lane, len(have) : need] = torch.tensor(new, dtype=torch.int32).to(self.device)
         have.extend(new)
+        self.held_positions[lane] = len(have) * self.block_size
 
     def grow_many(self, lanes, lengths) -> None:
         """`grow` for several lanes with one host-to-device copy and one scatter for every new
-        table entry (per-lane copies from pageable memory each wait for the stream)."""
+        table entry (per-lane copies from pageable memory each wait for the stream). A call in
+        which every lane already holds its blocks is one pass of builtin comparisons."""
+        cap = self.held_positions
+        pairs = list(zip(lanes, lengths, strict=True))
+        if all(int(n) <= cap[int(lane)] for lane, n in pairs):
+            return
         needs = []
-        for lane, length in zip(lanes, lengths, strict=True):
+        for lane, length in pairs:
             need = (int(length) + self.block_size - 1) // self.block_size
             if need > self.max_blocks:
                 raise ValueError(f"lane {lane}: {length} positions exceed the table's {self.max_blocks} blocks")
@@ -417,6 +424,7 @@ class BlockTables:
                 blk = self._free.pop()
                 have.append(blk)
                 upd.append((lane, col, blk))
+            cap[lane] = len(have) * self.block_size
         if not upd:
             return
         pin = self.table.is_cuda
@@ -426,6 +434,7 @@ class BlockTables:
     def release(self, lane: int) -> None:
         self._free.extend(reversed(self.host[lane]))
         self.host[lane] = []
+        self.held_positions[lane] = 0
         self.table[lane].zero_()
 
     def physical_rows(self, lanes: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
