@@ -355,6 +355,15 @@ int mtpk_draft_feed(const int64_t* tok, int64_t tok_stride, const int64_t* force
                     const int64_t* forced, int64_t forced_stride, int64_t step, int64_t* out,
                     int64_t out_stride, int64_t rows, void* stream);
 
+/* Rows through two index lists (the verify step's hidden-seed write-back,
+ * `scatter_time_active_rows`, graph_mtp.py:578-579): for j < rows, dst row dst_idx[j] (of
+ * dst_rows, dst_stride bytes apart) = src row src_idx[j] (of src_rows, src_stride bytes apart),
+ * row_bytes each; j is skipped when either index lies outside its table (e.g. slot -1 of a
+ * padding row). */
+int mtpk_copy_rows(const void* src, int64_t src_rows, int64_t src_stride, const int64_t* src_idx,
+                   void* dst, int64_t dst_rows, int64_t dst_stride, const int64_t* dst_idx,
+                   int64_t rows, int64_t row_bytes, void* stream);
+
 /* ---------------------------------------------------------------- rejection sampling
  * Sampling-mode acceptance for an MTP round at temperature T > 0. The reference engine has no
  * counterpart: it runs MTP rounds only for all-greedy batches (scheduler.py:1775-1793,

@@ -171,6 +171,11 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         c_int,
         [c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64, c_void_p],
     ),
+    "mtpk_copy_rows": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_int64, c_int64,
+         c_void_p],
+    ),
     "mtpk_argmax_keys": (c_int, [c_void_p, c_int, c_int64, c_int64, c_int64, c_void_p, c_void_p]),
     "mtpk_rejection_workspace_bytes": (c_int64, [c_int64, c_int, c_int64]),
     "mtpk_rejection_sample": (

@@ -115,6 +115,28 @@ __global__ __launch_bounds__(256) void k_draft_feed(const int64_t* __restrict__ 
   out[j * out_stride] = forced_n[j] > step ? forced[j * forced_stride] : tok[j * tok_stride];
 }
 
+// Row copy through two index lists (the verify step's seed write-back, `scatter_time_active_rows`
+// at graph_mtp.py:578-579): dst row dst_idx[j] = src row src_idx[j]; a row whose index lies
+// outside its table (a padding row's -1 slot) is skipped. One workgroup per row, 16-byte copies
+// when the rows allow them.
+__global__ __launch_bounds__(256) void k_copy_rows(const uint8_t* __restrict__ src, int64_t src_rows,
+                                                  int64_t src_stride, const int64_t* __restrict__ src_idx,
+                                                  uint8_t* __restrict__ dst, int64_t dst_rows,
+                                                  int64_t dst_stride, const int64_t* __restrict__ dst_idx,
+                                                  int64_t row_bytes, bool vec) {
+  const int64_t j = blockIdx.x;
+  const int64_t s = src_idx[j], d = dst_idx[j];
+  if (s < 0 || s >= src_rows || d < 0 || d >= dst_rows) return;  // uniform over the workgroup
+  const uint8_t* a = src + s * src_stride;
+  uint8_t* b = dst + d * dst_stride;
+  if (vec) {
+    for (int64_t i = threadIdx.x; i < row_bytes / 16; i += 256)
+      *reinterpret_cast<u32x4_t*>(b + 16 * i) = ld16(a + 16 * i);
+  } else {
+    for (int64_t i = threadIdx.x; i < row_bytes; i += 256) b[i] = a[i];
+  }
+}
+
 }  // namespace mtpk
 
 using namespace mtpk;
@@ -182,6 +204,21 @@ int mtpk_draft_feed(const int64_t* tok, int64_t tok_stride, const int64_t* force
   hipLaunchKernelGGL(k_draft_feed, dim3((unsigned)((rows + 255) / 256)), dim3(256), 0,
                      (hipStream_t)stream, tok, tok_stride, forced_n, forced, forced_stride, step,
                      out, out_stride, rows);
+  return status_of(hipGetLastError());
+}
+
+int mtpk_copy_rows(const void* src, int64_t src_rows, int64_t src_stride, const int64_t* src_idx,
+                   void* dst, int64_t dst_rows, int64_t dst_stride, const int64_t* dst_idx,
+                   int64_t rows, int64_t row_bytes, void* stream) {
+  if (rows < 0 || rows > INT32_MAX || row_bytes < 0 || src_rows < 0 || dst_rows < 0) return MTPK_EINVAL;
+  if (!src_idx || !dst_idx || (row_bytes > 0 && (!src || !dst))) return MTPK_EINVAL;
+  if (src_stride < row_bytes || dst_stride < row_bytes) return MTPK_EINVAL;
+  if (rows == 0 || row_bytes == 0) return 0;
+  const bool vec = row_bytes % 16 == 0 && src_stride % 16 == 0 && dst_stride % 16 == 0 &&
+                   aligned16(src) && aligned16(dst);
+  hipLaunchKernelGGL(k_copy_rows, dim3((unsigned)rows), dim3(256), 0, (hipStream_t)stream,
+                     static_cast<const uint8_t*>(src), src_rows, src_stride, src_idx,
+                     static_cast<uint8_t*>(dst), dst_rows, dst_stride, dst_idx, row_bytes, vec);
   return status_of(hipGetLastError());
 }
 

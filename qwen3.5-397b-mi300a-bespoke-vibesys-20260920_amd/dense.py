@@ -54,7 +54,11 @@ def silu_linear(x: torch.Tensor, w_gate_up: torch.Tensor) -> torch.Tensor:
     return _run(x, w_gate_up, SILU, out)
 
 
-def argmax_linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
-    """First-occurrence argmax over the bf16 values of `x @ w.T`: int64 `[...]`."""
-    out = torch.empty(x.shape[:-1], dtype=torch.int64, device=x.device)
+def argmax_linear(x: torch.Tensor, w: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """First-occurrence argmax over the bf16 values of `x @ w.T`: int64 `[...]`, into `out`
+    (contiguous int64 of x's leading shape) when given."""
+    if out is None:
+        out = torch.empty(x.shape[:-1], dtype=torch.int64, device=x.device)
+    elif out.dtype != torch.int64 or out.shape != x.shape[:-1] or not out.is_contiguous():
+        raise ValueError(f"out must be a contiguous int64 {tuple(x.shape[:-1])} tensor")
     return _run(x, w, ARGMAX, out)

@@ -291,21 +291,23 @@ def _verify_rows(model, m, buf: MTPVerifyBuffers, ctx_len: int) -> None:
     dev = buf.pos.device
     pos, slots, active = buf.pos, buf.slot_rows, buf.active
     res = model.forward_rows(buf.token_matrix, slots, pos, ctx_len, block_table=buf.block_table,
-                             active=active, positions=buf.pos_grid)
-    logits = model.logits(res.hidden)
+                             active=active, positions=buf.pos_grid, final_norm=True)
+    normed = res.normed.reshape(b * t, -1)
     out = AcceptResult(buf.accept_len, buf.lengths, buf.packed_src, buf.packed_cu, buf.conv_idx,
                        buf.keep, buf.bonus, buf.next_pos, buf.budget_left, buf.live, buf.hidden_src)
     draft = buf.token_matrix[:, 1:]
     if dev.type == "cuda":
         keys = None
-        if b * t <= KEY_ROWS:  # the accept launch finishes the argmax
-            keys = mtp_mod.argmax_keys(logits.reshape(b * t, -1))
+        if model.fused_argmax(b * t, normed):  # the LM head GEMM with the argmax in its epilogue
+            model.next_tokens(normed, out=buf.step_argmax.view(-1))
+        elif b * t <= KEY_ROWS:  # the accept launch finishes the argmax
+            keys = mtp_mod.argmax_keys(model.unembed(normed))
         else:
-            buf.step_argmax.copy_(model.argmax(logits).view(b, t))
+            buf.step_argmax.copy_(model.argmax(model.unembed(normed)).view(b, t))
         greedy_accept(buf.step_argmax, draft, active, pos, buf.budget, buf.stops, buf.conv_k1,
                       out=out, keys=keys, forced_n=buf.forced_n)
     else:
-        buf.step_argmax.copy_(model.argmax(logits).view(b, t))
+        buf.step_argmax.copy_(model.argmax(model.unembed(normed)).view(b, t))
         accept_torch(buf.step_argmax, draft, active, pos, buf.budget, buf.stops, buf.conv_k1,
                      buf.forced_n, out)
     if dev.type == "cuda":  # the fill's commit slots: -1 on padding rows, which commit nothing
@@ -319,9 +321,30 @@ def _verify_rows(model, m, buf: MTPVerifyBuffers, ctx_len: int) -> None:
                                   block_table=buf.block_table, base_pos=pos)
     else:
         mtp_mod.cache_target_rows(model, m, buf.token_matrix, previous, grid, buf.write_rows, out.keep)
-    seed = res.hidden.reshape(b * t, -1)[out.hidden_src]
-    # padding rows name an idle lane and write back its own seed: no row of the round writes it
-    model.hidden_cache[slots] = torch.where(active[:, None], seed, model.hidden_cache[slots])
+    if dev.type == "cuda":  # one launch: slot commit_slots[j] <- verify row hidden_src[j]
+        copy_rows(res.hidden.reshape(b * t, -1), out.hidden_src, model.hidden_cache, buf.commit_slots)
+    else:
+        seed = res.hidden.reshape(b * t, -1)[out.hidden_src]
+        # padding rows name an idle lane and write back its own seed: no row of the round writes it
+        model.hidden_cache[slots] = torch.where(active[:, None], seed, model.hidden_cache[slots])
+
+
+def copy_rows(src: torch.Tensor, src_idx: torch.Tensor, dst: torch.Tensor, dst_idx: torch.Tensor) -> None:
+    """`dst[dst_idx[j]] = src[src_idx[j]]` on device 2-D tensors of one dtype and row width (rows
+    at any stride), skipping every j whose index lies outside its table: `mtpk_copy_rows`."""
+    device = _mtpk.require_device(src, src_idx, dst, dst_idx)
+    n = src_idx.shape[0]
+    if (src.dim() != 2 or dst.dim() != 2 or src.dtype != dst.dtype or src.shape[1] != dst.shape[1]
+            or src.stride(1) != 1 or dst.stride(1) != 1):
+        raise ValueError("src and dst must be 2-D of one dtype and width, rows contiguous")
+    if src_idx.shape != (n,) or dst_idx.shape != (n,) or src_idx.dtype != torch.int64 \
+            or dst_idx.dtype != torch.int64:
+        raise ValueError("src_idx and dst_idx must be int64 vectors of one length")
+    es = src.element_size()
+    _mtpk.check(_mtpk.lib().mtpk_copy_rows(
+        src.data_ptr(), src.shape[0], src.stride(0) * es, src_idx.contiguous().data_ptr(),
+        dst.data_ptr(), dst.shape[0], dst.stride(0) * es, dst_idx.contiguous().data_ptr(), n,
+        src.shape[1] * es, _mtpk.stream_of(device)), "mtpk_copy_rows")  # fmt: skip
 
 
 def _ctx_bound(model) -> int:

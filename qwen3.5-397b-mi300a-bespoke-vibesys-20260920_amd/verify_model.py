@@ -121,12 +121,12 @@ def _dense_wide_rows(rows: int, w: torch.Tensor) -> bool:
     return 64 < rows <= dense.MAX_ROWS and 2048 <= n <= 4096 and k >= 1024
 
 
-FUSED_ARGMAX_ROWS = 64
-"""Greedy LM-head rows up to which `next_tokens` runs the GEMM with the argmax in its epilogue.
-Measured on [M, 4096] x [248320, 4096] bf16 against hipBLASLt + the argmax kernel: 390 against
-401 us at 16 rows, 421 against 416 us at 48, 427 against 433 us at 64; at 192 rows the library
-path stays (521 us with its argmax pass against 552 us for the wide form with the argmax in its
-epilogue, `dense.argmax_linear`)."""
+FUSED_ARGMAX_ROWS = 192
+"""Greedy LM-head rows up to which `next_tokens` runs the GEMM with the argmax in its epilogue
+(the logits never reach memory). Measured on [M, 4096] x [248320, 4096] bf16 against the
+library GEMM + the argmax kernel: 390 against 401 us at 16 rows, 404 against 423 us at 48,
+427 against 433 us at 64, and at 192 rows (the wide form, `dense.argmax_linear`) 506.5 against
+519-520 us (hipBLASLt or rocBLAS, graph replay over two weight copies)."""
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
@@ -541,6 +541,7 @@ class VerifyOut:
 
     hidden: torch.Tensor
     dn_rows: dict[int, DeltaNetRows] = field(default_factory=dict)
+    normed: torch.Tensor | None = None  # the final-normed rows, when asked for
 
 
 class Model:
@@ -785,7 +786,8 @@ class Model:
     def forward_rows(self, ids: torch.Tensor, lanes, base_pos: torch.Tensor, ctx_len: int, *,
                      block_table: torch.Tensor | None = None,
                      active: torch.Tensor | None = None,
-                     positions: torch.Tensor | None = None) -> VerifyOut:
+                     positions: torch.Tensor | None = None,
+                     final_norm: bool = False) -> VerifyOut:
         """The wide forward over fed tokens `ids` `[B, t]` at positions `base_pos[b] + s`
         (`verify_and_commit`'s layer loop, `mtp.py:767-772`). Writes the rows' K/V; DeltaNet
         state is left for `commit`. `ctx_len` is a host bound on `max(base_pos) + t`.
@@ -793,7 +795,9 @@ class Model:
         `block_table` `[B, blocks]` (a round buffer's, `graph_mtp.py:141-178`) replaces the
         lanes' own tables for the attention reads and the K/V writes; rows with `active` False
         (padding) read their slot's state but write no K/V. `positions` (optional) is
-        `base_pos[:, None] + arange(t)` precomputed (a round buffer's `pos_grid`)."""
+        `base_pos[:, None] + arange(t)` precomputed (a round buffer's `pos_grid`). With
+        `final_norm`, `res.normed` also holds the final-normed rows (the last residual add and
+        the norm in one launch)."""
         c = self.cfg
         lanes = self.lane_index(lanes)
         base_pos = base_pos.to(self.device, torch.long)
@@ -816,7 +820,10 @@ class Model:
             x, hm = add_rmsnorm(x, mixer, w["post_norm"], c.eps)
             b, t, _ = hm.shape
             pending = self.moe(w, hm.reshape(b * t, -1)).view(b, t, -1)
-        res.hidden = x + pending
+        if final_norm:
+            res.hidden, res.normed = add_rmsnorm(x, pending, self.final_norm, c.eps)
+        else:
+            res.hidden = x + pending
         return res
 
     def commit(self, res: VerifyOut, lanes, lengths: torch.Tensor,
@@ -836,15 +843,20 @@ class Model:
     def logits(self, hidden: torch.Tensor) -> torch.Tensor:
         return self.unembed(rmsnorm(hidden, self.final_norm, self.cfg.eps))
 
-    def next_tokens(self, normed: torch.Tensor) -> torch.Tensor:
+    def fused_argmax(self, rows: int, normed: torch.Tensor) -> bool:
+        """Whether `next_tokens` takes the GEMM with the argmax epilogue for these rows."""
+        return rows <= FUSED_ARGMAX_ROWS and dense.fits(normed, self.lm_head)
+
+    def next_tokens(self, normed: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
         """Greedy next token of final-normed rows `[..., hidden]`: `argmax(unembed(normed))`.
-        Up to FUSED_ARGMAX_ROWS bf16 device rows take the skinny GEMM with its argmax epilogue
-        (the logits never reach memory; same first-occurrence rule over the bf16 logits,
-        `mtp.py:640-658`)."""
+        Up to FUSED_ARGMAX_ROWS bf16 device rows take the GEMM with its argmax epilogue (the
+        logits never reach memory; same first-occurrence rule over the bf16 logits,
+        `mtp.py:640-658`). `out` (optional, int64 of the leading shape) receives the ids."""
         rows = normed.numel() // normed.shape[-1]
-        if rows <= FUSED_ARGMAX_ROWS and dense.fits(normed, self.lm_head):
-            return dense.argmax_linear(normed, self.lm_head)
-        return self.argmax(self.unembed(normed))
+        if self.fused_argmax(rows, normed):
+            return dense.argmax_linear(normed, self.lm_head, out)
+        ids = self.argmax(self.unembed(normed))
+        return ids if out is None else out.copy_(ids.view(out.shape))
 
     def argmax(self, logits: torch.Tensor) -> torch.Tensor:
         """First-occurrence argmax over the vocab (the HIP kernel on a device)."""

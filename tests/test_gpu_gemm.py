@@ -68,6 +68,16 @@ def test_argmax_linear_is_the_argmax_of_its_bf16_logits(dev, m, n):
     assert torch.equal(idx[clear], ref.argmax(-1)[clear])
 
 
+def test_argmax_linear_into_a_given_tensor(dev):
+    """`out=` receives the same ids (a round buffer's step_argmax rows, written in place)."""
+    x, w = _inputs(dev, 192, 4096, 248320, 9)
+    out = torch.full((192,), -5, dtype=torch.int64, device=dev)
+    assert dense.argmax_linear(x, w, out) is out
+    assert torch.equal(out, dense.argmax_linear(x, w))
+    with pytest.raises(ValueError):
+        dense.argmax_linear(x, w, torch.empty(191, dtype=torch.int64, device=dev))
+
+
 def test_ties_pick_the_lowest_column(dev):
     x = torch.ones(3, 256, dtype=torch.bfloat16, device=dev)
     w = torch.zeros(640, 256, dtype=torch.bfloat16, device=dev)

@@ -533,3 +533,22 @@ def test_draft_feed_takes_forced_ids_while_they_last(dev) -> None:
         tm[:, s + 1] = torch.where(forced_n > s, forced[:, s], greedy[:, s])
     assert torch.equal(dtm.cpu(), tm)
 
+
+def test_copy_rows_skips_rows_outside_the_tables(dev) -> None:
+    """`graph_mtp.copy_rows` (`mtpk_copy_rows`, the seed write-back): `dst[dst_idx[j]] =
+    src[src_idx[j]]`, rows at strides, 16-byte and byte copies; a row whose source or target
+    index lies outside its table (slot -1 of a padding row) is skipped."""
+    g = torch.Generator().manual_seed(4)
+    for dtype, width in ((torch.bfloat16, 4096), (torch.float32, 5)):
+        src = torch.randn(12, width + 8, generator=g).to(dtype)[:, :width]  # rows at a stride
+        dst = torch.randn(6, width, generator=g).to(dtype)
+        src_idx = torch.tensor([3, 0, 11, 7, 2, 12])
+        dst_idx = torch.tensor([5, -1, 0, 2, 6, 1])
+        want = dst.clone()
+        for s_, d_ in zip(src_idx.tolist(), dst_idx.tolist(), strict=True):
+            if 0 <= s_ < 12 and 0 <= d_ < 6:
+                want[d_] = src[s_]
+        got = dst.to(dev)
+        graph_mtp.copy_rows(src.to(dev), src_idx.to(dev), got, dst_idx.to(dev))
+        assert torch.equal(got.cpu(), want), dtype
+
