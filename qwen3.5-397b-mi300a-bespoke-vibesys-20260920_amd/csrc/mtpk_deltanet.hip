@@ -9,7 +9,9 @@
 // column: its dk (16..128) values stay in registers for all t steps, and one 64-lane wave
 // covers 64 columns of one (row, head). q and k are the same for the whole wave and come in through
 // LDS; the state is read once (dword loads, 256 contiguous bytes per wave
-// instruction) and, in commit mode, written back once in place.
+// instruction) and, in commit mode, written back once in place. At dk = 128 (the real model)
+// a lane owns 4 columns over a quarter of the rows instead (16-byte state loads, the column
+// sums finished by DPP adds in the lane quad; k_delta_rule_kg below).
 //
 // Verify mode (lengths == NULL): t steps from the committed state, outputs for every step, the
 // state is not written. Commit mode: row j replays its accepted prefix, min(lengths[j], t)
@@ -134,10 +136,161 @@ __global__ __launch_bounds__(kWave) void k_delta_rule(
   }
 }
 
+// The k_dim = 128 form (dv a multiple of 64): the rows of a matrix are cut into KG groups of
+// 128 / KG and lane (cg = l / KG, kg = l % KG) owns the 4 adjacent columns 4 cg .. 4 cg + 3 of
+// its block (64 4 / KG columns) over row group kg, so the state comes in with 16-byte loads
+// (128 / KG per lane; every wave instruction reads KG row segments of 16 columns each) instead
+// of 128 dword loads, and each step reads only its row group of k and q back from LDS. A
+// column's sums over the row groups (S^T k and S^T q) are DPP butterfly adds inside the KG
+// adjacent lanes, which leave the same bits in all of them, so every lane applies the same
+// delta to its rows. The first 4 lanes of each group write the group's 4 output columns.
+template <int CTRL>
+__device__ inline float dn_dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, x), CTRL, 0xf, 0xf, false));
+}
+template <int KG>
+__device__ inline float group_sum(float x) {
+  x += dn_dpp<0xB1>(x);  // quad_perm [1, 0, 3, 2]
+  x += dn_dpp<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+  if (KG == 8) x += dn_dpp<0x141>(x);  // row_half_mirror: the other quad of the 8 lanes
+  return x;
+}
+
+template <int KG, bool OUT, bool COMMIT>
+__global__ __launch_bounds__(kWave, KG == 8 ? 4 : (OUT && COMMIT) ? 2 : 3) void k_delta_rule_kg(
+    float* __restrict__ state, int64_t slots_total, const int64_t* __restrict__ slot, int t,
+    int heads, int rep, int dv, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ g, const float* __restrict__ beta,
+    const int64_t* __restrict__ lengths, float* __restrict__ out) {
+  static_assert(KG == 4 || KG == 8, "row groups of 32 or 16");
+  constexpr int DK = 128, QR = DK / KG, CW = 4 * kWave / KG;  // rows per group, columns per wave
+  const int nblk = dv / CW;
+  const int bh = blockIdx.x / nblk;  // row * heads + head; a matrix's blocks are adjacent ids
+  const int row = bh / heads, head = bh - row * heads;
+  const int lane = threadIdx.x, cg = lane / KG, kg = lane % KG;
+  const int base = (blockIdx.x - bh * nblk) * CW;  // the block's first column
+  const int col4 = base + 4 * cg;                   // this lane's first state column
+  const int64_t s_idx = slot ? slot[row] : row;
+  const int64_t o_row = (int64_t)head * dv + col4 + kg;  // kg < 4: the output column it writes
+  if (s_idx < 0 || s_idx >= slots_total) {  // no such slot: zero outputs, no state access
+    if (OUT && kg < 4)
+      for (int st = 0; st < t; ++st) out[((int64_t)row * t + st) * heads * dv + o_row] = 0.f;
+    return;  // uniform over the one-wave workgroup
+  }
+  const rsrc_t rsm = make_rsrc(state + ((s_idx * heads + head) * DK) * (int64_t)dv, (uint32_t)(DK * dv * 4));
+  const uint32_t voff = ((uint32_t)(QR * kg) * (uint32_t)dv + (uint32_t)col4) * 4u, drow = (uint32_t)dv * 4u;
+  f32x4_t s[QR];  // s[i] = row QR kg + i, columns col4 .. col4 + 3
+#pragma unroll
+  for (int i = 0; i < QR; ++i) s[i] = __builtin_bit_cast(f32x4_t, buf16(rsm, voff, drow * (uint32_t)i));
+  int n = t;
+  if (COMMIT) n = (int)min(max(lengths[row], (int64_t)0), (int64_t)t);
+  const int qk_heads = heads / rep, kh = head / rep;
+  // k and q pass through LDS as in the general form; step st + 1's inputs load while step st runs
+  __shared__ __attribute__((aligned(16))) float kq[2][2][DK];
+  float nk[2], nq[2], ng = 0.f, nbt = 0.f;
+  f32x4_t nv = {0.f, 0.f, 0.f, 0.f};
+  auto step_load = [&](int st) {
+    const int64_t rs = (int64_t)row * t + (st < n ? st : 0);
+    const int64_t qk_off = (rs * qk_heads + kh) * DK, hv = rs * heads + head;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      nk[p] = k[qk_off + p * kWave + lane];
+      nq[p] = OUT ? q[qk_off + p * kWave + lane] : 0.f;
+    }
+    nv = *reinterpret_cast<const f32x4_t*>(v + hv * dv + col4);
+    ng = g[hv];
+    nbt = beta[hv];
+  };
+  if (n > 0) step_load(0);
+  for (int st = 0; st < n; ++st) {
+    const int b = st & 1;
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      kq[b][0][p * kWave + lane] = nk[p];
+      if (OUT) kq[b][1][p * kWave + lane] = nq[p];
+    }
+    const float decay = __expf(ng), bt = nbt;
+    const f32x4_t vv = nv;
+    __syncthreads();  // this step's k and q are in LDS (a one-wave workgroup)
+    if (st + 1 < n) step_load(st + 1);
+    const float4* kk = reinterpret_cast<const float4*>(&kq[b][0][QR * kg]);
+    const float4* qq = reinterpret_cast<const float4*>(&kq[b][1][QR * kg]);
+    float m[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i4 = 0; i4 < QR / 4; ++i4) {
+      const float4 kv = kk[i4];
+      const float kr[4] = {kv.x, kv.y, kv.z, kv.w};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 4 * i4 + e;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          s[i][c] *= decay;
+          m[c] = fmaf(s[i][c], kr[e], m[c]);
+        }
+      }
+    }
+    float delta[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) delta[c] = (vv[c] - group_sum<KG>(m[c])) * bt;
+    asm volatile("" ::: "memory");
+    float o[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i4 = 0; i4 < QR / 4; ++i4) {
+      const float4 kv = kk[i4];
+      const float kr[4] = {kv.x, kv.y, kv.z, kv.w};
+      float qr[4] = {0.f, 0.f, 0.f, 0.f};
+      if (OUT) {
+        const float4 qv = qq[i4];
+        qr[0] = qv.x;
+        qr[1] = qv.y;
+        qr[2] = qv.z;
+        qr[3] = qv.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int i = 4 * i4 + e;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          s[i][c] = fmaf(kr[e], delta[c], s[i][c]);
+          if (OUT) o[c] = fmaf(s[i][c], qr[e], o[c]);
+        }
+      }
+    }
+    if (OUT) {
+      float mine = 0.f;  // column col4 + kg (kg < 4), by selects (no indexed registers)
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const float sum = group_sum<KG>(o[c]);
+        if (kg == c) mine = sum;
+      }
+      if (kg < 4) out[((int64_t)row * t + st) * heads * dv + o_row] = mine;
+    }
+  }
+  if (COMMIT) {
+#pragma unroll
+    for (int i = 0; i < QR; ++i)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, s[i]), rsm, (int)voff,
+                                             (int)(drow * (uint32_t)i), 0);
+  }
+}
+// Four row groups (164-168 VGPRs, three waves per SIMD): at config 5 (48 rows x 64 heads of
+// 128 x 128, t = 4) the verify pass takes 47.4 us against 52.9 us for the dword form; eight row
+// groups (four waves per SIMD) took 49.8 us. The commit (a state read and write, 83-88 us) is
+// at device-copy speed in every form.
+constexpr int kDnKG = 4;
+
 template <int DK, bool OUT, bool COMMIT>
 int launch_delta_rule(float* state, int64_t slots_total, const int64_t* slot, int rows, int t, int heads, int rep,
                       int dv, const float* q, const float* k, const float* v, const float* g,
                       const float* beta, const int64_t* lengths, float* out, hipStream_t st) {
+  constexpr int kCols = 4 * kWave / kDnKG;  // columns per wave of the k_dim = 128 form
+  if (DK == 128 && dv % kCols == 0 && aligned16(state) && aligned16(v)) {
+    const int64_t grid = (int64_t)rows * heads * (dv / kCols);
+    if (grid > INT32_MAX) return MTPK_EINVAL;
+    hipLaunchKernelGGL((k_delta_rule_kg<kDnKG, OUT, COMMIT>), dim3((unsigned)grid), dim3(kWave), 0, st, state, slots_total, slot, t, heads, rep, dv, q, k, v, g, beta, lengths, out);
+    return status_of(hipGetLastError());
+  }
   const int64_t grid = (int64_t)rows * heads * ((dv + kWave - 1) / kWave);
   if (grid > INT32_MAX) return MTPK_EINVAL;
   hipLaunchKernelGGL((k_delta_rule<DK, OUT, COMMIT>), dim3((unsigned)grid), dim3(kWave), 0, st, state, slots_total, slot, t, heads, rep, dv, q, k, v, g, beta, lengths, out);

@@ -103,6 +103,27 @@ def test_config5_batch_matches_oracle(dev) -> None:
     assert torch.isfinite(again).all()
 
 
+def test_config5_heads_out_of_range_slots_and_unit_lengths(dev) -> None:
+    """The k_dim = 128 form (16-byte state loads, quarter-row lanes): rows whose slot lies
+    outside the pool get zero outputs and touch no state; commit lengths of 0, 1 and t advance
+    each valid slot by exactly that prefix."""
+    pool, slots, q, k, v, g, beta = _case(21, 6, 4, 2, 128, 128, 4, 3)
+    bad = np.array([slots[0], 6, slots[2], -2], np.int64)
+    ok = [0, 2]
+    _, want = dn.delta_rule_rows(pool, bad[ok], q[ok], k[ok], v[ok], g[ok], beta[ok])
+    tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, bad, q, k, v, g, beta)
+    out = deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb).cpu().numpy()
+    np.testing.assert_allclose(out[ok], want, rtol=RTOL, atol=ATOL)
+    assert not out[[1, 3]].any()
+    assert torch.equal(tp.cpu(), torch.from_numpy(pool))
+    lengths = np.array([1, 3, 3, 0], np.int64)
+    want_pool, _ = dn.delta_rule_rows(pool, bad[ok], q[ok], k[ok], v[ok], g[ok], beta[ok], lengths[ok])
+    deltanet.delta_rule(tp, ts, tq, tk, tv, tg, tb, torch.from_numpy(lengths).to(dev), want_out=False)
+    np.testing.assert_allclose(tp.cpu().numpy(), want_pool, rtol=RTOL, atol=ATOL)
+    others = [sl for sl in range(6) if sl not in bad[ok]]
+    assert torch.equal(tp.cpu()[others], torch.from_numpy(pool)[others])
+
+
 def test_rejects_bad_shapes(dev) -> None:
     pool, slots, q, k, v, g, beta = _case(3, 4, 2, 1, 16, 16, 2, 2)
     tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, slots.astype(np.int64), q, k, v, g, beta)
