@@ -249,6 +249,24 @@ int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint
                    int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
                    int expert_hi, float* top_w, int32_t* top_i, void* workspace,
                    int64_t workspace_bytes, void* out, void* stream);
+
+/* mtpk_moe_layer followed by the residual form of the next RMSNorm, fused into the layer's last
+ * launch (the `x, h = add_rmsnorm(x, moe_out, w)` that starts the next decoder layer, or the
+ * final norm; model.py:587-604 with its residual add): sum_out = bf16(residual + out) and
+ * normed_out = sum_out * rsqrt(mean(sum_out^2) + eps) * (1 + norm_w), bf16 [tokens, hidden],
+ * each equal to mtpk_moe_layer's out followed by mtpk_rownorm's residual form bit for bit; the
+ * layer output itself is not stored. tokens > mtpk_moe_direct_max_tokens() (the work-unit path)
+ * and hidden 2048 or 4096; otherwise MTPK_EINVAL. */
+int mtpk_moe_layer_add_norm(const uint16_t* h, int64_t tokens, int64_t hidden,
+                            const uint16_t* router_gate, int64_t router_rows,
+                            const uint16_t* shared_gate_up, const uint16_t* shared_down,
+                            int64_t shared_inter, const uint8_t* gate_up,
+                            const uint8_t* gate_up_scale, const uint8_t* down,
+                            const uint8_t* down_scale, int64_t local_experts, int64_t inter_dim,
+                            int top_k, int expert_lo, int expert_hi, float* top_w, int32_t* top_i,
+                            void* workspace, int64_t workspace_bytes, const uint16_t* residual,
+                            const uint16_t* norm_w, float eps, uint16_t* sum_out,
+                            uint16_t* normed_out, void* stream);
 /* 1 when `mtpk_moe_layer` accepts these operands (given a large enough workspace), else 0: the
  * same checks, run without a launch and without dereferencing a pointer (pointers are tested
  * for null and 16-byte alignment only). Lets a caller choose the unfused launches up front, as

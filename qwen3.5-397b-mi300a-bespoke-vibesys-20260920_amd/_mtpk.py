@@ -95,6 +95,12 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
          c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_void_p, c_void_p,
          c_void_p, c_int64, c_void_p, c_void_p],
     ),
+    "mtpk_moe_layer_add_norm": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_void_p, c_void_p,
+         c_void_p, c_int64, c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p, c_void_p],
+    ),
     "mtpk_moe_layer_supported": (
         c_int,
         [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p,

@@ -210,4 +210,35 @@ __device__ inline int wave_incl_scan(int v, int lane) {
   return v;
 }
 
+// Eight consecutive f32 or bf16 values of p at element i, as floats (bf16: one 16-byte load), and
+// the inverse (bf16 rounded to nearest even); the row norms and the fused MoE combine + norm.
+__device__ inline void load8(const void* p, int dt, int64_t i, float* v) {
+  if (dt == MTPK_F32) {
+    const float* f = reinterpret_cast<const float*>(p) + i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = f[j];
+  } else {
+    const u32x4_t d = ld16(reinterpret_cast<const uint16_t*>(p) + i);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[2 * j] = bits_f32(d[j] << 16);
+      v[2 * j + 1] = bits_f32(d[j] & 0xffff0000u);
+    }
+  }
+}
+
+__device__ inline void store8(void* p, int dt, int64_t i, const float* v) {
+  if (dt == MTPK_F32) {
+    float* f = reinterpret_cast<float*>(p) + i;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) f[j] = v[j];
+  } else {
+    u32x4_t d;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      d[j] = (uint32_t)f32_to_bf16(v[2 * j]) | ((uint32_t)f32_to_bf16(v[2 * j + 1]) << 16);
+    *reinterpret_cast<u32x4_t*>(reinterpret_cast<uint16_t*>(p) + i) = d;
+  }
+}
+
 }  // namespace mtpk

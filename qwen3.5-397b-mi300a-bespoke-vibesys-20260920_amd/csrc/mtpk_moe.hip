@@ -1448,6 +1448,122 @@ __global__ __launch_bounds__(256) void k_moe_combine(
   for (int c = 0; c < 4; ++c) store_float(out, odt, (int64_t)t * H + n + c, acc[c]);
 }
 
+// The combine followed by the next norm's residual add, in one launch (the last launch of a MoE
+// layer whose output feeds `add_rmsnorm(x, moe_out, w)`, model.py:587-604): one workgroup of
+// 256 NCH threads per token, thread c taking the 8 columns 8c .. 8c + 7, which are chunk c / 256
+// of thread c % 256 in k_rownorm_row<NCH>. Each thread issues all of its loads at once (the live
+// assignments' y rows, the shared term's split-K planes, x and the norm weight), computes
+// k_moe_combine's value (the same j-order sum, shared term and bf16 rounding), then
+// s = bf16(x + value) and its squares; thread (i, r) continues the running sum of squares of
+// thread (i - 1, r) through LDS, so the sums the last 256 threads reduce are the row kernel's,
+// and y = s * rsqrt(mean(s^2) + eps) * (1 + w). sum_out and normed equal the combine launch
+// followed by the residual-form row norm bit for bit; the layer output itself is not stored.
+template <int NCH>
+__global__ __launch_bounds__(256 * NCH) void k_moe_combine_norm(
+    const float* __restrict__ y, const void* __restrict__ a_expert, int edt,
+    const void* __restrict__ a_weight, int wdt, int top_k, int H, int lo, int hi, SharedTerm st,
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ nw, float eps,
+    uint16_t* __restrict__ sum_out, uint16_t* __restrict__ normed) {
+  constexpr int G = kCombineGroup, kPl = 8;  // assignments per pass, shared planes held at once
+  __shared__ float run[256];
+  __shared__ float part[4];
+  const int t = blockIdx.x, tid = threadIdx.x, lane = tid & (kWave - 1);
+  const int chunk = tid >> 8, r = tid & 255;
+  const int n = tid * 8;  // == (r + 256 chunk) * 8
+  const int64_t base = (int64_t)t * H + n;
+  float xv[8], wn[8];
+  load8(x, MTPK_BF16, base, xv);
+  load8(nw, MTPK_BF16, n, wn);
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  for (int j0 = 0; j0 < top_k; j0 += G) {
+    float w[G];
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+      const int j = j0 + q;
+      w[q] = 0.f;
+      if (j < top_k) {
+        const int64_t a = (int64_t)t * top_k + j;
+        const int64_t e = load_index(a_expert, edt, a);
+        const float wv = load_float(a_weight, wdt, a);
+        if (e >= lo && e < hi) w[q] = wv;
+      }
+    }
+    u32x4_t yv[G][2];
+#pragma unroll
+    for (int q = 0; q < G; ++q) {
+      const float* row = y + ((int64_t)t * top_k + j0 + q) * H + n;
+      yv[q][0] = w[q] != 0.f ? ld16(row) : zero16();
+      yv[q][1] = w[q] != 0.f ? ld16(row + 4) : zero16();
+    }
+#pragma unroll
+    for (int q = 0; q < G; ++q)
+      if (w[q] != 0.f)
+#pragma unroll
+        for (int c = 0; c < 8; ++c) acc[c] += w[q] * bits_f32(yv[q][c >> 2][c & 3]);
+  }
+  float o[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) o[c] = round_to(MTPK_BF16, acc[c]);
+  if (shared_active(st)) {
+    const float gs = shared_gate(st, t, MTPK_BF16);
+    float sv[8];
+    if (st.part) {  // split-K planes summed in split order (shared_value's arithmetic)
+#pragma unroll
+      for (int c = 0; c < 8; ++c) sv[c] = 0.f;
+      for (int k0 = 0; k0 < st.ks; k0 += kPl) {
+        u32x4_t pv[kPl][2];
+#pragma unroll
+        for (int k = 0; k < kPl; ++k) {
+          const float* pl = st.part + (k0 + k) * st.plane + base;
+          pv[k][0] = k0 + k < st.ks ? ld16(pl) : zero16();
+          pv[k][1] = k0 + k < st.ks ? ld16(pl + 4) : zero16();
+        }
+#pragma unroll
+        for (int k = 0; k < kPl; ++k)
+          if (k0 + k < st.ks)
+#pragma unroll
+            for (int c = 0; c < 8; ++c) sv[c] += bits_f32(pv[k][c >> 2][c & 3]);
+      }
+#pragma unroll
+      for (int c = 0; c < 8; ++c) sv[c] = round_to(MTPK_BF16, sv[c]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) sv[c] = load_float(st.shared, st.sdt, base + c);
+    }
+#pragma unroll
+    for (int c = 0; c < 8; ++c) o[c] = o[c] + round_to(MTPK_BF16, gs * sv[c]);  // add_shared
+  }
+  float v[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) v[c] = round_to(MTPK_BF16, xv[c] + round_to(MTPK_BF16, o[c]));
+  store8(sum_out, MTPK_BF16, base, v);
+  // the row kernel's per-thread sum of squares runs over chunks 0 .. NCH - 1 in order
+  float ss = 0.f;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) {
+    if (i > 0) {
+      __syncthreads();
+      if (chunk == i) ss = run[r];
+    }
+    if (chunk == i) {
+#pragma unroll
+      for (int c = 0; c < 8; ++c) ss += v[c] * v[c];
+      if (i + 1 < NCH) run[r] = ss;
+    }
+  }
+  if (chunk == NCH - 1) {
+    ss = wave_sum(ss);
+    if (lane == 0) part[r / kWave] = ss;
+  }
+  __syncthreads();
+  ss = (part[0] + part[1]) + (part[2] + part[3]);
+  const float inv = rsqrtf(ss / (float)H + eps);
+  float yn[8];
+#pragma unroll
+  for (int c = 0; c < 8; ++c) yn[c] = (v[c] * inv) * (1.f + wn[c]);
+  store8(normed, MTPK_BF16, base, yn);
+}
+
 // The combine of rows that already carry their routing weight (the staging of a down
 // projection that applies the weight in its epilogue): out[t, n..n+3] = sum_j y[t*top_k + j]
 // over live assignments (expert in [lo, hi) and weight != 0; dead rows are never read), in j
@@ -2283,14 +2399,27 @@ int mtpk_moe_layer_supported(const void* h, int64_t tokens, int64_t hidden, cons
   return 1;
 }
 
-int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint16_t* router_gate,
-                   int64_t router_rows, const uint16_t* shared_gate_up,
-                   const uint16_t* shared_down, int64_t shared_inter, const uint8_t* gate_up,
-                   const uint8_t* gate_up_scale, const uint8_t* down, const uint8_t* down_scale,
-                   int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
-                   int expert_hi, float* top_w, int32_t* top_i, void* workspace,
-                   int64_t workspace_bytes, void* out, void* stream) {
-  if (!workspace || !out || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MTPK_EINVAL;
+}  // extern "C"
+
+namespace {
+
+// The next norm's residual form, fused into a layer's last launch (mtpk_moe_layer_add_norm).
+struct AddNorm {
+  const uint16_t* x;  // residual rows [tokens, hidden]
+  const uint16_t* w;  // norm weight [hidden]
+  float eps;
+  uint16_t* sum_out;  // x + the layer's output
+  uint16_t* normed;   // rmsnorm(sum_out) * (1 + w)
+};
+
+int moe_layer_run(const uint16_t* h, int64_t tokens, int64_t hidden, const uint16_t* router_gate,
+                  int64_t router_rows, const uint16_t* shared_gate_up,
+                  const uint16_t* shared_down, int64_t shared_inter, const uint8_t* gate_up,
+                  const uint8_t* gate_up_scale, const uint8_t* down, const uint8_t* down_scale,
+                  int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
+                  int expert_hi, float* top_w, int32_t* top_i, void* workspace,
+                  int64_t workspace_bytes, void* out, const AddNorm* an, void* stream) {
+  if (!workspace || (!out && !an) || (reinterpret_cast<uintptr_t>(workspace) & 255u) != 0) return MTPK_EINVAL;
   if (!mtpk_moe_layer_supported(h, tokens, hidden, router_gate, router_rows, shared_gate_up,
                                 shared_down, shared_inter, gate_up, gate_up_scale, down, down_scale,
                                 local_experts, inter_dim, top_k, expert_lo, expert_hi))
@@ -2345,6 +2474,7 @@ int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint
   const int tt = gemm_tt(tokens);
   static_assert(kDirectMaxTokens <= 16, "the direct path's GEMM tiles hold one token tile");
   if (tokens <= kDirectMaxTokens && single_gate_up_ok((int)hidden) && single_down_ok((int)inter_dim)) {
+    if (an) return MTPK_EINVAL;  // the direct path's down launch writes the output itself
     const UnitSrc src = unit_direct(ti, MTPK_I32, tw, MTPK_F32, expert_lo, expert_hi, a);
     const bool sv = (hidden / 32) % 32 == 0;
 #define MTPK_GSG(TT_)                                                                          \
@@ -2385,11 +2515,63 @@ int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint
   rc = mtpk_moe_down(inter, 2, a, inter_dim, down, down_scale, local_experts, hidden, sorted,
                      units, n_units, mu, y, stream);
   if (rc) return rc;
+  if (an) {
+    const dim3 g1((unsigned)tokens);
+#define MTPK_CN(N_)                                                                             \
+  hipLaunchKernelGGL(k_moe_combine_norm<N_>, g1, dim3(256 * N_), 0, st, y, ti, MTPK_I32, tw, MTPK_F32, \
+                     top_k, (int)hidden, expert_lo, expert_hi, sh, an->x, an->w, an->eps,          \
+                     an->sum_out, an->normed)
+    if (hidden == 2048)
+      MTPK_CN(1);
+    else
+      MTPK_CN(2);
+#undef MTPK_CN
+    return status_of(hipGetLastError());
+  }
   const dim3 grid((unsigned)((hidden / 4 + 255) / 256), (unsigned)tokens);
   hipLaunchKernelGGL(tokens < kCombineWideTokens ? k_moe_combine<kCombineGroup> : k_moe_combine<4>,
                      grid, dim3(256), 0, st, y, ti, MTPK_I32, tw, MTPK_F32, top_k,
                      (int)hidden, expert_lo, expert_hi, out, MTPK_BF16, sh);
   return status_of(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+int mtpk_moe_layer(const uint16_t* h, int64_t tokens, int64_t hidden, const uint16_t* router_gate,
+                   int64_t router_rows, const uint16_t* shared_gate_up,
+                   const uint16_t* shared_down, int64_t shared_inter, const uint8_t* gate_up,
+                   const uint8_t* gate_up_scale, const uint8_t* down, const uint8_t* down_scale,
+                   int64_t local_experts, int64_t inter_dim, int top_k, int expert_lo,
+                   int expert_hi, float* top_w, int32_t* top_i, void* workspace,
+                   int64_t workspace_bytes, void* out, void* stream) {
+  if (!out) return MTPK_EINVAL;
+  return moe_layer_run(h, tokens, hidden, router_gate, router_rows, shared_gate_up, shared_down,
+                       shared_inter, gate_up, gate_up_scale, down, down_scale, local_experts,
+                       inter_dim, top_k, expert_lo, expert_hi, top_w, top_i, workspace,
+                       workspace_bytes, out, nullptr, stream);
+}
+
+int mtpk_moe_layer_add_norm(const uint16_t* h, int64_t tokens, int64_t hidden,
+                            const uint16_t* router_gate, int64_t router_rows,
+                            const uint16_t* shared_gate_up, const uint16_t* shared_down,
+                            int64_t shared_inter, const uint8_t* gate_up,
+                            const uint8_t* gate_up_scale, const uint8_t* down,
+                            const uint8_t* down_scale, int64_t local_experts, int64_t inter_dim,
+                            int top_k, int expert_lo, int expert_hi, float* top_w, int32_t* top_i,
+                            void* workspace, int64_t workspace_bytes, const uint16_t* residual,
+                            const uint16_t* norm_w, float eps, uint16_t* sum_out,
+                            uint16_t* normed_out, void* stream) {
+  if (!residual || !norm_w || !sum_out || !normed_out) return MTPK_EINVAL;
+  if (tokens <= kDirectMaxTokens || (hidden != 2048 && hidden != 4096)) return MTPK_EINVAL;
+  if (!aligned16(residual) || !aligned16(norm_w) || !aligned16(sum_out) || !aligned16(normed_out))
+    return MTPK_EINVAL;
+  const AddNorm an{residual, norm_w, eps, sum_out, normed_out};
+  return moe_layer_run(h, tokens, hidden, router_gate, router_rows, shared_gate_up, shared_down,
+                       shared_inter, gate_up, gate_up_scale, down, down_scale, local_experts,
+                       inter_dim, top_k, expert_lo, expert_hi, top_w, top_i, workspace,
+                       workspace_bytes, nullptr, &an, stream);
 }
 
 }  // extern "C"

@@ -296,8 +296,7 @@ def draft_step(model, mtp: MTP, hid: torch.Tensor, tok: torch.Tensor, rope_pos: 
                               block_table, block_table.shape[1],
                               None if active is None else active[:, None])
     x, hm = vm.add_rmsnorm(x, attn, w["post_norm"], c.eps)
-    _, normed = vm.add_rmsnorm(x, model.moe(w, hm[:, 0])[:, None], mtp.norm, c.eps)
-    normed = normed[:, 0]
+    _, normed = model.moe_add_norm(w, hm[:, 0], x[:, 0], mtp.norm)
     nxt = model.next_tokens(normed)[:, None]
     return normed, nxt
 

@@ -20,6 +20,8 @@ the result is fp32-accurate rather than bf16-rounded in the middle.
 
 from __future__ import annotations
 
+import functools
+
 import os
 from collections.abc import Callable
 
@@ -310,7 +312,8 @@ def fused_moe_layer(
     out: torch.Tensor | None = None,
     workspace: torch.Tensor | None = None,
     routing_out: tuple[torch.Tensor, torch.Tensor] | None = None,
-) -> torch.Tensor:
+    add_norm: tuple[torch.Tensor, torch.Tensor, float] | None = None,
+):
     """The whole MoE layer of `Model.moe` (`model.py:2800-2873`) for bf16 rows `h` `[T, hidden]`:
     router GEMM (`router_gate` = the experts' router rows, then the shared gate's row, as
     `fuse_moe_dense` concatenates them, `model.py:913-928`), softmax top-k renormalised
@@ -326,6 +329,11 @@ def fused_moe_layer(
     `routing_out` = (top_w f32 [T, top_k], top_i int32 [T, top_k]) receives the routing when
     given. `workspace` is optional scratch of `layer_workspace_bytes(...)` bytes; without it the
     call takes the grow-only per-stream workspace `fused_moe` uses.
+
+    `add_norm = (x, w, eps)` fuses the next norm's residual form into the last launch and
+    returns `(x + out, rmsnorm(x + out, w, eps))` instead of `out`, both bf16 `[T, hidden]` and
+    bit-identical to `rownorm.add_rmsnorm(x, out, w, eps)` (`mtpk_moe_layer_add_norm`; only
+    for more than `direct_max_tokens()` rows and hidden 2048 or 4096, see `add_norm_supported`).
     """
     lo, hi = expert_range
     if h.dtype != torch.bfloat16 or h.dim() != 2 or not h.is_contiguous():
@@ -364,6 +372,30 @@ def fused_moe_layer(
     if nbytes <= 0:
         raise ValueError("unsupported fused_moe_layer sizes (tokens 1..256)")
     ws = _workspace(device, nbytes, workspace)
+    if add_norm is not None:
+        x, w_norm, eps = add_norm
+        if not add_norm_supported(tokens, hidden):
+            raise ValueError(f"add_norm takes more than {direct_max_tokens()} rows and hidden "
+                             "2048 or 4096")
+        if (x.shape != (tokens, hidden) or x.dtype != torch.bfloat16 or not x.is_contiguous()
+                or w_norm.shape != (hidden,) or w_norm.dtype != torch.bfloat16
+                or not w_norm.is_contiguous()):
+            raise ValueError("add_norm needs contiguous bf16 x [T, hidden] and w [hidden]")
+        total = torch.empty(tokens, hidden, dtype=h.dtype, device=device)
+        normed = torch.empty_like(total)
+        _mtpk.check(
+            lib.mtpk_moe_layer_add_norm(
+                h.data_ptr(), tokens, hidden, router_gate.data_ptr(), router_rows,
+                shared_gate_up.data_ptr(), shared_down.data_ptr(), shared_inter,
+                gate_up.data_ptr(), experts["gate_up_scale"].data_ptr(),
+                down.data_ptr(), experts["down_scale"].data_ptr(), local, intermediate,
+                top_k, lo, hi, tw_ptr, ti_ptr, ws.data_ptr(), ws.numel() * ws.element_size(),
+                x.data_ptr(), w_norm.data_ptr(), float(eps), total.data_ptr(), normed.data_ptr(),
+                _mtpk.stream_of(device),
+            ),
+            "mtpk_moe_layer_add_norm",
+        )  # fmt: skip
+        return total, normed
     _mtpk.check(
         lib.mtpk_moe_layer(
             h.data_ptr(), tokens, hidden, router_gate.data_ptr(), router_rows,
@@ -376,6 +408,17 @@ def fused_moe_layer(
         "mtpk_moe_layer",
     )  # fmt: skip
     return out
+
+
+@functools.lru_cache(maxsize=None)
+def direct_max_tokens() -> int:
+    """Rows up to which the MoE layer takes the direct path (`mtpk_moe_direct_max_tokens`)."""
+    return int(_mtpk.lib().mtpk_moe_direct_max_tokens())
+
+
+def add_norm_supported(tokens: int, hidden: int) -> bool:
+    """Whether `fused_moe_layer(..., add_norm=)` takes these sizes (the work-unit path)."""
+    return tokens > direct_max_tokens() and hidden in (2048, 4096)
 
 
 def workspace_bytes(tokens: int, top_k: int, local_experts: int, intermediate: int, hidden: int,

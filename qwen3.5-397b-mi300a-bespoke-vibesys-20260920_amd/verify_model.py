@@ -658,6 +658,26 @@ class Model:
                                               mxfp4.dequant_torch)
         return routed + torch.sigmoid(routing[:, c.experts :]) * shared
 
+    def moe_add_norm(self, w: dict, h: torch.Tensor, x: torch.Tensor,
+                     norm_w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """`add_rmsnorm(x, moe(w, h), norm_w)` with `x` of `h`'s rows: `(x + moe, normed)`. On
+        a device, where the whole-layer launches take `h`, the residual add and the norm ride in
+        the layer's last launch (`mxfp4_gemv.fused_moe_layer(add_norm=)`, the same bits)."""
+        c = self.cfg
+        rows = h.numel() // h.shape[-1]
+        if (h.device.type == "cuda" and self.route_log is None and mxfp4_gemv.available(h.device)
+                and x.dtype == torch.bfloat16 and norm_w.dtype == torch.bfloat16
+                and mxfp4_gemv.add_norm_supported(rows, c.hidden)):
+            hc = h.reshape(rows, -1).contiguous()
+            if mxfp4_gemv.layer_fits(hc, w["router_gate"], w["shared_gate_up"], w["shared_down"],
+                                     w["experts"], c.top_k, (0, c.experts)):
+                s, n = mxfp4_gemv.fused_moe_layer(
+                    hc, w["router_gate"], w["shared_gate_up"], w["shared_down"], w["experts"],
+                    c.top_k, (0, c.experts),
+                    add_norm=(x.reshape(rows, -1).contiguous(), norm_w.contiguous(), c.eps))
+                return s.view(x.shape), n.view(x.shape)
+        return add_rmsnorm(x, self.moe(w, h.reshape(rows, -1)).view(x.shape), norm_w, c.eps)
+
     def _layer_of(self, w: dict):
         for i, lw in enumerate(self.layers):
             if lw is w:
@@ -804,13 +824,10 @@ class Model:
         keep = None if active is None else active[:, None].expand(ids.shape[0], ids.shape[1])
         x = self.embed[ids.to(self.device)]
         res = VerifyOut(x)
-        pending = None  # the previous layer's MoE output, added in front of the next norm
+        n_layers = len(c.layer_types)
+        h = rmsnorm(x, self.layers[0]["in_norm"], c.eps)
         for i, ty in enumerate(c.layer_types):
             w, pool = self.layers[i], self.pool[i]
-            if pending is None:
-                h = rmsnorm(x, w["in_norm"], c.eps)
-            else:
-                x, h = add_rmsnorm(x, pending, w["in_norm"], c.eps)
             if ty == ATTN:
                 mixer = self.attention_rows(w, pool, h, lanes, base_pos, ctx_len, block_table, keep,
                                             positions)
@@ -818,12 +835,17 @@ class Model:
                 mixer, rows = self.deltanet_verify(w, pool, h, lanes)
                 res.dn_rows[i] = rows
             x, hm = add_rmsnorm(x, mixer, w["post_norm"], c.eps)
-            b, t, _ = hm.shape
-            pending = self.moe(w, hm.reshape(b * t, -1)).view(b, t, -1)
+            # the MoE output joins the residual stream in front of the next norm (the next
+            # layer's input norm, or the final norm): one fused launch where the layer allows
+            nxt = self.layers[i + 1]["in_norm"] if i + 1 < n_layers else (self.final_norm if final_norm else None)
+            if nxt is None:
+                b, t, _ = hm.shape
+                x = x + self.moe(w, hm.reshape(b * t, -1)).view(x.shape)
+            else:
+                x, h = self.moe_add_norm(w, hm, x, nxt)
+        res.hidden = x
         if final_norm:
-            res.hidden, res.normed = add_rmsnorm(x, pending, self.final_norm, c.eps)
-        else:
-            res.hidden = x + pending
+            res.normed = h
         return res
 
     def commit(self, res: VerifyOut, lanes, lengths: torch.Tensor,

@@ -14,6 +14,7 @@ import torch
 import dense
 import mxfp4_gemv
 import router_fused
+import rownorm
 from tests.test_gpu_moe import H, I, E, TOP_K, real_layer, torch_fp32_reference  # noqa: F401
 
 pytestmark = pytest.mark.gpu
@@ -64,6 +65,42 @@ def test_fused_layer_equals_the_unfused_launches(real_layer, dense_layer, tokens
     assert torch.equal(g_i, w_i)
     assert torch.equal(g_w, w_w)
     assert torch.equal(got, want)
+
+
+@pytest.mark.parametrize("tokens", [5, 48, 192, 256])
+def test_fused_add_norm_equals_the_layer_then_the_residual_norm(real_layer, dense_layer, tokens):
+    """`fused_moe_layer(add_norm=(x, w, eps))` (the combine, the residual add and the next
+    RMSNorm in the layer's last launch) returns `rownorm.add_rmsnorm(x, fused_moe_layer(h), w,
+    eps)` bit for bit, and the same routing."""
+    dev = torch.device("cuda:0")
+    print(f"fused MoE layer + add_norm M={tokens}", flush=True)
+    g = torch.Generator(dev).manual_seed(300 + tokens)
+    h = torch.randn(tokens, H, device=dev, generator=g).to(torch.bfloat16)
+    x = (torch.randn(tokens, H, device=dev, generator=g) * 4).to(torch.bfloat16)
+    w = (torch.randn(H, device=dev, generator=g) * 0.1).to(torch.bfloat16)
+    out, tw, ti = fused(h, dense_layer, real_layer)
+    want_s, want_n = rownorm.add_rmsnorm(x, out, w, 1e-6)
+    tw2 = torch.empty_like(tw)
+    ti2 = torch.empty_like(ti)
+    got_s, got_n = mxfp4_gemv.fused_moe_layer(h, dense_layer["router_gate"], dense_layer["shared_gate_up"],
+                                              dense_layer["shared_down"], real_layer, TOP_K, (0, E),
+                                              routing_out=(tw2, ti2), add_norm=(x, w, 1e-6))
+    assert torch.equal(ti2, ti) and torch.equal(tw2, tw)
+    assert torch.equal(got_s, want_s)
+    assert torch.equal(got_n, want_n)
+
+
+def test_fused_add_norm_refuses_the_direct_path(real_layer, dense_layer):
+    """At most `direct_max_tokens()` rows the layer's down launch writes its output itself: the
+    fused form is refused (callers take the layer and then the row norm)."""
+    dev = torch.device("cuda:0")
+    n = mxfp4_gemv.direct_max_tokens()
+    assert not mxfp4_gemv.add_norm_supported(n, H) and mxfp4_gemv.add_norm_supported(n + 1, H)
+    h = torch.randn(n, H, device=dev).to(torch.bfloat16)
+    with pytest.raises(ValueError):
+        mxfp4_gemv.fused_moe_layer(h, dense_layer["router_gate"], dense_layer["shared_gate_up"],
+                                   dense_layer["shared_down"], real_layer, TOP_K, (0, E),
+                                   add_norm=(h, torch.zeros(H, dtype=torch.bfloat16, device=dev), 1e-6))
 
 
 def layer_reference(h, dl, experts, top_i, top_w):
