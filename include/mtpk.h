@@ -461,6 +461,20 @@ int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, int64_t s
                      int64_t proj_stride, const int64_t* idx, int64_t batch, int64_t channels,
                      int64_t k1, int64_t t, void* stream);
 
+/* A DeltaNet layer's whole commit (`deltanet_verify_rollback`, model.py:3907-3972): the delta
+ * rule's commit mode (mtpk_delta_rule with lengths, no outputs) and the conv-window update
+ * (mtpk_conv_commit, conv_state of conv_slots_total slots) for the same rows and slots, in one
+ * launch when k_dim is 128 and v_dim a multiple of 64 (the conv rows run as extra one-wave
+ * workgroups beside the state stream), else as the two launches. The results are those of the
+ * two calls. */
+int mtpk_deltanet_commit(float* state, int64_t slots_total, const int64_t* slot, int64_t rows,
+                         int64_t t, int64_t heads, int64_t qk_heads, int64_t k_dim, int64_t v_dim,
+                         const float* q, const float* k, const float* v, const float* g,
+                         const float* beta, const int64_t* lengths, void* conv_state,
+                         int conv_dtype, int64_t conv_slots_total, const void* proj,
+                         int64_t proj_stride, const int64_t* conv_idx, int64_t channels, int64_t k1,
+                         void* stream);
+
 /* ---------------------------------------------------------------- skinny bf16 GEMM
  * y[M, N] = x[M, K] . w[N, K]^T for M <= 256 token rows, bf16 in, fp32 accumulation: the
  * weight-bandwidth-bound linears of the MTP draft and verify steps (fc, q/k/v/o and DeltaNet

@@ -128,6 +128,12 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         [c_void_p, c_int, c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64,
          c_int64, c_void_p],
     ),
+    "mtpk_deltanet_commit": (
+        c_int,
+        [c_void_p, c_int64, c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int64, c_void_p,
+         c_int64, c_void_p, c_int64, c_int64, c_void_p],
+    ),
     "mtpk_moe_dense_workspace_bytes": (c_int64, [c_int64, c_int64, c_int64, c_int64, c_int64]),
     "mtpk_moe_dense": (
         c_int,

@@ -157,18 +157,18 @@ __device__ inline float group_sum(float x) {
 }
 
 template <int KG, bool OUT, bool COMMIT>
-__global__ __launch_bounds__(kWave, KG == 8 ? 4 : (OUT && COMMIT) ? 2 : 3) void k_delta_rule_kg(
-    float* __restrict__ state, int64_t slots_total, const int64_t* __restrict__ slot, int t,
+__device__ inline void delta_rule_kg_body(
+    int bid, float* __restrict__ state, int64_t slots_total, const int64_t* __restrict__ slot, int t,
     int heads, int rep, int dv, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ g, const float* __restrict__ beta,
     const int64_t* __restrict__ lengths, float* __restrict__ out) {
   static_assert(KG == 4 || KG == 8, "row groups of 32 or 16");
   constexpr int DK = 128, QR = DK / KG, CW = 4 * kWave / KG;  // rows per group, columns per wave
   const int nblk = dv / CW;
-  const int bh = blockIdx.x / nblk;  // row * heads + head; a matrix's blocks are adjacent ids
+  const int bh = bid / nblk;  // row * heads + head; a matrix's blocks are adjacent ids
   const int row = bh / heads, head = bh - row * heads;
   const int lane = threadIdx.x, cg = lane / KG, kg = lane % KG;
-  const int base = (blockIdx.x - bh * nblk) * CW;  // the block's first column
+  const int base = (bid - bh * nblk) * CW;  // the block's first column
   const int col4 = base + 4 * cg;                   // this lane's first state column
   const int64_t s_idx = slot ? slot[row] : row;
   const int64_t o_row = (int64_t)head * dv + col4 + kg;  // kg < 4: the output column it writes
@@ -273,6 +273,16 @@ __global__ __launch_bounds__(kWave, KG == 8 ? 4 : (OUT && COMMIT) ? 2 : 3) void 
       __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4_t, s[i]), rsm, (int)voff,
                                              (int)(drow * (uint32_t)i), 0);
   }
+}
+
+template <int KG, bool OUT, bool COMMIT>
+__global__ __launch_bounds__(kWave, KG == 8 ? 4 : (OUT && COMMIT) ? 2 : 3) void k_delta_rule_kg(
+    float* __restrict__ state, int64_t slots_total, const int64_t* __restrict__ slot, int t,
+    int heads, int rep, int dv, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ g, const float* __restrict__ beta,
+    const int64_t* __restrict__ lengths, float* __restrict__ out) {
+  delta_rule_kg_body<KG, OUT, COMMIT>((int)blockIdx.x, state, slots_total, slot, t, heads, rep, dv,
+                                      q, k, v, g, beta, lengths, out);
 }
 // Four row groups (164-168 VGPRs, three waves per SIMD): at config 5 (48 rows x 64 heads of
 // 128 x 128, t = 4) the verify pass takes 47.4 us against 52.9 us for the dword form; eight row
@@ -409,14 +419,25 @@ __global__ __launch_bounds__(kPrepThreadsDn) void k_deltanet_prep(DnPrepArgs a) 
 // window becomes columns idx[b][0 .. k1) of [stored window | the t new raw columns]. A thread
 // owns one (row, channel) and reads all of its sources before it writes, so the in-place update
 // cannot read a value it has already replaced.
-__global__ __launch_bounds__(256) void k_conv_commit(void* __restrict__ conv, int dt,
-                                                     const int64_t* __restrict__ slot,
-                                                     int64_t slots_total,
-                                                     const void* __restrict__ proj,
-                                                     int64_t proj_stride, const int64_t* __restrict__ idx,
-                                                     int B, int C, int k1, int t) {
-  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
-  if (i >= (int64_t)B * C) return;
+struct ConvJob {
+  void* conv;
+  int dt;
+  const int64_t* slot;
+  int64_t slots_total;
+  const void* proj;
+  int64_t proj_stride;
+  const int64_t* idx;
+  int B, C, k1, t;
+};
+
+__device__ inline void conv_commit_one(const ConvJob& j, int64_t i) {
+  void* __restrict__ conv = j.conv;
+  const int dt = j.dt, C = j.C, k1 = j.k1, t = j.t;
+  const int64_t* __restrict__ slot = j.slot;
+  const int64_t* __restrict__ idx = j.idx;
+  const void* __restrict__ proj = j.proj;
+  const int64_t slots_total = j.slots_total, proj_stride = j.proj_stride;
+  if (i >= (int64_t)j.B * C) return;
   const int b = (int)(i / C), c = (int)(i - (int64_t)b * C);
   if (slot[b] < 0 || slot[b] >= slots_total) return;  // no such slot: nothing to update
   const int64_t base = (slot[b] * C + c) * k1;
@@ -428,6 +449,26 @@ __global__ __launch_bounds__(256) void k_conv_commit(void* __restrict__ conv, in
                   : load_float(proj, dt, ((int64_t)b * t + p - k1) * proj_stride + c);
   }
   for (int w = 0; w < k1; ++w) store_float(conv, dt, base + w, v[w]);
+}
+
+__global__ __launch_bounds__(256) void k_conv_commit(ConvJob j) {
+  conv_commit_one(j, (int64_t)blockIdx.x * 256 + threadIdx.x);
+}
+
+// A DeltaNet layer's whole commit in one launch: the delta rule's commit blocks (k_dim = 128
+// form) first, then one-wave blocks of the conv-window update, which run beside the state
+// stream instead of in a launch of their own.
+__global__ __launch_bounds__(kWave, 3) void k_dn_commit(
+    float* __restrict__ state, int64_t slots_total, const int64_t* __restrict__ slot, int t,
+    int heads, int rep, int dv, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ g, const float* __restrict__ beta,
+    const int64_t* __restrict__ lengths, int dr_blocks, ConvJob cj) {
+  if ((int)blockIdx.x >= dr_blocks) {  // uniform over the one-wave workgroup
+    conv_commit_one(cj, ((int64_t)blockIdx.x - dr_blocks) * kWave + threadIdx.x);
+    return;
+  }
+  delta_rule_kg_body<kDnKG, false, true>((int)blockIdx.x, state, slots_total, slot, t, heads, rep,
+                                         dv, q, k, v, g, beta, lengths, nullptr);
 }
 
 }  // namespace mtpk
@@ -503,9 +544,48 @@ int mtpk_conv_commit(void* conv_state, int dtype, const int64_t* slot, int64_t s
   if (batch * channels > INT32_MAX) return MTPK_EINVAL;
   if (batch == 0) return 0;
   const int64_t n = batch * channels;
+  const ConvJob cj{conv_state, dtype, slot, slots_total, proj, proj_stride, idx,
+                   (int)batch, (int)channels, (int)k1, (int)t};
   hipLaunchKernelGGL(k_conv_commit, dim3((unsigned)((n + 255) / 256)), dim3(256), 0,
-                     (hipStream_t)stream, conv_state, dtype, slot, slots_total, proj, proj_stride, idx,
-                     (int)batch, (int)channels, (int)k1, (int)t);
+                     (hipStream_t)stream, cj);
+  return status_of(hipGetLastError());
+}
+
+int mtpk_deltanet_commit(float* state, int64_t slots_total, const int64_t* slot, int64_t rows,
+                         int64_t t, int64_t heads, int64_t qk_heads, int64_t k_dim, int64_t v_dim,
+                         const float* q, const float* k, const float* v, const float* g,
+                         const float* beta, const int64_t* lengths, void* conv_state,
+                         int conv_dtype, int64_t conv_slots_total, const void* proj,
+                         int64_t proj_stride, const int64_t* conv_idx, int64_t channels, int64_t k1,
+                         void* stream) {
+  constexpr int kCols = 4 * kWave / kDnKG;
+  if (!lengths || !slot) return MTPK_EINVAL;
+  const bool fused = k_dim == 128 && v_dim % kCols == 0 && aligned16(state) && aligned16(v) &&
+                     rows * heads * (v_dim / kCols) + (rows * channels + kWave - 1) / kWave <= INT32_MAX;
+  if (!fused) {  // the two launches
+    const int rc = mtpk_delta_rule(state, slots_total, slot, rows, t, heads, qk_heads, k_dim, v_dim,
+                                   q, k, v, g, beta, lengths, nullptr, stream);
+    if (rc) return rc;
+    return mtpk_conv_commit(conv_state, conv_dtype, slot, conv_slots_total, proj, proj_stride,
+                            conv_idx, rows, channels, k1, t, stream);
+  }
+  // the argument checks of both launches
+  if (!state || !q || !k || !v || !g || !beta || !conv_state || !proj || !conv_idx) return MTPK_EINVAL;
+  if (rows < 0 || t < 1 || t > INT32_MAX / 2 || heads <= 0 || qk_heads <= 0 || heads % qk_heads)
+    return MTPK_EINVAL;
+  if (v_dim > 4096 || slots_total <= 0) return MTPK_EINVAL;
+  if (slots_total * heads * k_dim * v_dim >= (int64_t(1) << 40)) return MTPK_EINVAL;
+  if (conv_dtype != MTPK_F32 && conv_dtype != MTPK_BF16) return MTPK_EINVAL;
+  if (channels < 1 || k1 < 1 || k1 > kConvMaxK1 || proj_stride < channels || conv_slots_total < 1)
+    return MTPK_EINVAL;
+  if (rows == 0) return 0;
+  const int dr = (int)(rows * heads * (v_dim / kCols));
+  const int64_t conv_blocks = (rows * channels + kWave - 1) / kWave;
+  const ConvJob cj{conv_state, conv_dtype, slot, conv_slots_total, proj, proj_stride, conv_idx,
+                   (int)rows, (int)channels, (int)k1, (int)t};
+  hipLaunchKernelGGL(k_dn_commit, dim3((unsigned)(dr + conv_blocks)), dim3(kWave), 0,
+                     (hipStream_t)stream, state, slots_total, slot, (int)t, (int)heads,
+                     (int)(heads / qk_heads), (int)v_dim, q, k, v, g, beta, lengths, dr, cj);
   return status_of(hipGetLastError());
 }
 

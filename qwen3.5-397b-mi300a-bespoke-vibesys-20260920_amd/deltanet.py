@@ -68,6 +68,43 @@ def delta_rule(state: torch.Tensor, slots: torch.Tensor | None, q: torch.Tensor,
     return out
 
 
+def commit(state: torch.Tensor, conv_state: torch.Tensor, slots: torch.Tensor, q: torch.Tensor,
+           k: torch.Tensor, v: torch.Tensor, g: torch.Tensor, beta: torch.Tensor,
+           lengths: torch.Tensor, proj: torch.Tensor, idx: torch.Tensor, channels: int) -> None:
+    """`delta_rule(state, slots, q, k, v, g, beta, lengths, want_out=False)` and
+    `conv_commit(conv_state, slots, proj, idx, channels)` as one launch where the layer's sizes
+    allow it (`mtpk_deltanet_commit`); same arguments, same results."""
+    device = _mtpk.require_device(state, conv_state, slots, q, k, v, g, beta, lengths, proj, idx)
+    if state.dtype != torch.float32 or state.dim() != 4 or not state.is_contiguous():
+        raise ValueError("state must be a contiguous f32 [slots, heads, k_dim, v_dim] tensor")
+    n_slots, heads, k_dim, v_dim = state.shape
+    rows, t, qk_heads, qk_dim = q.shape
+    if k.shape != q.shape or qk_dim != k_dim or heads % qk_heads or k_dim not in (16, 32, 64, 128):
+        raise ValueError("q/k do not match the state")
+    if (tuple(v.shape) != (rows, t, heads, v_dim) or tuple(g.shape) != (rows, t, heads)
+            or tuple(beta.shape) != (rows, t, heads)):
+        raise ValueError("v/g/beta do not match q and the state")
+    if tuple(slots.shape) != (rows,) or tuple(lengths.shape) != (rows,):
+        raise ValueError(f"slots and lengths must be [{rows}]")
+    rs = _mtpk.row_stride(proj)
+    if proj.shape[:2] != (rows, t) or proj.stride(2) != 1 or rs is None:
+        raise ValueError("proj must be [B, t, P] with contiguous rows")
+    if proj.dtype != conv_state.dtype or not conv_state.is_contiguous():
+        raise ValueError("conv_state must be contiguous and of proj's dtype")
+    k1 = conv_state.shape[-1]
+    ix = idx.to(torch.int64).contiguous()
+    if ix.shape != (rows, k1):
+        raise ValueError(f"idx must be [{rows}, {k1}]")
+    sl = slots.to(device, torch.int64).contiguous()
+    ln = lengths.to(device, torch.int64).contiguous()
+    f32 = [x.to(torch.float32).contiguous() for x in (q, k, v, g, beta)]
+    _mtpk.check(_mtpk.lib().mtpk_deltanet_commit(
+        state.data_ptr(), n_slots, sl.data_ptr(), rows, t, heads, qk_heads, k_dim, v_dim,
+        *(x.data_ptr() for x in f32), ln.data_ptr(), conv_state.data_ptr(),
+        _mtpk.float_code(conv_state.dtype), conv_state.shape[0], proj.data_ptr(), rs, ix.data_ptr(),
+        channels, k1, _mtpk.stream_of(device)), "mtpk_deltanet_commit")  # fmt: skip
+
+
 def prep(proj: torch.Tensor, conv_state: torch.Tensor, slots: torch.Tensor, conv_w: torch.Tensor,
          a_log: torch.Tensor, dt_bias: torch.Tensor, k_heads: int, k_dim: int, v_heads: int,
          v_dim: int, eps: float = 1e-6) -> tuple[torch.Tensor, ...]:

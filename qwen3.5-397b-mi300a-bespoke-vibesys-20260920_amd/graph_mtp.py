@@ -17,6 +17,7 @@ from dataclasses import dataclass
 import torch
 
 import _mtpk
+import rownorm
 import mtp as mtp_mod
 import verify_model as vm
 
@@ -76,6 +77,7 @@ class MTPVerifyBuffers:
         self.write_rows = torch.zeros(capacity, t, **long)
         self.slot_rows = torch.zeros(capacity, **long)
         self.draft_hidden = torch.zeros(capacity, hidden, dtype=dtype, device=device)
+        self.draft_seed = torch.zeros(capacity, hidden, dtype=dtype, device=device)  # its final norm
         self.step_argmax = torch.zeros(capacity, t, **long)
         self.accept_len = torch.zeros(capacity, **long)
         self.budget = torch.full((capacity,), t, **long)
@@ -249,7 +251,10 @@ def _draft_rows(model, m, buf: MTPVerifyBuffers) -> None:
     fill-time copy `buf.draft_hidden`, reading the MTP cache through `buf.block_table`. A row
     with `forced_n[j] > 0` feeds (and keeps) its forced tokens instead of its first drafts.
     Padding rows (`active` False) write no MTP cache row. No host read."""
-    hid = mtp_mod.draft_seed(model, buf.draft_hidden)
+    if buf.draft_hidden.is_cuda:  # the seed kept in the buffer: the verify's MTP cache rows reuse it
+        hid = rownorm.rmsnorm(buf.draft_hidden, model.final_norm, model.cfg.eps, out=buf.draft_seed)
+    else:
+        hid = mtp_mod.draft_seed(model, buf.draft_hidden)
     tok = buf.token_matrix[:, :1]
     on_device = vm.kv_write_in_kernel(model)
     for s in range(m.k):
@@ -315,12 +320,20 @@ def _verify_rows(model, m, buf: MTPVerifyBuffers, ctx_len: int) -> None:
     else:
         model.commit(res, slots, out.lengths, conv_idx=out.conv_idx, active=active)
     grid = buf.pos_grid
-    previous = torch.cat([buf.draft_hidden[:, None], res.hidden[:, :-1]], dim=1)
+    if dev.type == "cuda":
+        # the final-normed previous rows: the draft's seed, then the forward's own normed rows
+        # (the same kernel over the same values as `draft_seed` of the raw rows)
+        previous = torch.cat([buf.draft_seed[:, None], res.normed[:, :-1]], dim=1)
+        seeded = True
+    else:
+        previous = torch.cat([buf.draft_hidden[:, None], res.hidden[:, :-1]], dim=1)
+        seeded = False
     if vm.kv_write_in_kernel(model):
         mtp_mod.cache_target_rows(model, m, buf.token_matrix, previous, grid, None, out.keep,
-                                  block_table=buf.block_table, base_pos=pos)
+                                  block_table=buf.block_table, base_pos=pos, seeded=seeded)
     else:
-        mtp_mod.cache_target_rows(model, m, buf.token_matrix, previous, grid, buf.write_rows, out.keep)
+        mtp_mod.cache_target_rows(model, m, buf.token_matrix, previous, grid, buf.write_rows, out.keep,
+                                  seeded=seeded)
     if dev.type == "cuda":  # one launch: slot commit_slots[j] <- verify row hidden_src[j]
         copy_rows(res.hidden.reshape(b * t, -1), out.hidden_src, model.hidden_cache, buf.commit_slots)
     else:

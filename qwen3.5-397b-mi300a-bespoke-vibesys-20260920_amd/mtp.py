@@ -325,17 +325,19 @@ def draft(model, mtp: MTP, hidden: torch.Tensor, tokens: list[int], slots: list[
 def cache_target_rows(model, mtp: MTP, tokens: torch.Tensor, raw_previous_hidden: torch.Tensor,
                       positions: torch.Tensor, write_rows: torch.Tensor | None,
                       keep: torch.Tensor | None = None, *, block_table: torch.Tensor | None = None,
-                      base_pos: torch.Tensor | None = None) -> None:
+                      base_pos: torch.Tensor | None = None, seeded: bool = False) -> None:
     """Write the MTP layer's canonical K/V for fed tokens from the target's hidden stream
     (`mtp.py:440-485`): token `tokens[b, s]` at `positions[b, s]` paired with the target's raw
     hidden state of the previous position. Rows with `keep` False are left as they are.
     When `verify_model.kv_write_in_kernel(model)`, `block_table` `[B, blocks]` with `base_pos`
     `[B]` (`positions[b, s] = base_pos[b] + s`) replace `write_rows`: RoPE rides on the k norm
-    and one kernel writes the K/V rows through the table."""
+    and one kernel writes the K/V rows through the table. `seeded`: the hidden rows given are
+    already final-normed (`draft_seed` of the raw ones, e.g. the forward's own normed rows)."""
     import verify_model as vm
 
     c, w = model.cfg, mtp.weights
-    x = _combine_rows(model, mtp, draft_seed(model, raw_previous_hidden), tokens)
+    seed = raw_previous_hidden if seeded else draft_seed(model, raw_previous_hidden)
+    x = _combine_rows(model, mtp, seed, tokens)
     x = vm.rmsnorm(x, w["in_norm"], c.eps)
     lead = tokens.shape
     if vm.kv_write_in_kernel(model) and block_table is not None and base_pos is not None:

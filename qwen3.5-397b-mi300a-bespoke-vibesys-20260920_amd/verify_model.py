@@ -778,14 +778,15 @@ class Model:
         if self.device.type == "cuda":
             # the kernels skip a row whose slot lies outside the pool: padding commits nothing
             slots = lanes if active is None else torch.where(active, lanes, torch.full_like(lanes, -1))
-            if rows.proj is not None:
-                deltanet.conv_commit(pool["conv"], slots, rows.proj, idx, c.conv_dim)
-            else:
-                window = torch.cat([pool["conv"][lanes], rows.raw_qkv], dim=-1)  # [B, C, k1 + t]
-                new = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
-                if active is not None:
-                    new = torch.where(active[:, None, None], new, pool["conv"][lanes])
-                pool["conv"][lanes] = new
+            if rows.proj is not None:  # the state and the conv window in one launch
+                deltanet.commit(pool["rec"], pool["conv"], slots, rows.q, rows.k, rows.v, rows.g,
+                                rows.beta, n, rows.proj, idx, c.conv_dim)
+                return
+            window = torch.cat([pool["conv"][lanes], rows.raw_qkv], dim=-1)  # [B, C, k1 + t]
+            new = torch.gather(window, 2, idx[:, None, :].expand(-1, window.shape[1], -1))
+            if active is not None:
+                new = torch.where(active[:, None, None], new, pool["conv"][lanes])
+            pool["conv"][lanes] = new
             deltanet.delta_rule(pool["rec"], slots, rows.q, rows.k, rows.v, rows.g, rows.beta, n,
                                 want_out=False)
             return

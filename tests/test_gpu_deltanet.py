@@ -124,6 +124,30 @@ def test_config5_heads_out_of_range_slots_and_unit_lengths(dev) -> None:
     assert torch.equal(tp.cpu()[others], torch.from_numpy(pool)[others])
 
 
+@pytest.mark.parametrize("shape", [(9, 8, 2, 128, 128, 6, 3), (5, 4, 2, 16, 16, 3, 4)])
+def test_one_launch_commit_equals_the_two(dev, shape) -> None:
+    """`deltanet.commit` (`mtpk_deltanet_commit`: the state and the conv window in one launch at
+    k_dim 128, the two launches otherwise) leaves both pools exactly as `delta_rule(...,
+    lengths)` followed by `conv_commit` does, padding rows (slot -1) included."""
+    pool, slots, q, k, v, g, beta = _case(40 + sum(shape), *shape)
+    b, t = q.shape[:2]
+    slots = slots.astype(np.int64)
+    slots[-1] = -1  # a padding row
+    lengths = (np.arange(b) % (t + 1)).astype(np.int64)
+    gen = torch.Generator().manual_seed(3)
+    c, k1, n_conv = 40, 3, pool.shape[0]
+    proj = torch.randn(b, t, c + 8, generator=gen).to(torch.bfloat16).to(dev)
+    conv = torch.randn(n_conv, c, k1, generator=gen).to(torch.bfloat16).to(dev)
+    idx = (torch.from_numpy(lengths)[:, None] + torch.arange(k1)).clamp(max=k1 + t - 1).to(dev)
+    tp, ts, tq, tk, tv, tg, tb, tl = _dev(dev, pool, slots, q, k, v, g, beta, lengths)
+    want_p, want_c = tp.clone(), conv.clone()
+    deltanet.delta_rule(want_p, ts, tq, tk, tv, tg, tb, tl, want_out=False)
+    deltanet.conv_commit(want_c, ts, proj, idx, c)
+    deltanet.commit(tp, conv, ts, tq, tk, tv, tg, tb, tl, proj, idx, c)
+    assert torch.equal(tp, want_p)
+    assert torch.equal(conv, want_c)
+
+
 def test_rejects_bad_shapes(dev) -> None:
     pool, slots, q, k, v, g, beta = _case(3, 4, 2, 1, 16, 16, 2, 2)
     tp, ts, tq, tk, tv, tg, tb = _dev(dev, pool, slots.astype(np.int64), q, k, v, g, beta)
