@@ -610,6 +610,7 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
     """Config 5: speculative rounds (draft k steps, verify B*(k+1) rows, accept, commit)."""
     import torch
 
+    import blas_tune
     import graph_mtp
     import mtp
     import verify_model as vm
@@ -619,9 +620,13 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
                      expert_mode="bytes", moe_rows=b * (k + 1))
     mtp.attach(model, k=k, seed=1, expert_mode="bytes")
     # boot: capture the B-row bucket and validate the replay against the eager round
-    runner = graph_mtp.GraphMTPRunner(model, buckets=[b])
+    # boot also tunes the round's library GEMMs before the capture (blas_tune)
+    runner = graph_mtp.GraphMTPRunner(model, buckets=[b], tune_blas=True)
+    t_boot = time.perf_counter()
     validated = runner.prepare()
-    log(f"mtp round: captured bucket {b}, validation {'passed' if validated else 'FAILED (eager rounds)'}")
+    tuned = sorted(blas_tune.tuned_shapes())
+    log(f"mtp round: captured bucket {b} in {time.perf_counter() - t_boot:.1f}s, validation "
+        f"{'passed' if validated else 'FAILED (eager rounds)'}, tuned library GEMMs (m, n, k) {tuned}")
     start = ctx - 32
     for lane in range(b):
         model.blocks.grow(lane, start)
@@ -694,6 +699,7 @@ def mtp_round_bench(dev, b=48, k=3, ctx=8192, rounds=8):
         "weights": "random init (draft acceptance near zero)",
         "runner": "GraphMTPRunner (draft + verify + accept + commit replayed as one HIP graph)",
         "capture_validated": bool(validated),
+        "blas_tuned": [list(x) for x in tuned],
         "forced_full_accept": {
             "ms_per_round": round(f_wall * 1e3 / rounds, 3),
             "committed_per_round": round(f_committed / rounds, 2),

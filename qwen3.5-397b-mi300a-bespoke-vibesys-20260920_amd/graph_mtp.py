@@ -17,6 +17,7 @@ from dataclasses import dataclass
 import torch
 
 import _mtpk
+import blas_tune
 import rownorm
 import mtp as mtp_mod
 import verify_model as vm
@@ -651,11 +652,19 @@ class GraphMTPRunner(MTPVerifyRunner):
     the captured round, and rounds then run eagerly, or, under `SEED_MTP_REQUIRE_GRAPH=1`,
     `prepare()` raises. Without `prepare()`, a bucket is captured on its first round (which
     runs eagerly) and is not validated. `backend` is the capture backend: None for HIP graphs,
-    or `EagerBackend()`."""
+    or `EagerBackend()`. `tune_blas` (None: `MTPK_BLAS_TUNE=1` in the environment) runs each
+    bucket's eager round before its capture inside a `blas_tune.session`, so the round's library
+    GEMMs are captured with their tuned solutions (the reference's startup tuning,
+    `blas_tune.py:178-255`); it applies on a ROCm GPU only."""
 
     def __init__(self, model, backend=None, *, capacity: int | None = None,
-                 buckets: list[int] | None = None) -> None:
+                 buckets: list[int] | None = None, tune_blas: bool | None = None) -> None:
+        import os
+
         super().__init__(model, None, capacity, buckets)
+        if tune_blas is None:
+            tune_blas = os.environ.get("MTPK_BLAS_TUNE", "0") == "1"
+        self.tune_blas = bool(tune_blas)
         self.backend = CudaGraphBackend() if backend is None else backend
         self.graphs: dict[int, Callable[[], None]] = {}
         self.enabled = True
@@ -679,7 +688,8 @@ class GraphMTPRunner(MTPVerifyRunner):
 
     def _eager_round(self, buf: MTPVerifyBuffers) -> None:
         """The bucket's round run eagerly before its capture, on a side stream on a device (so
-        every lazy allocation and library handle exists before capture begins)."""
+        every lazy allocation and library handle exists before capture begins), and with
+        `tune_blas` inside a tuning session (so every library GEMM shape is searched first)."""
         dev = buf.pos.device
         if dev.type != "cuda":
             self._round(buf)
@@ -687,7 +697,11 @@ class GraphMTPRunner(MTPVerifyRunner):
         side = torch.cuda.Stream(dev)
         side.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(side):
-            self._round(buf)
+            if self.tune_blas and blas_tune.available():
+                with blas_tune.session(dev):
+                    self._round(buf)
+            else:
+                self._round(buf)
         torch.cuda.current_stream().wait_stream(side)
         torch.cuda.synchronize(dev)
 

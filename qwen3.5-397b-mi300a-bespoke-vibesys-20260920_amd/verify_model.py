@@ -32,6 +32,7 @@ import torch
 import torch.nn.functional as F
 
 import attention
+import blas_tune
 import deltanet
 import dense
 import mxfp4
@@ -113,12 +114,15 @@ MI355X; larger ones at <= 64 rows are bandwidth bound and the library GEMM is as
 
 
 def _dense_wide_rows(rows: int, w: torch.Tensor) -> bool:
-    """65..256 rows: the skinny GEMM's row groups beat the library GEMM on 2048..4096 output
-    rows with K >= 1024 (measured at 192 rows: [4096, 8192] 47 against 61 us, [4096, 1024] 10.2
-    against 11.4 us), where the library's tiles leave most of the GPU idle; wider N stays on the
-    library GEMM (the 192-row LM head: 881 against 494 us)."""
+    """65..256 rows: the skinny GEMM's row groups beat the library GEMM's default solution on
+    2048..4096 output rows with K >= 1024 (measured at 192 rows: [4096, 8192] 47 against 61 us,
+    [4096, 1024] 10.2 against 11.4 us), where the default tiles leave most of the GPU idle; wider
+    N stays on the library GEMM (the 192-row LM head: 881 against 494 us). A K >= 8192 shape
+    with a tuned library solution goes back to the library (`blas_tune`: 34.5 us at [4096, 8192])."""
     n, k = w.shape
-    return 64 < rows <= dense.MAX_ROWS and 2048 <= n <= 4096 and k >= 1024
+    if not (64 < rows <= dense.MAX_ROWS and 2048 <= n <= 4096 and k >= 1024):
+        return False
+    return not (k >= 8192 and blas_tune.prefers_library(rows, n, k))
 
 
 FUSED_ARGMAX_ROWS = 192
