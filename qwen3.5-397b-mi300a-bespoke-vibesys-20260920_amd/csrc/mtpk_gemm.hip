@@ -61,7 +61,8 @@ int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
   return status_of(hipGetLastError());
 }
 
-// The wide form (`gemm_wide`, 65..192 token rows on wide N: the verify LM head).
+// The wide form (`gemm_wide`, 17..192 token rows on wide N: the LM heads of the draft step, 48
+// rows, and of the verify step, 192 rows).
 // One workgroup of NW waves per 16 NW RT weight rows, one workgroup per CU. Wave w owns weight
 // rows 16 RT w .. + 16 RT - 1 (RT row tiles) against all TT token tiles, so one staged A
 // fragment feeds RT MFMAs and one weight fragment TT.
@@ -82,7 +83,9 @@ int launch_gemm_pair(const GemmArgs& a, const GemmArgs& b, hipStream_t st) {
 // Measured there (graph replay over two weight copies, MI355X): 552 us with the argmax epilogue
 // against 496 us for the library GEMM alone and 521 us with its argmax pass; the token rows'
 // staging (75% of the weight bytes: 192 rows against 256 per tile, the most the register file
-// holds accumulators for) costs about 100 us of it. The model keeps the library GEMM at 192 rows.
+// holds accumulators for) costs about 100 us of it. The verify head's later form (the 8-wave,
+// 2-row-tile configuration below) runs it in 506.5 us against 519-520 us for the library GEMM
+// and its argmax pass.
 // Epilogues: store (fp32 or bf16) or the first-occurrence argmax keys of bf16(y) per tile.
 template <int TT, int NW, int RT, int KC, int NB, int D>
 struct Wide {
@@ -97,10 +100,11 @@ struct Wide {
 // 8 waves x 2 row tiles (two waves per SIMD, 195 VGPRs) measured 566-575 us against 637 us for
 // 4 waves x 4 row tiles (accumulators shuffled between AGPRs and VGPRs in the loop); NB = 3
 // against 4, D = 8 against 4 and 128-K chunks were equal or slower.
-constexpr int kWideNW = 8, kWideRT = 2, kWideKC = 64, kWideNB = 3, kWideD = 4;
-template <int TT>
-using WideCfg = Wide<TT, kWideNW, kWideRT, kWideKC, kWideNB, kWideD>;
-constexpr int kWideRows = 16 * kWideRT * kWideNW;
+// At <= 64 rows (4 token tiles) the same form with RT = 4, 512-row tiles (194 VGPRs, one
+// workgroup per CU): 372-373 us at 48 rows against 393-395 us with RT = 2, where the token rows
+// are staged for twice as many tiles; NB = 4, 128-K chunks and 3 token tiles of 256-K chunks
+// were equal or slower.
+constexpr int kWideNW = 8, kWideKC = 64, kWideNB = 3, kWideD = 4;
 constexpr int kWideKStep = kWideKC * (kWideD / (kWideKC / 32));  // K per loop turn
 
 template <int TT, int NW, int RT, int KC, int NB, int D>
@@ -255,9 +259,9 @@ __global__ __launch_bounds__(NW * kWave, 1) void k_gemm_wide(GemmArgs a) {
     }
 }
 
-template <int TT>
+template <int TT, int RT>
 void launch_wide(const GemmArgs& a, int tiles, hipStream_t st) {
-  hipLaunchKernelGGL((k_gemm_wide<TT, kWideNW, kWideRT, kWideKC, kWideNB, kWideD>),
+  hipLaunchKernelGGL((k_gemm_wide<TT, kWideNW, RT, kWideKC, kWideNB, kWideD>),
                      dim3((unsigned)tiles), dim3(kWideNW * kWave), 0, st, a);
 }
 
@@ -360,10 +364,12 @@ int mtpk_gemm_bf16(const uint16_t* x, int64_t m, int64_t k, const uint16_t* w, i
     a.RG = 1;
     const int wtt = (int)((m + 15) / 16);
     static_assert(kGemmKC % kWideKStep == 0, "K (a multiple of kGemmKC) fills whole loop turns");
-    if (wtt <= 8)
-      launch_wide<8>(a, tiles, st);
+    if (wtt <= 4)
+      launch_wide<4, 4>(a, tiles, st);
+    else if (wtt <= 8)
+      launch_wide<8, 2>(a, tiles, st);
     else
-      launch_wide<12>(a, tiles, st);
+      launch_wide<12, 2>(a, tiles, st);
   } else if (epilogue == kEpiSilu)
     launch_gemm_tt<2, true>(a, tt, tiles, st);
   else

@@ -281,18 +281,23 @@ inline int gemm_waves(int64_t m, int64_t n, int epi) {
   return (m + 15) / 16 >= 3 && cols / 128 >= 2 * (int64_t)device_cu_count() ? 8 : 4;
 }
 
-// The wide form for 65..192 token rows on wide N (the verify LM head, mtpk_gemm.hip
-// k_gemm_wide): one row group of TT = ceil(M / 16) token tiles against 256-row weight tiles, the
-// token rows staged by direct-to-LDS loads. Every weight is read once for all rows; the 64-row
-// groups would stream the tile's weights once per group.
-constexpr int kWideMaxRows = 192;
+// The wide form for 17..192 token rows on wide N (the LM heads, mtpk_gemm.hip k_gemm_wide):
+// one row group of token tiles against 16 x 8 RT-row weight tiles, the token rows staged by
+// direct-to-LDS loads. Every weight is read once for all rows; the 64-row groups would stream the
+// tile's weights once per group. Up to 64 rows the rows are padded to four token tiles and a
+// tile is 512 weight rows (RT = 4), above that 8 or 12 token tiles against 256 rows (RT = 2,
+// the accumulators' share of the registers). Measured on [M, 4096] x [248320, 4096] with the
+// argmax epilogue: 372-374 us from 17 to 64 rows against 391-410 us for the 8-wave skinny tiles
+// (128 rows, the token rows staged per tile twice as often), equal at 16 rows.
+constexpr int kWideMinRows = 17, kWideMaxRows = 192;
 inline bool gemm_wide(int64_t m, int64_t n, int epi) {
-  return m > 64 && m <= kWideMaxRows && epi != kEpiSilu &&
+  return m >= kWideMinRows && m <= kWideMaxRows && epi != kEpiSilu &&
          gemm_cols(n, epi) >= 256 * 2 * (int64_t)device_cu_count();
 }
+inline int wide_row_tiles(int64_t m) { return m <= 64 ? 4 : 2; }
 
 inline int64_t gemm_tiles(int64_t m, int64_t n, int epi) {
-  const int64_t rows = gemm_wide(m, n, epi) ? 256 : 16 * gemm_waves(m, n, epi);
+  const int64_t rows = gemm_wide(m, n, epi) ? 16 * 8 * wide_row_tiles(m) : 16 * gemm_waves(m, n, epi);
   return (gemm_cols(n, epi) + rows - 1) / rows;
 }
 

@@ -128,9 +128,10 @@ def _dense_wide_rows(rows: int, w: torch.Tensor) -> bool:
 FUSED_ARGMAX_ROWS = 192
 """Greedy LM-head rows up to which `next_tokens` runs the GEMM with the argmax in its epilogue
 (the logits never reach memory). Measured on [M, 4096] x [248320, 4096] bf16 against the
-library GEMM + the argmax kernel: 390 against 401 us at 16 rows, 404 against 423 us at 48,
-427 against 433 us at 64, and at 192 rows (the wide form, `dense.argmax_linear`) 506.5 against
-519-520 us (hipBLASLt or rocBLAS, graph replay over two weight copies)."""
+library GEMM + the argmax kernel: 390 against 401 us at 16 rows (skinny tiles), 404 against 423
+us at 48 and 427 against 433 us at 64 on the skinny tiles, which the wide form's 512-row tiles
+then took to 372-374 us from 17 to 64 rows, and at 192 rows (the wide form's 256-row tiles)
+506.5 against 519-520 us (hipBLASLt or rocBLAS, graph replay over two weight copies)."""
 
 
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:

@@ -35,7 +35,9 @@ def _close(got, want):
                                    (192, 4096, 20608), (192, 8192, 4096), (100, 1024, 513),
                                    (256, 256, 66000), (130, 4096, 512),
                                    # the wide form: one group of up to 12 token tiles, 256-row tiles
-                                   (192, 4096, 248320), (100, 1024, 140000), (65, 512, 131100)])
+                                   (192, 4096, 248320), (100, 1024, 140000), (65, 512, 131100),
+                                   # ... and of 4 token tiles (17..64 rows, padded) on 512-row tiles
+                                   (17, 256, 131100), (48, 4096, 140001), (64, 1024, 131072)])
 def test_linear_matches_fp32(dev, m, k, n):
     x, w = _inputs(dev, m, k, n, m + n)
     assert dense.fits(x, w)
@@ -55,7 +57,7 @@ def test_silu_linear_matches_swiglu(dev, m, k, inter):
 
 
 @pytest.mark.parametrize("m,n", [(48, 248320), (1, 248320), (7, 1000), (192, 248320), (70, 5000),
-                                 (100, 248320), (150, 140001)])
+                                 (100, 248320), (150, 140001), (17, 248320), (64, 131073), (33, 140001)])
 def test_argmax_linear_is_the_argmax_of_its_bf16_logits(dev, m, n):
     x, w = _inputs(dev, m, 4096, n, 3 + m)
     idx = dense.argmax_linear(x, w)
