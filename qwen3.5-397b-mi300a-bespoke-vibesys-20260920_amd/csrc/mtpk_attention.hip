@@ -131,6 +131,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
   // step r % t). Lanes of A (row c) load their row; rows past R read zeros.
   const int rbase = kAttnRows * rg + 16 * wave;
   const int ra = rbase + c;
+  const bool wave_live = rbase < R;  // uniform
   bf16x8_t qa[G::kDs];
   {
     const bool live = ra < R;
@@ -220,6 +221,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_paged_attention(
     stage_store(key0);
     __syncthreads();
     if (kn < k1) stage_load(kn, p0, p1);  // next tile in flight meanwhile
+    // A wave whose 16 query rows all lie past R (t = 1: 16 rows per kv head, one wave's worth)
+    // stages its share of each tile and skips the tile's math and LDS reads.
+    if (!wave_live) continue;
 
     // S = Q K^T for keys key0 + (0..15) and key0 + 16 + (0..15)
     f32x4_t s0 = {0.f, 0.f, 0.f, 0.f}, s1 = {0.f, 0.f, 0.f, 0.f};
