@@ -64,7 +64,7 @@ def use_grouped(assignments: int, experts: int) -> bool:
     return assignments >= GROUPED_MIN_PER_EXPERT * max(experts, 1)
 
 
-_VERDICT_ATTR = "_mtpk_decode_exact"
+_SCALE_CHECK_ATTR = "_mtpk_decode_exact"
 """Attribute `supports` sets on the two scale tensors it checked: True when the in-register
 decode reproduces them, False when it refused them. It lives and dies with those tensor objects,
 so a freed address that a later tensor reuses inherits nothing, and a copy is checked anew."""
@@ -111,8 +111,8 @@ def supports(experts: dict) -> bool:
         and all(t.is_contiguous() for t in (gu, gus, dn, dns))
     )  # fmt: skip
     ok = bool(shapes and bw_scales_ok(experts))
-    setattr(gus, _VERDICT_ATTR, ok)
-    setattr(dns, _VERDICT_ATTR, ok)
+    setattr(gus, _SCALE_CHECK_ATTR, ok)
+    setattr(dns, _SCALE_CHECK_ATTR, ok)
     return ok
 
 
@@ -149,11 +149,11 @@ def _validate(x, experts, routing, top_k):
     if top_k > _mtpk.MAX_TOP_K:
         raise ValueError(f"top_k {top_k} exceeds {_mtpk.MAX_TOP_K}")
     gus, dns = experts["gate_up_scale"], experts["down_scale"]
-    verdict = (getattr(gus, _VERDICT_ATTR, None), getattr(dns, _VERDICT_ATTR, None))
+    verdict = (getattr(gus, _SCALE_CHECK_ATTR, None), getattr(dns, _SCALE_CHECK_ATTR, None))
     if None in verdict and x.device.type == "cuda" and not torch.cuda.is_current_stream_capturing():
         # scale tensors no loader checked (a copy, a hand-built dict): scanned once, here
         supports(experts)
-        verdict = (getattr(gus, _VERDICT_ATTR), getattr(dns, _VERDICT_ATTR))
+        verdict = (getattr(gus, _SCALE_CHECK_ATTR), getattr(dns, _SCALE_CHECK_ATTR))
     if False in verdict:
         raise ValueError("these experts failed supports(): a block with e8m0 scale 255 holds a "
                          "nonzero code, which the in-register decode cannot reproduce")
