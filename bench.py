@@ -523,6 +523,12 @@ def accept_bench(dev, b=48, k=3, vocab=248320, temperature=0.7):
         return graph_mtp.greedy_accept(sa, draft_tok, active, pos, budget, stops, 3)
 
     def rejection(c=0):
+        # the sampler's launches also write every acceptance output (mtpk_rejection_accept)
+        return graph_mtp.rejection_accept(targets[c], drafts[c], draft_tok, u_acc, u_smp,
+                                          temperature, active, pos, budget, stops, 3,
+                                          workspace=ws)[0]
+
+    def rejection_2(c=0):
         _, _, em, _ = graph_mtp.rejection_sample(targets[c], drafts[c], draft_tok, u_acc, u_smp,
                                                  temperature, workspace=ws)
         return graph_mtp.greedy_accept(em, draft_tok, active, pos, budget, stops, 3)
@@ -530,14 +536,17 @@ def accept_bench(dev, b=48, k=3, vocab=248320, temperature=0.7):
     us_g = _time_graph(greedy, 3, 30)
     us_g3 = _time_graph(greedy_3, 3, 30)
     us_r = _time_graph(rejection, 3, 30)
+    us_r2 = _time_graph(rejection_2, 3, 30)
     eager_g = _time_calls(lambda: greedy(0), 50)
     eager_r = _time_calls(lambda: rejection(0), 50)
     acc_g = float(greedy().accept_len.float().mean())
     if not torch.equal(greedy().accept_len, greedy_3().accept_len):
         raise RuntimeError("greedy acceptance: the two-launch and three-launch paths differ")
     acc_r = float(rejection().accept_len.float().mean())
+    if not torch.equal(rejection().bonus, rejection_2().bonus):
+        raise RuntimeError("rejection acceptance: the fused and the two-call paths differ")
     logit_bytes = b * t * vocab * 2
-    log(f"accept: greedy {us_g:.1f} us (argmax finished in a third launch {us_g3:.1f}), rejection {us_r:.1f} us (T={temperature}; graph replay, "
+    log(f"accept: greedy {us_g:.1f} us (argmax finished in a third launch {us_g3:.1f}), rejection {us_r:.1f} us (sample then accept as two calls {us_r2:.1f}; T={temperature}; graph replay, "
         f"eager calls {eager_g:.1f} / {eager_r:.1f} us), mean accept {acc_g:.2f} / {acc_r:.2f}")
     return {
         "workload": f"C4 acceptance, target/draft bf16 [{b}, {t}, {vocab}], T={temperature}",
@@ -546,6 +555,7 @@ def accept_bench(dev, b=48, k=3, vocab=248320, temperature=0.7):
         "greedy_gbs": round(logit_bytes / us_g / 1e3, 1),
         "greedy_us_three_launches": round(us_g3, 2),
         "rejection_us": round(us_r, 2),
+        "rejection_us_sample_then_accept": round(us_r2, 2),
         "rejection_gbs": round((logit_bytes + b * k * vocab * 2) / us_r / 1e3, 1),
         "greedy_us_eager": round(eager_g, 2),
         "rejection_us_eager": round(eager_r, 2),

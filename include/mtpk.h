@@ -39,7 +39,7 @@ const char* mtpk_status_string(int status);
 
 /* ABI revision of this header; bumped on any signature change. The library returns the value
  * it was built with, and the Python binding refuses a library whose value differs. */
-#define MTPK_ABI_VERSION 3
+#define MTPK_ABI_VERSION 4
 int mtpk_abi_version(void);
 
 /* ---------------------------------------------------------------- MXFP4 dequant
@@ -403,6 +403,23 @@ int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int6
                           const float* u_sample, float temperature, void* workspace,
                           int64_t workspace_bytes, int64_t* accept_len, int64_t* token,
                           int64_t* emitted, float* margin, void* stream);
+
+/* mtpk_rejection_sample followed by the round's acceptance outputs in the same launches: what
+ * mtpk_greedy_accept gives with `emitted` as the step argmax (stop ids, budget, every rollback
+ * index), here taken from the sampler's accept length a (the stop ids and the budget can only
+ * shorten the accept below a, through the drafts), so no acceptance launch follows. No reference
+ * counterpart (as mtpk_rejection_sample). Inputs as mtpk_rejection_sample, plus active u8 [B],
+ * pos / budget i64 [B], stops i64 [B, n_stops], conv_k1; outputs as mtpk_greedy_accept
+ * (accept_len, lengths, token, emitted required; the others may be NULL), B <= 1024. */
+int mtpk_rejection_accept(const void* target, const void* draft, int dtype, int64_t batch, int k,
+                          int64_t vocab, const int64_t* draft_tokens, const float* u_accept,
+                          const float* u_sample, float temperature, void* workspace,
+                          int64_t workspace_bytes, const uint8_t* active, const int64_t* pos,
+                          const int64_t* budget, const int64_t* stops, int n_stops, int conv_k1,
+                          int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                          int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                          int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                          int64_t* hidden_src, int64_t* token, int64_t* emitted, void* stream);
 
 /* Temperature sampling of one token per row, the draft step's sampler in sampling mode (the
  * reference's draft step is greedy only: mtp.py:640-658). logits f32|bf16 [rows, vocab]

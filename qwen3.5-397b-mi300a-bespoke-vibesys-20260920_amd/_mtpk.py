@@ -20,7 +20,7 @@ LIB_PATH = Path(os.environ.get("MTPK_LIB", str(HERE / "libmtpk.so")))
 F32, BF16, I32, I64, U8 = 0, 1, 2, 3, 4
 EINVAL, ENODEV, ETOOBIG = -1, -2, -3
 MOE_STATIC_SCRATCH = 64 << 20
-ABI_VERSION = 3
+ABI_VERSION = 4
 MAX_TOP_K = 32
 MAX_EXPERTS = 4096
 MAX_ROUTER_EXPERTS = 1024
@@ -194,6 +194,13 @@ _SIGNATURES: dict[str, tuple[object, list]] = {
         c_int,
         [c_void_p, c_void_p, c_int, c_int64, c_int, c_int64, c_void_p, c_void_p, c_void_p,
          ctypes.c_float, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "mtpk_rejection_accept": (
+        c_int,
+        [c_void_p, c_void_p, c_int, c_int64, c_int, c_int64, c_void_p, c_void_p, c_void_p,
+         ctypes.c_float, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_void_p],
     ),
     "mtpk_sample_workspace_bytes": (c_int64, [c_int64, c_int64]),
     "mtpk_sample_rows": (

@@ -150,6 +150,70 @@ __device__ inline float2 rs_row_stats(float2 v0, const float2* part, int64_t r, 
   return make_float2(m, wave_sum(s));
 }
 
+// The round's acceptance outputs in sampling mode (the outputs of greedy acceptance over the
+// emitted rows, `mtpk_greedy_accept`), made by the sampler's own launches. The sampler's accept
+// length a fixes all of them but the bonus token: emitted[s] is draft s for s < a and the drawn
+// token from a on, so the stop ids can only shorten the accept below a through the drafts, and
+// the budget clamps it the same way. lim = min(a, first stop among drafts 0 .. a - 1, budget - 1,
+// >= 0); lengths = lim + 1 on an active lane (1 otherwise), the bonus token emitted[lim]. Every
+// pointer but the inputs may be null, as for the greedy acceptance; `lengths` non-null turns
+// the outputs on.
+struct RsAccept {
+  const uint8_t* active;
+  const int64_t* pos;
+  const int64_t* budget;
+  const int64_t* stops;
+  int n_stops, conv_k1;
+  int64_t* accept_len;
+  int64_t* lengths;
+  int64_t* packed_src;
+  int32_t* packed_cu;
+  int64_t* conv_idx;
+  uint8_t* keep;
+  int64_t* bonus;
+  int64_t* next_pos;
+  int64_t* budget_left;
+  uint8_t* live;
+  int64_t* hidden_src;
+};
+
+__device__ inline bool rs_is_stop(const RsAccept& acc, int b, int64_t tok) {
+  const int64_t* srow = acc.stops + (int64_t)b * acc.n_stops;
+  bool hit = false;
+  for (int q = 0; q < acc.n_stops; ++q) hit |= srow[q] == tok;
+  return hit;
+}
+
+// Lane b's tables from the sampler's accept length a (one thread): returns lim.
+__device__ int rs_lane_tables(const RsAccept& acc, int b, int k, int a,
+                              const int64_t* __restrict__ draft_tokens) {
+  const int t = k + 1;
+  int lim = a;
+  for (int s = 0; s < a; ++s)
+    if (rs_is_stop(acc, b, draft_tokens[(int64_t)b * k + s])) {
+      lim = s;
+      break;
+    }
+  const int64_t bud = acc.budget[b];
+  if (bud - 1 < lim) lim = (int)(bud - 1);
+  if (lim < 0) lim = 0;
+  const bool act = acc.active[b] != 0;
+  const int len = act ? lim + 1 : 1;
+  if (acc.accept_len) acc.accept_len[b] = lim;
+  acc.lengths[b] = len;
+  if (acc.next_pos) acc.next_pos[b] = acc.pos[b] + lim + 1;
+  if (acc.budget_left) acc.budget_left[b] = bud - (lim + 1);
+  if (acc.hidden_src) acc.hidden_src[b] = (int64_t)b * t + lim;
+  if (acc.keep)
+    for (int s = 0; s < t; ++s) acc.keep[(int64_t)b * t + s] = (act && s <= lim) ? 1 : 0;
+  if (acc.conv_idx)
+    for (int w = 0; w < acc.conv_k1; ++w) {
+      const int v = len + w;
+      acc.conv_idx[(int64_t)b * acc.conv_k1 + w] = v < acc.conv_k1 + t - 1 ? v : acc.conv_k1 + t - 1;
+    }
+  return lim;
+}
+
 // Rejection decision for lane b by one workgroup of kDecideWaves waves: its waves take the t
 // verify rows in parallel (row softmax constants and the margin p(x) - u q(x)), then the first
 // negative margin is the accept length, and *s_item (LDS) the draw it leads to. Outputs are
@@ -161,7 +225,8 @@ __device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part
                                int k, float inv_t, const int64_t* __restrict__ draft_tokens,
                                const float* __restrict__ u_accept, int b, float* s_mg, float4* s_st,
                                RsItem* s_item, RsItem* __restrict__ items,
-                               int64_t* __restrict__ accept_len, float* __restrict__ margin) {
+                               int64_t* __restrict__ accept_len, float* __restrict__ margin,
+                               const RsAccept& acc) {
   const int t = k + 1;
   const int wv = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int64_t n_target = (int64_t)B * t;
@@ -210,7 +275,7 @@ __device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part
     it.trow = b * t + a;
     it.drow = a < k ? b * k + a : -1;
     it.a = a;
-    it.pad = 0;
+    it.pad = acc.lengths ? rs_lane_tables(acc, b, k, a, draft_tokens) : 0;  // lim
     it.mt = sa.x;
     it.st = sa.y;
     it.mq = sa.z;
@@ -247,14 +312,15 @@ __global__ __launch_bounds__(kWave) void k_rs_rows(const float2* __restrict__ pa
 __global__ __launch_bounds__(kRsThreads) void k_rs_decide(
     RsRows rr, const float2* __restrict__ part, int nchunk, int B, int k, float inv_t,
     const int64_t* __restrict__ draft_tokens, const float* __restrict__ u_accept,
-    RsItem* __restrict__ items, int64_t* __restrict__ accept_len, float* __restrict__ margin) {
+    RsItem* __restrict__ items, int64_t* __restrict__ accept_len, float* __restrict__ margin,
+    RsAccept acc) {
   static_assert(kRsThreads == kWave * kDecideWaves, "one decision per workgroup");
   __shared__ float s_mg[kMaxT];
   __shared__ float4 s_st[kMaxT];
   __shared__ RsItem s_item;
   const int b = blockIdx.x;
   rs_decide_lane(rr, part, nchunk, B, k, inv_t, draft_tokens, u_accept, b, s_mg, s_st, &s_item,
-                 items, accept_len, margin);
+                 items, accept_len, margin, acc);
 }
 
 // The draw weights in base-2 form: p = exp(l / T - mt) / st = exp2(l * a - bt) with a = log2(e) /
@@ -323,7 +389,7 @@ struct RsPickLds {
 __device__ void rs_pick(const RsRows& rr, const RsItem& it, const float2* row_mass, int nchunk,
                         float inv_t, float u, int64_t item, int64_t* __restrict__ token,
                         const int64_t* __restrict__ draft_tokens, int k,
-                        int64_t* __restrict__ emitted, RsPickLds& sh) {
+                        int64_t* __restrict__ emitted, RsPickLds& sh, const RsAccept& acc) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
   const int64_t dtok = emitted && tid < k ? draft_tokens[item * k + tid] : 0;
   if (wv == 0) {
@@ -407,17 +473,83 @@ __device__ void rs_pick(const RsRows& rr, const RsItem& it, const float2* row_ma
     if (tid == 0) token[item] = v;
     if (emitted) emitted[item * (k + 1) + tid] = tid < it.a ? dtok : v;
   }
+  // sampling-mode acceptance: the lane's bonus token emitted[lim] (lim in the item's pad) and
+  // whether the lane stays live, as the greedy acceptance over the emitted row gives them
+  if (acc.lengths && tid == 0) {
+    const int lim = it.pad;
+    const int64_t v = sh.best < 0 ? 0 : sh.best;
+    const int64_t bn = lim < it.a ? draft_tokens[item * k + lim] : v;
+    if (acc.bonus) acc.bonus[item] = bn;
+    if (acc.live)
+      acc.live[item] = (!rs_is_stop(acc, (int)item, bn) && acc.budget[item] - (lim + 1) > 0) ? 1 : 0;
+  }
+}
+
+// The pack offsets of sampling-mode acceptance, from the lanes' lengths (written by the decide
+// launch): packed_cu = exclusive prefix of lengths over the B lanes, and packed_src[dst] = lane
+// * t + local for the lane whose packed rows hold dst (as `mtpk_greedy_accept`). One workgroup,
+// four lanes per thread (B <= 1024).
+constexpr int kRsPackLanes = 4 * kRsThreads;
+
+__device__ void rs_pack(const RsAccept& acc, int B, int t) {
+  __shared__ int cu[kRsPackLanes + 1];
+  __shared__ int wtot[kRsThreads / kWave];
+  const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
+  int v[4], sum = 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = 4 * tid + q;
+    v[q] = j < B ? (int)acc.lengths[j] : 0;
+    sum += v[q];
+  }
+  const int inc = wave_incl_scan(sum, lane);
+  if (lane == kWave - 1) wtot[wv] = inc;
+  __syncthreads();
+  int run = inc - sum;
+  for (int w = 0; w < wv; ++w) run += wtot[w];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int j = 4 * tid + q;
+    run += v[q];
+    if (j < B) cu[j + 1] = run;
+  }
+  if (tid == 0) cu[0] = 0;
+  __syncthreads();
+  if (acc.packed_cu)
+    for (int j = tid; j <= B; j += kRsThreads) acc.packed_cu[j] = cu[j];
+  if (acc.packed_src)
+    for (int dst = tid; dst < B * t; dst += kRsThreads) {
+      int lo = 1, hi = B + 1;  // lane = #{i in 1..B : cu[i] <= dst}, clamped to B - 1
+      while (lo < hi) {
+        const int mid = (lo + hi) >> 1;
+        if (cu[mid] <= dst)
+          lo = mid + 1;
+        else
+          hi = mid;
+      }
+      int ln = lo - 1;
+      if (ln > B - 1) ln = B - 1;
+      int local = dst - cu[ln];
+      local = local < 0 ? 0 : (local > t - 1 ? t - 1 : local);
+      acc.packed_src[dst] = (int64_t)ln * t + local;
+    }
 }
 
 // The draw in a launch of its own (one workgroup per item), after the mass launch.
+// With sampling-mode acceptance one more workgroup (the last) makes the pack offsets.
 __global__ __launch_bounds__(kRsThreads) void k_rs_pick(
     RsRows rr, const RsItem* __restrict__ items, const float2* __restrict__ mass, int nchunk,
     float inv_t, const float* __restrict__ u_sample, int64_t* __restrict__ token,
-    const int64_t* __restrict__ draft_tokens, int k, int64_t* __restrict__ emitted) {
+    const int64_t* __restrict__ draft_tokens, int k, int64_t* __restrict__ emitted, int n_items,
+    RsAccept acc) {
   __shared__ RsPickLds sh;
   const int item = blockIdx.x;
+  if (item >= n_items) {  // uniform: the pack workgroup
+    rs_pack(acc, n_items, k + 1);
+    return;
+  }
   rs_pick(rr, items[item], mass + (int64_t)item * nchunk, nchunk, inv_t, u_sample[item], item,
-          token, draft_tokens, k, emitted, sh);
+          token, draft_tokens, k, emitted, sh, acc);
 }
 
 // Chunks per mass workgroup. Measured at config 4 (48 items of two 248320-logit rows): 1 chunk
@@ -539,12 +671,19 @@ int64_t mtpk_rejection_workspace_bytes(int64_t batch, int k, int64_t vocab) {
          align256(batch * nchunk * (int64_t)sizeof(float2));
 }
 
-int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int64_t batch, int k,
-                          int64_t vocab, const int64_t* draft_tokens, const float* u_accept,
-                          const float* u_sample, float temperature, void* workspace,
-                          int64_t workspace_bytes, int64_t* accept_len, int64_t* token,
-                          int64_t* emitted, float* margin, void* stream) {
-  if (!target || !u_sample || !workspace || !accept_len || !token) return MTPK_EINVAL;
+}  // extern "C"
+
+namespace {
+
+// The four launches of rejection sampling; with acc.lengths set also the acceptance outputs
+// (decide writes the lane tables, pick the bonus token and liveness, one more pick workgroup
+// the pack offsets).
+int rejection_launch(const void* target, const void* draft, int dtype, int64_t batch, int k,
+                     int64_t vocab, const int64_t* draft_tokens, const float* u_accept,
+                     const float* u_sample, float temperature, void* workspace,
+                     int64_t workspace_bytes, int64_t* accept_len, int64_t* token,
+                     int64_t* emitted, float* margin, const RsAccept& acc, void* stream) {
+  if (!target || !u_sample || !workspace || !token) return MTPK_EINVAL;
   if (dtype != MTPK_F32 && dtype != MTPK_BF16) return MTPK_EINVAL;
   if (batch <= 0 || batch > 65535 || k < 0 || k > 63 || vocab <= 0 || vocab > INT32_MAX / 2)
     return MTPK_EINVAL;
@@ -569,14 +708,52 @@ int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int6
   if (rc) return rc;
   hipLaunchKernelGGL(k_rs_decide, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, w.part,
                      (int)nchunk, (int)batch, k, inv_t, draft_tokens, u_accept, w.items, accept_len,
-                     margin);
+                     margin, acc);
   if ((rc = status_of(hipGetLastError()))) return rc;
   hipLaunchKernelGGL(k_rs_mass<kRsMassChunks>, dim3((unsigned)rs_groups(nchunk), (unsigned)batch),
                      dim3(kRsThreads), 0, st, rr, w.items, (int)nchunk, inv_t, w.mass);
   if ((rc = status_of(hipGetLastError()))) return rc;
-  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)batch), dim3(kRsThreads), 0, st, rr, w.items, w.mass,
-                     (int)nchunk, inv_t, u_sample, token, draft_tokens, k, emitted);
+  const bool pack = acc.lengths && (acc.packed_cu || acc.packed_src);
+  hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)(batch + (pack ? 1 : 0))), dim3(kRsThreads), 0, st, rr,
+                     w.items, w.mass, (int)nchunk, inv_t, u_sample, token, draft_tokens, k, emitted,
+                     (int)batch, acc);
   return status_of(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" {
+
+int mtpk_rejection_sample(const void* target, const void* draft, int dtype, int64_t batch, int k,
+                          int64_t vocab, const int64_t* draft_tokens, const float* u_accept,
+                          const float* u_sample, float temperature, void* workspace,
+                          int64_t workspace_bytes, int64_t* accept_len, int64_t* token,
+                          int64_t* emitted, float* margin, void* stream) {
+  if (!accept_len) return MTPK_EINVAL;
+  const RsAccept none{};
+  return rejection_launch(target, draft, dtype, batch, k, vocab, draft_tokens, u_accept, u_sample,
+                          temperature, workspace, workspace_bytes, accept_len, token, emitted,
+                          margin, none, stream);
+}
+
+int mtpk_rejection_accept(const void* target, const void* draft, int dtype, int64_t batch, int k,
+                          int64_t vocab, const int64_t* draft_tokens, const float* u_accept,
+                          const float* u_sample, float temperature, void* workspace,
+                          int64_t workspace_bytes, const uint8_t* active, const int64_t* pos,
+                          const int64_t* budget, const int64_t* stops, int n_stops, int conv_k1,
+                          int64_t* accept_len, int64_t* lengths, int64_t* packed_src,
+                          int32_t* packed_cu, int64_t* conv_idx, uint8_t* keep, int64_t* bonus,
+                          int64_t* next_pos, int64_t* budget_left, uint8_t* live,
+                          int64_t* hidden_src, int64_t* token, int64_t* emitted, void* stream) {
+  if (!active || !budget || !accept_len || !lengths) return MTPK_EINVAL;
+  if (batch > kRsPackLanes || n_stops < 0 || (n_stops > 0 && !stops) || conv_k1 < 0) return MTPK_EINVAL;
+  if (next_pos && !pos) return MTPK_EINVAL;
+  const RsAccept acc{active,     pos,     budget,  stops, n_stops,  conv_k1,     accept_len,
+                     lengths,    packed_src, packed_cu, conv_idx, keep, bonus, next_pos,
+                     budget_left, live,   hidden_src};
+  return rejection_launch(target, draft, dtype, batch, k, vocab, draft_tokens, u_accept, u_sample,
+                          temperature, workspace, workspace_bytes, nullptr, token, emitted, nullptr,
+                          acc, stream);
 }
 
 int64_t mtpk_sample_workspace_bytes(int64_t rows, int64_t vocab) {
@@ -609,8 +786,9 @@ int mtpk_sample_rows(const void* logits, int dtype, int64_t rows, int64_t vocab,
   hipLaunchKernelGGL(k_rs_mass<kRsMassChunks>, dim3((unsigned)rs_groups(nchunk), (unsigned)rows),
                      dim3(kRsThreads), 0, st, rr, w.items, (int)nchunk, inv_t, w.mass);
   if ((rc = status_of(hipGetLastError()))) return rc;
+  const RsAccept none{};
   hipLaunchKernelGGL(k_rs_pick, dim3((unsigned)rows), dim3(kRsThreads), 0, st, rr, w.items, w.mass,
-                     (int)nchunk, inv_t, u, token, nullptr, 0, nullptr);
+                     (int)nchunk, inv_t, u, token, nullptr, 0, nullptr, (int)rows, none);
   return status_of(hipGetLastError());
 }
 

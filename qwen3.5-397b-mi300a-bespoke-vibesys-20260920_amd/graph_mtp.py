@@ -848,11 +848,56 @@ def rejection_sample(target_logits: torch.Tensor, draft_logits: torch.Tensor, dr
 def rejection_accept(target_logits: torch.Tensor, draft_logits: torch.Tensor, draft_tokens: torch.Tensor,
                      u_accept: torch.Tensor, u_sample: torch.Tensor, temperature: float,
                      active: torch.Tensor, pos: torch.Tensor, budget: torch.Tensor, stops: torch.Tensor,
-                     conv_k1: int) -> tuple[AcceptResult, torch.Tensor]:
-    """Sampling-mode acceptance with the round's rollback indices: rejection sampling, then
-    `greedy_accept` over the emitted tokens (which applies the stop ids and the budget).
+                     conv_k1: int, *, workspace: torch.Tensor | None = None,
+                     out: AcceptResult | None = None) -> tuple[AcceptResult, torch.Tensor]:
+    """Sampling-mode acceptance with the round's rollback indices (`mtpk_rejection_accept`):
+    rejection sampling, and in the same launches what `greedy_accept` gives over the emitted
+    tokens (the stop ids and the budget applied), taken from the sampler's accept length.
     Returns `(AcceptResult, emitted [B, k+1])`; committed ids are `emitted[j, :a+1]`."""
-    _, _, emitted, _ = rejection_sample(target_logits, draft_logits, draft_tokens, u_accept, u_sample,
-                                        temperature)
-    res = greedy_accept(emitted, draft_tokens, active, pos, budget, stops, conv_k1)
-    return res, emitted
+    device = _mtpk.require_device(target_logits, draft_logits, draft_tokens, u_accept, u_sample,
+                                  active, pos, budget, stops)
+    b, t, vocab = target_logits.shape
+    k = t - 1
+    if draft_logits.shape != (b, k, vocab) or draft_logits.dtype != target_logits.dtype:
+        raise ValueError("draft_logits must be [B, k, V] of target_logits' dtype")
+    if draft_tokens.shape != (b, k) or draft_tokens.dtype != torch.int64:
+        raise ValueError("draft_tokens must be int64 [B, k]")
+    if u_accept.shape != (b, k) or u_sample.shape != (b,):
+        raise ValueError("u_accept must be [B, k] and u_sample [B]")
+    if not temperature > 0:
+        raise ValueError("rejection sampling needs temperature > 0 (greedy rounds use greedy_accept)")
+    for name, ten in (("pos", pos), ("budget", budget), ("stops", stops)):
+        if ten.dtype != torch.int64:
+            raise ValueError(f"{name} must be int64")
+    if active.dtype != torch.bool or active.shape != (b,) or stops.dim() != 2 or stops.shape[0] != b:
+        raise ValueError("active must be bool [B] and stops [B, S]")
+    tl, dl = target_logits.contiguous(), draft_logits.contiguous()
+    ua, us = u_accept.float().contiguous(), u_sample.float().contiguous()
+    dt = draft_tokens.contiguous()
+    st = stops.contiguous()
+    ws = workspace if workspace is not None else rejection_workspace(b, k, vocab, device)
+    long = dict(dtype=torch.long, device=device)
+    if out is None:
+        out = AcceptResult(
+            torch.empty(b, **long), torch.empty(b, **long), torch.empty(b * t, **long),
+            torch.empty(b + 1, dtype=torch.int32, device=device),
+            torch.empty(b, conv_k1, **long), torch.empty(b, t, dtype=torch.bool, device=device),
+            torch.empty(b, **long), torch.empty(b, **long), torch.empty(b, **long),
+            torch.empty(b, dtype=torch.bool, device=device), torch.empty(b, **long),
+        )
+    tok, emitted = torch.empty(b, **long), torch.empty(b, t, **long)
+    _mtpk.check(
+        _mtpk.lib().mtpk_rejection_accept(
+            tl.data_ptr(), dl.data_ptr(), _mtpk.float_code(tl.dtype), b, k, vocab, dt.data_ptr(),
+            ua.data_ptr(), us.data_ptr(), float(temperature), ws.data_ptr(), ws.numel(),
+            active.contiguous().data_ptr(), pos.contiguous().data_ptr(), budget.contiguous().data_ptr(),
+            st.data_ptr(), st.shape[1], conv_k1, out.accept_len.data_ptr(), out.lengths.data_ptr(),
+            out.packed_src.data_ptr(), out.packed_cu.data_ptr(),
+            out.conv_idx.data_ptr() if conv_k1 > 0 else None, out.keep.data_ptr(),
+            out.bonus.data_ptr(), out.next_pos.data_ptr(), out.budget_left.data_ptr(),
+            out.live.data_ptr(), out.hidden_src.data_ptr(), tok.data_ptr(), emitted.data_ptr(),
+            _mtpk.stream_of(device),
+        ),
+        "mtpk_rejection_accept",
+    )  # fmt: skip
+    return out, emitted

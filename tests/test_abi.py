@@ -124,6 +124,13 @@ def test_rejected_arguments_launch_nothing(lib):
     assert lib.mtpk_rejection_sample(fake, fake, 1, 4, 3, 100, fake, fake, fake, 0.0, fake, 1 << 30,
                                      fake, fake, None, None, None) == -1
     assert lib.mtpk_sample_rows(fake, 1, 4, 100, -1.0, fake, fake, 1 << 30, fake, None) == -1
+    # fused sampling-mode acceptance: no active mask, then more lanes than the pack takes
+    assert lib.mtpk_rejection_accept(fake, fake, 1, 4, 3, 100, fake, fake, fake, 0.7, fake, 1 << 30,
+                                     None, fake, fake, None, 0, 3, fake, fake, None, None, None,
+                                     None, None, None, None, None, None, fake, fake, None) == -1
+    assert lib.mtpk_rejection_accept(fake, fake, 1, 1025, 3, 100, fake, fake, fake, 0.7, fake,
+                                     1 << 40, fake, fake, fake, None, 0, 3, fake, fake, None, None,
+                                     None, None, None, None, None, None, None, fake, fake, None) == -1
     assert lib.mtpk_rejection_workspace_bytes(48, 3, 248320) >= 48 * 7 * 61 * 8
     assert lib.mtpk_sample_workspace_bytes(4, 100) == lib.mtpk_rejection_workspace_bytes(4, 0, 100)
     # gated delta rule: null state, unsupported k_dim, t out of range, neither output nor commit

@@ -203,3 +203,33 @@ def test_sample_rows_masked_chunk(dev) -> None:
         p = rj.softmax_t(logits[r].astype(np.float64), 0.7)
         assert _token_consistent(p, float(u[r]), int(got[r]))
         assert not 4096 <= got[r] < 8192
+
+
+@pytest.mark.parametrize("b,k,dtype", [(48, 3, torch.bfloat16), (300, 1, torch.float32),
+                                       (7, 0, torch.float32), (1024, 3, torch.bfloat16)])
+def test_fused_acceptance_equals_sample_then_greedy_accept(dev, b, k, dtype) -> None:
+    """`rejection_accept` (one pass: the sampler's launches also write every acceptance output)
+    equals `rejection_sample` followed by `greedy_accept` over the emitted tokens, bit for bit:
+    inactive lanes, budgets of 0..5, stop ids on drafts and on drawn tokens, and up to 1024
+    lanes (the pack's scan over several waves)."""
+    vocab = 3000
+    tt, dd, _, _, drafts, ua, us = _case(b, k, vocab, dtype, 40 + b + k, noise=0.7)
+    g = np.random.default_rng(b + k)
+    args = (tt.to(dev), dd.to(dev), torch.from_numpy(drafts).to(dev), torch.from_numpy(ua).to(dev),
+            torch.from_numpy(us).to(dev), 0.7)
+    _, _, emitted, _ = graph_mtp.rejection_sample(*args)
+    em = emitted.cpu().numpy()
+    active = torch.from_numpy(g.random(b) < 0.85).to(dev)
+    pos = torch.from_numpy(g.integers(0, 8000, b)).to(dev)
+    budget = torch.from_numpy(g.integers(0, 6, b)).to(dev)
+    stops = np.full((b, 3), -1, dtype=np.int64)
+    if k > 0:
+        stops[::3, 0] = drafts[::3, 0]          # a stop on the first draft
+    stops[1::4, 1] = em[1::4, min(1, k)]        # on a later column: a draft or the drawn token
+    stops = torch.from_numpy(stops).to(dev)
+    want = graph_mtp.greedy_accept(emitted, args[2], active, pos, budget, stops, 3)
+    got, em2 = graph_mtp.rejection_accept(*args, active, pos, budget, stops, 3)
+    assert torch.equal(em2, emitted)
+    for name in ("accept_len", "lengths", "packed_src", "packed_cu", "conv_idx", "keep", "bonus",
+                 "next_pos", "budget_left", "live", "hidden_src"):
+        assert torch.equal(getattr(got, name), getattr(want, name)), name
