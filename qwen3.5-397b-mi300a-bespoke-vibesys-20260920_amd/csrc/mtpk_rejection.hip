@@ -177,35 +177,68 @@ struct RsAccept {
   int64_t* hidden_src;
 };
 
-__device__ inline bool rs_is_stop(const RsAccept& acc, int b, int64_t tok) {
+// A lane's acceptance inputs that do not depend on the draw, loaded into registers where a
+// launch starts (stop ids and drafts up to kRsPre of them), so that the tables written after
+// the decision wait for no memory round trip.
+constexpr int kRsPre = 8;
+struct RsLanePre {
+  int64_t bud, pos;
+  bool act;
+  int64_t sv[kRsPre], dv[kRsPre];
+};
+
+__device__ inline RsLanePre rs_lane_pre(const RsAccept& acc, int b, int k,
+                                        const int64_t* __restrict__ draft_tokens) {
+  RsLanePre p;
+  p.bud = acc.budget[b];
+  p.pos = acc.pos ? acc.pos[b] : 0;
+  p.act = acc.active[b] != 0;
   const int64_t* srow = acc.stops + (int64_t)b * acc.n_stops;
+#pragma unroll
+  for (int u = 0; u < kRsPre; ++u) {
+    p.sv[u] = u < acc.n_stops ? srow[u] : 0;
+    p.dv[u] = u < k ? draft_tokens[(int64_t)b * k + u] : 0;
+  }
+  return p;
+}
+
+__device__ inline bool rs_is_stop(const RsAccept& acc, const RsLanePre& p, int b, int64_t tok) {
   bool hit = false;
-  for (int q = 0; q < acc.n_stops; ++q) hit |= srow[q] == tok;
+#pragma unroll
+  for (int u = 0; u < kRsPre; ++u) hit |= u < acc.n_stops && p.sv[u] == tok;
+  for (int q = kRsPre; q < acc.n_stops; ++q) hit |= acc.stops[(int64_t)b * acc.n_stops + q] == tok;
   return hit;
 }
 
+// draft s of lane b, from the registers when s < kRsPre (selects, not indexing)
+__device__ inline int64_t rs_draft(const RsLanePre& p, int b, int k, int s,
+                                   const int64_t* __restrict__ draft_tokens) {
+  int64_t v = 0;
+#pragma unroll
+  for (int u = 0; u < kRsPre; ++u) v = u == s ? p.dv[u] : v;
+  return s < kRsPre ? v : draft_tokens[(int64_t)b * k + s];
+}
+
 // Lane b's tables from the sampler's accept length a (one thread): returns lim.
-__device__ int rs_lane_tables(const RsAccept& acc, int b, int k, int a,
+__device__ int rs_lane_tables(const RsAccept& acc, const RsLanePre& p, int b, int k, int a,
                               const int64_t* __restrict__ draft_tokens) {
   const int t = k + 1;
   int lim = a;
   for (int s = 0; s < a; ++s)
-    if (rs_is_stop(acc, b, draft_tokens[(int64_t)b * k + s])) {
+    if (rs_is_stop(acc, p, b, rs_draft(p, b, k, s, draft_tokens))) {
       lim = s;
       break;
     }
-  const int64_t bud = acc.budget[b];
-  if (bud - 1 < lim) lim = (int)(bud - 1);
+  if (p.bud - 1 < lim) lim = (int)(p.bud - 1);
   if (lim < 0) lim = 0;
-  const bool act = acc.active[b] != 0;
-  const int len = act ? lim + 1 : 1;
+  const int len = p.act ? lim + 1 : 1;
   if (acc.accept_len) acc.accept_len[b] = lim;
   acc.lengths[b] = len;
-  if (acc.next_pos) acc.next_pos[b] = acc.pos[b] + lim + 1;
-  if (acc.budget_left) acc.budget_left[b] = bud - (lim + 1);
+  if (acc.next_pos) acc.next_pos[b] = p.pos + lim + 1;
+  if (acc.budget_left) acc.budget_left[b] = p.bud - (lim + 1);
   if (acc.hidden_src) acc.hidden_src[b] = (int64_t)b * t + lim;
   if (acc.keep)
-    for (int s = 0; s < t; ++s) acc.keep[(int64_t)b * t + s] = (act && s <= lim) ? 1 : 0;
+    for (int s = 0; s < t; ++s) acc.keep[(int64_t)b * t + s] = (p.act && s <= lim) ? 1 : 0;
   if (acc.conv_idx)
     for (int w = 0; w < acc.conv_k1; ++w) {
       const int v = len + w;
@@ -230,6 +263,8 @@ __device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part
   const int t = k + 1;
   const int wv = threadIdx.x / kWave, lane = threadIdx.x & (kWave - 1);
   const int64_t n_target = (int64_t)B * t;
+  RsLanePre pre{};
+  if (acc.lengths && threadIdx.x == 0) pre = rs_lane_pre(acc, b, k, draft_tokens);
   for (int i = wv; i < t; i += kDecideWaves) {
     // The rows' chunk partials, then the token and its two logits: the partials do not depend
     // on the token, so their loads are in flight while the token's chain runs.
@@ -275,7 +310,7 @@ __device__ void rs_decide_lane(const RsRows& rr, const float2* __restrict__ part
     it.trow = b * t + a;
     it.drow = a < k ? b * k + a : -1;
     it.a = a;
-    it.pad = acc.lengths ? rs_lane_tables(acc, b, k, a, draft_tokens) : 0;  // lim
+    it.pad = acc.lengths ? rs_lane_tables(acc, pre, b, k, a, draft_tokens) : 0;  // lim
     it.mt = sa.x;
     it.st = sa.y;
     it.mq = sa.z;
@@ -392,6 +427,12 @@ __device__ void rs_pick(const RsRows& rr, const RsItem& it, const float2* row_ma
                         int64_t* __restrict__ emitted, RsPickLds& sh, const RsAccept& acc) {
   const int tid = threadIdx.x, lane = tid & (kWave - 1), wv = tid / kWave;
   const int64_t dtok = emitted && tid < k ? draft_tokens[item * k + tid] : 0;
+  RsLanePre pre{};
+  int64_t lim_draft = 0;  // emitted[lim] when lim < a: draft lim
+  if (acc.lengths && tid == 0) {
+    pre = rs_lane_pre(acc, (int)item, k, draft_tokens);
+    if (it.pad < it.a) lim_draft = rs_draft(pre, (int)item, k, it.pad, draft_tokens);
+  }
   if (wv == 0) {
     const float2 m0 = lane < nchunk ? row_mass[lane] : make_float2(0.f, 0.f);
     float tr = m0.x, tp = m0.y;
@@ -478,10 +519,9 @@ __device__ void rs_pick(const RsRows& rr, const RsItem& it, const float2* row_ma
   if (acc.lengths && tid == 0) {
     const int lim = it.pad;
     const int64_t v = sh.best < 0 ? 0 : sh.best;
-    const int64_t bn = lim < it.a ? draft_tokens[item * k + lim] : v;
+    const int64_t bn = lim < it.a ? lim_draft : v;
     if (acc.bonus) acc.bonus[item] = bn;
-    if (acc.live)
-      acc.live[item] = (!rs_is_stop(acc, (int)item, bn) && acc.budget[item] - (lim + 1) > 0) ? 1 : 0;
+    if (acc.live) acc.live[item] = (!rs_is_stop(acc, pre, (int)item, bn) && pre.bud - (lim + 1) > 0) ? 1 : 0;
   }
 }
 
